@@ -1,0 +1,214 @@
+"""Benchmark of the paged decode attention hot path on one MI355X.
+
+Workload (default): Qwen2.5-7B-shape paged decode — 64 sequences, 28 query /
+4 KV heads (GQA 7), head_dim 128, block 16, bf16, context U{512..4096}, block
+tables drawn from a random permutation of a pool 1.25x the blocks needed,
+q/K/V ~ N(0, 1) (synthetic: random values, no checkpoint). One step = one
+decode-attention call for the whole batch (one layer).
+
+Timing: W warm-up calls, then K calls captured in one hipGraph and replayed
+between two events on the launch stream, with torch.cuda.synchronize() on
+both sides. Calls rotate over R disjoint copies of the pool + block tables so
+consecutive calls do not hit K/V left in the 256 MB MALL by the previous one.
+
+Prints one JSON line: value = achieved KV GB/s (algorithmic bytes sum(ctx) *
+2 * H_kv * D * 2 per call / time per call), plus us_per_call, a roofline
+object for the decode kernel and the CPU baseline: the oracle's restatement of
+the reference naive-gather fallback (gather -> repeat_kv -> masked softmax,
+in bf16 like the reference) timed on the host cores on the same inputs.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
+METRIC = "paged decode attn µs/call + achieved KV HBM GB/s (% of peak), Qwen2.5-7B shape"
+
+
+def _parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--config", default="qwen7b-bf16")
+    p.add_argument("--rotations", type=int, default=3)
+    p.add_argument("--partition", type=int, default=0, help="split-KV partition tokens (0 = library default)")
+    p.add_argument("--cpu-iters", type=int, default=3, help="timed CPU-baseline iterations (0 = skip)")
+    p.add_argument("--cpu-seqs", type=int, default=0, help="sequences in the CPU sample (0 = all)")
+    p.add_argument("--check", action="store_true", help="also check the output against the oracle")
+    return p.parse_args()
+
+
+def _gpu_decode(case, args):
+    from infrared_amd import kernels
+
+    cfg = case.config
+    dev = case.q.device
+    b, max_blocks = cfg.num_seqs, case.block_tables[0].shape[1]
+    part = args.partition or kernels.default_partition(b, cfg.num_kv_heads, max_blocks, cfg.block_size)
+    ws_bytes = kernels.decode_workspace_bytes(
+        b, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, max_blocks, cfg.block_size, part
+    )
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    outs = [torch.empty_like(case.q) for _ in case.block_tables]
+
+    def call(i: int) -> None:
+        r = i % len(case.block_tables)
+        kernels.paged_decode(
+            case.q, case.k_cache, case.v_cache, case.block_tables[r], case.context_lens,
+            cfg.block_size, cfg.scale, out=outs[r], partition_tokens=part, workspace=ws,
+        )
+
+    for i in range(args.warmup):
+        call(i)
+    torch.cuda.synchronize()
+
+    # eager (host-launched) timing, for reference
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(args.steps):
+        call(i)
+    e.record()
+    torch.cuda.synchronize()
+    eager_ms = s.elapsed_time(e) / args.steps
+
+    # graph-replayed timing: the K calls back to back on the device
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        call(0)
+    torch.cuda.current_stream().wait_stream(stream)
+    with torch.cuda.graph(graph):
+        for i in range(args.steps):
+            call(i)
+    graph.replay()  # warm replay
+    torch.cuda.synchronize()
+    s.record()
+    graph.replay()
+    e.record()
+    torch.cuda.synchronize()
+    graph_ms = s.elapsed_time(e) / args.steps
+    return part, ws_bytes, eager_ms, graph_ms, outs
+
+
+def _cpu_baseline(case, args):
+    from oracle import naive as O
+
+    cfg = case.config
+    n = args.cpu_seqs or cfg.num_seqs
+    bt = case.block_tables[0][:n].cpu()
+    ctx = case.context_lens[:n].cpu().tolist()
+    tables = [row.tolist() for row in bt]
+    t_max = max(ctx)
+    gs = O.decode_gather_slots(tables, ctx, cfg.block_size, t_max)
+    mask = O.decode_mask(ctx, t_max, cfg.dtype)
+    q = case.q[:n, None].cpu()
+    kc, vc = case.k_cache.cpu(), case.v_cache.cpu()
+    threads = torch.get_num_threads()
+    O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, cfg.n_rep)  # warm-up
+    times = []
+    for _ in range(args.cpu_iters):
+        t0 = time.perf_counter()
+        O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, cfg.n_rep)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    esize = torch.tensor([], dtype=cfg.dtype).element_size()
+    kv = sum(ctx) * 2 * cfg.num_kv_heads * cfg.head_dim * esize
+    return {
+        "value": round(kv / t / 1e9, 4),
+        "unit": "GB/s",
+        "us_per_call": round(t * 1e6, 1),
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n} of {cfg.num_seqs} sequences (sum ctx {sum(ctx)}), naive gather+repeat_kv+"
+        f"masked softmax in {str(cfg.dtype).replace('torch.', '')}, median of {args.cpu_iters} "
+        "after 1 warm-up, torch CPU",
+    }
+
+
+def main() -> int:
+    args = _parse()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures the single-GPU hot path only; --gpus {args.gpus} is not supported "
+            "(the decode kernel shards by sequence / KV head with no exchange, see DESIGN.md)",
+            file=sys.stderr,
+        )
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    from infrared_amd.workloads import make_decode_case
+
+    case = make_decode_case(args.config, "cuda", rotations=args.rotations)
+    cfg = case.config
+    kv = case.kv_bytes
+    part, ws_bytes, eager_ms, graph_ms, outs = _gpu_decode(case, args)
+    us = graph_ms * 1e3
+    gbps = kv / (graph_ms * 1e-3) / 1e9
+    check = None
+    if args.check:
+        from oracle import naive as O
+
+        ref = O.decode_reference(
+            case.q.cpu(), case.k_cache.cpu(), case.v_cache.cpu(), case.block_tables[0].cpu(),
+            case.context_lens.cpu(), cfg.block_size, cfg.scale,
+        )
+        check = round((outs[0].float().cpu() - ref).abs().max().item(), 6)
+    cpu = _cpu_baseline(case, args) if args.cpu_iters > 0 else None
+    esize = torch.tensor([], dtype=cfg.dtype).element_size()
+    line = {
+        "metric": METRIC,
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "us_per_call": round(us, 2),
+        "frac_of_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(graph_ms, 5),
+        "eager_ms_per_step": round(eager_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": str(cfg.dtype).replace("torch.", "").replace("bfloat16", "bf16").replace("float32", "f32"),
+        "data": "synthetic",
+        "config": {
+            "workload": f"{cfg.name} paged decode: {cfg.num_seqs} seqs, {cfg.num_q_heads}q/{cfg.num_kv_heads}kv "
+            f"heads, head_dim {cfg.head_dim}, block {cfg.block_size}, ctx {cfg.ctx_kind}[{cfg.ctx_lo},{cfg.ctx_hi}]",
+            "num_seqs": cfg.num_seqs,
+            "sum_ctx": int(case.context_lens.long().sum()),
+            "kv_bytes_per_call": kv,
+            "rotations": args.rotations,
+            "partition_tokens": part,
+            "workspace_bytes": ws_bytes,
+            "bytes_per_token": 2 * cfg.num_kv_heads * cfg.head_dim * esize,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbps, 2),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "timed": "decode call (split kernel + reduce), hipGraph replay, events on the launch stream",
+        },
+        "cpu_baseline": cpu,
+    }
+    if check is not None:
+        line["max_abs_err_vs_fp32_oracle"] = check
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,187 @@
+/*
+ * infrared_amd — C ABI of the MI355X (gfx950) paged-attention hot path.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, element strides and sizes (no framework types);
+ *   - launches asynchronously on the caller's `stream` and never synchronises,
+ *     allocates or frees device memory, so calls are hipGraph-capturable;
+ *   - returns 0 on success or a negative IR_E* code, with a thread-local
+ *     message readable through ir_last_error(); it never aborts or throws.
+ *
+ * Data layout (kept identical to the reference pool so callers that address
+ * `pool.k[layer, slot]` directly keep working):
+ *   K/V cache of one layer: [num_slots, num_kv_heads, head_dim], slot = block_id *
+ *   block_size + offset, head_dim contiguous (reference:
+ *   infrared/cache/paged_kv_cache.py:44-46).
+ *
+ * Device-side bounds problems (a slot or block id outside the pool, a context
+ * longer than the block table) never fault: the offending element is skipped
+ * and a bit is OR-ed into *err_flags (when err_flags is non-NULL) so the host
+ * can check it later without a synchronising call in the hot loop.
+ */
+#ifndef INFRARED_AMD_H
+#define INFRARED_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* ir_stream_t; /* a hipStream_t; NULL is the null stream */
+
+/* dtype codes */
+enum {
+  IR_DTYPE_F32 = 0,
+  IR_DTYPE_F16 = 1,
+  IR_DTYPE_BF16 = 2
+};
+
+/* return codes */
+enum {
+  IR_OK = 0,
+  IR_EINVAL = -1,       /* bad argument (shape, stride, alignment, dtype) */
+  IR_EUNSUPPORTED = -2, /* valid request this build has no kernel for */
+  IR_EWORKSPACE = -3,   /* workspace missing or too small */
+  IR_ELAUNCH = -4       /* the HIP runtime rejected the launch */
+};
+
+/* bits OR-ed into *err_flags by the kernels */
+enum {
+  IR_ERR_SLOT_RANGE = 1,     /* scatter slot >= num_slots (write skipped) */
+  IR_ERR_BLOCK_RANGE = 2,    /* block id outside [0, num_blocks) (block masked) */
+  IR_ERR_CONTEXT_RANGE = 4,  /* context_len > max_blocks*block_size (clamped) or < 0 */
+  IR_ERR_GATHER_RANGE = 8    /* gather slot outside [0, num_slots) (key masked) */
+};
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* ir_last_error(void);
+
+/* Version string of the library build. */
+const char* ir_version(void);
+
+/*
+ * KV-slot scatter: k_cache[slot_mapping[i]] = k[i]; v_cache[slot_mapping[i]] = v[i].
+ *
+ * Replaces PagedKVPool.write (infrared/cache/paged_kv_cache.py:48-57), i.e. the
+ * two index_put_ calls `self.k[layer_idx, slots] = k`, and the store_kvcache
+ * skeleton of docs/research/t4-triton-cudagraph-api.md:134-158.
+ *   k, v:        [n_tokens, num_kv_heads, head_dim], strides in elements
+ *                (token, head); head_dim stride is 1.
+ *   k_cache, v_cache: one layer of the pool, strides (slot, head) in elements.
+ *   slot_mapping: [n_tokens] int64 flat slot ids. A negative slot skips the row
+ *                (padding sentinel); a slot >= num_slots is skipped and flagged.
+ * Bit-exact copy semantics; duplicated slots must carry identical rows (the
+ * pad-by-repeat convention of infrared/engine/cuda_graph.py:22-25).
+ */
+int ir_kv_scatter(const void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                  const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                  void* k_cache, void* v_cache, int64_t cache_slot_stride,
+                  int64_t cache_head_stride, int64_t num_slots,
+                  const int64_t* slot_mapping, int64_t n_tokens, int num_kv_heads,
+                  int head_dim, int dtype, int32_t* err_flags, ir_stream_t stream);
+
+/*
+ * Slot gather: out_k[i] = k_cache[slots[i]], out_v[i] = v_cache[slots[i]].
+ *
+ * Replaces PagedKVPool.gather (infrared/cache/paged_kv_cache.py:59-72), the
+ * `self.k[layer_idx, flat]` indexing over gather_slots. Outputs are
+ * [n, num_kv_heads, head_dim] contiguous; a slot outside [0, num_slots) reads
+ * as zeros and is flagged with IR_ERR_GATHER_RANGE.
+ */
+int ir_gather_slots(const void* k_cache, const void* v_cache, int64_t cache_slot_stride,
+                    int64_t cache_head_stride, int64_t num_slots, const int64_t* slots,
+                    int64_t n, int num_kv_heads, int head_dim, int dtype, void* out_k,
+                    void* out_v, int32_t* err_flags, ir_stream_t stream);
+
+/*
+ * Paged gather through a block table (test/debug utility that shares the
+ * decode kernel's token -> slot address function):
+ *   out_k[b, t] = k_cache[block_tables[b, t / bs] * bs + t % bs] for t < context_lens[b],
+ *   zero for context_lens[b] <= t < max_ctx.
+ * Restates PagedKVPool.gather (infrared/cache/paged_kv_cache.py:59-72) with the
+ * gather_slots closed form of infrared/engine/paged_engine.py:306-314.
+ *   out_k, out_v: [num_seqs, max_ctx, num_kv_heads, head_dim] contiguous.
+ */
+int ir_paged_gather(const void* k_cache, const void* v_cache, int64_t cache_slot_stride,
+                    int64_t cache_head_stride, int64_t num_blocks, int block_size,
+                    const int32_t* block_tables, int64_t bt_stride, int max_blocks_per_seq,
+                    const int32_t* context_lens, int num_seqs, int max_ctx,
+                    int num_kv_heads, int head_dim, int dtype, void* out_k, void* out_v,
+                    int32_t* err_flags, ir_stream_t stream);
+
+/*
+ * Bytes of device workspace ir_paged_decode needs for this shape (0 when one
+ * partition covers the longest context). The workspace holds the split-KV
+ * partials: running max / sum [num_seqs, num_q_heads, parts] and the
+ * unnormalised accumulators [num_seqs, num_q_heads, parts, head_dim] in fp32.
+ */
+int64_t ir_paged_decode_workspace_size(int num_seqs, int num_q_heads, int num_kv_heads,
+                                       int head_dim, int max_blocks_per_seq, int block_size,
+                                       int partition_tokens);
+
+/* The partition size (tokens) ir_paged_decode picks when partition_tokens == 0. */
+int ir_paged_decode_default_partition(int num_seqs, int num_kv_heads, int max_blocks_per_seq,
+                                      int block_size);
+
+/*
+ * GQA paged decode attention, one query token per sequence.
+ *
+ * Replaces the decode use of _paged_attention_triton / _paged_attention_naive
+ * (infrared/model/triton_attention.py:110-129, :310-358) with the
+ * (block_tables, context_lens) signature of
+ * docs/research/t4-triton-cudagraph-api.md:79-127:
+ *   out[b, h] = softmax_t(scale * q[b, h] . K[b, t, h / n_rep]) @ V[b, t, h / n_rep],
+ *   t in [0, context_lens[b]), K/V rows addressed through block_tables[b].
+ *   q, out:       [num_seqs, num_q_heads, head_dim] (strides seq, head in elements).
+ *   block_tables: [num_seqs, bt_stride] int32 block ids, first max_blocks_per_seq used.
+ *   context_lens: [num_seqs] int32 (0 gives a zero output row).
+ *   partition_tokens: split-KV partition length in tokens (multiple of 16;
+ *                 0 = ir_paged_decode_default_partition). Sequences longer
+ *                 than one partition are merged by a log-sum-exp reduce.
+ *   workspace:    >= ir_paged_decode_workspace_size(...) bytes, 256-byte aligned.
+ * head_dim in {64, 128}; num_q_heads % num_kv_heads == 0; dtype f32/f16/bf16.
+ */
+int ir_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
+                    const void* k_cache, const void* v_cache, int64_t cache_slot_stride,
+                    int64_t cache_head_stride, int64_t num_blocks, int block_size,
+                    const int32_t* block_tables, int64_t bt_stride, int max_blocks_per_seq,
+                    const int32_t* context_lens, void* out, int64_t out_seq_stride,
+                    int64_t out_head_stride, int num_seqs, int num_q_heads,
+                    int num_kv_heads, int head_dim, float scale, int dtype,
+                    int partition_tokens, void* workspace, int64_t workspace_bytes,
+                    int32_t* err_flags, ir_stream_t stream);
+
+/*
+ * Paged attention over the reference's own per-forward metadata: per-key flat
+ * slot ids plus an additive mask. This is the exact contract of
+ * _paged_attention_triton / _paged_attention_naive
+ * (infrared/model/triton_attention.py:110-129, :310-358; mask semantics of
+ * infrared/model/layers.py:102-118), so every caller of the reference seam
+ * (eager decode, prefill with prefix hit, packed mixed steps, graph decode)
+ * runs unchanged.
+ *   q, out:       [B, Sq, num_q_heads, head_dim] (strides b, s, h in elements).
+ *   gather_slots: [B, T] int64 (strides b, t) flat slot ids; slots outside the
+ *                 pool are flagged and masked out.
+ *   mask:         additive, element (b, s, t) at mask + b*mb + s*ms + t*mt, of
+ *                 dtype mask_dtype (f32/f16/bf16); strides may be 0 (broadcast).
+ * Scores are q.k*scale + mask; a row whose keys are all masked with finfo.min
+ * averages V uniformly, as the reference softmax does.
+ */
+int ir_paged_attention_masked(const void* q, int64_t q_b_stride, int64_t q_s_stride,
+                              int64_t q_h_stride, const void* k_cache, const void* v_cache,
+                              int64_t cache_slot_stride, int64_t cache_head_stride,
+                              int64_t num_slots, const int64_t* gather_slots,
+                              int64_t gs_b_stride, int64_t gs_t_stride, const void* mask,
+                              int64_t mask_b_stride, int64_t mask_s_stride,
+                              int64_t mask_t_stride, int mask_dtype, void* out,
+                              int64_t out_b_stride, int64_t out_s_stride,
+                              int64_t out_h_stride, int batch, int seq_q, int seq_k,
+                              int num_q_heads, int num_kv_heads, int head_dim, float scale,
+                              int dtype, int32_t* err_flags, ir_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INFRARED_AMD_H */

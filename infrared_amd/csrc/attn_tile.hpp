@@ -1,0 +1,228 @@
+// Register-tile attention building blocks shared by the decode and the
+// gather_slots+mask kernels.
+//
+// A wavefront processes 16 keys at a time against up to 16 query "columns"
+// (the query heads of one GQA group, or (query token, head) pairs).
+// Lane l = 16*g + c (g = lane group 0..3, c = column 0..15):
+//   K operand : the 16 K rows, lane (g,c) holds pieces of key row c;
+//   Q operand : lane (g,c) holds the same pieces of column c's query row;
+//   S^T       : MFMA result, lane (g,c) register r = score of key 4g+r, column c;
+//   V operand : lane (g,c) holds head_dim/16 consecutive elements (from d =
+//               (head_dim/16)*c) of key rows 4g..4g+3;
+//   O^T acc   : lane (g,c) tile n register r = output d = (head_dim/16)*(4g+r) + n
+//               of column c, i.e. one lane owns 4*head_dim/16 consecutive d.
+#pragma once
+
+#include "common.hpp"
+
+namespace ir {
+
+template <int DT, int D>
+struct TileShape {
+  static constexpr bool k16 = DT != IR_DTYPE_F32;
+  static constexpr int EB = k16 ? 2 : 4;  // element bytes
+  static constexpr int TILES = D / 16;    // PV output tiles of 16 d-rows
+  // dwords of K one lane loads from its key row (16-bit: D/32 pieces of 8
+  // elements; f32: D/16 pieces of 4 elements)
+  static constexpr int KDW = k16 ? D / 8 : D / 4;
+  // dwords of V one lane loads from each of its 4 key rows
+  static constexpr int VDW = k16 ? TILES / 2 : TILES;
+};
+
+template <int DT, int D>
+struct Tile {
+  uint32_t k[TileShape<DT, D>::KDW];
+  uint32_t v[4][TileShape<DT, D>::VDW];
+};
+
+template <int D>
+struct State {
+  float m, l;
+  f32x4 acc[D / 16];
+};
+
+template <int D>
+__device__ __forceinline__ void state_init(State<D>& st) {
+  st.m = kNegInf;
+  st.l = 0.f;
+#pragma unroll
+  for (int n = 0; n < D / 16; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+template <int N>
+__device__ __forceinline__ void load_dwords(const uint8_t* p, uint32_t (&r)[N]) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const u32x4 x = ((const u32x4*)p)[i];
+      r[4 * i + 0] = x[0];
+      r[4 * i + 1] = x[1];
+      r[4 * i + 2] = x[2];
+      r[4 * i + 3] = x[3];
+    }
+  } else {
+    static_assert(N == 2, "row piece must be 8 or 16*k bytes");
+    const u32x2 x = *(const u32x2*)p;
+    r[0] = x[0];
+    r[1] = x[1];
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void zero_dwords(uint32_t (&r)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) r[i] = 0u;
+}
+
+// K (or Q) pieces of one head row for lane group g. The element order is the
+// MFMA k-slot order; K and Q use the same function so the contraction over
+// head_dim is exact whatever order that is.
+//   16-bit: piece j = elements [8*(4j+g), +8); f32: piece j = [16j+4g, +4).
+template <int DT, int D>
+__device__ __forceinline__ void load_k(const uint8_t* row, int g, uint32_t (&k)[TileShape<DT, D>::KDW]) {
+  typedef TileShape<DT, D> Sh;
+#pragma unroll
+  for (int j = 0; j < Sh::KDW / 4; ++j) {
+    const int d = Sh::k16 ? 8 * (4 * j + g) : 16 * j + 4 * g;
+    const u32x4 x = *(const u32x4*)(row + d * Sh::EB);
+    k[4 * j + 0] = x[0];
+    k[4 * j + 1] = x[1];
+    k[4 * j + 2] = x[2];
+    k[4 * j + 3] = x[3];
+  }
+}
+
+// V elements of one key row this lane needs: [TILES*c, TILES*c + TILES).
+template <int DT, int D>
+__device__ __forceinline__ void load_v(const uint8_t* row, int c, uint32_t (&v)[TileShape<DT, D>::VDW]) {
+  typedef TileShape<DT, D> Sh;
+  load_dwords<Sh::VDW>(row + Sh::TILES * c * Sh::EB, v);
+}
+
+// S^T = K . Q^T for one 16-key tile; lane (g,c) register r = key 4g+r, column c.
+template <int DT, int D>
+__device__ __forceinline__ f32x4 qk_tile(const uint32_t (&k)[TileShape<DT, D>::KDW],
+                                         const uint32_t (&qr)[TileShape<DT, D>::KDW]) {
+  typedef TileShape<DT, D> Sh;
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (Sh::k16) {
+#pragma unroll
+    for (int j = 0; j < Sh::KDW / 4; ++j) {
+      const u32x4 ka = {k[4 * j], k[4 * j + 1], k[4 * j + 2], k[4 * j + 3]};
+      const u32x4 qb = {qr[4 * j], qr[4 * j + 1], qr[4 * j + 2], qr[4 * j + 3]};
+      s = mfma_k32<DT>(ka, qb, s);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < Sh::KDW; ++j) s = mfma_f32_k4(__uint_as_float(k[j]), __uint_as_float(qr[j]), s);
+  }
+  return s;
+}
+
+// Online-softmax update with base-2 scores sv (-inf = key excluded) followed by
+// O^T += V^T . P^T. `vok[r]` says whether key row 4g+r may be read; rows that
+// may not are zeroed so 0 * V never meets a NaN pattern in stale pool memory.
+template <int DT, int D>
+__device__ __forceinline__ void softmax_pv(const float (&sv)[4], const uint32_t (&vin)[4][TileShape<DT, D>::VDW],
+                                           const bool (&vok)[4], State<D>& st) {
+  typedef TileShape<DT, D> Sh;
+  constexpr int TILES = Sh::TILES;
+  float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+  mx = wave_max_groups(mx);
+  const float m_new = fmaxf(st.m, mx);
+  const bool none = m_new == kNegInf;  // no key of this column seen yet
+  const float alpha = none ? 1.f : fast_exp2(st.m - m_new);
+  float p[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) p[r] = none ? 0.f : fast_exp2(sv[r] - m_new);
+  st.l = st.l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+  st.m = m_new;
+#pragma unroll
+  for (int n = 0; n < TILES; ++n) st.acc[n] *= alpha;
+  uint32_t v[4][Sh::VDW];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int i = 0; i < Sh::VDW; ++i) v[r][i] = vok[r] ? vin[r][i] : 0u;
+  if constexpr (Sh::k16) {
+    // P rounded to the input dtype, as softmax(...).to(q.dtype) does.
+    using E = Elem<DT>;
+    const u32x2 pb = {E::pack2(p[0], p[1]), E::pack2(p[2], p[3])};
+#pragma unroll
+    for (int n = 0; n < TILES; ++n) {
+      // element n of rows 4g..4g+3 -> the 4 k-slots of this lane (transpose)
+      const int wdw = n >> 1;
+      uint32_t lo, hi;
+      if ((n & 1) == 0) {
+        lo = (v[0][wdw] & 0xffffu) | (v[1][wdw] << 16);
+        hi = (v[2][wdw] & 0xffffu) | (v[3][wdw] << 16);
+      } else {
+        lo = (v[0][wdw] >> 16) | (v[1][wdw] & 0xffff0000u);
+        hi = (v[2][wdw] >> 16) | (v[3][wdw] & 0xffff0000u);
+      }
+      const u32x2 va = {lo, hi};
+      st.acc[n] = mfma_k16<DT>(va, pb, st.acc[n]);
+    }
+  } else {
+    // fp32: one 16x16x4 product per key row; k-slot = lane group.
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int n = 0; n < TILES; ++n) st.acc[n] = mfma_f32_k4(__uint_as_float(v[r][n]), p[r], st.acc[n]);
+  }
+}
+
+// LDS scratch for merging NW wavefronts' states of 16 columns.
+template <int NW, int D>
+struct MergeSmem {
+  float acc[NW][16][D + 4];
+  float m[NW][16];
+  float l[NW][16];
+};
+
+// Publishes this wavefront's state (after its cross-group sum of l).
+template <int NW, int D>
+__device__ __forceinline__ void merge_publish(MergeSmem<NW, D>& sm, const State<D>& st, int w, int g, int c) {
+  constexpr int TILES = D / 16;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int n = 0; n < TILES; ++n) sm.acc[w][c][TILES * (4 * g + r) + n] = st.acc[n][r];
+  if (g == 0) {
+    sm.m[w][c] = st.m;
+    sm.l[w][c] = st.l;
+  }
+}
+
+// Combined (M, L, o[d0..d0+3]) of column hc over the NW published states.
+template <int NW, int D>
+__device__ __forceinline__ void merge_column(const MergeSmem<NW, D>& sm, int hc, int d0, float& M, float& L,
+                                             float (&o)[4]) {
+  M = kNegInf;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) M = fmaxf(M, sm.m[w][hc]);
+  L = 0.f;
+  o[0] = o[1] = o[2] = o[3] = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const float mw = sm.m[w][hc];
+    const float wt = mw == kNegInf ? 0.f : fast_exp2(mw - M);
+    L += wt * sm.l[w][hc];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] += wt * sm.acc[w][hc][d0 + k];
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store4(uint8_t* dst, const float (&o)[4], float scale) {
+  if constexpr (DT == IR_DTYPE_F32) {
+    const f32x4 x = {o[0] * scale, o[1] * scale, o[2] * scale, o[3] * scale};
+    *(f32x4*)dst = x;
+  } else {
+    using E = Elem<DT>;
+    const u32x2 x = {E::pack2(o[0] * scale, o[1] * scale), E::pack2(o[2] * scale, o[3] * scale)};
+    *(u32x2*)dst = x;
+  }
+}
+
+}  // namespace ir

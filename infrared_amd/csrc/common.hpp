@@ -1,0 +1,172 @@
+// Shared device helpers for the gfx950 paged-attention kernels: element types,
+// conversions, MFMA wrappers and the token -> slot address function.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "infrared_amd.h"
+
+namespace ir {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_inff();
+
+// ---------------------------------------------------------------- conversions
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// Round-to-nearest-even float -> bf16 bits (NaN stays NaN), the rounding torch
+// applies in `.to(torch.bfloat16)`.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+  _Float16 x = __builtin_bit_cast(_Float16, (uint16_t)h);
+  return (float)x;
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16(float f) {
+  _Float16 x = (_Float16)f;
+  return (uint32_t)__builtin_bit_cast(uint16_t, x);
+}
+
+// Element-type traits. Storage is raw bits; arithmetic is always fp32.
+template <int DT>
+struct Elem;
+
+template <>
+struct Elem<IR_DTYPE_F32> {
+  typedef float storage;
+  static constexpr int bytes = 4;
+  __device__ __forceinline__ static float load(const storage* p) { return *p; }
+  __device__ __forceinline__ static storage from_f32(float f) { return f; }
+  __device__ __forceinline__ static float to_f32(storage s) { return s; }
+};
+
+template <>
+struct Elem<IR_DTYPE_BF16> {
+  typedef uint16_t storage;
+  static constexpr int bytes = 2;
+  __device__ __forceinline__ static float to_f32(storage s) { return bf16_to_f32(s); }
+  __device__ __forceinline__ static storage from_f32(float f) { return (storage)f32_to_bf16(f); }
+  // packs two fp32 values into one dword of two elements (lo first)
+  __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
+    return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+  }
+  __device__ __forceinline__ static float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  __device__ __forceinline__ static float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+};
+
+template <>
+struct Elem<IR_DTYPE_F16> {
+  typedef uint16_t storage;
+  static constexpr int bytes = 2;
+  __device__ __forceinline__ static float to_f32(storage s) { return f16_to_f32(s); }
+  __device__ __forceinline__ static storage from_f32(float f) { return (storage)f32_to_f16(f); }
+  __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
+    return f32_to_f16(lo) | (f32_to_f16(hi) << 16);
+  }
+  __device__ __forceinline__ static float lo(uint32_t w) { return f16_to_f32(w & 0xffffu); }
+  __device__ __forceinline__ static float hi(uint32_t w) { return f16_to_f32(w >> 16); }
+};
+
+// ---------------------------------------------------------------- MFMA wrappers
+//
+// 16x16 fp32-accumulator layout (all three shapes below): lane l, register r
+// holds D[row = 4*(l/16) + r][col = l%16]. Operand A (M x K) lane l holds
+// A[row = l%16][k-slots of lane group l/16]; operand B (K x N) lane l holds
+// B[k-slots of lane group l/16][col = l%16]. The kernels only rely on A and B
+// sharing the same k-slot assignment, which is what makes the contraction a
+// plain dot product over whatever element order the loads chose.
+
+// 16x16x32, 16-bit inputs: 8 elements (4 dwords) of A and B per lane.
+template <int DT>
+__device__ __forceinline__ f32x4 mfma_k32(u32x4 a, u32x4 b, f32x4 c);
+
+template <>
+__device__ __forceinline__ f32x4 mfma_k32<IR_DTYPE_BF16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+template <>
+__device__ __forceinline__ f32x4 mfma_k32<IR_DTYPE_F16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// 16x16x16, 16-bit inputs: 4 elements (2 dwords) of A and B per lane.
+template <int DT>
+__device__ __forceinline__ f32x4 mfma_k16(u32x2 a, u32x2 b, f32x4 c);
+
+template <>
+__device__ __forceinline__ f32x4 mfma_k16<IR_DTYPE_BF16>(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
+                                                    __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+}
+
+template <>
+__device__ __forceinline__ f32x4 mfma_k16<IR_DTYPE_F16>(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+}
+
+// 16x16x4 fp32: one element of A and B per lane (k-slot = lane group).
+__device__ __forceinline__ f32x4 mfma_f32_k4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------- misc
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float wave_max_groups(float x) {
+  // max over lanes l, l^16, l^32, l^48 (the four 16-lane groups)
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum_groups(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+__device__ __forceinline__ void flag_error(int32_t* err, int32_t bit) {
+  if (err) atomicOr(err, bit);
+}
+
+template <typename T>
+__device__ __forceinline__ T load_nt(const T* p) {
+  return __builtin_nontemporal_load(p);
+}
+
+// Flat slot of logical token `t` of a sequence whose block table row is `bt`:
+// bt[t / bs] * bs + t % bs (infrared/engine/paged_engine.py:621-625). Returns -1
+// (and flags) for a block id outside [0, num_blocks).
+__device__ __forceinline__ int64_t token_slot(const int32_t* bt, int t, int bs, int64_t num_blocks,
+                                              int32_t* err) {
+  const int blk = t / bs;
+  const int32_t bid = bt[blk];
+  if (bid < 0 || (int64_t)bid >= num_blocks) {
+    flag_error(err, IR_ERR_BLOCK_RANGE);
+    return -1;
+  }
+  return (int64_t)bid * bs + (t - blk * bs);
+}
+
+}  // namespace ir

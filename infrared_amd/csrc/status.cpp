@@ -1,0 +1,36 @@
+// Thread-local error state behind ir_last_error().
+#include "status.hpp"
+
+#include <stdarg.h>
+#include <stdio.h>
+
+namespace {
+thread_local char g_last_error[512] = "";
+}
+
+namespace ir {
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_last_error[0] = '\0';
+  return IR_OK;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(IR_ELAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+}  // namespace ir
+
+extern "C" const char* ir_last_error(void) { return g_last_error; }
+
+extern "C" const char* ir_version(void) { return "infrared_amd 0.1 gfx950"; }

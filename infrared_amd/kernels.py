@@ -1,0 +1,240 @@
+"""Tensor-level wrappers of the C ABI: validate shapes on the host, pass raw
+pointers and torch's current stream, raise ``RuntimeError`` on any failure.
+
+Each wrapper launches asynchronously and allocates at most its output (and
+the decode workspace when one is not supplied), so it can run under hipGraph
+capture.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from infrared_amd._lib import check, dtype_code, lib, ptr, require_device, stream_ptr
+
+
+def _last_dim_contiguous(name: str, t: torch.Tensor) -> None:
+    if t.stride(-1) != 1:
+        raise RuntimeError(f"{name}: the last (head_dim) dimension must be contiguous")
+
+
+def _cache_layer(name: str, cache: torch.Tensor) -> None:
+    if cache.dim() != 3:
+        raise RuntimeError(f"{name}: expected one pool layer [num_slots, num_kv_heads, head_dim]")
+    _last_dim_contiguous(name, cache)
+
+
+def kv_scatter(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    slots: torch.Tensor,
+    err_flags: torch.Tensor | None = None,
+) -> None:
+    """``k_cache[slots] = k; v_cache[slots] = v`` (``PagedKVPool.write`` semantics).
+
+    ``k``/``v``: ``[N, H_kv, D]``; ``slots``: ``[N]`` int64. Negative slots are
+    skipped (padding sentinel); slots ``>= num_slots`` are skipped and flagged.
+    """
+    dev = require_device(k_cache, v_cache, k, v, slots)
+    _cache_layer("kv_scatter", k_cache)
+    if v_cache.shape != k_cache.shape or v_cache.stride() != k_cache.stride():
+        raise RuntimeError("kv_scatter: k_cache and v_cache must have the same shape and strides")
+    n, h, d = k.shape
+    if v.shape != k.shape or (h, d) != tuple(k_cache.shape[1:]):
+        raise RuntimeError(
+            f"kv_scatter: k {tuple(k.shape)} / v {tuple(v.shape)} do not match pool rows "
+            f"{tuple(k_cache.shape[1:])}"
+        )
+    if k.dtype != k_cache.dtype or v.dtype != k_cache.dtype:
+        raise RuntimeError(f"kv_scatter: dtype mismatch ({k.dtype}, {v.dtype} vs pool {k_cache.dtype})")
+    if slots.dtype != torch.int64 or slots.shape != (n,):
+        raise RuntimeError(f"kv_scatter: slots must be int64 [{n}], got {slots.dtype} {tuple(slots.shape)}")
+    _last_dim_contiguous("kv_scatter k", k)
+    _last_dim_contiguous("kv_scatter v", v)
+    slots = slots.contiguous()
+    rc = lib().ir_kv_scatter(
+        ptr(k), k.stride(0), k.stride(1), ptr(v), v.stride(0), v.stride(1),
+        ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1), k_cache.shape[0],
+        ptr(slots), n, h, d, dtype_code(k_cache.dtype), ptr(err_flags), stream_ptr(dev),
+    )
+    check(rc, "ir_kv_scatter")
+
+
+def gather_slots(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    slots: torch.Tensor,
+    err_flags: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(k_cache[slots], v_cache[slots])`` for any-shaped int64 ``slots`` -> ``[*slots.shape, H, D]``."""
+    dev = require_device(k_cache, v_cache, slots)
+    _cache_layer("gather_slots", k_cache)
+    if slots.dtype != torch.int64:
+        raise RuntimeError("gather_slots: slots must be int64")
+    flat = slots.reshape(-1).contiguous()
+    h, d = k_cache.shape[1:]
+    out_k = torch.empty(flat.numel(), h, d, dtype=k_cache.dtype, device=dev)
+    out_v = torch.empty_like(out_k)
+    rc = lib().ir_gather_slots(
+        ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1), k_cache.shape[0],
+        ptr(flat), flat.numel(), h, d, dtype_code(k_cache.dtype), ptr(out_k), ptr(out_v),
+        ptr(err_flags), stream_ptr(dev),
+    )
+    check(rc, "ir_gather_slots")
+    return out_k.reshape(*slots.shape, h, d), out_v.reshape(*slots.shape, h, d)
+
+
+def paged_gather(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    block_size: int,
+    max_ctx: int,
+    err_flags: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dense ``[B, max_ctx, H_kv, D]`` K/V histories through the block tables (zero-padded)."""
+    dev = require_device(k_cache, v_cache, block_tables, context_lens)
+    _cache_layer("paged_gather", k_cache)
+    _check_tables("paged_gather", block_tables, context_lens)
+    b = block_tables.shape[0]
+    h, d = k_cache.shape[1:]
+    out_k = torch.empty(b, max_ctx, h, d, dtype=k_cache.dtype, device=dev)
+    out_v = torch.empty_like(out_k)
+    num_blocks = k_cache.shape[0] // block_size
+    rc = lib().ir_paged_gather(
+        ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1), num_blocks, block_size,
+        ptr(block_tables), block_tables.stride(0), block_tables.shape[1], ptr(context_lens), b,
+        max_ctx, h, d, dtype_code(k_cache.dtype), ptr(out_k), ptr(out_v), ptr(err_flags),
+        stream_ptr(dev),
+    )
+    check(rc, "ir_paged_gather")
+    return out_k, out_v
+
+
+def _check_tables(name: str, block_tables: torch.Tensor, context_lens: torch.Tensor) -> None:
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.stride(1) != 1:
+        raise RuntimeError(f"{name}: block_tables must be int32 [B, max_blocks] with contiguous rows")
+    if context_lens.dtype != torch.int32 or context_lens.shape != (block_tables.shape[0],):
+        raise RuntimeError(f"{name}: context_lens must be int32 [B]")
+    if not context_lens.is_contiguous():
+        raise RuntimeError(f"{name}: context_lens must be contiguous")
+
+
+def decode_workspace_bytes(
+    num_seqs: int, num_q_heads: int, num_kv_heads: int, head_dim: int, max_blocks: int,
+    block_size: int, partition_tokens: int = 0,
+) -> int:
+    return int(lib().ir_paged_decode_workspace_size(
+        num_seqs, num_q_heads, num_kv_heads, head_dim, max_blocks, block_size, partition_tokens
+    ))
+
+
+def default_partition(num_seqs: int, num_kv_heads: int, max_blocks: int, block_size: int) -> int:
+    return int(lib().ir_paged_decode_default_partition(num_seqs, num_kv_heads, max_blocks, block_size))
+
+
+def paged_decode(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    block_size: int,
+    scale: float,
+    out: torch.Tensor | None = None,
+    partition_tokens: int = 0,
+    workspace: torch.Tensor | None = None,
+    err_flags: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """GQA paged decode: ``q`` ``[B, H_q, D]`` -> ``[B, H_q, D]``.
+
+    ``block_tables`` int32 ``[B, max_blocks]``, ``context_lens`` int32 ``[B]``.
+    ``workspace`` (uint8, 256-byte aligned) is allocated when not given and the
+    longest possible context needs more than one partition.
+    """
+    dev = require_device(q, k_cache, v_cache, block_tables, context_lens)
+    _cache_layer("paged_decode", k_cache)
+    _check_tables("paged_decode", block_tables, context_lens)
+    if q.dim() != 3:
+        raise RuntimeError(f"paged_decode: q must be [B, H_q, D], got {tuple(q.shape)}")
+    b, hq, d = q.shape
+    h_kv = k_cache.shape[1]
+    if d != k_cache.shape[2] or q.dtype != k_cache.dtype or v_cache.shape != k_cache.shape:
+        raise RuntimeError("paged_decode: q / pool shape or dtype mismatch")
+    if block_tables.shape[0] != b:
+        raise RuntimeError("paged_decode: block_tables rows != batch")
+    _last_dim_contiguous("paged_decode q", q)
+    if out is None:
+        out = torch.empty(b, hq, d, dtype=q.dtype, device=dev)
+    max_blocks = block_tables.shape[1]
+    if partition_tokens <= 0:
+        partition_tokens = default_partition(b, h_kv, max_blocks, block_size)
+    need = decode_workspace_bytes(b, hq, h_kv, d, max_blocks, block_size, partition_tokens)
+    if need > 0 and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    rc = lib().ir_paged_decode(
+        ptr(q), q.stride(0), q.stride(1), ptr(k_cache), ptr(v_cache), k_cache.stride(0),
+        k_cache.stride(1), k_cache.shape[0] // block_size, block_size, ptr(block_tables),
+        block_tables.stride(0), max_blocks, ptr(context_lens), ptr(out), out.stride(0),
+        out.stride(1), b, hq, h_kv, d, float(scale), dtype_code(q.dtype), partition_tokens,
+        ptr(workspace) if need > 0 else None, need, ptr(err_flags), stream_ptr(dev),
+    )
+    check(rc, "ir_paged_decode")
+    return out
+
+
+def paged_attention_masked(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    gather_slots: torch.Tensor,
+    mask: torch.Tensor,
+    scale: float,
+    out: torch.Tensor | None = None,
+    err_flags: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Attention over per-key slots + additive mask (the reference seam's metadata).
+
+    ``q`` ``[B, Sq, H_q, D]``; ``gather_slots`` int64 ``[B, T]``; ``mask``
+    broadcastable to ``[B, 1, Sq, T]``. Returns ``[B, Sq, H_q, D]``.
+    """
+    dev = require_device(q, k_cache, v_cache, gather_slots, mask)
+    _cache_layer("paged_attention_masked", k_cache)
+    if q.dim() != 4:
+        raise RuntimeError(f"paged_attention_masked: q must be [B, Sq, H_q, D], got {tuple(q.shape)}")
+    b, sq, hq, d = q.shape
+    h_kv = k_cache.shape[1]
+    if d != k_cache.shape[2] or q.dtype != k_cache.dtype:
+        raise RuntimeError("paged_attention_masked: q / pool shape or dtype mismatch")
+    if gather_slots.dtype != torch.int64 or gather_slots.dim() != 2 or gather_slots.shape[0] != b:
+        raise RuntimeError("paged_attention_masked: gather_slots must be int64 [B, T]")
+    t = gather_slots.shape[1]
+    if mask.dim() != 4 or mask.shape[1] != 1:
+        raise RuntimeError(f"paged_attention_masked: mask must be [B, 1, Sq, T], got {tuple(mask.shape)}")
+    m = mask.expand(b, 1, sq, t)
+    _last_dim_contiguous("paged_attention_masked q", q)
+    if out is None:
+        out = torch.empty(b, sq, hq, d, dtype=q.dtype, device=dev)
+    rc = lib().ir_paged_attention_masked(
+        ptr(q), q.stride(0), q.stride(1), q.stride(2), ptr(k_cache), ptr(v_cache),
+        k_cache.stride(0), k_cache.stride(1), k_cache.shape[0], ptr(gather_slots),
+        gather_slots.stride(0), gather_slots.stride(1), ptr(m), m.stride(0), m.stride(2),
+        m.stride(3), dtype_code(m.dtype), ptr(out), out.stride(0), out.stride(1), out.stride(2),
+        b, sq, t, hq, h_kv, d, float(scale), dtype_code(q.dtype), ptr(err_flags), stream_ptr(dev),
+    )
+    check(rc, "ir_paged_attention_masked")
+    return out
+
+
+__all__ = [
+    "kv_scatter",
+    "gather_slots",
+    "paged_gather",
+    "paged_decode",
+    "paged_attention_masked",
+    "decode_workspace_bytes",
+    "default_partition",
+]

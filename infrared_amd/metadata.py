@@ -1,0 +1,106 @@
+"""Device-side paged metadata builders (the engine side of the seam).
+
+The reference engine builds per-step metadata with Python loops and one
+host->device copy per sequence (``infrared/engine/paged_engine.py:303-314``,
+``infrared/engine/cuda_graph.py:137-148``). These builders produce the same
+tensors vectorised, plus the ``block_tables``/``context_lens`` pair the HIP
+decode kernel reads, so a caller fills ``PagedContext`` directly:
+
+- ``slot(bt, p, bs) = bt[p // bs] * bs + p % bs`` (``paged_engine.py:621-625``);
+- ``gather_slots[i, p] = slot(bt_i, p)`` for ``p < ctx_i``, ``0`` after
+  (``paged_engine.py:306-314``);
+- decode mask ``0`` for ``col < ctx_i``, ``finfo(dtype).min`` after
+  (``paged_engine.py:630-638``).
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+
+import torch
+
+from infrared_amd.paged_kv_cache import PagedContext, PagedKVPool
+
+
+def slot(block_table: Sequence[int], pos: int, block_size: int) -> int:
+    """Flat physical slot of logical position ``pos``."""
+    return block_table[pos // block_size] * block_size + (pos % block_size)
+
+
+def blocks_for(num_tokens: int, block_size: int) -> int:
+    """Blocks ``num_tokens`` tokens occupy (ceil divide; ``block_manager.py:82-84``)."""
+    return (num_tokens + block_size - 1) // block_size
+
+
+def block_tables_tensor(
+    block_tables: Sequence[Sequence[int]], device: torch.device | str, width: int | None = None
+) -> torch.Tensor:
+    """``[B, width]`` int32, rows right-padded with block 0 (entries past a row's
+    context are never read)."""
+    w = max((len(r) for r in block_tables), default=0) if width is None else width
+    if any(len(r) > w for r in block_tables):
+        raise ValueError(f"a block table is longer than width {w}")
+    rows = [list(r) + [0] * (w - len(r)) for r in block_tables]
+    return torch.tensor(rows, dtype=torch.int32).reshape(len(rows), w).to(device)
+
+
+def gather_slots_from_tables(
+    block_tables: torch.Tensor, context_lens: torch.Tensor, block_size: int, t_max: int
+) -> torch.Tensor:
+    """``[B, t_max]`` int64 slot ids of each row's history; ``0`` past ``context_lens``."""
+    pos = torch.arange(t_max, device=block_tables.device)
+    blk = torch.clamp(pos // block_size, max=max(block_tables.shape[1] - 1, 0))
+    ids = block_tables.long().index_select(1, blk) if block_tables.shape[1] else torch.zeros(
+        block_tables.shape[0], t_max, dtype=torch.long, device=block_tables.device
+    )
+    slots = ids * block_size + (pos % block_size)
+    valid = pos[None, :] < context_lens.long()[:, None]
+    return torch.where(valid, slots, torch.zeros_like(slots))
+
+
+def decode_mask(
+    context_lens: torch.Tensor, max_len: int, dtype: torch.dtype
+) -> torch.Tensor:
+    """Additive ``[B, 1, 1, max_len]``: 0 for ``col < ctx``, ``finfo(dtype).min`` after."""
+    cols = torch.arange(max_len, device=context_lens.device)
+    invalid = cols[None, :] >= context_lens.long()[:, None]
+    mask = torch.zeros(context_lens.shape[0], 1, 1, max_len, dtype=dtype, device=context_lens.device)
+    return mask.masked_fill(invalid[:, None, None, :], torch.finfo(dtype).min)
+
+
+def decode_write_slots(
+    block_tables: torch.Tensor, num_cached: torch.Tensor, block_size: int
+) -> torch.Tensor:
+    """``[B]`` int64 slot of each sequence's new token (position ``num_cached``)."""
+    nc = num_cached.long()
+    blk = (nc // block_size)[:, None]
+    ids = torch.gather(block_tables.long(), 1, blk)[:, 0]
+    return ids * block_size + nc % block_size
+
+
+def decode_context(
+    pool: PagedKVPool,
+    block_tables: Sequence[Sequence[int]],
+    num_cached: Sequence[int],
+    *,
+    t_max: int | None = None,
+    use_triton: bool = True,
+    mask_dtype: torch.dtype | None = None,
+) -> tuple[PagedContext, torch.Tensor]:
+    """One batched decode step's ``PagedContext`` + mask, as ``_decode_logits_eager``
+    builds them (``infrared/engine/paged_engine.py:290-332``) plus the block-table fields.
+
+    Each sequence's new token sits at position ``num_cached[i]`` and attends
+    ``[0, num_cached[i]]`` (``context_len = num_cached + 1``).
+    """
+    dev = pool.device
+    bs = pool.block_size
+    ctx = [n + 1 for n in num_cached]
+    width = max(blocks_for(c, bs) for c in ctx)
+    bt = block_tables_tensor([list(r)[:width] for r in block_tables], dev, width)
+    cl = torch.tensor(ctx, dtype=torch.int32, device=dev)
+    t = max(ctx) if t_max is None else t_max
+    gs = gather_slots_from_tables(bt, cl, bs, t)
+    ws = decode_write_slots(bt, torch.tensor(list(num_cached), device=dev), bs)
+    mask = decode_mask(cl, t, mask_dtype or pool.dtype)
+    return PagedContext(pool, ws, gs, use_triton, bt, cl), mask

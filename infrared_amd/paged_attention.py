@@ -1,0 +1,85 @@
+"""The attention seam: ``paged_attention(q, k, v, paged, mask, layer_idx, scale, n_rep)``.
+
+Same signature and contract as the reference dispatcher
+(``infrared/model/triton_attention.py:81-107``), which ``Attention.forward``
+calls once per layer (``infrared/model/layers.py:178-180``):
+
+1. scatter this step's K/V into the pool at ``paged.write_slots`` (HIP scatter
+   kernel, ``infrared/model/triton_attention.py:101-104``);
+2. attend over the paged history with a HIP kernel:
+
+   - ``paged.use_triton`` and ``paged.block_tables``/``paged.context_lens`` set
+     and one query token per sequence: the GQA decode kernel (split-KV +
+     log-sum-exp reduce) over the block tables; the mask is then implied by
+     ``context_lens`` (key ``t`` valid iff ``t < context_lens[b]``, the decode
+     mask of ``infrared/engine/paged_engine.py:630-638``);
+   - otherwise: the kernel that reads ``gather_slots`` + the additive ``mask``
+     exactly as the reference's naive path does
+     (``infrared/model/triton_attention.py:110-129``).
+
+``paged`` may be this package's ``PagedContext`` or any object with the same
+attributes (the reference's own ``PagedContext`` works: it simply lacks the
+block-table fields). There is no CPU path and no Triton: tensors must live on
+the ROCm device and the HIP library must be built.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from infrared_amd import kernels
+
+
+def paged_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    paged,
+    mask: torch.Tensor | None,
+    layer_idx: int,
+    scale: float,
+    n_rep: int,
+) -> torch.Tensor:
+    """Write this step's K/V into the pool, then attend over the paged history.
+
+    ``q`` ``[B, Sq, H, D]`` (RoPE applied); ``k``/``v`` ``[B, Sq, H_kv, D]``;
+    ``mask`` ``[B, 1, Sq, T]`` additive (may be ``None`` on the block-table path).
+    Returns ``[B, Sq, H, D]``.
+    """
+    pool = paged.pool
+    h_kv, d = k.shape[-2], k.shape[-1]
+    b, sq, hq, dq = q.shape
+    if dq != d or hq != h_kv * n_rep:
+        raise RuntimeError(
+            f"paged_attention: q {tuple(q.shape)} inconsistent with k {tuple(k.shape)} and n_rep={n_rep}"
+        )
+    pool.write(layer_idx, k.reshape(-1, h_kv, d), v.reshape(-1, h_kv, d), paged.write_slots)
+    k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
+    err = getattr(pool, "err_flags", None)
+
+    block_tables = getattr(paged, "block_tables", None)
+    context_lens = getattr(paged, "context_lens", None)
+    if paged.use_triton and block_tables is not None and context_lens is not None and sq == 1:
+        ws = None
+        if hasattr(pool, "workspace"):
+            need = kernels.decode_workspace_bytes(
+                b, hq, h_kv, d, block_tables.shape[1], pool.block_size
+            )
+            ws = pool.workspace(need) if need > 0 else None
+        out = kernels.paged_decode(
+            q.reshape(b, hq, d), k_layer, v_layer, block_tables, context_lens,
+            pool.block_size, scale, workspace=ws, err_flags=err,
+        )
+        out = out.view(b, 1, hq, d)
+    else:
+        if paged.gather_slots is None or mask is None:
+            raise RuntimeError(
+                "paged_attention: gather_slots and mask are required unless block_tables/"
+                "context_lens drive a single-token decode"
+            )
+        out = kernels.paged_attention_masked(
+            q, k_layer, v_layer, paged.gather_slots, mask, scale, err_flags=err
+        )
+    if getattr(pool, "strict", False):
+        pool.check_errors()
+    return out

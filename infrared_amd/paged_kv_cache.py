@@ -1,0 +1,161 @@
+"""Shared paged K/V pool and per-forward paged metadata (MI355X build).
+
+Same public surface as the reference's ``infrared/cache/paged_kv_cache.py``:
+
+- ``PagedKVPool(num_layers, num_blocks, block_size, num_kv_heads, head_dim,
+  dtype, device)`` with ``.k`` / ``.v`` of shape ``[num_layers, num_blocks *
+  block_size, num_kv_heads, head_dim]`` (``infrared/cache/paged_kv_cache.py:30-46``),
+  ``.write(layer_idx, k, v, slots)`` (``:48-57``) and ``.gather(layer_idx,
+  gather_slots)`` (``:59-72``).
+- ``PagedContext(pool, write_slots, gather_slots, use_triton=True)``
+  (``:75-91``), with optional device-side fields the fast kernels read:
+  ``block_tables`` ``[B, max_blocks]`` int32, ``context_lens`` ``[B]`` int32.
+
+The layout is kept flat so a token at slot ``s`` is row ``s`` (callers write
+``pool.k[layer, a:b]`` directly). ``write`` runs the HIP scatter kernel;
+``gather`` runs the HIP slot-gather. The pool lives in device memory only:
+CPU tensors are rejected rather than handled by a fallback.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from infrared_amd import kernels
+from infrared_amd._lib import (
+    ERR_BLOCK_RANGE,
+    ERR_CONTEXT_RANGE,
+    ERR_GATHER_RANGE,
+    ERR_SLOT_RANGE,
+)
+
+_ERR_NAMES = {
+    ERR_SLOT_RANGE: "write slot outside the pool",
+    ERR_BLOCK_RANGE: "block id outside the pool",
+    ERR_CONTEXT_RANGE: "context length outside the block table",
+    ERR_GATHER_RANGE: "gather slot outside the pool",
+}
+
+
+class PagedKVPool:
+    """Flat K/V slot pool on a ROCm device, addressed by slot id ``block * size + off``.
+
+    ``strict=True`` synchronises after every kernel and raises on any
+    out-of-range slot / block id the kernels flagged (debug mode). Otherwise
+    flags accumulate on the device and ``check_errors()`` reports them.
+    """
+
+    def __init__(
+        self,
+        num_layers: int,
+        num_blocks: int,
+        block_size: int,
+        num_kv_heads: int,
+        head_dim: int,
+        dtype: torch.dtype,
+        device: torch.device | str = "cuda",
+        *,
+        strict: bool = False,
+    ) -> None:
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise RuntimeError(
+                f"PagedKVPool lives in ROCm device memory; device {device} is not supported"
+            )
+        self.num_layers = num_layers
+        self.num_blocks = num_blocks
+        self.block_size = block_size
+        self.num_slots = num_blocks * block_size
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.dtype = dtype
+        self.device = device
+        self.strict = strict
+        shape = (num_layers, self.num_slots, num_kv_heads, head_dim)
+        self.k = torch.zeros(shape, dtype=dtype, device=device)
+        self.v = torch.zeros(shape, dtype=dtype, device=device)
+        self.err_flags = torch.zeros(1, dtype=torch.int32, device=device)
+        self._workspace: torch.Tensor | None = None
+
+    # --- reference surface ------------------------------------------------
+
+    def write(
+        self, layer_idx: int, k: torch.Tensor, v: torch.Tensor, slots: torch.Tensor
+    ) -> None:
+        """Scatter this step's K/V (``[N, num_kv_heads, head_dim]``) into ``slots`` (``[N]`` int64)."""
+        kernels.kv_scatter(self.k[layer_idx], self.v[layer_idx], k, v, slots, self.err_flags)
+        if self.strict:
+            self.check_errors()
+
+    def gather(
+        self, layer_idx: int, gather_slots: torch.Tensor
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """Per-query histories: ``gather_slots`` ``[B, T]`` int64 -> ``[B, T, H, D]`` K and V.
+
+        Same values as the reference's ``self.k[layer_idx, flat]`` indexing, read
+        by the HIP slot-gather kernel. A slot outside the pool reads as zeros and
+        is flagged (``IndexError`` from ``check_errors()``, or at once when strict).
+        """
+        out = kernels.gather_slots(self.k[layer_idx], self.v[layer_idx], gather_slots, self.err_flags)
+        if self.strict:
+            self.check_errors()
+        return out
+
+    # --- MI355X additions ---------------------------------------------------
+
+    def gather_blocks(
+        self,
+        layer_idx: int,
+        block_tables: torch.Tensor,
+        context_lens: torch.Tensor,
+        max_ctx: int,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """Dense zero-padded histories ``[B, max_ctx, H, D]`` through block tables (HIP kernel)."""
+        out = kernels.paged_gather(
+            self.k[layer_idx], self.v[layer_idx], block_tables, context_lens,
+            self.block_size, max_ctx, self.err_flags,
+        )
+        if self.strict:
+            self.check_errors()
+        return out
+
+    def workspace(self, nbytes: int) -> torch.Tensor:
+        """A cached device buffer of at least ``nbytes`` (split-KV partials).
+
+        Grow it outside hipGraph capture (the graph decoder's warm-up does) so a
+        captured graph keeps pointing at live memory.
+        """
+        if self._workspace is None or self._workspace.numel() < nbytes:
+            self._workspace = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+        return self._workspace
+
+    def check_errors(self) -> None:
+        """Synchronises, raises ``IndexError`` for any flagged range error, then clears the flags."""
+        flags = int(self.err_flags.item())
+        if flags:
+            self.err_flags.zero_()
+            names = [n for bit, n in _ERR_NAMES.items() if flags & bit]
+            raise IndexError("paged kernels flagged: " + ", ".join(names))
+
+
+@dataclass(slots=True)
+class PagedContext:
+    """Per-forward paged metadata handed to the attention layer.
+
+    ``write_slots`` ``[N]`` int64 — flat slots of this step's new K/V, in query
+    token order. ``gather_slots`` ``[B, T]`` int64 — per query row, the slots of
+    its history (right-padded), read together with the caller's additive mask.
+    ``use_triton`` keeps the reference's field name: ``True`` lets the dispatcher
+    take the block-table kernels when ``block_tables``/``context_lens`` are
+    present; ``False`` forces the kernel that reads ``gather_slots`` + mask.
+    Both are HIP kernels; there is no Triton and no CPU path.
+    """
+
+    pool: PagedKVPool
+    write_slots: torch.Tensor
+    gather_slots: torch.Tensor | None = None
+    use_triton: bool = True
+    block_tables: torch.Tensor | None = None
+    context_lens: torch.Tensor | None = None

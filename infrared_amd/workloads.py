@@ -1,0 +1,144 @@
+"""Seeded synthetic paged-attention workloads at the benchmark shapes.
+
+Decode workloads (one query token per sequence):
+
+- ``qwen0.5b-fp32``: 8 seqs, 14 q / 2 kv heads, head_dim 64, block 16, fp32,
+  context U{1..512}, pool of 512 blocks, scale 1/8.
+- ``qwen7b-bf16``: 64 seqs, 28 q / 4 kv heads, head_dim 128, block 16, bf16,
+  context U{512..4096}, pool 1.25x the blocks needed.
+- ``qwen7b-skewed``: 16 seqs, 28/4 heads, head_dim 128, bf16, context
+  round(lognormal(8, 1.2)) clipped to [16, 32768], pool 1.25x.
+
+Each sequence's block table is a consecutive chunk of one random permutation
+of the pool's block ids (non-contiguous physical blocks). q and the whole K/V
+pool are N(0, 1) drawn in fp32 and cast to the workload dtype. Metadata is
+drawn on the CPU from ``torch.Generator(seed)``; q/K/V are drawn on the target
+device from a generator with the same seed. ``rotations > 1`` lays out that
+many disjoint copies of the block tables over one larger pool (each with its
+own K/V values) so back-to-back calls can walk different memory.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass(frozen=True)
+class DecodeConfig:
+    name: str
+    num_seqs: int
+    num_q_heads: int
+    num_kv_heads: int
+    head_dim: int
+    block_size: int
+    dtype: torch.dtype
+    ctx_kind: str  # "uniform" | "lognormal"
+    ctx_lo: int
+    ctx_hi: int
+    pool_blocks: int | None = None  # None: ceil(1.25 * blocks needed)
+    lognormal_mu: float = 0.0
+    lognormal_sigma: float = 1.0
+    seed: int = 0
+
+    @property
+    def n_rep(self) -> int:
+        return self.num_q_heads // self.num_kv_heads
+
+    @property
+    def scale(self) -> float:
+        return self.head_dim**-0.5
+
+
+DECODE_CONFIGS: dict[str, DecodeConfig] = {
+    "qwen0.5b-fp32": DecodeConfig(
+        "qwen0.5b-fp32", 8, 14, 2, 64, 16, torch.float32, "uniform", 1, 512, pool_blocks=512, seed=1
+    ),
+    "qwen7b-bf16": DecodeConfig(
+        "qwen7b-bf16", 64, 28, 4, 128, 16, torch.bfloat16, "uniform", 512, 4096, seed=2
+    ),
+    "qwen7b-skewed": DecodeConfig(
+        "qwen7b-skewed", 16, 28, 4, 128, 16, torch.bfloat16, "lognormal", 16, 32768,
+        lognormal_mu=8.0, lognormal_sigma=1.2, seed=3,
+    ),
+}
+
+
+@dataclass
+class DecodeCase:
+    config: DecodeConfig
+    q: torch.Tensor  # [B, H_q, D]
+    k_cache: torch.Tensor  # [num_slots, H_kv, D] (one layer)
+    v_cache: torch.Tensor
+    block_tables: list[torch.Tensor]  # per rotation, int32 [B, max_blocks]
+    context_lens: torch.Tensor  # int32 [B]
+    pool_blocks: int  # blocks per rotation
+
+    @property
+    def block_size(self) -> int:
+        return self.config.block_size
+
+    @property
+    def kv_bytes(self) -> int:
+        """Algorithmic K+V bytes one call reads: sum(ctx) * 2 * H_kv * D * sizeof."""
+        c = self.config
+        esize = torch.tensor([], dtype=c.dtype).element_size()
+        return int(self.context_lens.long().sum()) * 2 * c.num_kv_heads * c.head_dim * esize
+
+
+def context_lengths(cfg: DecodeConfig, gen: torch.Generator) -> torch.Tensor:
+    if cfg.ctx_kind == "uniform":
+        return torch.randint(cfg.ctx_lo, cfg.ctx_hi + 1, (cfg.num_seqs,), generator=gen)
+    x = torch.empty(cfg.num_seqs, dtype=torch.float64).log_normal_(
+        cfg.lognormal_mu, cfg.lognormal_sigma, generator=gen
+    )
+    return torch.clamp(torch.round(x), cfg.ctx_lo, cfg.ctx_hi).long()
+
+
+def make_decode_case(
+    config: str | DecodeConfig,
+    device: torch.device | str,
+    *,
+    seed: int | None = None,
+    rotations: int = 1,
+    num_seqs: int | None = None,
+) -> DecodeCase:
+    cfg = DECODE_CONFIGS[config] if isinstance(config, str) else config
+    if num_seqs is not None:
+        cfg = DecodeConfig(**{**cfg.__dict__, "num_seqs": num_seqs})
+    seed = cfg.seed if seed is None else seed
+    gen = torch.Generator().manual_seed(seed)
+    bs = cfg.block_size
+    ctx = context_lengths(cfg, gen)
+    nblk = (ctx + bs - 1) // bs
+    need = int(nblk.sum())
+    pool_blocks = cfg.pool_blocks or math.ceil(1.25 * need)
+    if pool_blocks < need:
+        raise ValueError(f"{cfg.name}: pool of {pool_blocks} blocks < {need} needed")
+    width = int(nblk.max())
+    tables = []
+    for r in range(rotations):
+        perm = torch.randperm(pool_blocks, generator=gen) + r * pool_blocks
+        bt = torch.zeros(cfg.num_seqs, width, dtype=torch.int32)
+        off = 0
+        for i, n in enumerate(nblk.tolist()):
+            bt[i, :n] = perm[off : off + n].to(torch.int32)
+            off += n
+        tables.append(bt.to(device))
+    dgen = torch.Generator(device=device).manual_seed(seed)
+    num_slots = rotations * pool_blocks * bs
+    shape = (num_slots, cfg.num_kv_heads, cfg.head_dim)
+    q = torch.randn(cfg.num_seqs, cfg.num_q_heads, cfg.head_dim, generator=dgen, device=device)
+    k = torch.randn(shape, generator=dgen, device=device)
+    v = torch.randn(shape, generator=dgen, device=device)
+    return DecodeCase(
+        config=cfg,
+        q=q.to(cfg.dtype),
+        k_cache=k.to(cfg.dtype),
+        v_cache=v.to(cfg.dtype),
+        block_tables=tables,
+        context_lens=ctx.to(torch.int32).to(device),
+        pool_blocks=pool_blocks,
+    )

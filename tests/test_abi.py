@@ -1,0 +1,121 @@
+"""The C ABI without a GPU: the library loads, exports every symbol the header
+declares, the ctypes table matches the header, and argument validation fails
+with error codes and messages before any device work."""
+
+from __future__ import annotations
+
+import ast
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+from infrared_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "infrared_amd.h")
+
+
+def _declared() -> dict[str, int]:
+    """Function name -> parameter count, parsed from the header."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(ir_\w+)\s*\(([^;{]*?)\)\s*;", text):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_library_is_built_and_loads():
+    assert os.path.exists(_lib.LIB_PATH), "run __graft_entry__.build() first"
+    assert _lib.lib().ir_version().decode().startswith("infrared_amd")
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    decl = _declared()
+    assert {"ir_kv_scatter", "ir_paged_decode", "ir_paged_attention_masked", "ir_gather_slots"} <= set(decl)
+    lib = _lib.lib()
+    for name, nparams in decl.items():
+        assert hasattr(lib, name), f"{name} not exported"
+        assert name in _lib.SIGNATURES, f"{name} missing from the ctypes table"
+        assert len(_lib.SIGNATURES[name][1]) == nparams, f"{name}: ctypes arity != header"
+    assert set(_lib.SIGNATURES) <= set(decl)
+
+
+def test_validation_errors_report_codes_and_messages():
+    lib = _lib.lib()
+    # unknown dtype
+    rc = lib.ir_kv_scatter(None, 0, 0, None, 0, 0, None, None, 0, 0, 0, None, 1, 1, 64, 99, None, None)
+    assert rc == -1 and b"dtype" in lib.ir_last_error()
+    # zero tokens is a successful no-op (no device work)
+    rc = lib.ir_kv_scatter(None, 0, 0, None, 0, 0, None, None, 0, 0, 0, None, 0, 1, 64, 2, None, None)
+    assert rc == 0 and lib.ir_last_error() == b""
+    # unsupported head_dim
+    rc = lib.ir_paged_decode(
+        None, 0, 0, None, None, 0, 0, 1, 16, None, 0, 1, None, None, 0, 0, 1, 8, 2, 96, 1.0, 2, 0,
+        None, 0, None, None,
+    )
+    assert rc == -2 and b"head_dim" in lib.ir_last_error()
+    # heads not a multiple of kv heads
+    rc = lib.ir_paged_decode(
+        None, 0, 0, None, None, 0, 0, 1, 16, None, 0, 1, None, None, 0, 0, 1, 7, 2, 128, 1.0, 2, 0,
+        None, 0, None, None,
+    )
+    assert rc == -1 and b"multiple" in lib.ir_last_error()
+    # null pointers with work to do
+    rc = lib.ir_paged_attention_masked(
+        None, 0, 0, 0, None, None, 0, 0, 10, None, 0, 0, None, 0, 0, 0, 2, None, 0, 0, 0, 1, 1, 4,
+        4, 2, 128, 1.0, 2, None, None,
+    )
+    assert rc == -1 and b"null" in lib.ir_last_error()
+
+
+def test_decode_workspace_and_partition_helpers():
+    lib = _lib.lib()
+    p = lib.ir_paged_decode_default_partition(64, 4, 256, 16)
+    assert p % 16 == 0 and 256 <= p <= 8192
+    # one partition covers everything -> no workspace
+    assert lib.ir_paged_decode_workspace_size(8, 14, 2, 64, 32, 16, 512) == 0
+    # 4096-token tables with 512-token partitions: 8 partitions of fp32 partials
+    ws = lib.ir_paged_decode_workspace_size(64, 28, 4, 128, 256, 16, 512)
+    rows = 64 * 28 * 8
+    assert ws >= rows * 128 * 4 + rows * 2 * 4
+
+
+def test_no_product_module_imports_triton_or_the_oracle():
+    pkg = os.path.join(ROOT, "infrared_amd")
+    for name in os.listdir(pkg):
+        if not name.endswith(".py"):
+            continue
+        tree = ast.parse(open(os.path.join(pkg, name)).read())
+        for node in ast.walk(tree):
+            mods = []
+            if isinstance(node, ast.Import):
+                mods = [a.name for a in node.names]
+            elif isinstance(node, ast.ImportFrom) and node.module:
+                mods = [node.module]
+            for m in mods:
+                assert not m.startswith("triton"), f"{name} imports {m}"
+                assert not m.startswith("oracle"), f"{name} imports {m}"
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    code = (
+        "import infrared_amd._lib as L\n"
+        f"L.LIB_PATH = {str(tmp_path / 'absent.so')!r}\n"
+        "try:\n    L.lib()\nexcept RuntimeError as e:\n    print('RAISED', e)\n"
+    )
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, cwd=ROOT)
+    assert "RAISED" in res.stdout and "no non-HIP fallback" in res.stdout
+
+
+def test_pool_rejects_cpu_device():
+    import torch
+
+    from infrared_amd import PagedKVPool
+
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        PagedKVPool(1, 4, 16, 2, 64, torch.float32, device="cpu")

@@ -1,0 +1,119 @@
+"""The drop-in seam on the GPU: ``paged_attention`` with the reference's call
+signature (both the block-table path and the gather_slots+mask path), the
+pool's write/gather surface, and hipGraph capture/replay of a decode step."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from infrared_amd import PagedContext, PagedKVPool, metadata, paged_attention
+from infrared_amd.hip_graph import HipGraphDecoder, build_decode_static_inputs
+from oracle import naive as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def test_reference_style_single_block_pool():
+    """The reference's own GPU parity case (tests/test_triton_attention.py:155-187):
+    b=2, sq=4, 2 kv heads, n_rep=2, d=64, causal mask over this step's tokens."""
+    b, sq, h_kv, n_rep, d = 2, 4, 2, 2, 64
+    torch.manual_seed(0)
+    q = torch.randn(b, sq, h_kv * n_rep, d, device=DEV)
+    k = torch.randn(b, sq, h_kv, d, device=DEV)
+    v = torch.randn(b, sq, h_kv, d, device=DEV)
+    allowed = torch.arange(sq, device=DEV)[None, :] <= torch.arange(sq, device=DEV)[:, None]
+    mask = torch.zeros(b, 1, sq, sq, device=DEV).masked_fill(~allowed[None, None], torch.finfo(torch.float32).min)
+    n = b * sq
+    pool = PagedKVPool(1, 1, n, h_kv, d, torch.float32, device=DEV, strict=True)
+    ctx = PagedContext(pool, torch.arange(n, device=DEV), torch.arange(n, device=DEV).reshape(b, sq))
+    got = paged_attention(q, k, v, ctx, mask, 0, d**-0.5, n_rep)
+    want = O.masked_attention(
+        q.cpu(), O.repeat_kv(k.cpu(), n_rep), O.repeat_kv(v.cpu(), n_rep), mask.cpu(), d**-0.5
+    )
+    assert (got.cpu() - want).abs().max().item() <= 1e-4
+
+
+@pytest.mark.parametrize("use_triton", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_step_through_seam(use_triton, dtype):
+    """One batched decode step as the engine issues it (infrared/engine/paged_engine.py:290-332):
+    scatter the new K/V, then attend; the block-table path and the mask path both
+    match the oracle run on the same pool."""
+    g = torch.Generator().manual_seed(7)
+    bs, h_kv, n_rep, d, b = 16, 4, 7, 128, 9
+    num_cached = torch.randint(0, 900, (b,), generator=g).tolist()
+    perm = torch.randperm(600, generator=g).tolist()
+    tables, off = [], 0
+    for nc in num_cached:
+        nb = metadata.blocks_for(nc + 1, bs)
+        tables.append(perm[off : off + nb])
+        off += nb
+    pool = PagedKVPool(2, 600, bs, h_kv, d, dtype, device=DEV, strict=True)
+    pool.k.normal_()
+    pool.v.normal_()
+    paged, mask = metadata.decode_context(pool, tables, num_cached, use_triton=use_triton)
+    q = torch.randn(b, 1, h_kv * n_rep, d, device=DEV).to(dtype)
+    k = torch.randn(b, 1, h_kv, d, device=DEV).to(dtype)
+    v = torch.randn(b, 1, h_kv, d, device=DEV).to(dtype)
+    k_ref, v_ref = pool.k[1].cpu().clone(), pool.v[1].cpu().clone()
+    out = paged_attention(q, k, v, paged, mask, 1, d**-0.5, n_rep)
+    O.pool_write(k_ref, v_ref, k.reshape(-1, h_kv, d).cpu(), v.reshape(-1, h_kv, d).cpu(), paged.write_slots.cpu())
+    assert torch.equal(pool.k[1].cpu(), k_ref) and torch.equal(pool.v[1].cpu(), v_ref)
+    ref = O.paged_attention_naive(
+        q.float().cpu(), k_ref.float(), v_ref.float(), paged.gather_slots.cpu(), mask.float().cpu(), d**-0.5, n_rep
+    )
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert (out.float().cpu() - ref).abs().max().item() <= tol
+
+
+def test_pool_gather_matches_indexing_and_strict_raises():
+    pool = PagedKVPool(2, 8, 4, 2, 64, torch.bfloat16, device=DEV, strict=True)
+    pool.k.normal_()
+    pool.v.normal_()
+    gs = torch.randint(0, 32, (3, 5), device=DEV)
+    k, v = pool.gather(1, gs)
+    assert torch.equal(k, pool.k[1][gs]) and torch.equal(v, pool.v[1][gs])
+    with pytest.raises(IndexError, match="slot"):
+        pool.write(0, torch.zeros(1, 2, 64, device=DEV, dtype=torch.bfloat16),
+                   torch.zeros(1, 2, 64, device=DEV, dtype=torch.bfloat16),
+                   torch.tensor([32], device=DEV))
+
+
+def test_hip_graph_decode_replay_matches_eager():
+    """Capture a 3-layer decode step (scatter + attention per layer) per bucket and
+    replay it across growing contexts; every replay equals the eager step bit for bit."""
+    bs, h_kv, n_rep, d, layers = 16, 4, 7, 128, 3
+    dtype = torch.bfloat16
+    pool = PagedKVPool(layers, 512, bs, h_kv, d, dtype, device=DEV)
+    pool.k.normal_()
+    pool.v.normal_()
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    qkv = torch.randn(layers, 8, 1, h_kv * (n_rep + 2), d, generator=gen, device=DEV).to(dtype)
+
+    def step(buf, paged):
+        # K/V are a function of the token id, so pad-by-repeat rows write the
+        # same rows to the same slots, as a real model's would
+        outs = []
+        ids = buf.ids[:, 0]
+        for layer in range(layers):
+            x = qkv[layer].index_select(0, ids)
+            q = x[:, :, : h_kv * n_rep].contiguous()
+            k = x[:, :, h_kv * n_rep : h_kv * (n_rep + 1)].contiguous()
+            v = x[:, :, h_kv * (n_rep + 1) :].contiguous()
+            outs.append(paged_attention(q, k, v, paged, buf.mask, layer, d**-0.5, n_rep))
+        return torch.stack(outs, dim=1)  # [B, layers, 1, H, D]
+
+    dec = HipGraphDecoder(None, pool, max_num_seqs=8, t_max=1024, block_size=bs, step_fn=step)
+    tables = [list(range(i * 64, i * 64 + 64)) for i in range(6)]
+    for it, num_cached in enumerate([[5, 100, 300], [6, 101, 301], [17, 700, 2, 40, 900]]):
+        b = len(num_cached)
+        got = dec.decode(tables[:b], num_cached, list(range(b))).clone()
+        inp = build_decode_static_inputs(
+            tables[:b], num_cached, list(range(b)), b, 1024, bs, DEV, dtype
+        )
+        paged = PagedContext(pool, inp.write_slots, inp.gather_slots, True, inp.block_tables, inp.context_lens)
+        want = step(inp, paged)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {it} differs"
