@@ -44,6 +44,10 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--cpu-iters", type=int, default=3, help="timed CPU-baseline iterations (0 = skip)")
     p.add_argument("--cpu-seqs", type=int, default=0, help="sequences in the CPU sample (0 = all)")
     p.add_argument("--check", action="store_true", help="also check the output against the oracle")
+    p.add_argument("--mode", choices=("graph", "eager"), default="graph",
+                   help="time a hipGraph replay of the K calls (default) or host-launched calls")
+    p.add_argument("--copy-calib-mib", type=int, default=0,
+                   help="after timing, run 10 device copies of this many MiB (counter calibration)")
     return p.parse_args()
 
 
@@ -57,7 +61,7 @@ def _gpu_decode(case, args):
     ws_bytes = kernels.decode_workspace_bytes(
         b, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, max_blocks, cfg.block_size, part
     )
-    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
     outs = [torch.empty_like(case.q) for _ in case.block_tables]
 
     def call(i: int) -> None:
@@ -80,6 +84,8 @@ def _gpu_decode(case, args):
     torch.cuda.synchronize()
     eager_ms = s.elapsed_time(e) / args.steps
 
+    if args.mode == "eager":
+        return part, ws_bytes, eager_ms, eager_ms, outs
     # graph-replayed timing: the K calls back to back on the device
     graph = torch.cuda.CUDAGraph()
     stream = torch.cuda.Stream()
@@ -135,6 +141,16 @@ def _cpu_baseline(case, args):
     }
 
 
+def _traffic(config: str) -> tuple[int | None, str | None]:
+    """HBM bytes per decode launch measured with rocprofv3 counters, if recorded."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"decode_{config}_traffic.json")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        rec = json.load(f)
+    return int(rec["hbm_bytes_per_launch"]), os.path.relpath(path, os.path.dirname(path) + "/..")
+
+
 def main() -> int:
     args = _parse()
     if args.gpus != 1:
@@ -164,7 +180,14 @@ def main() -> int:
             case.context_lens.cpu(), cfg.block_size, cfg.scale,
         )
         check = round((outs[0].float().cpu() - ref).abs().max().item(), 6)
+    if args.copy_calib_mib > 0:
+        src = torch.empty(args.copy_calib_mib << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     cpu = _cpu_baseline(case, args) if args.cpu_iters > 0 else None
+    traffic, traffic_src = _traffic(args.config)
     esize = torch.tensor([], dtype=cfg.dtype).element_size()
     line = {
         "metric": METRIC,
@@ -199,8 +222,9 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
-            "timed": "decode call (split kernel + reduce), hipGraph replay, events on the launch stream",
+            "traffic": traffic,
+            "traffic_source": traffic_src,
+            "timed": f"decode call, {args.mode} launches, events on the launch stream",
         },
         "cpu_baseline": cpu,
     }

@@ -113,8 +113,11 @@ int ir_paged_gather(const void* k_cache, const void* v_cache, int64_t cache_slot
 /*
  * Bytes of device workspace ir_paged_decode needs for this shape (0 when one
  * partition covers the longest context). The workspace holds the split-KV
- * partials: running max / sum [num_seqs, num_q_heads, parts] and the
- * unnormalised accumulators [num_seqs, num_q_heads, parts, head_dim] in fp32.
+ * arrival counters (one int32 per sequence x KV head x group of 16 query
+ * heads) and the partials: unnormalised accumulators [num_seqs, num_q_heads,
+ * parts, head_dim] and running max / sum [num_seqs, num_q_heads, parts, 2], fp32.
+ * The caller zero-fills it once before first use; every call leaves the
+ * counters at zero again. Calls sharing a workspace must be stream-ordered.
  */
 int64_t ir_paged_decode_workspace_size(int num_seqs, int num_q_heads, int num_kv_heads,
                                        int head_dim, int max_blocks_per_seq, int block_size,
@@ -136,10 +139,13 @@ int ir_paged_decode_default_partition(int num_seqs, int num_kv_heads, int max_bl
  *   q, out:       [num_seqs, num_q_heads, head_dim] (strides seq, head in elements).
  *   block_tables: [num_seqs, bt_stride] int32 block ids, first max_blocks_per_seq used.
  *   context_lens: [num_seqs] int32 (0 gives a zero output row).
- *   partition_tokens: split-KV partition length in tokens (multiple of 16;
- *                 0 = ir_paged_decode_default_partition). Sequences longer
- *                 than one partition are merged by a log-sum-exp reduce.
- *   workspace:    >= ir_paged_decode_workspace_size(...) bytes, 256-byte aligned.
+ *   partition_tokens: split-KV partition length in tokens (multiple of 16,
+ *                 at most 4096; 0 = ir_paged_decode_default_partition). A sequence longer
+ *                 than one partition is split across workgroups whose partials
+ *                 the last-arriving workgroup merges (log-sum-exp), all in one
+ *                 launch.
+ *   workspace:    >= ir_paged_decode_workspace_size(...) bytes, 256-byte
+ *                 aligned, zero-filled before its first use.
  * head_dim in {64, 128}; num_q_heads % num_kv_heads == 0; dtype f32/f16/bf16.
  */
 int ir_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_stride,

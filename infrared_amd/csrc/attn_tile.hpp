@@ -41,9 +41,12 @@ struct State {
   f32x4 acc[D / 16];
 };
 
+// Running max starts at -FLT_MAX (finite): a column that has seen no key yet
+// then gets exp2(-inf - m) = 0 for absent keys instead of a NaN, and its first
+// real tile always raises the max.
 template <int D>
 __device__ __forceinline__ void state_init(State<D>& st) {
-  st.m = kNegInf;
+  st.m = -__FLT_MAX__;
   st.l = 0.f;
 #pragma unroll
   for (int n = 0; n < D / 16; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -99,6 +102,120 @@ __device__ __forceinline__ void load_v(const uint8_t* row, int c, uint32_t (&v)[
   load_dwords<Sh::VDW>(row + Sh::TILES * c * Sh::EB, v);
 }
 
+// ---------------------------------------------------------------- K staged through LDS
+//
+// The QK MFMA wants lane (g,c) to own a head_dim run of key row c, but loading
+// it that way makes every load instruction touch 16 rows x 64 B. Instead the
+// K tile is loaded like V -- each instruction reads RPI whole rows, 1 KiB
+// contiguous in a head-major pool -- written to a per-wavefront LDS tile and
+// read back in operand layout. 16-byte chunk k of row t lives at LDS offset
+// t * ROWB + 16 * (k ^ (t % CPR)): the XOR swizzle keeps both the row-wise
+// writes and the column-wise operand reads free of bank conflicts.
+template <int DT, int D>
+struct KStage {
+  static constexpr int ROWB = D * TileShape<DT, D>::EB;  // bytes of one K row of one head
+  static constexpr int CPR = ROWB / 16;                  // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;                   // rows per load instruction
+  static constexpr int NI = 16 / RPI;                    // load instructions per 16-row tile
+  static constexpr int BYTES = 16 * ROWB;                // LDS bytes of one tile
+  static_assert(NI * 4 == TileShape<DT, D>::KDW, "K staging and operand sizes differ");
+};
+
+// Row of the tile that lane `lane` loads in instruction i, and its chunk.
+template <int DT, int D>
+__device__ __forceinline__ int kstage_row(int i, int lane) {
+  typedef KStage<DT, D> KS;
+  return i * KS::RPI + lane / KS::CPR;
+}
+
+template <int DT, int D>
+__device__ __forceinline__ int kstage_chunk(int lane) {
+  return lane % KStage<DT, D>::CPR;
+}
+
+// Loads this lane's pieces of the K tile; row_ptr(t) is the byte address of
+// key row t (0..15) of the tile for this lane.
+template <int DT, int D, bool NT, typename RowPtr>
+__device__ __forceinline__ void kstage_load(RowPtr row_ptr, int lane, uint32_t (&k)[TileShape<DT, D>::KDW]) {
+  typedef KStage<DT, D> KS;
+#pragma unroll
+  for (int i = 0; i < KS::NI; ++i) {
+    const u32x4* p = (const u32x4*)(row_ptr(kstage_row<DT, D>(i, lane)) + 16 * kstage_chunk<DT, D>(lane));
+    const u32x4 x = NT ? __builtin_nontemporal_load(p) : *p;
+    k[4 * i + 0] = x[0];
+    k[4 * i + 1] = x[1];
+    k[4 * i + 2] = x[2];
+    k[4 * i + 3] = x[3];
+  }
+}
+
+// Token held by MFMA row c of the staged-K operand: tok(c) = 4*(c%4) + c/4.
+// The QK result then gives lane group g, register r the score of token
+// 4r + g, so the four V rows a lane group needs for register r are tokens
+// 4r..4r+3 -- one contiguous 1 KiB load across the lane groups.
+__device__ __forceinline__ int staged_token(int c) { return 4 * (c & 3) + (c >> 2); }
+
+// Writes the loaded pieces to the wavefront's LDS tile and reads back the QK
+// operand (lane (g,c): token staged_token(c), chunks 4j+g), same element order
+// as load_k.
+template <int DT, int D>
+__device__ __forceinline__ void kstage_transpose(uint8_t* lds, int lane, const uint32_t (&kin)[TileShape<DT, D>::KDW],
+                                                 uint32_t (&kout)[TileShape<DT, D>::KDW]) {
+  typedef KStage<DT, D> KS;
+  const int ch = kstage_chunk<DT, D>(lane);
+#pragma unroll
+  for (int i = 0; i < KS::NI; ++i) {
+    const int t = kstage_row<DT, D>(i, lane);
+    *(u32x4*)(lds + t * KS::ROWB + 16 * (ch ^ (t % KS::CPR))) =
+        u32x4{kin[4 * i], kin[4 * i + 1], kin[4 * i + 2], kin[4 * i + 3]};
+  }
+  // the operand reads below take rows other lanes wrote: keep them after the
+  // writes (LDS executes one wavefront's accesses in order)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int g = lane >> 4, t = staged_token(lane & 15);
+#pragma unroll
+  for (int j = 0; j < KS::NI; ++j) {
+    const u32x4 x = *(const u32x4*)(lds + t * KS::ROWB + 16 * ((4 * j + g) ^ (t % KS::CPR)));
+    kout[4 * j + 0] = x[0];
+    kout[4 * j + 1] = x[1];
+    kout[4 * j + 2] = x[2];
+    kout[4 * j + 3] = x[3];
+  }
+  // the next tile's writes must follow these reads
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// N dwords from p (16- or 8-byte loads), optionally non-temporal.
+template <int N, bool NT>
+__device__ __forceinline__ void load_dwords_nt(const uint8_t* p, uint32_t (&v)[N]) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const u32x4 x = NT ? __builtin_nontemporal_load((const u32x4*)p + i) : ((const u32x4*)p)[i];
+      v[4 * i + 0] = x[0];
+      v[4 * i + 1] = x[1];
+      v[4 * i + 2] = x[2];
+      v[4 * i + 3] = x[3];
+    }
+  } else {
+    static_assert(N == 2, "row piece must be 8 or 16*k bytes");
+    const u32x2 x = NT ? __builtin_nontemporal_load((const u32x2*)p) : *(const u32x2*)p;
+    v[0] = x[0];
+    v[1] = x[1];
+  }
+}
+
+// V elements of one key row this lane needs, optionally non-temporal.
+template <int DT, int D, bool NT>
+__device__ __forceinline__ void load_v_nt(const uint8_t* row, int c, uint32_t (&v)[TileShape<DT, D>::VDW]) {
+  typedef TileShape<DT, D> Sh;
+  load_dwords_nt<Sh::VDW, NT>(row + Sh::TILES * c * Sh::EB, v);
+}
+
 // S^T = K . Q^T for one 16-key tile; lane (g,c) register r = key 4g+r, column c.
 template <int DT, int D>
 __device__ __forceinline__ f32x4 qk_tile(const uint32_t (&k)[TileShape<DT, D>::KDW],
@@ -119,31 +236,43 @@ __device__ __forceinline__ f32x4 qk_tile(const uint32_t (&k)[TileShape<DT, D>::K
   return s;
 }
 
-// Online-softmax update with base-2 scores sv (-inf = key excluded) followed by
-// O^T += V^T . P^T. `vok[r]` says whether key row 4g+r may be read; rows that
-// may not are zeroed so 0 * V never meets a NaN pattern in stale pool memory.
-template <int DT, int D>
+// Lazy rescale: the running max of a column only moves when a tile's max
+// exceeds it by more than kRescaleSlack (log2 units). The result is the same
+// softmax -- numerator and denominator use the same max -- with unnormalised
+// probabilities bounded by 2^kRescaleSlack, and the accumulator rescale (a
+// pass over every output register) runs only on the rare tiles that raise a
+// max (a wave-uniform branch).
+constexpr float kRescaleSlack = 8.f;
+
+// Online-softmax update with base-2 scores sv (-inf = key absent) followed by
+// O^T += V^T . P^T. Unless FULL, `vok[r]` says whether key row 4g+r may be
+// read; rows that may not are zeroed so 0 * V never meets a NaN pattern in
+// stale pool memory. FULL tiles (every key present) skip that masking.
+template <int DT, int D, bool FULL>
 __device__ __forceinline__ void softmax_pv(const float (&sv)[4], const uint32_t (&vin)[4][TileShape<DT, D>::VDW],
                                            const bool (&vok)[4], State<D>& st) {
   typedef TileShape<DT, D> Sh;
   constexpr int TILES = Sh::TILES;
   float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
   mx = wave_max_groups(mx);
-  const float m_new = fmaxf(st.m, mx);
-  const bool none = m_new == kNegInf;  // no key of this column seen yet
-  const float alpha = none ? 1.f : fast_exp2(st.m - m_new);
+  const bool grow = mx > st.m + kRescaleSlack;
+  if (__any(grow)) {
+    const float m_new = grow ? mx : st.m;
+    const float alpha = fast_exp2(st.m - m_new);  // 1 if unchanged, 0 from the start value
+    st.l *= alpha;
+#pragma unroll
+    for (int n = 0; n < TILES; ++n) st.acc[n] *= alpha;
+    st.m = m_new;
+  }
   float p[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) p[r] = none ? 0.f : fast_exp2(sv[r] - m_new);
-  st.l = st.l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-  st.m = m_new;
-#pragma unroll
-  for (int n = 0; n < TILES; ++n) st.acc[n] *= alpha;
+  for (int r = 0; r < 4; ++r) p[r] = fast_exp2(sv[r] - st.m);
+  st.l += (p[0] + p[1]) + (p[2] + p[3]);
   uint32_t v[4][Sh::VDW];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int i = 0; i < Sh::VDW; ++i) v[r][i] = vok[r] ? vin[r][i] : 0u;
+    for (int i = 0; i < Sh::VDW; ++i) v[r][i] = (FULL || vok[r]) ? vin[r][i] : 0u;
   if constexpr (Sh::k16) {
     // P rounded to the input dtype, as softmax(...).to(q.dtype) does.
     using E = Elem<DT>;

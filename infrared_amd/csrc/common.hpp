@@ -16,6 +16,9 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_inff();
@@ -62,9 +65,10 @@ struct Elem<IR_DTYPE_BF16> {
   static constexpr int bytes = 2;
   __device__ __forceinline__ static float to_f32(storage s) { return bf16_to_f32(s); }
   __device__ __forceinline__ static storage from_f32(float f) { return (storage)f32_to_bf16(f); }
-  // packs two fp32 values into one dword of two elements (lo first)
+  // packs two fp32 values into one dword of two elements (lo first), rounding
+  // to nearest even (one v_cvt_pk_bf16_f32)
   __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
-    return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
   }
   __device__ __forceinline__ static float lo(uint32_t w) { return __uint_as_float(w << 16); }
   __device__ __forceinline__ static float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -77,7 +81,7 @@ struct Elem<IR_DTYPE_F16> {
   __device__ __forceinline__ static float to_f32(storage s) { return f16_to_f32(s); }
   __device__ __forceinline__ static storage from_f32(float f) { return (storage)f32_to_f16(f); }
   __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
-    return f32_to_f16(lo) | (f32_to_f16(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
   }
   __device__ __forceinline__ static float lo(uint32_t w) { return f16_to_f32(w & 0xffffu); }
   __device__ __forceinline__ static float hi(uint32_t w) { return f16_to_f32(w >> 16); }
@@ -156,17 +160,21 @@ __device__ __forceinline__ T load_nt(const T* p) {
 }
 
 // Flat slot of logical token `t` of a sequence whose block table row is `bt`:
-// bt[t / bs] * bs + t % bs (infrared/engine/paged_engine.py:621-625). Returns -1
-// (and flags) for a block id outside [0, num_blocks).
-__device__ __forceinline__ int64_t token_slot(const int32_t* bt, int t, int bs, int64_t num_blocks,
-                                              int32_t* err) {
+// bt[t / bs] * bs + t % bs (infrared/engine/paged_engine.py:621-625), or -1 for
+// a block id outside [0, num_blocks). Does not report; see token_slot.
+__device__ __forceinline__ int64_t token_slot_or_neg(const int32_t* bt, int t, int bs, int64_t num_blocks) {
   const int blk = t / bs;
   const int32_t bid = bt[blk];
-  if (bid < 0 || (int64_t)bid >= num_blocks) {
-    flag_error(err, IR_ERR_BLOCK_RANGE);
-    return -1;
-  }
+  if (bid < 0 || (int64_t)bid >= num_blocks) return -1;
   return (int64_t)bid * bs + (t - blk * bs);
+}
+
+// token_slot_or_neg that also flags IR_ERR_BLOCK_RANGE for a bad block id.
+__device__ __forceinline__ int64_t token_slot(const int32_t* bt, int t, int bs, int64_t num_blocks,
+                                              int32_t* err) {
+  const int64_t s = token_slot_or_neg(bt, t, bs, num_blocks);
+  if (s < 0) flag_error(err, IR_ERR_BLOCK_RANGE);
+  return s;
 }
 
 }  // namespace ir

@@ -125,7 +125,7 @@ __global__ __launch_bounds__(kWaves * 64) void paged_masked_kernel(MaskedArgs a)
         sv[r] = kNegInf;
       }
     }
-    softmax_pv<DT, D>(sv, tl.v, vok, st);
+    softmax_pv<DT, D, false>(sv, tl.v, vok, st);
   }
   st.l = wave_sum_groups(st.l);
 

@@ -152,8 +152,9 @@ def paged_decode(
     """GQA paged decode: ``q`` ``[B, H_q, D]`` -> ``[B, H_q, D]``.
 
     ``block_tables`` int32 ``[B, max_blocks]``, ``context_lens`` int32 ``[B]``.
-    ``workspace`` (uint8, 256-byte aligned) is allocated when not given and the
-    longest possible context needs more than one partition.
+    ``workspace`` (uint8, 256-byte aligned, zero-filled before first use; the
+    kernel leaves its arrival counters at zero) is allocated when not given and
+    the longest possible context needs more than one partition.
     """
     dev = require_device(q, k_cache, v_cache, block_tables, context_lens)
     _cache_layer("paged_decode", k_cache)
@@ -174,7 +175,7 @@ def paged_decode(
         partition_tokens = default_partition(b, h_kv, max_blocks, block_size)
     need = decode_workspace_bytes(b, hq, h_kv, d, max_blocks, block_size, partition_tokens)
     if need > 0 and (workspace is None or workspace.numel() < need):
-        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        workspace = torch.zeros(need, dtype=torch.uint8, device=dev)
     rc = lib().ir_paged_decode(
         ptr(q), q.stride(0), q.stride(1), ptr(k_cache), ptr(v_cache), k_cache.stride(0),
         k_cache.stride(1), k_cache.shape[0] // block_size, block_size, ptr(block_tables),

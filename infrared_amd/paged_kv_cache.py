@@ -11,10 +11,23 @@ Same public surface as the reference's ``infrared/cache/paged_kv_cache.py``:
   (``:75-91``), with optional device-side fields the fast kernels read:
   ``block_tables`` ``[B, max_blocks]`` int32, ``context_lens`` ``[B]`` int32.
 
-The layout is kept flat so a token at slot ``s`` is row ``s`` (callers write
-``pool.k[layer, a:b]`` directly). ``write`` runs the HIP scatter kernel;
-``gather`` runs the HIP slot-gather. The pool lives in device memory only:
-CPU tensors are rejected rather than handled by a fallback.
+Indexing is the reference's: ``pool.k[layer, s]`` is the ``[num_kv_heads,
+head_dim]`` row of slot ``s`` and callers may write ``pool.k[layer, a:b]``
+directly. The physical layout is a choice:
+
+- ``layout="head_major"`` (default): storage ``[L, num_kv_heads, num_slots,
+  head_dim]``, exposed as the ``[L, num_slots, num_kv_heads, head_dim]`` view.
+  One KV head's block of 16 tokens is then 16 * head_dim contiguous elements
+  (4 KiB in bf16 at head_dim 128), which the decode kernel streams with
+  fully contiguous 1 KiB load instructions.
+- ``layout="slot_major"``: the reference's contiguous ``[L, num_slots,
+  num_kv_heads, head_dim]`` storage (a KV head's block is 16 pieces of
+  ``head_dim`` elements strided by a whole slot row).
+
+Every kernel takes the slot and head strides, so both layouts run the same
+code. ``write`` runs the HIP scatter kernel; ``gather`` runs the HIP
+slot-gather. The pool lives in device memory only: CPU tensors are rejected
+rather than handled by a fallback.
 """
 
 from __future__ import annotations
@@ -58,6 +71,7 @@ class PagedKVPool:
         device: torch.device | str = "cuda",
         *,
         strict: bool = False,
+        layout: str = "head_major",
     ) -> None:
         device = torch.device(device)
         if device.type != "cuda":
@@ -73,9 +87,17 @@ class PagedKVPool:
         self.dtype = dtype
         self.device = device
         self.strict = strict
-        shape = (num_layers, self.num_slots, num_kv_heads, head_dim)
-        self.k = torch.zeros(shape, dtype=dtype, device=device)
-        self.v = torch.zeros(shape, dtype=dtype, device=device)
+        self.layout = layout
+        if layout == "head_major":
+            store = (num_layers, num_kv_heads, self.num_slots, head_dim)
+            self.k = torch.zeros(store, dtype=dtype, device=device).permute(0, 2, 1, 3)
+            self.v = torch.zeros(store, dtype=dtype, device=device).permute(0, 2, 1, 3)
+        elif layout == "slot_major":
+            shape = (num_layers, self.num_slots, num_kv_heads, head_dim)
+            self.k = torch.zeros(shape, dtype=dtype, device=device)
+            self.v = torch.zeros(shape, dtype=dtype, device=device)
+        else:
+            raise ValueError(f"unknown pool layout {layout!r} (head_major, slot_major)")
         self.err_flags = torch.zeros(1, dtype=torch.int32, device=device)
         self._workspace: torch.Tensor | None = None
 
@@ -122,13 +144,14 @@ class PagedKVPool:
         return out
 
     def workspace(self, nbytes: int) -> torch.Tensor:
-        """A cached device buffer of at least ``nbytes`` (split-KV partials).
+        """A cached, zero-filled device buffer of at least ``nbytes`` (split-KV
+        counters and partials; the decode kernel leaves the counters at zero).
 
         Grow it outside hipGraph capture (the graph decoder's warm-up does) so a
         captured graph keeps pointing at live memory.
         """
         if self._workspace is None or self._workspace.numel() < nbytes:
-            self._workspace = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+            self._workspace = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
         return self._workspace
 
     def check_errors(self) -> None:

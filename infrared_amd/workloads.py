@@ -15,7 +15,10 @@ pool are N(0, 1) drawn in fp32 and cast to the workload dtype. Metadata is
 drawn on the CPU from ``torch.Generator(seed)``; q/K/V are drawn on the target
 device from a generator with the same seed. ``rotations > 1`` lays out that
 many disjoint copies of the block tables over one larger pool (each with its
-own K/V values) so back-to-back calls can walk different memory.
+own K/V values) so back-to-back calls can walk different memory. The K/V
+layer tensors are ``[num_slots, H_kv, D]`` views of head-major storage
+``[H_kv, num_slots, D]`` by default (``layout="slot_major"`` gives the
+contiguous reference layout).
 """
 
 from __future__ import annotations
@@ -104,6 +107,7 @@ def make_decode_case(
     seed: int | None = None,
     rotations: int = 1,
     num_seqs: int | None = None,
+    layout: str = "head_major",
 ) -> DecodeCase:
     cfg = DECODE_CONFIGS[config] if isinstance(config, str) else config
     if num_seqs is not None:
@@ -131,13 +135,18 @@ def make_decode_case(
     num_slots = rotations * pool_blocks * bs
     shape = (num_slots, cfg.num_kv_heads, cfg.head_dim)
     q = torch.randn(cfg.num_seqs, cfg.num_q_heads, cfg.head_dim, generator=dgen, device=device)
-    k = torch.randn(shape, generator=dgen, device=device)
-    v = torch.randn(shape, generator=dgen, device=device)
+    k = torch.randn(shape, generator=dgen, device=device).to(cfg.dtype)
+    v = torch.randn(shape, generator=dgen, device=device).to(cfg.dtype)
+    if layout == "head_major":
+        k = k.permute(1, 0, 2).contiguous().permute(1, 0, 2)
+        v = v.permute(1, 0, 2).contiguous().permute(1, 0, 2)
+    elif layout != "slot_major":
+        raise ValueError(f"unknown layout {layout!r}")
     return DecodeCase(
         config=cfg,
         q=q.to(cfg.dtype),
-        k_cache=k.to(cfg.dtype),
-        v_cache=v.to(cfg.dtype),
+        k_cache=k,
+        v_cache=v,
         block_tables=tables,
         context_lens=ctx.to(torch.int32).to(device),
         pool_blocks=pool_blocks,

@@ -29,13 +29,17 @@ def _err():
 # ------------------------------------------------------------------ scatter
 
 
+@pytest.mark.parametrize("head_major", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("h_kv,d", [(2, 64), (4, 128), (1, 8), (3, 4)])
-def test_scatter_bit_exact_vs_index_put(dtype, h_kv, d):
+def test_scatter_bit_exact_vs_index_put(dtype, h_kv, d, head_major):
     g = torch.Generator(device=DEV).manual_seed(d + h_kv)
     num_slots, n = 512, 97
     base = torch.randn(num_slots, h_kv, d, generator=g, device=DEV).to(dtype)
-    kc, vc = base.clone(), (base * -1).clone()
+    if head_major:
+        base = base.permute(1, 0, 2).contiguous().permute(1, 0, 2)
+    kc, vc = base.clone(), (base * -1).clone()  # clone keeps the strides
+    assert kc.stride() == base.stride()
     k = torch.randn(n, h_kv, d, generator=g, device=DEV).to(dtype)
     v = torch.randn(n, h_kv, d, generator=g, device=DEV).to(dtype)
     slots = torch.randperm(num_slots, device=DEV)[:n]
@@ -159,15 +163,18 @@ def _check_decode(case, partition_tokens=0, seqs=None):
     return out
 
 
-def test_decode_qwen05b_fp32_parity():
+@pytest.mark.parametrize("layout", ["head_major", "slot_major"])
+def test_decode_qwen05b_fp32_parity(layout):
     """Qwen2.5-0.5B shape, fp32: 8 seqs, 14/2 heads, D=64, ctx U[1,512]; bar 1e-4."""
-    _check_decode(make_decode_case("qwen0.5b-fp32", DEV))
+    _check_decode(make_decode_case("qwen0.5b-fp32", DEV, layout=layout))
 
 
+@pytest.mark.parametrize("layout", ["head_major", "slot_major"])
 @pytest.mark.parametrize("partition_tokens", [0, 256, 4096])
-def test_decode_qwen7b_bf16_full_size_parity(partition_tokens):
-    """Qwen2.5-7B shape, bf16, full batch of 64 with ctx U[512,4096]; bar 2e-2 vs fp32."""
-    _check_decode(make_decode_case("qwen7b-bf16", DEV), partition_tokens)
+def test_decode_qwen7b_bf16_full_size_parity(partition_tokens, layout):
+    """Qwen2.5-7B shape, bf16, full batch of 64 with ctx U[512,4096]; bar 2e-2 vs fp32,
+    in both pool layouts."""
+    _check_decode(make_decode_case("qwen7b-bf16", DEV, layout=layout), partition_tokens)
 
 
 def test_decode_skewed_long_context_split_kv():
@@ -214,6 +221,31 @@ def test_decode_zero_context_row_and_determinism():
     )
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("partition_tokens", [64, 512])
+def test_decode_fused_merge_repeatable_and_counters_clean(partition_tokens):
+    """Many split-KV partitions per sequence, merged by the last-arriving workgroup:
+    50 back-to-back calls sharing one workspace give bit-identical outputs, match
+    the oracle, and leave every arrival counter at zero."""
+    case = make_decode_case("qwen7b-bf16", DEV)
+    cfg = case.config
+    bt = case.block_tables[0]
+    need = kernels.decode_workspace_bytes(64, 28, 4, 128, bt.shape[1], 16, partition_tokens)
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    outs = [
+        kernels.paged_decode(case.q, case.k_cache, case.v_cache, bt, case.context_lens, 16, cfg.scale,
+                             partition_tokens=partition_tokens, workspace=ws)
+        for _ in range(50)
+    ]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    counters = ws[: 64 * 4 * 4].view(torch.int32)
+    assert counters.eq(0).all()
+    ref = O.decode_reference(case.q.cpu(), case.k_cache.cpu(), case.v_cache.cpu(), bt.cpu(),
+                             case.context_lens.cpu(), 16, cfg.scale)
+    assert (outs[0].float().cpu() - ref).abs().max().item() <= TOL[cfg.dtype]
 
 
 def test_decode_flags_bad_block_ids_and_contexts():

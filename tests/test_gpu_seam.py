@@ -68,6 +68,27 @@ def test_decode_step_through_seam(use_triton, dtype):
     assert (out.float().cpu() - ref).abs().max().item() <= tol
 
 
+@pytest.mark.parametrize("layout", ["head_major", "slot_major"])
+def test_pool_direct_slot_writes_feed_the_kernels(layout):
+    """Reference callers write history straight into ``pool.k[layer, a:b]``
+    (tests/test_cuda_graph.py:199-203); the kernels read it back in both layouts."""
+    bs, h_kv, d = 8, 2, 64
+    pool = PagedKVPool(2, 4, bs, h_kv, d, torch.float32, device=DEV, layout=layout)
+    assert pool.k.shape == (2, 32, h_kv, d)
+    k0 = torch.randn(3, h_kv, d, device=DEV)
+    k1 = torch.randn(5, h_kv, d, device=DEV)
+    pool.k[1, 0:3] = k0
+    pool.v[1, 0:3] = k0 * 2
+    pool.k[1, 8:13] = k1
+    pool.v[1, 8:13] = k1 * 2
+    k, v = pool.gather(1, torch.tensor([[0, 1, 2, 8, 9]], device=DEV))
+    assert torch.equal(k[0, :3], k0) and torch.equal(k[0, 3:], k1[:2]) and torch.equal(v[0, :3], k0 * 2)
+    bt = torch.tensor([[0], [1]], dtype=torch.int32, device=DEV)
+    cl = torch.tensor([3, 5], dtype=torch.int32, device=DEV)
+    gk, gv = pool.gather_blocks(1, bt, cl, 6)
+    assert torch.equal(gk[0, :3], k0) and torch.equal(gk[1, :5], k1) and gk[0, 3:].eq(0).all()
+
+
 def test_pool_gather_matches_indexing_and_strict_raises():
     pool = PagedKVPool(2, 8, 4, 2, 64, torch.bfloat16, device=DEV, strict=True)
     pool.k.normal_()
