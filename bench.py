@@ -156,7 +156,7 @@ def main() -> int:
     if args.gpus != 1:
         print(
             f"bench.py measures the single-GPU hot path only; --gpus {args.gpus} is not supported "
-            "(the decode kernel shards by sequence / KV head with no exchange, see DESIGN.md)",
+            "(the decode kernel shards by sequence or KV head with no exchange inside attention)",
             file=sys.stderr,
         )
         return 2
