@@ -186,6 +186,36 @@ int ir_paged_attention_masked(const void* q, int64_t q_b_stride, int64_t q_s_str
                               int num_q_heads, int num_kv_heads, int head_dim, float scale,
                               int dtype, int32_t* err_flags, ir_stream_t stream);
 
+/*
+ * Chunked prefill / prefix-hit prefill / packed mixed step over block tables
+ * (16-bit dtypes, MFMA). Replaces the Sq > 1 uses of
+ * _paged_attention_triton / _paged_attention_naive
+ * (infrared/model/triton_attention.py:110-129, :310-358) with the
+ * (block_tables, cu_seqlens_q, q_start) form of the engine's prefill and mixed
+ * steps (infrared/engine/paged_engine.py:194-207, :461-516):
+ *   query token i of sequence b (packed row cu_seqlens_q[b] + i) is at
+ *   position q_start[b] + i and attends keys t <= q_start[b] + i of sequence b,
+ *   K/V rows addressed through block_tables[b] -- the causal-with-offset mask of
+ *   infrared/model/inputs.py:33-54 and, per sequence, the varlen mask of
+ *   infrared/model/inputs.py:57-85 (a decode row is a one-token sequence).
+ *   q, out:       [total_q, num_q_heads, head_dim] (strides token, head in elements).
+ *   cu_seqlens_q: [num_seqs + 1] int32, non-decreasing, cu_seqlens_q[num_seqs] <= total_q.
+ *   q_start:      [num_seqs] int32, tokens already cached (the first query's position).
+ *   max_q_len:    upper bound of the per-sequence query counts (sizes the grid).
+ * Keys q_start[b] + q_len_b beyond the table (max_blocks_per_seq * block_size) set
+ * IR_ERR_CONTEXT_RANGE and are clamped; a bad block id sets IR_ERR_BLOCK_RANGE and
+ * the key is skipped. head_dim in {64, 128}; dtype bf16 or f16 (fp32 returns
+ * IR_EUNSUPPORTED: use ir_paged_attention_masked).
+ */
+int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                     const void* k_cache, const void* v_cache, int64_t cache_slot_stride,
+                     int64_t cache_head_stride, int64_t num_blocks, int block_size,
+                     const int32_t* block_tables, int64_t bt_stride, int max_blocks_per_seq,
+                     const int32_t* cu_seqlens_q, const int32_t* q_start, int num_seqs,
+                     int total_q, int max_q_len, void* out, int64_t out_tok_stride,
+                     int64_t out_head_stride, int num_q_heads, int num_kv_heads, int head_dim,
+                     float scale, int dtype, int32_t* err_flags, ir_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,201 +1,21 @@
-// GQA paged decode attention for gfx950 (one query token per sequence).
+// GQA paged decode attention for gfx950 (split-KV partitions) and the C ABI
+// of the decode entry points.
 //
-// Work decomposition: one workgroup per (sequence, KV head, head group of <=16
-// query heads, partition of `part_tokens` keys). Its kWaves wavefronts take
-// the partition's 16-token tiles round-robin. Per tile a wavefront
-//   1. loads the 16 K rows and 16 V rows of its KV head straight from the pool
-//      with 16-byte loads (each row of one head is head_dim contiguous
-//      elements; the K/V tile is fetched once and serves every query head of
-//      the GQA group),
-//   2. scores S^T[token][head] = K . Q^T with MFMA (rows = 16 tokens, columns =
-//      the group's query heads, padded to 16),
-//   3. runs the online softmax in base 2 on the MFMA accumulator: per head the
-//      16 scores sit in 4 registers of 4 lane groups, so the tile max needs two
-//      cross-group shuffles,
-//   4. accumulates O^T[d][head] += V^T . P^T with MFMA, where the P^T operand is
-//      exactly the lane's own four probabilities and the V^T operand is a
-//      register-level 4x(head_dim/16) transpose of the loaded V rows.
-// Loads run one tile ahead of the math (a register ring), and the block ids
-// of a wavefront's tiles are fetched up front, one per lane, so no load waits
-// on a block-table read.
-//
-// The wavefronts' (max, sum, acc) states merge through LDS. A sequence that
-// fits one partition writes its output directly. Longer ones write fp32
-// partials; the last workgroup of a (sequence, KV head, head group) to finish
-// -- found with an arrival counter in the workspace -- merges them with
-// log-sum-exp weights and resets the counter to zero, so one launch does the
-// whole call and the workspace is clean for the next one.
-//
-// Algorithm parity: the one-shot softmax of infrared/model/layers.py:102-118
-// over the gathered history (infrared/model/triton_attention.py:110-129), with
-// the streaming max/sum update of infrared/model/triton_attention.py:135-177 and
-// the exp2 fold of infrared/model/triton_attention.py:249. For 16-bit dtypes
-// the probabilities are rounded to the input dtype before the PV product, as
-// `softmax(scores.float()).to(q.dtype)` does in the reference.
+// One workgroup per (unit, partition of `part_tokens` keys); the tile math is
+// in paged_decode.hpp. The wavefronts' (max, sum, acc) states merge through
+// LDS. A sequence that fits one partition writes its output directly. Longer
+// ones write fp32 partials that a second launch merges with log-sum-exp
+// weights (or, with IR_DECODE_MERGE=fused, the last workgroup of the unit to
+// finish -- found with an arrival counter in the workspace -- merges them and
+// resets the counter).
 #include <stdlib.h>
 #include <string.h>
 
-#include "attn_tile.hpp"
+#include "paged_decode.hpp"
 #include "status.hpp"
 
 namespace ir {
 namespace {
-
-constexpr int kMaxWaveTiles = 64;  // tiles per wavefront (one block id per lane)
-constexpr int kMaxPartition = 16 * kMaxWaveTiles * 4;  // tokens (4 wavefronts)
-
-struct DecodeArgs {
-  const void* q;
-  int64_t q_seq, q_head;  // elements
-  const void* kc;
-  const void* vc;
-  int64_t c_slot, c_head;  // elements
-  int64_t num_blocks;
-  int bs;
-  const int32_t* bt;
-  int64_t bt_stride;
-  int max_blocks;
-  const int32_t* ctx;
-  void* out;
-  int64_t o_seq, o_head;  // elements
-  int num_seqs, num_q_heads, num_kv_heads, n_rep, n_hg;
-  float scale_log2;
-  int part_tokens, max_parts;
-  int32_t* counters;  // [seq][kv_head][head group], zero at rest
-  float* ws_o;        // [seq][q_head][part][D]
-  float* ws_ml;       // [seq][q_head][part][2]
-  int32_t* err;
-};
-
-// Issues the loads of the tile starting at key t0 and returns a 4-bit mask of
-// which of this lane's keys 4r+g (r = 0..3) may be used (the keys whose scores
-// and V rows this lane holds, see staged_token). Every load is issued unconditionally and nothing else
-// touches memory here: an unusable key (bad block id, past the context) reads
-// row 0 of the pool instead and is masked in the math, and a bad block id only
-// sets `bad` (reported once after the loop). That keeps the hardware wait
-// counts exact, with no load-free or extra-memory-op path.
-// BS16: `bid` is the tile's wave-uniform block id; otherwise every lane
-// resolves its own keys through the block table.
-// Per-lane byte offsets of this lane's K pieces and V rows inside a 16-token
-// tile, relative to the tile's first row; constant across tiles when the tile
-// is one block's contiguous rows, so a tile load is uniform base + offset.
-template <int DT, int D>
-struct LaneOffsets {
-  uint32_t k[KStage<DT, D>::NI];
-  uint32_t v[4];
-};
-
-template <int DT, int D>
-__device__ __forceinline__ LaneOffsets<DT, D> lane_offsets(int lane, int64_t slot_bytes) {
-  typedef TileShape<DT, D> Sh;
-  LaneOffsets<DT, D> o;
-  const int g = lane >> 4, c = lane & 15;
-#pragma unroll
-  for (int i = 0; i < KStage<DT, D>::NI; ++i)
-    o.k[i] = (uint32_t)(kstage_row<DT, D>(i, lane) * slot_bytes + 16 * kstage_chunk<DT, D>(lane));
-#pragma unroll
-  for (int r = 0; r < 4; ++r) o.v[r] = (uint32_t)((4 * r + g) * slot_bytes + Sh::TILES * c * Sh::EB);
-  return o;
-}
-
-template <int DT, int D, bool BS16>
-__device__ __forceinline__ uint32_t load_tile(const DecodeArgs& a, const int32_t* bt_row, int32_t bid,
-                                              const uint8_t* kc, const uint8_t* vc, const LaneOffsets<DT, D>& lo,
-                                              int t0, int t_end, int lane, Tile<DT, D>& tl, bool& bad) {
-  typedef TileShape<DT, D> Sh;
-  const int g = lane >> 4, c = lane & 15;
-  const int64_t slot_bytes = a.c_slot * Sh::EB;
-  if constexpr (BS16) {
-    // The whole tile lies in one block, and every row of a block is inside the
-    // pool even past the context end. The tile base is wave-uniform.
-    const int blk = t0 / a.bs;
-    const bool ok = bid >= 0 && (int64_t)bid < a.num_blocks;
-    bad |= !ok;
-    const int64_t base = ok ? (int64_t)bid * a.bs + (t0 - blk * a.bs) : 0;
-    const uint8_t* tk = kc + base * slot_bytes;
-    const uint8_t* tv = vc + base * slot_bytes;
-#pragma unroll
-    for (int i = 0; i < KStage<DT, D>::NI; ++i) {
-      const u32x4 x = __builtin_nontemporal_load((const u32x4*)(tk + lo.k[i]));
-      tl.k[4 * i + 0] = x[0];
-      tl.k[4 * i + 1] = x[1];
-      tl.k[4 * i + 2] = x[2];
-      tl.k[4 * i + 3] = x[3];
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) load_dwords_nt<Sh::VDW, true>(tv + lo.v[r], tl.v[r]);
-    uint32_t m = 0;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) m |= (ok && t0 + 4 * r + g < t_end) ? (1u << r) : 0u;
-    return m;
-  } else {
-    kstage_load<DT, D, true>(
-        [&](int t) {
-          const int tk = t0 + t;
-          const int64_t ks = tk < t_end ? token_slot_or_neg(bt_row, tk, a.bs, a.num_blocks) : 0;
-          bad |= ks < 0;
-          return kc + (ks >= 0 ? ks : 0) * slot_bytes;
-        },
-        lane, tl.k);
-    uint32_t m = 0;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tv = t0 + 4 * r + g;
-      const int64_t vs = tv < t_end ? token_slot_or_neg(bt_row, tv, a.bs, a.num_blocks) : -1;
-      load_v_nt<DT, D, true>(vc + (vs >= 0 ? vs : 0) * slot_bytes, c, tl.v[r]);
-      m |= vs >= 0 ? (1u << r) : 0u;
-    }
-    return m;
-  }
-}
-
-// kmask: which of this lane's keys 4r+g are usable; a tile whose keys are
-// all usable in every lane takes the unmasked path.
-template <int DT, int D>
-__device__ __forceinline__ void compute_tile(const Tile<DT, D>& tl, const uint32_t (&qr)[TileShape<DT, D>::KDW],
-                                             uint32_t kmask, float scale_log2, uint8_t* kst, int lane, State<D>& st) {
-  uint32_t kop[TileShape<DT, D>::KDW];
-  kstage_transpose<DT, D>(kst, lane, tl.k, kop);
-  const f32x4 s = qk_tile<DT, D>(kop, qr);
-  float sv[4];
-  bool vok[4];
-  if (__all(kmask == 0xfu)) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      vok[r] = true;
-      sv[r] = s[r] * scale_log2;
-    }
-    softmax_pv<DT, D, true>(sv, tl.v, vok, st);
-  } else {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      vok[r] = (kmask >> r) & 1u;
-      sv[r] = vok[r] ? s[r] * scale_log2 : kNegInf;
-    }
-    softmax_pv<DT, D, false>(sv, tl.v, vok, st);
-  }
-}
-
-// Context length of `seq`, clamped to what its block table can hold (flagged).
-__device__ __forceinline__ int clamp_ctx(const DecodeArgs& a, int seq, bool report) {
-  int ctx = a.ctx[seq];
-  const int cap = a.max_blocks * a.bs;
-  if (ctx < 0 || ctx > cap) {
-    if (report) flag_error(a.err, IR_ERR_CONTEXT_RANGE);
-    ctx = ctx < 0 ? 0 : cap;
-  }
-  return ctx;
-}
-
-// Device-scope (sc1) accesses for the split-KV partials: written through to
-// the device coherence point and read back from it, so one workgroup can merge
-// what workgroups on other XCDs wrote without a cache-wide fence.
-__device__ __forceinline__ void store_dev(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_dev(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Log-sum-exp merge of the partitions of (seq, heads head0..head0+nh) into out.
 template <int DT, int D, bool DEV>
@@ -206,20 +26,9 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs& a, int seq, int
     const int hc = it / (D / 4);
     const int d0 = (it - hc * (D / 4)) * 4;
     const int64_t row0 = ((int64_t)seq * a.num_q_heads + head0 + hc) * a.max_parts;
-    const float* ml = a.ws_ml + row0 * 2;
-    float M = kNegInf;
-    for (int p = 0; p < nparts; ++p) M = fmaxf(M, DEV ? load_dev(ml + 2 * p) : ml[2 * p]);
-    float L = 0.f;
-    float o[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int p = 0; p < nparts; ++p) {
-      const float mp = DEV ? load_dev(ml + 2 * p) : ml[2 * p];
-      const float lp = DEV ? load_dev(ml + 2 * p + 1) : ml[2 * p + 1];
-      const float wt = mp == kNegInf ? 0.f : fast_exp2(mp - M);
-      L += wt * lp;
-      const float* src = a.ws_o + (row0 + p) * D + d0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) o[k] += wt * (DEV ? load_dev(src + k) : src[k]);
-    }
+    float o[4], L;
+    lse_merge(a.ws_o + row0 * D + d0, D, a.ws_ml + row0 * 2, 2, nparts,
+              [](const float* p) { return DEV ? load_dev(p) : *p; }, o, L);
     const float inv = L > 0.f ? 1.f / L : 0.f;
     store4<DT>((uint8_t*)a.out + ((int64_t)seq * a.o_seq + (int64_t)(head0 + hc) * a.o_head + d0) * EB, o, inv);
   }
@@ -257,63 +66,23 @@ void paged_decode_kernel(DecodeArgs a) {
   if (part >= nparts) return;
   const int t_begin = part * a.part_tokens;
   const int t_end = min(ctx, t_begin + a.part_tokens);
+  const int tile_lo = t_begin >> 4;
   // (an empty pool has nothing to read: every key is unusable)
-  const int ntiles = (t_end > t_begin && a.num_blocks > 0) ? (t_end - t_begin + 15) >> 4 : 0;
-  // this wavefront's tiles: partition tiles w, w + NW, ...
-  const int my_tiles = ntiles > w ? (ntiles - w + NW - 1) / NW : 0;
+  const int tile_hi = (t_end > t_begin && a.num_blocks > 0) ? (t_end + 15) >> 4 : tile_lo;
 
   const int h_local = hg * 16 + c;
-  const bool head_ok = h_local < a.n_rep;
-  const int qh = kvh * a.n_rep + h_local;
-
   const int32_t* bt_row = a.bt + (int64_t)seq * a.bt_stride;
-  // Block ids of this wavefront's tiles, lane j holding tile j (a wavefront
-  // has at most kMaxWaveTiles tiles), fetched once so no tile load waits on a
-  // block-table read.
-  int32_t bid_lane = 0;
-  if constexpr (BS16) {
-    if (lane < my_tiles) bid_lane = bt_row[(t_begin + 16 * (w + NW * lane)) / a.bs];
-  }
   const uint8_t* kc = (const uint8_t*)a.kc + (int64_t)kvh * a.c_head * EB;
   const uint8_t* vc = (const uint8_t*)a.vc + (int64_t)kvh * a.c_head * EB;
   const LaneOffsets<DT, D> lo = lane_offsets<DT, D>(lane, a.c_slot * EB);
-
-  // Q^T operand, same k-slot assignment as the K loads; padded heads are zero.
   uint32_t qr[Sh::KDW];
-  if (head_ok)
-    load_k<DT, D>((const uint8_t*)a.q + ((int64_t)seq * a.q_seq + (int64_t)qh * a.q_head) * EB, g, qr);
-  else
-    zero_dwords(qr);
+  load_query<DT, D>(a, seq, kvh * a.n_rep + h_local, h_local < a.n_rep, g, qr);
 
   State<D> st;
   state_init(st);
-
-  auto tile_t0 = [&](int i) { return t_begin + 16 * (w + NW * i); };
   bool bad = false;
-  auto issue = [&](int i, Tile<DT, D>& tl) -> uint32_t {
-    const int32_t bid = BS16 ? __builtin_amdgcn_readlane(bid_lane, i) : 0;
-    return load_tile<DT, D, BS16>(a, bt_row, bid, kc, vc, lo, tile_t0(i), t_end, lane, tl, bad);
-  };
-
-  // Register ring of DEPTH tiles: while one tile is in the math, the next
-  // DEPTH-1 tiles' loads are in flight. The loop body is straight-line so the
-  // loads' wait counts stay exact: issues past the end re-read the last tile
-  // (still in L2) and a slot past the end is computed with an empty key mask,
-  // which changes nothing.
-  if (my_tiles > 0) {
-    const int last = my_tiles - 1;
-    Tile<DT, D> ring[DEPTH];
-    uint32_t mk[DEPTH];
-#pragma unroll
-    for (int r = 0; r < DEPTH; ++r) mk[r] = issue(min(r, last), ring[r]);
-    for (int i = 0; i < my_tiles; i += DEPTH) {
-#pragma unroll
-      for (int r = 0; r < DEPTH; ++r) {
-        compute_tile<DT, D>(ring[r], qr, i + r < my_tiles ? mk[r] : 0u, a.scale_log2, kstage[w], lane, st);
-        mk[r] = issue(min(i + r + DEPTH, last), ring[r]);
-      }
-    }
-  }
+  attend_tiles<DT, D, BS16, NW, DEPTH>(a, bt_row, kc, vc, lo, qr, tile_lo, tile_hi, t_end, kstage[w], lane, w, st,
+                                       bad);
   if (bad) flag_error(a.err, IR_ERR_BLOCK_RANGE);
   st.l = wave_sum_groups(st.l);
 
@@ -324,14 +93,7 @@ void paged_decode_kernel(DecodeArgs a) {
   const int nh = min(16, a.n_rep - hg * 16);
   const int head0 = kvh * a.n_rep + hg * 16;
   if (nparts == 1) {
-    for (int it = threadIdx.x; it < nh * (D / 4); it += NW * 64) {
-      const int hc = it / (D / 4);
-      const int d0 = (it - hc * (D / 4)) * 4;
-      float M, L, o[4];
-      merge_column<NW, D>(sm, hc, d0, M, L, o);
-      const float inv = L > 0.f ? 1.f / L : 0.f;
-      store4<DT>((uint8_t*)a.out + ((int64_t)seq * a.o_seq + (int64_t)(head0 + hc) * a.o_head + d0) * EB, o, inv);
-    }
+    store_merged<DT, D, NW>(a, sm, seq, head0, nh);
     return;
   }
 
@@ -392,13 +154,13 @@ __global__ __launch_bounds__(256) void paged_decode_reduce(DecodeArgs a) {
   merge_partials<DT, D, false>(a, seq, kvh * a.n_rep + hg * 16, nh, nparts, threadIdx.x, 256);
 }
 
-int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
-
 int max_parts_for(int max_blocks, int bs, int part_tokens) {
   const int64_t cap = (int64_t)max_blocks * bs;
   const int64_t p = (cap + part_tokens - 1) / part_tokens;
   return p < 1 ? 1 : (int)p;
 }
+
+int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
 // Workspace layout: [counters: units int32][partial acc: rows x D fp32][max,sum: rows x 2 fp32],
 // each region 256-byte aligned.
@@ -527,6 +289,8 @@ extern "C" int ir_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_he
   IR_REQUIRE(partition_tokens % 16 == 0 && partition_tokens <= kMaxPartition,
              "ir_paged_decode: partition_tokens %d must be a multiple of 16 and at most %d", partition_tokens,
              kMaxPartition);
+  IR_REQUIRE((int64_t)max_blocks_per_seq * block_size <= (int64_t)1 << 30,
+             "ir_paged_decode: block tables of %d x %d tokens exceed 2^30 keys", max_blocks_per_seq, block_size);
   // A 16-token tile starting at a multiple of 16 stays inside one block when the
   // block size is a multiple of 16: then the block id is wave-uniform.
   const bool bs16 = block_size % 16 == 0;
@@ -555,11 +319,11 @@ extern "C" int ir_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_he
   a.n_hg = (a.n_rep + 15) / 16;
   a.scale_log2 = scale * kLog2e;
   a.part_tokens = partition_tokens;
-  a.max_parts = max_parts_for(max_blocks_per_seq, block_size, partition_tokens);
   a.counters = nullptr;
   a.ws_o = nullptr;
   a.ws_ml = nullptr;
   a.err = err_flags;
+  a.max_parts = max_parts_for(max_blocks_per_seq, block_size, partition_tokens);
   IR_REQUIRE(a.max_parts <= 65535, "ir_paged_decode: %d partitions exceed the grid limit", a.max_parts);
   if (a.max_parts > 1) {
     const int64_t need = ir_paged_decode_workspace_size(num_seqs, num_q_heads, num_kv_heads, head_dim,

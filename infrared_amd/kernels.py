@@ -230,12 +230,63 @@ def paged_attention_masked(
     return out
 
 
+def paged_prefill(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    q_start: torch.Tensor,
+    max_q_len: int,
+    block_size: int,
+    scale: float,
+    out: torch.Tensor | None = None,
+    err_flags: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Causal paged attention for packed query chunks: ``q`` ``[total_q, H_q, D]``.
+
+    Sequence ``b`` owns rows ``cu_seqlens_q[b]:cu_seqlens_q[b+1]`` (int32
+    ``[B+1]``); its query ``i`` is at position ``q_start[b] + i`` (int32 ``[B]``)
+    and attends keys ``0..q_start[b]+i`` through ``block_tables[b]``. ``max_q_len``
+    bounds the per-sequence query counts (host value, sizes the grid).
+    """
+    dev = require_device(q, k_cache, v_cache, block_tables, cu_seqlens_q, q_start)
+    _cache_layer("paged_prefill", k_cache)
+    if q.dim() != 3:
+        raise RuntimeError(f"paged_prefill: q must be [total_q, H_q, D], got {tuple(q.shape)}")
+    total_q, hq, d = q.shape
+    h_kv = k_cache.shape[1]
+    if d != k_cache.shape[2] or q.dtype != k_cache.dtype or v_cache.shape != k_cache.shape:
+        raise RuntimeError("paged_prefill: q / pool shape or dtype mismatch")
+    if v_cache.stride() != k_cache.stride():
+        raise RuntimeError("paged_prefill: k_cache and v_cache must share strides")
+    b = block_tables.shape[0]
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.stride(1) != 1:
+        raise RuntimeError("paged_prefill: block_tables must be int32 [B, max_blocks] with unit column stride")
+    for name, t, n in (("cu_seqlens_q", cu_seqlens_q, b + 1), ("q_start", q_start, b)):
+        if t.dtype != torch.int32 or t.shape != (n,) or not t.is_contiguous():
+            raise RuntimeError(f"paged_prefill: {name} must be contiguous int32 [{n}]")
+    _last_dim_contiguous("paged_prefill q", q)
+    if out is None:
+        out = torch.empty(total_q, hq, d, dtype=q.dtype, device=dev)
+    rc = lib().ir_paged_prefill(
+        ptr(q), q.stride(0), q.stride(1), ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
+        k_cache.shape[0] // block_size, block_size, ptr(block_tables), block_tables.stride(0),
+        block_tables.shape[1], ptr(cu_seqlens_q), ptr(q_start), b, total_q, int(max_q_len), ptr(out),
+        out.stride(0), out.stride(1), hq, h_kv, d, float(scale), dtype_code(q.dtype), ptr(err_flags),
+        stream_ptr(dev),
+    )
+    check(rc, "ir_paged_prefill")
+    return out
+
+
 __all__ = [
     "kv_scatter",
     "gather_slots",
     "paged_gather",
     "paged_decode",
     "paged_attention_masked",
+    "paged_prefill",
     "decode_workspace_bytes",
     "default_partition",
 ]

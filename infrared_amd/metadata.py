@@ -10,7 +10,11 @@ decode kernel reads, so a caller fills ``PagedContext`` directly:
 - ``gather_slots[i, p] = slot(bt_i, p)`` for ``p < ctx_i``, ``0`` after
   (``paged_engine.py:306-314``);
 - decode mask ``0`` for ``col < ctx_i``, ``finfo(dtype).min`` after
-  (``paged_engine.py:630-638``).
+  (``paged_engine.py:630-638``);
+- packed prefill / mixed steps (``paged_engine.py:194-207``, ``:461-516``):
+  ``write_slots`` of every new token in packing order, ``cu_seqlens_q`` /
+  ``q_start`` for the prefill kernel and, on request, the reference's packed
+  ``gather_slots`` + varlen mask (``infrared/model/inputs.py:57-85``).
 """
 
 from __future__ import annotations
@@ -104,3 +108,65 @@ def decode_context(
     ws = decode_write_slots(bt, torch.tensor(list(num_cached), device=dev), bs)
     mask = decode_mask(cl, t, mask_dtype or pool.dtype)
     return PagedContext(pool, ws, gs, use_triton, bt, cl), mask
+
+
+def prefill_context(
+    pool: PagedKVPool,
+    block_tables: Sequence[Sequence[int]],
+    num_cached: Sequence[int],
+    q_lens: Sequence[int],
+    *,
+    use_triton: bool = True,
+    with_mask: bool = False,
+    mask_dtype: torch.dtype | None = None,
+) -> tuple[PagedContext, torch.Tensor | None]:
+    """``PagedContext`` of one packed step: sequence ``i`` forwards ``q_lens[i]``
+    new tokens at positions ``num_cached[i] ..``, packed in sequence order into
+    one ``B = 1`` frame (a decode row is ``q_len = 1``).
+
+    ``with_mask`` also builds the reference's packed metadata -- ``gather_slots``
+    ``[1, K]`` over the union of the sequences' keys and the varlen mask
+    ``[1, 1, Q, K]`` -- for the gather_slots + mask kernel (fp32, or
+    ``use_triton=False``); it is quadratic in the step size.
+    """
+    dev = pool.device
+    bs = pool.block_size
+    if not (len(block_tables) == len(num_cached) == len(q_lens)):
+        raise ValueError("block_tables, num_cached and q_lens must have one entry per sequence")
+    lengths = [c + n for c, n in zip(num_cached, q_lens)]
+    width = max(blocks_for(n, bs) for n in lengths) if lengths else 0
+    rows = [list(r)[: max(width, 1)] for r in block_tables]
+    bt = block_tables_tensor(rows, dev, width)
+    cu = [0]
+    for n in q_lens:
+        cu.append(cu[-1] + n)
+    write = [slot(r, p, bs) for r, c, n in zip(rows, num_cached, q_lens) for p in range(c, c + n)]
+    ctx = PagedContext(
+        pool,
+        torch.tensor(write, dtype=torch.int64, device=dev),
+        None,
+        use_triton,
+        bt,
+        None,
+        torch.tensor(cu, dtype=torch.int32, device=dev),
+        torch.tensor(list(num_cached), dtype=torch.int32, device=dev),
+        max(q_lens, default=0),
+    )
+    if not with_mask:
+        return ctx, None
+    k_seq, k_pos, gslots = [], [], []
+    for i, (r, n) in enumerate(zip(rows, lengths)):
+        for p in range(n):
+            k_seq.append(i)
+            k_pos.append(p)
+            gslots.append(slot(r, p, bs))
+    q_seq = torch.tensor([i for i, n in enumerate(q_lens) for _ in range(n)], device=dev)
+    q_pos = torch.tensor([c + j for c, n in zip(num_cached, q_lens) for j in range(n)], device=dev)
+    k_seq_t = torch.tensor(k_seq, device=dev)
+    k_pos_t = torch.tensor(k_pos, device=dev)
+    allowed = (q_seq[:, None] == k_seq_t[None, :]) & (k_pos_t[None, :] <= q_pos[:, None])
+    dtype = mask_dtype or pool.dtype
+    mask = torch.zeros(1, 1, len(q_seq), len(k_seq), dtype=dtype, device=dev)
+    mask = mask.masked_fill(~allowed[None, None], torch.finfo(dtype).min)
+    ctx.gather_slots = torch.tensor([gslots], dtype=torch.int64, device=dev)
+    return ctx, mask

@@ -8,6 +8,12 @@ calls once per layer (``infrared/model/layers.py:178-180``):
    kernel, ``infrared/model/triton_attention.py:101-104``);
 2. attend over the paged history with a HIP kernel:
 
+   - ``paged.use_triton``, 16-bit dtype and ``paged.block_tables`` +
+     ``paged.cu_seqlens_q`` + ``paged.q_start`` set: the chunked-prefill MFMA
+     kernel over the packed query tokens (prefix-hit prefill and mixed
+     prefill + decode steps); the mask is implied: query ``i`` of sequence
+     ``b`` sees keys ``<= q_start[b] + i`` of its own sequence (the masks of
+     ``infrared/model/inputs.py:33-85``);
    - ``paged.use_triton`` and ``paged.block_tables``/``paged.context_lens`` set
      and one query token per sequence: the GQA decode kernel (split-KV +
      log-sum-exp reduce) over the block tables; the mask is then implied by
@@ -59,7 +65,21 @@ def paged_attention(
 
     block_tables = getattr(paged, "block_tables", None)
     context_lens = getattr(paged, "context_lens", None)
-    if paged.use_triton and block_tables is not None and context_lens is not None and sq == 1:
+    cu_seqlens_q = getattr(paged, "cu_seqlens_q", None)
+    q_start = getattr(paged, "q_start", None)
+    if (
+        paged.use_triton
+        and block_tables is not None
+        and cu_seqlens_q is not None
+        and q_start is not None
+        and q.dtype in (torch.bfloat16, torch.float16)
+    ):
+        max_q = getattr(paged, "max_q_len", 0) or b * sq
+        out = kernels.paged_prefill(
+            q.reshape(b * sq, hq, d), k_layer, v_layer, block_tables, cu_seqlens_q, q_start, max_q,
+            pool.block_size, scale, err_flags=err,
+        ).view(b, sq, hq, d)
+    elif paged.use_triton and block_tables is not None and context_lens is not None and sq == 1:
         ws = None
         if hasattr(pool, "workspace"):
             need = kernels.decode_workspace_bytes(

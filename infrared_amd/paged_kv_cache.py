@@ -171,9 +171,16 @@ class PagedContext:
     token order. ``gather_slots`` ``[B, T]`` int64 — per query row, the slots of
     its history (right-padded), read together with the caller's additive mask.
     ``use_triton`` keeps the reference's field name: ``True`` lets the dispatcher
-    take the block-table kernels when ``block_tables``/``context_lens`` are
-    present; ``False`` forces the kernel that reads ``gather_slots`` + mask.
-    Both are HIP kernels; there is no Triton and no CPU path.
+    take the block-table kernels when their fields are present; ``False``
+    forces the kernel that reads ``gather_slots`` + mask. All are HIP kernels;
+    there is no Triton and no CPU path.
+
+    Block-table fields (additions; the reference's context has none):
+    ``block_tables`` ``[B, max_blocks]`` int32 per sequence; for a one-token
+    decode ``context_lens`` ``[B]`` int32; for prefill / mixed steps over
+    packed query tokens ``cu_seqlens_q`` ``[B + 1]`` int32 (sequence ``b`` owns
+    packed rows ``cu[b]:cu[b+1]``), ``q_start`` ``[B]`` int32 (its cached
+    prefix length) and ``max_q_len`` (host bound on the chunk sizes).
     """
 
     pool: PagedKVPool
@@ -182,3 +189,6 @@ class PagedContext:
     use_triton: bool = True
     block_tables: torch.Tensor | None = None
     context_lens: torch.Tensor | None = None
+    cu_seqlens_q: torch.Tensor | None = None
+    q_start: torch.Tensor | None = None
+    max_q_len: int = 0

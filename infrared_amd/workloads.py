@@ -9,6 +9,14 @@ Decode workloads (one query token per sequence):
 - ``qwen7b-skewed``: 16 seqs, 28/4 heads, head_dim 128, bf16, context
   round(lognormal(8, 1.2)) clipped to [16, 32768], pool 1.25x.
 
+Prefill workload (``make_prefill_case``):
+
+- ``qwen7b-prefill``: 8 sequences, each a 512-token chunk after a cached
+  prefix of 16 * U{0..512} tokens (0..8192); sequences 2i and 2i+1 share the
+  prefix length and the prefix's block ids (prefix caching shares full
+  blocks), 28 q / 4 kv heads, head_dim 128, block 16, bf16, pool 1.25x the
+  distinct blocks needed.
+
 Each sequence's block table is a consecutive chunk of one random permutation
 of the pool's block ids (non-contiguous physical blocks). q and the whole K/V
 pool are N(0, 1) drawn in fp32 and cast to the workload dtype. Metadata is
@@ -149,5 +157,139 @@ def make_decode_case(
         v_cache=v,
         block_tables=tables,
         context_lens=ctx.to(torch.int32).to(device),
+        pool_blocks=pool_blocks,
+    )
+
+
+@dataclass(frozen=True)
+class PrefillConfig:
+    name: str
+    num_seqs: int
+    chunk: int  # query tokens per sequence
+    num_q_heads: int
+    num_kv_heads: int
+    head_dim: int
+    block_size: int
+    dtype: torch.dtype
+    prefix_blocks_max: int  # prefix = block_size * U{0..prefix_blocks_max}
+    seed: int = 0
+
+    @property
+    def n_rep(self) -> int:
+        return self.num_q_heads // self.num_kv_heads
+
+    @property
+    def scale(self) -> float:
+        return self.head_dim**-0.5
+
+
+PREFILL_CONFIGS: dict[str, PrefillConfig] = {
+    "qwen7b-prefill": PrefillConfig("qwen7b-prefill", 8, 512, 28, 4, 128, 16, torch.bfloat16, 512, seed=4),
+}
+
+
+@dataclass
+class PrefillCase:
+    config: PrefillConfig
+    q: torch.Tensor  # [total_q, H_q, D] packed
+    k_cache: torch.Tensor  # [num_slots, H_kv, D]
+    v_cache: torch.Tensor
+    block_tables: list[torch.Tensor]  # per rotation, int32 [B, max_blocks]
+    cu_seqlens_q: torch.Tensor  # int32 [B + 1]
+    q_start: torch.Tensor  # int32 [B] (cached prefix lengths)
+    q_lens: list[int]
+    prefixes: list[int]
+    pool_blocks: int  # blocks per rotation
+
+    @property
+    def flops(self) -> int:
+        """Unmasked-pair flops: 4 * H_q * D * sum(q * prefix + q (q + 1) / 2)."""
+        c = self.config
+        pairs = sum(n * p + n * (n + 1) // 2 for n, p in zip(self.q_lens, self.prefixes))
+        return 4 * c.num_q_heads * c.head_dim * pairs
+
+    @property
+    def kv_bytes(self) -> int:
+        """Distinct K+V bytes the call needs (shared prefix blocks counted once)."""
+        c = self.config
+        esize = torch.tensor([], dtype=c.dtype).element_size()
+        blocks = len({int(x) for row, n in zip(self.block_tables[0].tolist(), self._nblocks()) for x in row[:n]})
+        return blocks * c.block_size * 2 * c.num_kv_heads * c.head_dim * esize
+
+    def _nblocks(self) -> list[int]:
+        bs = self.config.block_size
+        return [(p + n + bs - 1) // bs for p, n in zip(self.prefixes, self.q_lens)]
+
+
+def make_prefill_case(
+    config: str | PrefillConfig,
+    device: torch.device | str,
+    *,
+    seed: int | None = None,
+    rotations: int = 1,
+    prefixes: list[int] | None = None,
+    q_lens: list[int] | None = None,
+    layout: str = "head_major",
+) -> PrefillCase:
+    """Seeded prefill chunks over a paged pool; ``prefixes``/``q_lens`` override the
+    drawn prefix lengths / chunk sizes (pairs then share only full prefix blocks)."""
+    cfg = PREFILL_CONFIGS[config] if isinstance(config, str) else config
+    seed = cfg.seed if seed is None else seed
+    gen = torch.Generator().manual_seed(seed)
+    bs, b = cfg.block_size, cfg.num_seqs
+    if prefixes is None:
+        pairs = torch.randint(0, cfg.prefix_blocks_max + 1, ((b + 1) // 2,), generator=gen)
+        prefixes = [int(pairs[i // 2]) * bs for i in range(b)]
+    q_lens = [cfg.chunk] * b if q_lens is None else list(q_lens)
+    if len(prefixes) != b or len(q_lens) != b:
+        raise ValueError("prefixes / q_lens must have one entry per sequence")
+    # pair (2i, 2i+1) shares the full blocks of a common prefix
+    shared = [min(prefixes[i], prefixes[i ^ 1] if (i ^ 1) < b else prefixes[i]) // bs for i in range(b)]
+    own = [(p + n + bs - 1) // bs - shared[i] for i, (p, n) in enumerate(zip(prefixes, q_lens))]
+    need = sum(shared[i] for i in range(0, b, 2)) + sum(own)
+    pool_blocks = math.ceil(1.25 * need) + 1
+    width = max(s + o for s, o in zip(shared, own))
+    tables = []
+    for r in range(rotations):
+        perm = (torch.randperm(pool_blocks, generator=gen) + r * pool_blocks).tolist()
+        off = 0
+        rows = [None] * b
+        for i in range(0, b, 2):
+            pre = perm[off : off + shared[i]]
+            off += shared[i]
+            for j in (i, i + 1):
+                if j >= b:
+                    continue
+                mine = perm[off : off + own[j]]
+                off += own[j]
+                rows[j] = pre + mine
+        bt = torch.zeros(b, width, dtype=torch.int32)
+        for i, row in enumerate(rows):
+            bt[i, : len(row)] = torch.tensor(row, dtype=torch.int32)
+        tables.append(bt.to(device))
+    dgen = torch.Generator(device=device).manual_seed(seed)
+    num_slots = rotations * pool_blocks * bs
+    shape = (num_slots, cfg.num_kv_heads, cfg.head_dim)
+    cu = [0]
+    for n in q_lens:
+        cu.append(cu[-1] + n)
+    q = torch.randn(cu[-1], cfg.num_q_heads, cfg.head_dim, generator=dgen, device=device)
+    k = torch.randn(shape, generator=dgen, device=device).to(cfg.dtype)
+    v = torch.randn(shape, generator=dgen, device=device).to(cfg.dtype)
+    if layout == "head_major":
+        k = k.permute(1, 0, 2).contiguous().permute(1, 0, 2)
+        v = v.permute(1, 0, 2).contiguous().permute(1, 0, 2)
+    elif layout != "slot_major":
+        raise ValueError(f"unknown layout {layout!r}")
+    return PrefillCase(
+        config=cfg,
+        q=q.to(cfg.dtype),
+        k_cache=k,
+        v_cache=v,
+        block_tables=tables,
+        cu_seqlens_q=torch.tensor(cu, dtype=torch.int32, device=device),
+        q_start=torch.tensor(prefixes, dtype=torch.int32, device=device),
+        q_lens=q_lens,
+        prefixes=list(prefixes),
         pool_blocks=pool_blocks,
     )

@@ -23,13 +23,20 @@ Restated functions and the reference lines they follow:
 - ``decode_reference`` (new) per-sequence decode over the block tables with no
   padding, in a chosen float dtype; equal to ``paged_attention_naive`` on
   the gather_slots/mask the engine builds (pinned in tests/test_oracle.py).
+- ``prefill_reference`` (new) per-sequence causal attention of packed query
+  chunks after a cached prefix, over the block tables; equal to
+  ``paged_attention_naive`` on the prefill metadata of
+  infrared/engine/paged_engine.py:194-207 (``attention_mask``) and on the
+  packed mixed-step metadata of infrared/engine/paged_engine.py:461-516
+  (``varlen_mask``) (pinned in tests/test_oracle.py).
 
 How each is pinned (tests/test_oracle.py): ``masked_attention`` against
 torch's SDPA and an fp64 brute force; the streaming/split variants against
 the one-shot softmax for many block/partition sizes; metadata against the
 reference tests' known-answer values (tests/golden/reference_kats.json);
-``decode_reference`` against ``paged_attention_naive`` and closed forms
-(one-hot scores, constant V).
+``decode_reference`` and ``prefill_reference`` against
+``paged_attention_naive`` on the engine's metadata and closed forms (one-hot
+scores, constant V).
 """
 
 from __future__ import annotations
@@ -260,4 +267,51 @@ def decode_reference(
         s = torch.einsum("grd,ngd->grn", qi, k) * scale
         p = torch.softmax(s, dim=-1)
         out[i] = torch.einsum("grn,ngd->grd", p, v).reshape(hq, d)
+    return out
+
+
+# --------------------------------------------------------------------- per-sequence prefill
+
+
+def prefill_reference(
+    q: torch.Tensor,
+    k_layer: torch.Tensor,
+    v_layer: torch.Tensor,
+    block_tables: torch.Tensor,
+    cu_seqlens_q: Sequence[int] | torch.Tensor,
+    q_start: Sequence[int] | torch.Tensor,
+    block_size: int,
+    scale: float,
+    compute_dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """Causal attention of packed query chunks over the block tables.
+
+    ``q`` ``[total_q, H_q, D]``; sequence ``b`` owns rows
+    ``cu_seqlens_q[b]:cu_seqlens_q[b+1]``, whose query ``i`` is at position
+    ``q_start[b] + i`` and attends keys ``0 .. q_start[b] + i`` of the sequence.
+    Returns ``[total_q, H_q, D]`` in ``compute_dtype``.
+    """
+    total_q, hq, d = q.shape
+    h_kv = k_layer.shape[1]
+    n_rep = hq // h_kv
+    cu = [int(x) for x in (cu_seqlens_q.tolist() if torch.is_tensor(cu_seqlens_q) else cu_seqlens_q)]
+    qs = [int(x) for x in (q_start.tolist() if torch.is_tensor(q_start) else q_start)]
+    bt = block_tables.cpu().long()
+    out = torch.zeros(total_q, hq, d, dtype=compute_dtype)
+    for b in range(len(qs)):
+        lo, hi = cu[b], cu[b + 1]
+        if hi <= lo:
+            continue
+        n_keys = qs[b] + (hi - lo)
+        pos = torch.arange(n_keys)
+        slots = bt[b, pos // block_size] * block_size + pos % block_size
+        k = k_layer[slots].to(compute_dtype)  # [n_keys, H_kv, D]
+        v = v_layer[slots].to(compute_dtype)
+        qb = q[lo:hi].to(compute_dtype).reshape(hi - lo, h_kv, n_rep, d)
+        s = torch.einsum("igrd,ngd->grin", qb, k) * scale
+        q_pos = qs[b] + torch.arange(hi - lo)
+        allowed = pos[None, :] <= q_pos[:, None]  # [i, n]
+        s = s.masked_fill(~allowed, float("-inf"))
+        p = torch.softmax(s, dim=-1)
+        out[lo:hi] = torch.einsum("grin,ngd->igrd", p, v).reshape(hi - lo, hq, d)
     return out

@@ -210,42 +210,66 @@ def test_decode_shape_sweep(dtype, h_q, h_kv, d, bs, part):
     _check_decode(case, part)
 
 
-def test_decode_zero_context_row_and_determinism():
-    case = make_decode_case("qwen7b-bf16", DEV, num_seqs=6)
-    case.context_lens[2] = 0
-    a = _check_decode(case, 256)
-    assert a[2].float().abs().max().item() == 0.0
-    b = kernels.paged_decode(
-        case.q, case.k_cache, case.v_cache, case.block_tables[0], case.context_lens, 16,
-        case.config.scale, partition_tokens=256,
-    )
-    torch.cuda.synchronize()
-    assert torch.equal(a, b)
+# Batches mixing empty, one-token and long rows (one row spanning many
+# partitions), a single 32k-token row, and a batch wider than one workgroup.
+_MIX_CFG = DecodeConfig("mixed-lengths", 8, 28, 4, 128, 16, torch.bfloat16, "uniform", 5000, 5000, seed=11)
 
 
-@pytest.mark.parametrize("partition_tokens", [64, 512])
-def test_decode_fused_merge_repeatable_and_counters_clean(partition_tokens):
-    """Many split-KV partitions per sequence, merged by the last-arriving workgroup:
-    50 back-to-back calls sharing one workspace give bit-identical outputs, match
-    the oracle, and leave every arrival counter at zero."""
-    case = make_decode_case("qwen7b-bf16", DEV)
+@pytest.mark.parametrize("partition_tokens", [0, 64, 4096])
+def test_decode_mixed_lengths_with_empty_rows(partition_tokens):
+    case = make_decode_case(_MIX_CFG, DEV)
+    case.context_lens.copy_(torch.tensor([0, 1, 5000, 0, 17, 4096, 0, 2048], dtype=torch.int32))
+    out = _check_decode(case, partition_tokens)
+    for r in (0, 3, 6):
+        assert out[r].float().abs().max().item() == 0.0
+
+
+@pytest.mark.parametrize("ctx", [1, 16, 32768])
+def test_decode_single_sequence(ctx):
+    """One sequence: a single key, one full tile, and 32k keys (8 default
+    partitions per unit, merged by the reduce launch)."""
+    cfg = DecodeConfig(f"one-seq-{ctx}", 1, 28, 4, 128, 16, torch.bfloat16, "uniform", ctx, ctx, seed=ctx)
+    _check_decode(make_decode_case(cfg, DEV), 0)
+
+
+def test_decode_large_batch():
+    cfg = DecodeConfig("batch-600", 600, 8, 2, 64, 16, torch.float16, "uniform", 1, 64, seed=5)
+    _check_decode(make_decode_case(cfg, DEV), 0)
+
+
+def test_decode_all_rows_empty():
+    case = make_decode_case(_MIX_CFG, DEV)
+    case.context_lens.zero_()
+    out = _check_decode(case, 0)
+    assert out.float().abs().max().item() == 0.0
+
+
+def test_decode_shared_workspace_across_different_splits():
+    """The partial rows start as garbage (every int32 = 2) and are shared by calls
+    whose splits differ; each call matches the oracle and repeats bit for bit."""
+    case = make_decode_case(_MIX_CFG, DEV)
     cfg = case.config
     bt = case.block_tables[0]
-    need = kernels.decode_workspace_bytes(64, 28, 4, 128, bt.shape[1], 16, partition_tokens)
-    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
-    outs = [
-        kernels.paged_decode(case.q, case.k_cache, case.v_cache, bt, case.context_lens, 16, cfg.scale,
-                             partition_tokens=partition_tokens, workspace=ws)
-        for _ in range(50)
+    need = kernels.decode_workspace_bytes(8, 28, 4, 128, bt.shape[1], 16, 256)
+    ws = torch.full((need // 4,), 2, dtype=torch.int32, device=DEV).view(torch.uint8)
+    ws[:256].zero_()  # arrival counters
+    lens = [
+        torch.tensor([5000, 5000, 5000, 5000, 5000, 5000, 5000, 5000], dtype=torch.int32),
+        torch.tensor([0, 1, 5000, 0, 17, 4096, 0, 2048], dtype=torch.int32),
+        torch.tensor([33, 0, 0, 0, 0, 0, 0, 4999], dtype=torch.int32),
     ]
-    torch.cuda.synchronize()
-    for o in outs[1:]:
-        assert torch.equal(o, outs[0])
-    counters = ws[: 64 * 4 * 4].view(torch.int32)
-    assert counters.eq(0).all()
-    ref = O.decode_reference(case.q.cpu(), case.k_cache.cpu(), case.v_cache.cpu(), bt.cpu(),
-                             case.context_lens.cpu(), 16, cfg.scale)
-    assert (outs[0].float().cpu() - ref).abs().max().item() <= TOL[cfg.dtype]
+    for cl in lens:
+        cl = cl.to(DEV)
+        outs = [
+            kernels.paged_decode(case.q, case.k_cache, case.v_cache, bt, cl, 16, cfg.scale, partition_tokens=256,
+                                 workspace=ws)
+            for _ in range(2)
+        ]
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[1])
+        ref = O.decode_reference(case.q.cpu(), case.k_cache.cpu(), case.v_cache.cpu(), bt.cpu(), cl.cpu(), 16,
+                                 cfg.scale)
+        assert (outs[0].float().cpu() - ref).abs().max().item() <= TOL[cfg.dtype]
 
 
 def test_decode_flags_bad_block_ids_and_contexts():

@@ -1,0 +1,141 @@
+"""GPU parity of the chunked-prefill MFMA kernel (ir_paged_prefill, through the
+C ABI) against the CPU oracle's per-sequence causal restatement
+(oracle.naive.prefill_reference) on the same seeded inputs.
+
+Bar: max-abs error <= 2e-2 for bf16/fp16 against the fp32 reference.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from infrared_amd import kernels
+from infrared_amd._lib import ERR_BLOCK_RANGE, ERR_CONTEXT_RANGE
+from infrared_amd.workloads import PrefillConfig, make_decode_case, make_prefill_case
+from oracle import naive as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+TOL = 2e-2
+
+
+def _run(case, err=None, bt=None):
+    cfg = case.config
+    bt = case.block_tables[0] if bt is None else bt
+    return kernels.paged_prefill(
+        case.q, case.k_cache, case.v_cache, bt, case.cu_seqlens_q, case.q_start, max(case.q_lens),
+        cfg.block_size, cfg.scale, err_flags=err,
+    )
+
+
+def _check(case):
+    cfg = case.config
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = _run(case, err)
+    torch.cuda.synchronize()
+    assert err.item() == 0
+    ref = O.prefill_reference(
+        case.q.cpu(), case.k_cache.cpu(), case.v_cache.cpu(), case.block_tables[0].cpu(),
+        case.cu_seqlens_q.cpu(), case.q_start.cpu(), cfg.block_size, cfg.scale,
+    )
+    diff = (out.float().cpu() - ref).abs().max().item()
+    assert diff <= TOL, f"{cfg.name}: max-abs {diff}"
+    return out
+
+
+def test_prefill_qwen7b_full_size_parity():
+    """8 x 512-token chunks after prefixes up to 8192 (pairs sharing prefix blocks)."""
+    case = make_prefill_case("qwen7b-prefill", DEV)
+    assert max(case.prefixes) > 2048
+    _check(case)
+
+
+def test_prefill_ragged_chunks_and_prefixes():
+    """Chunks of 1..512 tokens after prefixes that end mid-block, one empty chunk."""
+    case = make_prefill_case(
+        "qwen7b-prefill", DEV, prefixes=[0, 37, 512, 1000, 3, 3, 0, 5], q_lens=[1, 31, 100, 512, 0, 9, 64, 33]
+    )
+    _check(case)
+
+
+_SWEEP = [
+    # (dtype, h_q, h_kv, d, bs)
+    (torch.bfloat16, 28, 4, 128, 16),
+    (torch.bfloat16, 8, 8, 64, 16),
+    (torch.bfloat16, 16, 2, 128, 32),
+    (torch.bfloat16, 24, 2, 64, 4),  # 12 heads per KV head: two head groups of 8
+    (torch.float16, 28, 4, 128, 1),
+    (torch.float16, 12, 3, 64, 8),
+]
+
+
+@pytest.mark.parametrize("dtype,h_q,h_kv,d,bs", _SWEEP)
+@pytest.mark.parametrize("layout", ["head_major", "slot_major"])
+def test_prefill_shape_sweep(dtype, h_q, h_kv, d, bs, layout):
+    """GQA groups 1..12 (one or two head groups per workgroup), both head dims,
+    block sizes 1..32, both pool layouts, ragged chunks."""
+    cfg = PrefillConfig(f"pf-{h_q}-{h_kv}-{d}-{bs}", 5, 0, h_q, h_kv, d, bs, dtype, 0, seed=h_q * d + bs)
+    case = make_prefill_case(cfg, DEV, prefixes=[0, 17, 64, 200, 95], q_lens=[33, 64, 1, 130, 47], layout=layout)
+    _check(case)
+
+
+def test_prefill_block_id_cache_reload():
+    """Block size 1 and a 2600-token context: the workgroup's staged block ids
+    (1024 at a time) are refilled mid-walk."""
+    cfg = PrefillConfig("pf-bs1-long", 2, 0, 8, 2, 64, 1, torch.bfloat16, 0, seed=3)
+    _check(make_prefill_case(cfg, DEV, prefixes=[2500, 1100], q_lens=[100, 40]))
+
+
+def test_prefill_packed_mixed_step_matches_decode_kernel():
+    """A mixed step: 6 decode rows (one-token chunks) and 2 prefill chunks packed
+    in one call. The decode rows also match the decode kernel on the same pool."""
+    cfg = PrefillConfig("pf-mixed", 8, 0, 28, 4, 128, 16, torch.bfloat16, 0, seed=21)
+    prefixes = [700, 1500, 99, 2047, 16, 3000, 0, 256]
+    q_lens = [1, 1, 1, 1, 1, 1, 256, 200]
+    case = make_prefill_case(cfg, DEV, prefixes=prefixes, q_lens=q_lens)
+    out = _check(case)
+    rows = [0, 1, 2, 3, 4, 5]
+    q_dec = case.q[rows]
+    ctx = torch.tensor([p + 1 for p in prefixes[:6]], dtype=torch.int32, device=DEV)
+    dec = kernels.paged_decode(q_dec, case.k_cache, case.v_cache, case.block_tables[0][:6].contiguous(), ctx, 16,
+                               cfg.scale)
+    torch.cuda.synchronize()
+    assert (dec.float() - out[rows].float()).abs().max().item() <= TOL
+
+
+def test_prefill_deterministic():
+    case = make_prefill_case("qwen7b-prefill", DEV, prefixes=[0, 40, 300, 1000, 5, 5, 0, 0],
+                             q_lens=[512, 100, 64, 200, 1, 2, 3, 4])
+    a = _run(case)
+    b = _run(case)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_prefill_flags_bad_block_ids_and_overlong_context():
+    case = make_prefill_case("qwen7b-prefill", DEV, prefixes=[32, 0, 0, 0, 0, 0, 0, 0], q_lens=[16] * 8)
+    bt = case.block_tables[0].clone()
+    bt[0, 1] = case.pool_blocks + 7  # key 16..31 of sequence 0: outside the pool
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    _run(case, err, bt)
+    torch.cuda.synchronize()
+    assert err.item() & ERR_BLOCK_RANGE
+    # a chunk reaching past what its table can hold
+    err.zero_()
+    qs = case.q_start.clone()
+    qs[1] = bt.shape[1] * 16
+    kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[0], case.cu_seqlens_q, qs, 16, 16,
+                          case.config.scale, err_flags=err)
+    torch.cuda.synchronize()
+    assert err.item() & ERR_CONTEXT_RANGE
+
+
+def test_prefill_fp32_is_refused():
+    case = make_decode_case("qwen0.5b-fp32", DEV, num_seqs=2)
+    q = case.q.reshape(-1, case.q.shape[1], case.q.shape[2])
+    cu = torch.tensor([0, 1, 2], dtype=torch.int32, device=DEV)
+    qs = torch.tensor([3, 4], dtype=torch.int32, device=DEV)
+    with pytest.raises(RuntimeError, match="fp32"):
+        kernels.paged_prefill(q, case.k_cache, case.v_cache, case.block_tables[0], cu, qs, 1, 16, 0.125)

@@ -68,6 +68,37 @@ def test_decode_step_through_seam(use_triton, dtype):
     assert (out.float().cpu() - ref).abs().max().item() <= tol
 
 
+@pytest.mark.parametrize("use_triton", [True, False])
+def test_packed_prefill_and_decode_step_through_seam(use_triton):
+    """A mixed step as the engine packs it (infrared/engine/paged_engine.py:461-516):
+    two prefill chunks (one after a cached prefix) and three decode rows in one
+    B=1 frame. The block-table path (prefill MFMA kernel) and the reference's
+    gather_slots + varlen-mask path both match the oracle on the same pool."""
+    g = torch.Generator().manual_seed(8)
+    bs, h_kv, n_rep, d = 16, 4, 7, 128
+    num_cached = [0, 300, 41, 1000, 7]
+    q_lens = [77, 130, 1, 1, 1]
+    perm = torch.randperm(400, generator=g).tolist()
+    tables, off = [], 0
+    for nc, n in zip(num_cached, q_lens):
+        nb = metadata.blocks_for(nc + n, bs)
+        tables.append(perm[off : off + nb])
+        off += nb
+    pool = PagedKVPool(1, 400, bs, h_kv, d, torch.bfloat16, device=DEV, strict=True)
+    pool.k.normal_()
+    pool.v.normal_()
+    paged, mask = metadata.prefill_context(pool, tables, num_cached, q_lens, use_triton=use_triton, with_mask=True)
+    total = sum(q_lens)
+    q = torch.randn(1, total, h_kv * n_rep, d, device=DEV).to(torch.bfloat16)
+    k = torch.randn(1, total, h_kv, d, device=DEV).to(torch.bfloat16)
+    v = torch.randn(1, total, h_kv, d, device=DEV).to(torch.bfloat16)
+    out = paged_attention(q, k, v, paged, mask, 0, d**-0.5, n_rep)
+    bt = metadata.block_tables_tensor(tables, "cpu")
+    ref = O.prefill_reference(q[0].cpu(), pool.k[0].cpu(), pool.v[0].cpu(), bt, paged.cu_seqlens_q.cpu(),
+                              num_cached, bs, d**-0.5)
+    assert (out[0].float().cpu() - ref).abs().max().item() <= 2e-2
+
+
 @pytest.mark.parametrize("layout", ["head_major", "slot_major"])
 def test_pool_direct_slot_writes_feed_the_kernels(layout):
     """Reference callers write history straight into ``pool.k[layer, a:b]``

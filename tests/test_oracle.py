@@ -146,6 +146,83 @@ def test_decode_reference_one_hot_and_constant_v():
     assert torch.allclose(out, torch.full_like(out, 0.37), atol=1e-6)
 
 
+def _prefill_case(prefixes, q_lens, h_kv, n_rep, d, bs, seed):
+    """Pool + per-sequence block tables (random distinct blocks) + packed q."""
+    g = torch.Generator().manual_seed(seed)
+    lengths = [p + n for p, n in zip(prefixes, q_lens)]
+    need = sum((n + bs - 1) // bs for n in lengths)
+    nblocks = need + 3
+    perm = torch.randperm(nblocks, generator=g).tolist()
+    tables, off = [], 0
+    for n in lengths:
+        nb = (n + bs - 1) // bs
+        tables.append(perm[off : off + nb])
+        off += nb
+    width = max(len(t) for t in tables)
+    bt = torch.tensor([t + [0] * (width - len(t)) for t in tables], dtype=torch.int32)
+    k = torch.randn(nblocks * bs, h_kv, d, generator=g)
+    v = torch.randn(nblocks * bs, h_kv, d, generator=g)
+    cu = [0]
+    for n in q_lens:
+        cu.append(cu[-1] + n)
+    q = torch.randn(cu[-1], h_kv * n_rep, d, generator=g)
+    return q, k, v, bt, cu, tables
+
+
+@pytest.mark.parametrize("bs", [4, 16])
+@pytest.mark.parametrize("n_rep", [1, 7])
+def test_prefill_reference_matches_engine_prefill(bs, n_rep):
+    """Per-sequence chunk after a cached prefix == the engine's prefill metadata
+    (gather_slots over [0, length) + attention_mask([0], num_cached, q_len, length))
+    through the naive gather / repeat_kv / masked softmax path."""
+    prefixes, q_lens = [0, 5, 37, 16], [9, 1, 20, 16]
+    q, k, v, bt, cu, tables = _prefill_case(prefixes, q_lens, 2, n_rep, 32, bs, seed=bs + n_rep)
+    ref = O.prefill_reference(q, k, v, bt, cu, prefixes, bs, 32**-0.5)
+    for b, (nc, n) in enumerate(zip(prefixes, q_lens)):
+        length = nc + n
+        gs = torch.tensor([[O.slot(tables[b], p, bs) for p in range(length)]])
+        mask = O.attention_mask([0], nc, n, length, torch.float32)
+        naive = O.paged_attention_naive(q[None, cu[b] : cu[b + 1]], k, v, gs, mask, 32**-0.5, n_rep)[0]
+        assert torch.allclose(naive, ref[cu[b] : cu[b + 1]], atol=1e-5)
+
+
+def test_prefill_reference_matches_packed_varlen_step():
+    """All sequences packed into one row (B=1) over the union of their keys with
+    varlen_mask, as the mixed step builds it, == per-sequence prefill_reference."""
+    prefixes, q_lens = [3, 0, 30, 12], [1, 7, 1, 5]  # decode rows are one-token chunks
+    q, k, v, bt, cu, tables = _prefill_case(prefixes, q_lens, 2, 3, 16, 8, seed=4)
+    ref = O.prefill_reference(q, k, v, bt, cu, prefixes, 8, 0.25)
+    k_seq, k_pos, slots = [], [], []
+    for b, (nc, n) in enumerate(zip(prefixes, q_lens)):
+        for p in range(nc + n):
+            k_seq.append(b)
+            k_pos.append(p)
+            slots.append(O.slot(tables[b], p, 8))
+    q_seq = torch.tensor([b for b, n in enumerate(q_lens) for _ in range(n)])
+    q_pos = torch.tensor([nc + i for nc, n in zip(prefixes, q_lens) for i in range(n)])
+    mask = O.varlen_mask(q_seq, q_pos, torch.tensor(k_seq), torch.tensor(k_pos), torch.float32)
+    naive = O.paged_attention_naive(q[None], k, v, torch.tensor([slots]), mask, 0.25, 3)[0]
+    assert torch.allclose(naive, ref, atol=1e-5)
+
+
+def test_prefill_reference_closed_forms():
+    """The first query of a fresh sequence sees only key 0 (output = V row 0); a
+    constant V returns the constant; fp64 brute force agrees on a tiny case."""
+    prefixes, q_lens = [0, 4], [6, 3]
+    q, k, v, bt, cu, tables = _prefill_case(prefixes, q_lens, 1, 2, 8, 4, seed=5)
+    out = O.prefill_reference(q, k, v, bt, cu, prefixes, 4, 8**-0.5)
+    assert torch.allclose(out[0], v[tables[0][0] * 4, 0].expand(2, -1), atol=1e-6)
+    out_c = O.prefill_reference(q, k, torch.full_like(v, -1.5), bt, cu, prefixes, 4, 8**-0.5)
+    assert torch.allclose(out_c, torch.full_like(out_c, -1.5), atol=1e-6)
+    # brute force on sequence 1 (prefix 4, 3 queries at positions 4..6)
+    keys = torch.tensor([O.slot(tables[1], p, 4) for p in range(7)])
+    allowed = (torch.arange(7)[None, :] <= torch.arange(4, 7)[:, None])[None].expand(1, -1, -1).numpy()
+    ref = bruteforce.attention_loops(
+        q[None, cu[1] : cu[2]].numpy(), k[keys][None].numpy(), v[keys][None].numpy(), allowed, 8**-0.5, 2
+    )[0]
+    assert np.abs(out[cu[1] : cu[2]].numpy() - ref).max() < 1e-5
+
+
 def test_naive_bf16_close_to_fp32():
     """The bf16 restatement (bf16 einsums, fp32 softmax) stays within 2e-2 of fp32."""
     q, k, v, bt, ctx, tables = _paged_decode_case(4, 2, 7, 128, 16, 64, 200, seed=3)
@@ -238,6 +315,20 @@ def test_pins_reject_planted_mistakes(monkeypatch):
         orig = O.masked_attention
         m.setattr(O, "masked_attention", lambda q_, k_, v_, mk, s: orig(q_, k_, v_, mk * 0, s))
         assert np.abs(run() - ref).max() > 1e-2
+    # prefill causal bound off by one (keys < position instead of <=)
+    pq, pk, pv, pbt, pcu, ptab = _prefill_case([5, 0], [4, 3], 1, 2, 8, 4, seed=13)
+    good = O.prefill_reference(pq, pk, pv, pbt, pcu, [5, 0], 4, 8**-0.5)
+    gs = torch.tensor([[O.slot(ptab[0], p, 4) for p in range(9)]])
+    naive = O.paged_attention_naive(pq[None, :4], pk, pv, gs, O.attention_mask([0], 5, 4, 9, torch.float32),
+                                    8**-0.5, 2)[0]
+    assert torch.allclose(naive, good[:4], atol=1e-5)
+    # the same path with the causal bound off by one is rejected by that pin
+    bad_allowed = torch.arange(9)[None, :] < (5 + torch.arange(4))[:, None]
+    bad = O.masked_attention(
+        pq[None, :4], O.repeat_kv(pk[gs[0]][None], 2), O.repeat_kv(pv[gs[0]][None], 2),
+        torch.zeros(1, 1, 4, 9).masked_fill(~bad_allowed[None, None], torch.finfo(torch.float32).min), 8**-0.5,
+    )[0]
+    assert (bad - good[:4]).abs().max() > 1e-2
     # transposed PV operand in the split-KV merge: weights by the wrong partition max
     qq, kk, vv, mm, _, sc = _causal_case(1, 2, 20, 1, 1, 8, seed=12)
     good = O.masked_attention(qq, kk, vv, mm, sc)
