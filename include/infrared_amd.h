@@ -204,7 +204,7 @@ int ir_paged_attention_masked(const void* q, int64_t q_b_stride, int64_t q_s_str
  *   max_q_len:    upper bound of the per-sequence query counts (sizes the grid).
  * Keys q_start[b] + q_len_b beyond the table (max_blocks_per_seq * block_size) set
  * IR_ERR_CONTEXT_RANGE and are clamped; a bad block id sets IR_ERR_BLOCK_RANGE and
- * the key is skipped. head_dim in {64, 128}; dtype bf16 or f16 (fp32 returns
+ * that block's keys read as zeros. head_dim in {64, 128}; dtype bf16 or f16 (fp32 returns
  * IR_EUNSUPPORTED: use ir_paged_attention_masked).
  */
 int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_head_stride,

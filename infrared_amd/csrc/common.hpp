@@ -150,6 +150,24 @@ __device__ __forceinline__ float wave_sum_groups(float x) {
   return x;
 }
 
+// The same two reductions with gfx950's lane-swap instructions (no LDS
+// round trip): permlane32_swap pairs lane l with l^32, permlane16_swap pairs
+// 16-lane rows 0<->1 and 2<->3. Both outputs of a swap are combined, so which
+// one carries which half does not matter for a symmetric operation.
+__device__ __forceinline__ float wave_max_groups_swap(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float wave_sum_groups_swap(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 __device__ __forceinline__ void flag_error(int32_t* err, int32_t bit) {
   if (err) atomicOr(err, bit);
 }

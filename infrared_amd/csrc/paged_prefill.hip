@@ -11,27 +11,34 @@
 // infrared/engine/paged_engine.py:461-516 (a decode row is a sequence with one
 // query token at position context - 1).
 //
-// Work decomposition: one workgroup per (32-token query block, KV head, group
-// of NW query heads of that KV head, sequence); heaviest query blocks (most
-// keys) are dispatched first. Wavefront w owns query head w of the group and
-// the block's 32 query tokens (two 16-token column tiles). The workgroup walks
-// the keys in 64-key tiles staged in LDS, double buffered: the next tile's
-// global loads are in flight (in registers) while the current one is in the
-// math, and they are written to the other LDS buffer afterwards.
+// Work decomposition: one workgroup of 8 wavefronts (two per SIMD) per (query
+// block, KV head, sequence); heaviest query blocks (most keys) are dispatched
+// first. A query block is TQ = 256 / n_rep tokens, so the block's (token,
+// query head) pairs of the GQA group -- column j = token-in-block * n_rep +
+// head -- fill 256 columns almost exactly (7 heads: 36 tokens, 252 columns);
+// wavefront w owns columns 32w .. 32w+31 (two 16-column tiles). Every column
+// of a workgroup reads the same KV head, so each K/V element staged in LDS
+// feeds 32 columns per wavefront read. The workgroup walks the keys in
+// 64-key tiles staged in LDS, double buffered: the next tile's global loads
+// are in flight (in registers) while the current one is in the math, and they
+// are written to the other LDS buffer afterwards.
 //   K tile : row-major [64 keys][D] (+16 bytes a row against bank conflicts);
 //   V tile : transposed [D][64 keys] (+8 bytes a row), written from pairs of
 //            keys, so one d column of 4 consecutive keys is one 8-byte read.
 // Per tile a wavefront computes S^T = K . Q^T with 16x16x32 MFMA (rows = keys,
-// columns = its query tokens; Q^T stays in registers for the whole walk), the
-// online softmax in base 2 down each column (a lane owns one query column, so
-// the running max/sum and the rescale are lane-local), and O^T += V^T . P^T
-// where P^T is exactly the lane's own probabilities of the S^T tiles.
-// Only tiles that cross the causal diagonal or the last key are masked.
+// columns = its (token, head) pairs; Q^T stays in registers for the whole
+// walk), the online softmax in base 2 down each column (a lane owns one
+// column per column tile, so the running max/sum and the rescale are
+// lane-local), and O^T += V^T . P^T where P^T is exactly the lane's own
+// probabilities of the S^T tiles. Only tiles that cross the causal diagonal
+// or the last key are masked.
 //
 // Parity: the one-shot softmax of infrared/model/layers.py:102-118 over the
 // gathered history (infrared/model/triton_attention.py:110-129), streaming as
 // in infrared/model/triton_attention.py:135-177; probabilities are rounded to
 // the input dtype before the PV product, as softmax(...).to(q.dtype) does.
+#include <type_traits>
+
 #include "attn_tile.hpp"
 #include "status.hpp"
 
@@ -47,7 +54,8 @@ struct PrefillArgs {
   const void* vc;
   int64_t c_slot, c_head;  // elements
   int64_t num_blocks;
-  int bs;
+  int bs, bs_shift;  // bs_shift = log2(bs) for a power-of-two block size, else -1
+  int c_slot32;      // c_slot when the fast addressing path applies
   const int32_t* bt;
   int64_t bt_stride;
   int max_blocks;
@@ -56,14 +64,16 @@ struct PrefillArgs {
   int num_seqs, total_q, n_qblocks;
   void* out;
   int64_t o_tok, o_head;  // elements
-  int num_q_heads, num_kv_heads, n_rep, n_hgp;
+  int num_q_heads, num_kv_heads, n_rep, tq;  // tq: query tokens per workgroup
   float scale_log2;
   int32_t* err;
 };
 
-template <int D, int NW>
+template <int D>
 struct PShape {
-  static constexpr int TQ = 32;   // query tokens per workgroup (2 column tiles)
+  static constexpr int NW = 8;    // wavefronts per workgroup (two per SIMD)
+  static constexpr int CT = 2;    // 16-column tiles per wavefront
+  static constexpr int COLS = NW * CT * 16;  // (token, head) columns per workgroup
   static constexpr int BN = 64;   // keys per tile
   static constexpr int NT = NW * 64;
   static constexpr int KROW = D + 8;   // elements per K row in LDS
@@ -76,32 +86,33 @@ struct PShape {
   static constexpr int DTL = D / 16;  // d tiles of O^T
 };
 
-template <int DT, int D, int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(1)))
+// FAST: power-of-two block size and a pool layer small enough for 24-bit slot
+// and stride products (32-bit element offsets).
+template <int DT, int D, bool FAST>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_prefill_kernel(PrefillArgs a) {
-  typedef PShape<D, NW> S;
+  typedef PShape<D> S;
   constexpr int EB = 2;
-  constexpr int TQ = S::TQ, BN = S::BN, NT = S::NT;
-  __shared__ __attribute__((aligned(16))) uint16_t ks_lds[2][BN * S::KROW];
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[2][D * S::VROW];
+  constexpr int CT = S::CT, BN = S::BN, NT = S::NT;
+  __shared__ __attribute__((aligned(16))) uint16_t ks_lds[3][BN * S::KROW];
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[3][D * S::VROW];
   __shared__ int32_t bt_lds[kBtCache];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
+  const int TQ = a.tq;
 
-  // ---- which (query block, KV head, head group, sequence): heaviest first
-  const int per_tb = a.num_kv_heads * a.n_hgp * a.num_seqs;
+  // ---- which (query block, KV head, sequence): heaviest first
+  const int per_tb = a.num_kv_heads * a.num_seqs;
   const int tb = a.n_qblocks - 1 - (int)(blockIdx.x / per_tb);
-  int rest = (int)(blockIdx.x % per_tb);
+  const int rest = (int)(blockIdx.x % per_tb);
   const int seq = rest % a.num_seqs;
-  rest /= a.num_seqs;
-  const int hgp = rest % a.n_hgp;
-  const int kvh = rest / a.n_hgp;
+  const int kvh = rest / a.num_seqs;
 
   int q_lo = a.cu_q[seq];
   int q_len = a.cu_q[seq + 1] - q_lo;
   if (q_lo < 0 || q_len < 0 || q_lo + q_len > a.total_q) {
-    if (tid == 0 && tb == 0 && kvh == 0 && hgp == 0) flag_error(a.err, IR_ERR_CONTEXT_RANGE);
+    if (tid == 0 && tb == 0 && kvh == 0) flag_error(a.err, IR_ERR_CONTEXT_RANGE);
     return;
   }
   const int tq0 = tb * TQ;
@@ -109,30 +120,38 @@ void paged_prefill_kernel(PrefillArgs a) {
   int p0 = a.q_start[seq];
   const int cap = a.max_blocks * a.bs;
   if (p0 < 0 || (int64_t)p0 + q_len > cap) {
-    if (tid == 0 && tb == 0 && kvh == 0 && hgp == 0) flag_error(a.err, IR_ERR_CONTEXT_RANGE);
+    if (tid == 0 && tb == 0 && kvh == 0) flag_error(a.err, IR_ERR_CONTEXT_RANGE);
     p0 = p0 < 0 ? 0 : p0;
   }
   // keys this block needs: up to its last query's position, within the table
   const int kmax = min(cap, p0 + min(q_len, tq0 + TQ));
   const int nkb = kmax > 0 && a.num_blocks > 0 ? (kmax + BN - 1) / BN : 0;
 
-  const int h_local = hgp * NW + w;
-  const bool active = h_local < a.n_rep;
-  const int head = kvh * a.n_rep + h_local;
+  // columns of this lane: tile ct holds column j = 32 w + 16 ct + c, i.e.
+  // token tq0 + j / n_rep, query head kvh * n_rep + j % n_rep
+  int col_tok[CT], col_head[CT];
+  bool col_ok[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const int j = w * (CT * 16) + ct * 16 + c;
+    const int t = j / a.n_rep;
+    col_tok[ct] = tq0 + t;
+    col_head[ct] = kvh * a.n_rep + (j - t * a.n_rep);
+    col_ok[ct] = t < TQ && tq0 + t < q_len;
+  }
   const int32_t* bt_row = a.bt + (int64_t)seq * a.bt_stride;
   const uint16_t* kc = (const uint16_t*)a.kc + (int64_t)kvh * a.c_head;
   const uint16_t* vc = (const uint16_t*)a.vc + (int64_t)kvh * a.c_head;
 
-  // ---- Q^T operands: lane (g, c) holds d = 32 ks + 8 g .. +7 of query column c
-  u32x4 qreg[2][S::KS];
+  // ---- Q^T operands: lane (g, c) holds d = 32 ks + 8 g .. +7 of its column
+  u32x4 qreg[CT][S::KS];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int t = tq0 + qt * 16 + c;
-    const bool ok = active && t < q_len;
-    const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)(q_lo + (ok ? t : 0)) * a.q_tok + (int64_t)head * a.q_head;
+  for (int ct = 0; ct < CT; ++ct) {
+    const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)(q_lo + (col_ok[ct] ? col_tok[ct] : 0)) * a.q_tok +
+                           (int64_t)(col_ok[ct] ? col_head[ct] : 0) * a.q_head;
 #pragma unroll
     for (int ks = 0; ks < S::KS; ++ks)
-      qreg[qt][ks] = ok ? *(const u32x4*)(qrow + ks * 32 + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+      qreg[ct][ks] = col_ok[ct] ? *(const u32x4*)(qrow + ks * 32 + 8 * g) : u32x4{0u, 0u, 0u, 0u};
   }
 
   // ---- block-id cache: ids [bt_base, bt_base + kBtCache) of this sequence
@@ -145,16 +164,29 @@ void paged_prefill_kernel(PrefillArgs a) {
     bt_base = base;
   };
   bool bad = false;
-  // slot of absolute key k (< kmax), or -1 (then masked out, V zeroed)
-  auto slot_of = [&](int k) -> int64_t {
-    if (k >= kmax) return -1;
-    const int blk = k / a.bs;
-    const int32_t bid = bt_lds[blk - bt_base];
-    if (bid < 0 || (int64_t)bid >= a.num_blocks) {
-      bad = true;
-      return -1;
+  // Slot of absolute key k and whether it may be used: keys at or past kmax are
+  // masked out; a bad block id is flagged and its K and V read as zeros. Every
+  // load is issued (from slot 0 when unusable) and zeroed afterwards.
+  auto slot_of = [&](int k, bool& use) -> int64_t {
+    const bool in = k < kmax;
+    const int kk = in ? k : 0;
+    if constexpr (FAST) {
+      const int blk = kk >> a.bs_shift;
+      const int32_t bid = bt_lds[blk - bt_base];
+      use = in && (uint32_t)bid < (uint32_t)a.num_blocks;
+      bad |= in && !use;
+      const int sl = use ? (bid << a.bs_shift) | (kk & (a.bs - 1)) : 0;
+      return (int64_t)(uint32_t)__mul24(sl, a.c_slot32);  // element offset
+    } else {
+      const int blk = kk / a.bs;
+      const int32_t bid = bt_lds[blk - bt_base];
+      use = in && bid >= 0 && (int64_t)bid < a.num_blocks;
+      bad |= in && !use;
+      return use ? ((int64_t)bid * a.bs + (kk - blk * a.bs)) * a.c_slot : 0;
     }
-    return (int64_t)bid * a.bs + (k - blk * a.bs);
+  };
+  auto zero_unless = [](u32x4 x, bool keep) {
+    return u32x4{keep ? x[0] : 0u, keep ? x[1] : 0u, keep ? x[2] : 0u, keep ? x[3] : 0u};
   };
 
   u32x4 kreg[S::KPT];
@@ -162,27 +194,28 @@ void paged_prefill_kernel(PrefillArgs a) {
   // Global loads of key tile kb into registers (whole workgroup, uniform call).
   auto load_regs = [&](int kb) {
     const int k0 = kb * BN;
-    const int last_blk = (min(k0 + BN, kmax) - 1) / a.bs;
-    if (last_blk >= bt_base + kBtCache) fill_bt(k0 / a.bs);
+    const int k_last = min(k0 + BN, kmax) - 1;
+    const int last_blk = FAST ? k_last >> a.bs_shift : k_last / a.bs;
+    if (last_blk >= bt_base + kBtCache) fill_bt(FAST ? k0 >> a.bs_shift : k0 / a.bs);
 #pragma unroll
     for (int i = 0; i < S::KPT; ++i) {
       const int q = tid + NT * i;
-      kreg[i] = u32x4{0u, 0u, 0u, 0u};
-      if (q < S::KCH) {
+      if (S::KCH % NT == 0 || q < S::KCH) {
         const int key = q / (D / 8), part = q % (D / 8);
-        const int64_t s = slot_of(k0 + key);
-        if (s >= 0) kreg[i] = *(const u32x4*)(kc + s * a.c_slot + part * 8);
+        bool use;
+        const int64_t sl = slot_of(k0 + key, use);
+        kreg[i] = zero_unless(*(const u32x4*)(kc + sl + part * 8), use);
       }
     }
 #pragma unroll
     for (int i = 0; i < S::VPT; ++i) {
       const int v = tid + NT * i;
-      vreg[i][0] = vreg[i][1] = u32x4{0u, 0u, 0u, 0u};
-      if (v < S::VPR) {
+      if (S::VPR % NT == 0 || v < S::VPR) {
         const int pr = v % (BN / 2), part = v / (BN / 2);
-        const int64_t s0 = slot_of(k0 + 2 * pr), s1 = slot_of(k0 + 2 * pr + 1);
-        if (s0 >= 0) vreg[i][0] = *(const u32x4*)(vc + s0 * a.c_slot + part * 8);
-        if (s1 >= 0) vreg[i][1] = *(const u32x4*)(vc + s1 * a.c_slot + part * 8);
+        bool u0, u1;
+        const int64_t s0 = slot_of(k0 + 2 * pr, u0), s1 = slot_of(k0 + 2 * pr + 1, u1);
+        vreg[i][0] = zero_unless(*(const u32x4*)(vc + s0 + part * 8), u0);
+        vreg[i][1] = zero_unless(*(const u32x4*)(vc + s1 + part * 8), u1);
       }
     }
   };
@@ -202,91 +235,118 @@ void paged_prefill_kernel(PrefillArgs a) {
       if (v < S::VPR) {
         const int pr = v % (BN / 2), part = v / (BN / 2);
         const u32x4 x0 = vreg[i][0], x1 = vreg[i][1];
+        uint16_t* dst = &vt_lds[buf][part * 8 * S::VROW + 2 * pr];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t lo = (x0[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-          const uint32_t hi = (x1[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-          *(uint32_t*)&vt_lds[buf][(part * 8 + e) * S::VROW + 2 * pr] = lo | (hi << 16);
+        for (int e = 0; e < 4; ++e) {
+          // element 2e / 2e+1 of both keys -> (key 2pr, key 2pr+1) pairs
+          *(uint32_t*)(dst + (2 * e) * S::VROW) = __builtin_amdgcn_perm(x1[e], x0[e], 0x05040100u);
+          *(uint32_t*)(dst + (2 * e + 1) * S::VROW) = __builtin_amdgcn_perm(x1[e], x0[e], 0x07060302u);
         }
       }
     }
   };
 
-  // ---- online softmax state, per column tile: lane owns query column c
-  f32x4 acc[2][S::DTL];
-  float m[2], l[2];
+  // ---- online softmax state, per column tile: lane owns column c of it
+  f32x4 acc[CT][S::DTL];
+  float m[CT], l[CT];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < CT; ++qt) {
     m[qt] = -__FLT_MAX__;
     l[qt] = 0.f;
 #pragma unroll
     for (int dt = 0; dt < S::DTL; ++dt) acc[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   const int qpos0 = p0 + tq0;  // position of the block's first query
+  int col_lim[CT];             // last key each column may see
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) col_lim[ct] = min(p0 + col_tok[ct], kmax - 1);
 
-  auto compute = [&](int buf, int k0) {
-    const uint16_t* kb_lds = ks_lds[buf];
-    const uint16_t* vb_lds = vt_lds[buf];
-    f32x4 s[2][4];
+  // S^T += K . Q^T for key tile kt (< 4), k-step ks (< KS) of the tile staged
+  // at kb_lds.
+  auto qk_step = [&](const uint16_t* kb_lds, int kt, int ks, f32x4 (&x)[CT][4]) {
+    const u32x4 ka = *(const u32x4*)&kb_lds[(kt * 16 + c) * S::KROW + ks * 32 + 8 * g];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
+    for (int ct = 0; ct < CT; ++ct) x[ct][kt] = mfma_k32<DT>(ka, qreg[ct][ks], x[ct][kt]);
+  };
+  auto zero_s = [](f32x4 (&x)[CT][4]) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) s[qt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int ks = 0; ks < S::KS; ++ks) {
-        const u32x4 ka = *(const u32x4*)&kb_lds[(kt * 16 + c) * S::KROW + ks * 32 + 8 * g];
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) s[qt][kt] = mfma_k32<DT>(ka, qreg[qt][ks], s[qt][kt]);
-      }
-    // masking is needed only where the tile crosses the diagonal or the end
-    const bool full = k0 + BN - 1 <= qpos0 && k0 + BN <= kmax;
+      for (int kt = 0; kt < 4; ++kt) x[ct][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+
+  // One key tile kb, software pipelined: the raw scores `cur` of tile kb are
+  // ready; while their exponentials run on the VALU, the scores `nxt` of tile
+  // kb + 1 (already staged) are computed on the MFMA pipe (NX), then
+  // O^T += V^T . P^T for tile kb. Scores stay raw (scale > 0 keeps the max
+  // where it is); the base-2 scale is folded into the exponent:
+  // p = exp2(s * scale_log2 - m).
+  auto step = [&](auto nx_tag, int kb, f32x4 (&cur)[CT][4], f32x4 (&nxt)[CT][4]) {
+    constexpr bool NX = decltype(nx_tag)::value;
     using E = Elem<DT>;
-    u32x4 pb[2][2];
+    const int k0 = kb * BN;
+    // only tiles that cross the causal diagonal or the last key are masked
+    if (!(k0 + BN - 1 <= qpos0 && k0 + BN <= kmax)) {
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      float sv[4][4];
-      const int lim = min(qpos0 + qt * 16 + c, kmax - 1);  // last key this column may see
+      for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float x = s[qt][kt][r] * a.scale_log2;
-          sv[kt][r] = (full || k0 + kt * 16 + 4 * g + r <= lim) ? x : kNegInf;
-        }
+          for (int r = 0; r < 4; ++r)
+            if (k0 + kt * 16 + 4 * g + r > col_lim[ct]) cur[ct][kt][r] = kNegInf;
+    }
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
       float mx = kNegInf;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
-        mx = fmaxf(mx, fmaxf(fmaxf(sv[kt][0], sv[kt][1]), fmaxf(sv[kt][2], sv[kt][3])));
-      mx = wave_max_groups(mx);
-      const bool grow = mx > m[qt] + kRescaleSlack;
+        mx = fmaxf(mx, fmaxf(fmaxf(cur[ct][kt][0], cur[ct][kt][1]), fmaxf(cur[ct][kt][2], cur[ct][kt][3])));
+      mx = wave_max_groups_swap(mx) * a.scale_log2;
+      const bool grow = mx > m[ct] + kRescaleSlack;
       if (__any(grow)) {
-        const float m_new = grow ? mx : m[qt];
-        const float alpha = fast_exp2(m[qt] - m_new);
-        l[qt] *= alpha;
+        const float m_new = grow ? mx : m[ct];
+        const float alpha = fast_exp2(m[ct] - m_new);
+        l[ct] *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < S::DTL; ++dt) acc[qt][dt] *= alpha;
-        m[qt] = m_new;
+        for (int dt = 0; dt < S::DTL; ++dt) acc[ct][dt] *= alpha;
+        m[ct] = m_new;
       }
-      float p[4][4];
-      float ls = 0.f;
+    }
+    // next tile's scores (MFMA) interleaved with this tile's exponentials (VALU)
+    const uint16_t* kn = ks_lds[(kb + 1) % 3];
+    if constexpr (NX) zero_s(nxt);
+    float ls[CT];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+    for (int ct = 0; ct < CT; ++ct) ls[ct] = 0.f;
+    // NQK = 4 * KS score MFMA steps, SPS of this lane's CT * 16 scores each
+    constexpr int NQK = 4 * S::KS, SPS = CT * 16 / NQK;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          p[kt][r] = fast_exp2(sv[kt][r] - m[qt]);
-          ls += p[kt][r];
-        }
-      l[qt] += ls;
-      // P^T operands of the two 32-key steps: k-slots 0..3 = keys 4g..4g+3 of
-      // tile 2st, k-slots 4..7 = keys 4g..4g+3 of tile 2st+1
+    for (int t = 0; t < NQK; ++t) {
+      if constexpr (NX) qk_step(kn, t % 4, t / 4, nxt);
+#pragma unroll
+      for (int j = 0; j < SPS; ++j) {
+        const int i = t * SPS + j;
+        const int ct = i / 16, kt = (i % 16) / 4, r = i % 4;
+        const float pv = fast_exp2(__builtin_fmaf(cur[ct][kt][r], a.scale_log2, -m[ct]));
+        ls[ct] += pv;
+        cur[ct][kt][r] = pv;
+      }
+    }
+    // P^T operands of the two 32-key steps: k-slots 0..3 = keys 4g..4g+3 of
+    // tile 2st, k-slots 4..7 = keys 4g..4g+3 of tile 2st+1
+    u32x4 pb[CT][2];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      l[ct] += ls[ct];
 #pragma unroll
       for (int st = 0; st < 2; ++st)
-        pb[qt][st] = u32x4{E::pack2(p[2 * st][0], p[2 * st][1]), E::pack2(p[2 * st][2], p[2 * st][3]),
-                           E::pack2(p[2 * st + 1][0], p[2 * st + 1][1]), E::pack2(p[2 * st + 1][2], p[2 * st + 1][3])};
+        pb[ct][st] = u32x4{E::pack2(cur[ct][2 * st][0], cur[ct][2 * st][1]),
+                           E::pack2(cur[ct][2 * st][2], cur[ct][2 * st][3]),
+                           E::pack2(cur[ct][2 * st + 1][0], cur[ct][2 * st + 1][1]),
+                           E::pack2(cur[ct][2 * st + 1][2], cur[ct][2 * st + 1][3])};
     }
     // O^T += V^T . P^T; V^T operand: d row c of the tile, the same key slots
+    const uint16_t* vb_lds = vt_lds[kb % 3];
 #pragma unroll
     for (int st = 0; st < 2; ++st)
 #pragma unroll
@@ -296,37 +356,59 @@ void paged_prefill_kernel(PrefillArgs a) {
         const u32x2 hi = *(const u32x2*)(row + 16 + 4 * g);
         const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) acc[qt][dt] = mfma_k32<DT>(va, pb[qt][st], acc[qt][dt]);
+        for (int ct = 0; ct < CT; ++ct) acc[ct][dt] = mfma_k32<DT>(va, pb[ct][st], acc[ct][dt]);
       }
   };
 
-  // ---- walk the key tiles: tile kb in the math while kb + 1 sits in LDS
-  // (written after kb's math) and kb + 2 is in flight in registers
+  // ---- walk the key tiles through a 3-deep LDS ring: tile kb (V) and tile
+  // kb + 1 (K) are read while tile kb + 2 is written from registers and tile
+  // kb + 3 is in flight from global memory
+  auto tail = [&](int kb) {
+    if (kb + 2 < nkb) store_regs((kb + 2) % 3);
+    if (kb + 3 < nkb) load_regs(kb + 3);
+    __syncthreads();
+  };
   if (nkb > 0) {
     fill_bt(0);
     load_regs(0);
     store_regs(0);
-    if (nkb > 1) load_regs(1);
+    if (nkb > 1) {
+      load_regs(1);
+      store_regs(1);
+    }
+    if (nkb > 2) load_regs(2);
     __syncthreads();
-    for (int kb = 0; kb < nkb; ++kb) {
-      if (active) compute(kb & 1, kb * BN);
-      if (kb + 1 < nkb) store_regs((kb + 1) & 1);
-      if (kb + 2 < nkb) load_regs(kb + 2);
-      __syncthreads();
+    f32x4 sa[CT][4], sb[CT][4];
+    zero_s(sa);
+#pragma unroll
+    for (int t = 0; t < 4 * S::KS; ++t) qk_step(ks_lds[0], t % 4, t / 4, sa);
+    int kb = 0;
+    // two tiles per trip so the score buffers swap roles without copies
+    for (; kb + 2 < nkb; kb += 2) {
+      step(std::true_type{}, kb, sa, sb);
+      tail(kb);
+      step(std::true_type{}, kb + 1, sb, sa);
+      tail(kb + 1);
+    }
+    if (kb + 1 < nkb) {
+      step(std::true_type{}, kb, sa, sb);
+      tail(kb);
+      step(std::false_type{}, kb + 1, sb, sa);
+    } else {
+      step(std::false_type{}, kb, sa, sb);
     }
   }
   if (bad) flag_error(a.err, IR_ERR_BLOCK_RANGE);
-  if (!active) return;
 
   // ---- normalise and store: lane (g, c) register r of d tile dt = output
-  // d = 16 dt + 4 g + r of query column c
+  // d = 16 dt + 4 g + r of column c
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const float lsum = wave_sum_groups(l[qt]);
+  for (int qt = 0; qt < CT; ++qt) {
+    const float lsum = wave_sum_groups_swap(l[qt]);
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    const int t = tq0 + qt * 16 + c;
-    if (t >= q_len) continue;
-    uint8_t* orow = (uint8_t*)a.out + ((int64_t)(q_lo + t) * a.o_tok + (int64_t)head * a.o_head) * EB;
+    if (!col_ok[qt]) continue;
+    uint8_t* orow =
+        (uint8_t*)a.out + ((int64_t)(q_lo + col_tok[qt]) * a.o_tok + (int64_t)col_head[qt] * a.o_head) * EB;
 #pragma unroll
     for (int dt = 0; dt < S::DTL; ++dt) {
       const float o[4] = {acc[qt][dt][0], acc[qt][dt][1], acc[qt][dt][2], acc[qt][dt][3]};
@@ -336,17 +418,20 @@ void paged_prefill_kernel(PrefillArgs a) {
 }
 
 template <int DT, int D>
-int launch_prefill(const PrefillArgs& a0, hipStream_t s) {
-  PrefillArgs a = a0;
-  const int nw = a.n_rep <= 4 ? 4 : 8;
-  a.n_hgp = (a.n_rep + nw - 1) / nw;
-  const int64_t grid = (int64_t)a.n_qblocks * a.num_kv_heads * a.n_hgp * a.num_seqs;
+int launch_prefill(const PrefillArgs& a, hipStream_t s) {
+  const int64_t grid = (int64_t)a.n_qblocks * a.num_kv_heads * a.num_seqs;
   if (grid <= 0) return ok();
   if (grid > 0x7fffffff) return fail(IR_EINVAL, "ir_paged_prefill: grid of %lld workgroups too large", (long long)grid);
-  if (nw == 4)
-    hipLaunchKernelGGL((paged_prefill_kernel<DT, D, 4>), dim3((unsigned)grid), dim3(256), 0, s, a);
+  // fast addressing: slot and stride below 2^23 (24-bit products) and every
+  // element offset of the layer below 2^31
+  const int64_t slots = a.num_blocks * a.bs;
+  const bool fast = a.bs_shift >= 0 && slots < (1 << 23) && a.c_slot < (1 << 23) &&
+                    (slots * a.c_slot + a.c_head * a.num_kv_heads) < ((int64_t)1 << 31);
+  const dim3 block(PShape<D>::NT);
+  if (fast)
+    hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true>), dim3((unsigned)grid), block, 0, s, a);
   else
-    hipLaunchKernelGGL((paged_prefill_kernel<DT, D, 8>), dim3((unsigned)grid), dim3(512), 0, s, a);
+    hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false>), dim3((unsigned)grid), block, 0, s, a);
   return check_launch("ir_paged_prefill");
 }
 
@@ -371,10 +456,12 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
              "ir_paged_prefill: bad sizes");
   IR_REQUIRE(num_q_heads % num_kv_heads == 0, "ir_paged_prefill: num_q_heads %d not a multiple of num_kv_heads %d",
              num_q_heads, num_kv_heads);
+  IR_REQUIRE(num_q_heads / num_kv_heads <= 256, "ir_paged_prefill: more than 256 query heads per KV head");
   if (head_dim != 64 && head_dim != 128)
     return fail(IR_EUNSUPPORTED, "ir_paged_prefill: head_dim %d not supported (64, 128)", head_dim);
   IR_REQUIRE((int64_t)max_blocks_per_seq * block_size <= (int64_t)1 << 30,
              "ir_paged_prefill: block tables of %d x %d tokens exceed 2^30 keys", max_blocks_per_seq, block_size);
+  IR_REQUIRE(scale > 0.f, "ir_paged_prefill: scale must be positive");
   if (num_seqs == 0 || total_q == 0 || max_q_len == 0) return ok();
   IR_REQUIRE(q && k_cache && v_cache && block_tables && cu_seqlens_q && q_start && out,
              "ir_paged_prefill: null pointer");
@@ -393,6 +480,8 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
   a.c_head = cache_head_stride;
   a.num_blocks = num_blocks;
   a.bs = block_size;
+  a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
+  a.c_slot32 = (int)(cache_slot_stride < (1 << 23) ? cache_slot_stride : 0);
   a.bt = block_tables;
   a.bt_stride = bt_stride;
   a.max_blocks = max_blocks_per_seq;
@@ -400,14 +489,14 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
   a.q_start = q_start;
   a.num_seqs = num_seqs;
   a.total_q = total_q;
-  a.n_qblocks = (max_q_len + 31) / 32;
+  a.n_rep = num_q_heads / num_kv_heads;
+  a.tq = PShape<128>::COLS / a.n_rep;
+  a.n_qblocks = (max_q_len + a.tq - 1) / a.tq;
   a.out = out;
   a.o_tok = out_tok_stride;
   a.o_head = out_head_stride;
   a.num_q_heads = num_q_heads;
   a.num_kv_heads = num_kv_heads;
-  a.n_rep = num_q_heads / num_kv_heads;
-  a.n_hgp = 1;
   a.scale_log2 = scale * kLog2e;
   a.err = err_flags;
   hipStream_t s = (hipStream_t)stream;
