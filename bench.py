@@ -11,6 +11,14 @@ between two events on the launch stream, with torch.cuda.synchronize() on
 both sides. Calls rotate over R disjoint copies of the pool + block tables so
 consecutive calls do not hit K/V left in the 256 MB MALL by the previous one.
 
+Other workloads (``--workload``): ``prefill`` -- 8 sequences x 512-token
+chunks after cached prefixes of up to 8192 tokens (pairs sharing prefix
+blocks), one call of the chunked-prefill MFMA kernel per step, value in
+TFLOP/s of unmasked (query, key) pairs; ``mixed`` -- one 28-layer engine step
+of 224 decode rows (context U{256..4096}) + 4 x 256-token prefill chunks
+(scatter + decode + prefill per layer) replayed as one hipGraph, value in us
+per step.
+
 Prints one JSON line: value = achieved KV GB/s (algorithmic bytes sum(ctx) *
 2 * H_kv * D * 2 per call / time per call), plus us_per_call, a roofline
 object for the decode kernel and the CPU baseline: the oracle's restatement of
@@ -30,6 +38,7 @@ import time
 import torch
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 METRIC = "paged decode attn µs/call + achieved KV HBM GB/s (% of peak), Qwen2.5-7B shape"
 
 
@@ -38,7 +47,8 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--config", default="qwen7b-bf16")
+    p.add_argument("--workload", choices=("decode", "prefill", "mixed"), default="decode")
+    p.add_argument("--config", default=None, help="decode: qwen7b-bf16 (default) | qwen0.5b-fp32 | qwen7b-skewed")
     p.add_argument("--rotations", type=int, default=3)
     p.add_argument("--partition", type=int, default=0, help="split-KV partition tokens (0 = library default)")
     p.add_argument("--cpu-iters", type=int, default=3, help="timed CPU-baseline iterations (0 = skip)")
@@ -46,6 +56,7 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--check", action="store_true", help="also check the output against the oracle")
     p.add_argument("--mode", choices=("graph", "eager"), default="graph",
                    help="time a hipGraph replay of the K calls (default) or host-launched calls")
+    p.add_argument("--no-overlap", action="store_true", help="mixed: decode and prefill on one stream")
     p.add_argument("--copy-calib-mib", type=int, default=0,
                    help="after timing, run 10 device copies of this many MiB (counter calibration)")
     return p.parse_args()
@@ -151,6 +162,152 @@ def _traffic(config: str) -> tuple[int | None, str | None]:
     return int(rec["hbm_bytes_per_launch"]), os.path.relpath(path, os.path.dirname(path) + "/..")
 
 
+def _bench_prefill(args) -> dict:
+    """8 x 512-token chunks after cached prefixes: one prefill call per step."""
+    from infrared_amd import kernels
+    from infrared_amd.workloads import make_prefill_case
+
+    case = make_prefill_case("qwen7b-prefill", "cuda", rotations=args.rotations)
+    cfg = case.config
+    out = torch.empty_like(case.q)
+
+    def call(i: int) -> None:
+        kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[i % len(case.block_tables)],
+                              case.cu_seqlens_q, case.q_start, cfg.chunk, cfg.block_size, cfg.scale, out=out)
+
+    ms = _time_graph(call, args)
+    tflops = case.flops / (ms * 1e-3) / 1e12
+    cpu = None
+    if args.cpu_iters > 0:
+        from oracle import naive as O
+
+        # bounded sample: the reference's naive path for one chunk (sequence 0)
+        b = 0
+        n, pre = case.q_lens[b], case.prefixes[b]
+        row = case.block_tables[0][b].cpu().tolist()
+        gs = torch.tensor([[O.slot(row, p, cfg.block_size) for p in range(pre + n)]])
+        mask = O.attention_mask([0], pre, n, pre + n, cfg.dtype)
+        q = case.q[None, :n].cpu()
+        kc, vc = case.k_cache.cpu(), case.v_cache.cpu()
+        O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, cfg.n_rep)
+        times = []
+        for _ in range(args.cpu_iters):
+            t0 = time.perf_counter()
+            O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, cfg.n_rep)
+            times.append(time.perf_counter() - t0)
+        t = statistics.median(times)
+        fl = 4 * cfg.num_q_heads * cfg.head_dim * (n * pre + n * (n + 1) // 2)
+        cpu = {"value": round(fl / t / 1e12, 6), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+               "kind": "port",
+               "sample": f"sequence 0 only ({n} queries after a {pre}-token prefix), naive gather+repeat_kv+masked "
+               f"softmax in bf16, median of {args.cpu_iters} after 1 warm-up, torch CPU"}
+    return {
+        "metric": "paged prefill TFLOP/s (unmasked pairs), 8 x 512-token chunks after cached prefixes, Qwen2.5-7B shape",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "us_per_call": round(ms * 1e3, 2),
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{cfg.name}: {cfg.num_seqs} chunks of {cfg.chunk} after prefixes {case.prefixes}, "
+                   f"{cfg.num_q_heads}q/{cfg.num_kv_heads}kv heads, head_dim {cfg.head_dim}, block {cfg.block_size}",
+                   "flops_per_call": case.flops, "kv_bytes_per_call": case.kv_bytes, "rotations": args.rotations},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "timed": "prefill call, graph launches, events on the launch stream"},
+        "cpu_baseline": cpu,
+    }
+
+
+def _bench_mixed(args) -> dict:
+    """One 28-layer mixed step (scatter + decode + prefill per layer) per graph replay."""
+    from infrared_amd.mixed_step import MixedStep, make_mixed_case
+
+    cfg, pool, batch, inputs = make_mixed_case("qwen7b-mixed", "cuda")
+    step = MixedStep(pool, batch, inputs, cfg.scale, overlap=not args.no_overlap)
+    step.capture()
+    for _ in range(max(1, args.warmup // 10)):
+        step.replay()
+    torch.cuda.synchronize()
+    n = max(1, args.steps // 20)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(n):
+        step.replay()
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / n
+    esize = 2
+    dec_bytes = int(batch.dec_ctx.long().sum()) * 2 * cfg.num_kv_heads * cfg.head_dim * esize * cfg.num_layers
+    pairs = cfg.num_prefill * (cfg.chunk * cfg.prefix + cfg.chunk * (cfg.chunk + 1) // 2)
+    pre_flops = 4 * cfg.num_q_heads * cfg.head_dim * pairs * cfg.num_layers
+    n_new = batch.write_slots.numel()
+    scatter_bytes = 2 * n_new * cfg.num_kv_heads * cfg.head_dim * esize * 2 * cfg.num_layers
+    gbps = dec_bytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if args.cpu_iters > 0:
+        from oracle import naive as O
+
+        # bounded sample: one layer's decode rows through the reference's naive path
+        nd = min(cfg.num_decode, 32)
+        ctx = batch.dec_ctx[:nd].cpu().tolist()
+        tables = [r.tolist() for r in batch.dec_tables[:nd].cpu()]
+        t_max = max(ctx)
+        gs = O.decode_gather_slots(tables, ctx, cfg.block_size, t_max)
+        mask = O.decode_mask(ctx, t_max, cfg.dtype)
+        q = inputs.q_dec[0, :nd, None].cpu()
+        kc, vc = pool.k[0].cpu(), pool.v[0].cpu()
+        O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, cfg.num_q_heads // cfg.num_kv_heads)
+        times = []
+        for _ in range(args.cpu_iters):
+            t0 = time.perf_counter()
+            O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, cfg.num_q_heads // cfg.num_kv_heads)
+            times.append(time.perf_counter() - t0)
+        t = statistics.median(times)
+        kvb = sum(ctx) * 2 * cfg.num_kv_heads * cfg.head_dim * esize
+        cpu = {"value": round(kvb / t / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"{nd} of {cfg.num_decode} decode rows of one layer (prefill and scatter not included), "
+               f"naive gather+repeat_kv+masked softmax in bf16, median of {args.cpu_iters}, torch CPU"}
+    return {
+        "metric": "mixed engine step us per 28-layer hipGraph replay (224 decode rows + 4 x 256-token prefill chunks)",
+        "value": round(ms * 1e3, 2), "unit": "us/step", "us_per_layer": round(ms * 1e3 / cfg.num_layers, 2),
+        "ms_per_step": round(ms, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{cfg.name}: {cfg.num_layers} layers, {cfg.num_decode} decode rows ctx U"
+                   f"[{cfg.decode_ctx_lo},{cfg.decode_ctx_hi}], {cfg.num_prefill} x {cfg.chunk}-token chunks, "
+                   f"{cfg.num_q_heads}q/{cfg.num_kv_heads}kv heads, head_dim {cfg.head_dim}, block {cfg.block_size}",
+                   "decode_kv_bytes_per_step": dec_bytes, "prefill_flops_per_step": pre_flops,
+                   "scatter_bytes_per_step": scatter_bytes, "overlap_streams": not args.no_overlap,
+                   "replays": n},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "timed": "whole step (decode KV bytes / step time: scatter and prefill time included)"},
+        "cpu_baseline": cpu,
+    }
+
+
+def _time_graph(call, args) -> float:
+    """ms per call: warm-up, then K calls captured in one hipGraph and replayed
+    between events on the launch stream."""
+    for i in range(args.warmup):
+        call(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        call(0)
+    torch.cuda.current_stream().wait_stream(stream)
+    with torch.cuda.graph(graph):
+        for i in range(args.steps):
+            call(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    graph.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / args.steps
+
+
 def main() -> int:
     args = _parse()
     if args.gpus != 1:
@@ -163,8 +320,14 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
+    if args.workload != "decode":
+        line = _bench_prefill(args) if args.workload == "prefill" else _bench_mixed(args)
+        line.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup})
+        print(json.dumps(line), flush=True)
+        return 0
     from infrared_amd.workloads import make_decode_case
 
+    args.config = args.config or "qwen7b-bf16"
     case = make_decode_case(args.config, "cuda", rotations=args.rotations)
     cfg = case.config
     kv = case.kv_bytes
