@@ -152,9 +152,9 @@ def _cpu_baseline(case, args):
     }
 
 
-def _traffic(config: str) -> tuple[int | None, str | None]:
-    """HBM bytes per decode launch measured with rocprofv3 counters, if recorded."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"decode_{config}_traffic.json")
+def _traffic(name: str) -> tuple[int | None, str | None]:
+    """HBM bytes per launch of a kernel/workload measured with rocprofv3 counters, if recorded."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"{name}_traffic.json")
     if not os.path.exists(path):
         return None, None
     with open(path) as f:
@@ -175,7 +175,9 @@ def _bench_prefill(args) -> dict:
         kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[i % len(case.block_tables)],
                               case.cu_seqlens_q, case.q_start, cfg.chunk, cfg.block_size, cfg.scale, out=out)
 
-    ms = _time_graph(call, args)
+    ms = _time_graph(call, args) if args.mode == "graph" else _time_eager(call, args)
+    if args.copy_calib_mib > 0:
+        _copy_calibration(args.copy_calib_mib)
     tflops = case.flops / (ms * 1e-3) / 1e12
     cpu = None
     if args.cpu_iters > 0:
@@ -210,8 +212,8 @@ def _bench_prefill(args) -> dict:
                    f"{cfg.num_q_heads}q/{cfg.num_kv_heads}kv heads, head_dim {cfg.head_dim}, block {cfg.block_size}",
                    "flops_per_call": case.flops, "kv_bytes_per_call": case.kv_bytes, "rotations": args.rotations},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                     "timed": "prefill call, graph launches, events on the launch stream"},
+                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": _traffic("prefill_qwen7b-prefill")[0],
+                     "timed": f"prefill call, {args.mode} launches, events on the launch stream"},
         "cpu_baseline": cpu,
     }
 
@@ -283,6 +285,29 @@ def _bench_mixed(args) -> dict:
     }
 
 
+def _time_eager(call, args) -> float:
+    """ms per call over K host-launched calls after W warm-up calls."""
+    for i in range(args.warmup):
+        call(i)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(args.steps):
+        call(i)
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / args.steps
+
+
+def _copy_calibration(mib: int) -> None:
+    """10 device copies of ``mib`` MiB: a known-size reference for the byte counters."""
+    src = torch.empty(mib << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 def _time_graph(call, args) -> float:
     """ms per call: warm-up, then K calls captured in one hipGraph and replayed
     between events on the launch stream."""
@@ -344,13 +369,9 @@ def main() -> int:
         )
         check = round((outs[0].float().cpu() - ref).abs().max().item(), 6)
     if args.copy_calib_mib > 0:
-        src = torch.empty(args.copy_calib_mib << 20, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(10):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+        _copy_calibration(args.copy_calib_mib)
     cpu = _cpu_baseline(case, args) if args.cpu_iters > 0 else None
-    traffic, traffic_src = _traffic(args.config)
+    traffic, traffic_src = _traffic(f"decode_{args.config}")
     esize = torch.tensor([], dtype=cfg.dtype).element_size()
     line = {
         "metric": METRIC,
