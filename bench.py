@@ -17,7 +17,8 @@ blocks), one call of the chunked-prefill MFMA kernel per step, value in
 TFLOP/s of unmasked (query, key) pairs; ``mixed`` -- one 28-layer engine step
 of 224 decode rows (context U{256..4096}) + 4 x 256-token prefill chunks
 (scatter + decode + prefill per layer) replayed as one hipGraph, value in us
-per step.
+per step; ``rope`` -- the fused rotary embedding + KV scatter of one such step's
+layer (1,248 new tokens, 28 q / 4 kv heads), value in GB/s of algorithmic bytes.
 
 Prints one JSON line: value = achieved KV GB/s (algorithmic bytes sum(ctx) *
 2 * H_kv * D * 2 per call / time per call), plus us_per_call, a roofline
@@ -47,7 +48,7 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--workload", choices=("decode", "prefill", "mixed"), default="decode")
+    p.add_argument("--workload", choices=("decode", "prefill", "mixed", "rope"), default="decode")
     p.add_argument("--config", default=None, help="decode: qwen7b-bf16 (default) | qwen0.5b-fp32 | qwen7b-skewed")
     p.add_argument("--rotations", type=int, default=3)
     p.add_argument("--partition", type=int, default=0, help="split-KV partition tokens (0 = library default)")
@@ -285,6 +286,43 @@ def _bench_mixed(args) -> dict:
     }
 
 
+def _bench_rope(args) -> dict:
+    """Fused RoPE + KV scatter for one mixed-step layer: 1,248 tokens, 28 q / 4 kv heads."""
+    from infrared_amd import kernels
+    from oracle import naive as O
+
+    n, hq, hkv, d, dtype = 1248, 28, 4, 128, torch.bfloat16
+    num_slots = 1 << 20  # a 1 Mi-slot pool layer (2 GiB for K+V): writes land far apart
+    g = torch.Generator(device="cuda").manual_seed(6)
+    q = torch.randn(n, hq, d, generator=g, device="cuda").to(dtype)
+    k = torch.randn(n, hkv, d, generator=g, device="cuda").to(dtype)
+    v = torch.randn(n, hkv, d, generator=g, device="cuda").to(dtype)
+    kc = torch.zeros(hkv, num_slots, d, dtype=dtype, device="cuda").permute(1, 0, 2)
+    vc = torch.zeros_like(kc.permute(1, 0, 2)).permute(1, 0, 2)
+    pos = torch.randint(0, 4096, (n,), generator=torch.Generator().manual_seed(6))
+    cos, sin = (t.to("cuda") for t in O.rotary_cos_sin(pos, d, 1_000_000.0))
+    slots = torch.randperm(num_slots, device="cuda")[:n]
+    q_out = torch.empty_like(q)
+
+    def call(i: int) -> None:
+        kernels.rope_kv_scatter(q, k, v, cos, sin, kc, vc, slots, q_out=q_out)
+
+    ms = _time_graph(call, args) if args.mode == "graph" else _time_eager(call, args)
+    nbytes = (2 * n * hq * d + 4 * n * hkv * d) * 2 + 2 * n * d * 4 + n * 8
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": "fused RoPE + KV scatter GB/s (1,248 tokens, 28q/4kv heads, head_dim 128)",
+        "value": round(gbps, 2), "unit": "GB/s", "us_per_call": round(ms * 1e3, 3), "ms_per_step": round(ms, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "one mixed-step layer: rotate q (in/out) and k, write k/v into a head-major pool",
+                   "bytes_per_call": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "timed": f"rope+scatter call, {args.mode} launches, events on the launch stream"},
+        "cpu_baseline": None,
+    }
+
+
 def _time_eager(call, args) -> float:
     """ms per call over K host-launched calls after W warm-up calls."""
     for i in range(args.warmup):
@@ -346,7 +384,7 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
     if args.workload != "decode":
-        line = _bench_prefill(args) if args.workload == "prefill" else _bench_mixed(args)
+        line = {"prefill": _bench_prefill, "mixed": _bench_mixed, "rope": _bench_rope}[args.workload](args)
         line.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup})
         print(json.dumps(line), flush=True)
         return 0

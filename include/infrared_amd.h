@@ -216,6 +216,32 @@ int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
                      int64_t out_head_stride, int num_q_heads, int num_kv_heads, int head_dim,
                      float scale, int dtype, int32_t* err_flags, ir_stream_t stream);
 
+/*
+ * Fused rotary embedding + KV-slot scatter. Replaces, per layer,
+ * apply_rotary_pos_emb (infrared/model/layers.py:79-89, called at :164) followed by
+ * PagedKVPool.write (infrared/cache/paged_kv_cache.py:48-57, called from
+ * infrared/model/triton_attention.py:101-104):
+ *   q_out[i, h] = rope(q[i, h]);  k_cache[slot_mapping[i], h] = rope(k[i, h]);
+ *   v_cache[slot_mapping[i], h] = v[i, h],
+ *   rope(x) = x * c + rotate_half(x) * s, rotate_half(x) = (-x[D/2:], x[:D/2]),
+ *   c, s = cos[i], sin[i] rounded to the activation dtype first, every product and
+ *   the sum rounded to the dtype (the reference's tensor ops; bit-identical).
+ *   q, q_out: [n_tokens, num_q_heads, head_dim] (q_out may alias q); k, v:
+ *   [n_tokens, num_kv_heads, head_dim]; cos, sin: fp32 [n_tokens, head_dim] rows
+ *   (cs_tok_stride elements apart), as RotaryEmbedding returns them.
+ * Slot semantics as ir_kv_scatter (negative = skip, >= num_slots = skip + flag).
+ * head_dim a multiple of 16; all rows (cos/sin included) 16-byte aligned.
+ */
+int ir_rope_kv_scatter(const void* q, int64_t q_tok_stride, int64_t q_head_stride, void* q_out,
+                       int64_t qo_tok_stride, int64_t qo_head_stride, const void* k,
+                       int64_t k_tok_stride, int64_t k_head_stride, const void* v,
+                       int64_t v_tok_stride, int64_t v_head_stride, const float* cos,
+                       const float* sin, int64_t cs_tok_stride, void* k_cache, void* v_cache,
+                       int64_t cache_slot_stride, int64_t cache_head_stride, int64_t num_slots,
+                       const int64_t* slot_mapping, int64_t n_tokens, int num_q_heads,
+                       int num_kv_heads, int head_dim, int dtype, int32_t* err_flags,
+                       ir_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

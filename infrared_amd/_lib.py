@@ -62,6 +62,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32,
          _c_i32, _c_i32, _c_i32, _c_i32, _c_f32, _c_i32, _c_p, _c_p],
     ),
+    "ir_rope_kv_scatter": (
+        _c_i32,
+        [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64,
+         _c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i32, _c_i32,
+         _c_i32, _c_i32, _c_p, _c_p],
+    ),
     "ir_paged_prefill": (
         _c_i32,
         [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i64, _c_i32,

@@ -318,11 +318,23 @@ void paged_prefill_kernel(PrefillArgs a) {
     float ls[CT];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) ls[ct] = 0.f;
-    // NQK = 4 * KS score MFMA steps, SPS of this lane's CT * 16 scores each
+    // NQK = 4 * KS score MFMA steps, SPS of this lane's CT * 16 scores each.
+    // Program order is kept step by step (sched_barrier): each step's K operand
+    // was read one step earlier, its MFMAs go to the matrix pipe and the
+    // exponentials of SPS scores fill the VALU meanwhile.
     constexpr int NQK = 4 * S::KS, SPS = CT * 16 / NQK;
+    auto k_operand = [&](int t) {
+      return *(const u32x4*)&kn[((t % 4) * 16 + c) * S::KROW + (t / 4) * 32 + 8 * g];
+    };
+    u32x4 ka_next = NX ? k_operand(0) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int t = 0; t < NQK; ++t) {
-      if constexpr (NX) qk_step(kn, t % 4, t / 4, nxt);
+      if constexpr (NX) {
+        const u32x4 ka = ka_next;
+        if (t + 1 < NQK) ka_next = k_operand(t + 1);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) nxt[ct][t % 4] = mfma_k32<DT>(ka, qreg[ct][t / 4], nxt[ct][t % 4]);
+      }
 #pragma unroll
       for (int j = 0; j < SPS; ++j) {
         const int i = t * SPS + j;
@@ -331,6 +343,7 @@ void paged_prefill_kernel(PrefillArgs a) {
         ls[ct] += pv;
         cur[ct][kt][r] = pv;
       }
+      // (no scheduling barrier)
     }
     // P^T operands of the two 32-key steps: k-slots 0..3 = keys 4g..4g+3 of
     // tile 2st, k-slots 4..7 = keys 4g..4g+3 of tile 2st+1
@@ -346,18 +359,23 @@ void paged_prefill_kernel(PrefillArgs a) {
                            E::pack2(cur[ct][2 * st + 1][2], cur[ct][2 * st + 1][3])};
     }
     // O^T += V^T . P^T; V^T operand: d row c of the tile, the same key slots
+    // (operands read one step ahead)
     const uint16_t* vb_lds = vt_lds[kb % 3];
+    auto v_operand = [&](int t) {
+      const uint16_t* row = vb_lds + ((t % S::DTL) * 16 + c) * S::VROW + (t / S::DTL) * 32;
+      const u32x2 lo = *(const u32x2*)(row + 4 * g);
+      const u32x2 hi = *(const u32x2*)(row + 16 + 4 * g);
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
+    u32x4 va_next = v_operand(0);
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
+    for (int t = 0; t < 2 * S::DTL; ++t) {
+      const u32x4 va = va_next;
+      if (t + 1 < 2 * S::DTL) va_next = v_operand(t + 1);
 #pragma unroll
-      for (int dt = 0; dt < S::DTL; ++dt) {
-        const uint16_t* row = vb_lds + (dt * 16 + c) * S::VROW + st * 32;
-        const u32x2 lo = *(const u32x2*)(row + 4 * g);
-        const u32x2 hi = *(const u32x2*)(row + 16 + 4 * g);
-        const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) acc[ct][dt] = mfma_k32<DT>(va, pb[ct][st], acc[ct][dt]);
-      }
+      for (int ct = 0; ct < CT; ++ct)
+        acc[ct][t % S::DTL] = mfma_k32<DT>(va, pb[ct][t / S::DTL], acc[ct][t % S::DTL]);
+    }
   };
 
   // ---- walk the key tiles through a 3-deep LDS ring: tile kb (V) and tile

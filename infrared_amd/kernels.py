@@ -230,6 +230,57 @@ def paged_attention_masked(
     return out
 
 
+def rope_kv_scatter(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    slots: torch.Tensor,
+    q_out: torch.Tensor | None = None,
+    err_flags: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Rotary embedding of ``q`` (returned, ``[N, H_q, D]``) and ``k``, with the rotated
+    ``k`` and ``v`` written into the pool layer at ``slots`` -- ``apply_rotary_pos_emb``
+    followed by ``PagedKVPool.write`` in one launch, bit-identical to them.
+
+    ``cos``/``sin``: fp32 ``[N, D]`` (``RotaryEmbedding`` output flattened over batch
+    and sequence). ``q_out`` may be ``q`` itself (in place).
+    """
+    dev = require_device(q, k, v, cos, sin, k_cache, v_cache, slots)
+    _cache_layer("rope_kv_scatter", k_cache)
+    if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape:
+        raise RuntimeError("rope_kv_scatter: q [N, H_q, D], k and v [N, H_kv, D] expected")
+    n, hq, d = q.shape
+    if k.shape[0] != n or k.shape[2] != d or k.shape[1:] != k_cache.shape[1:]:
+        raise RuntimeError("rope_kv_scatter: k/v rows do not match q or the pool")
+    if q.dtype != k.dtype or k.dtype != k_cache.dtype or v.dtype != k.dtype:
+        raise RuntimeError("rope_kv_scatter: dtype mismatch")
+    if v_cache.stride() != k_cache.stride():
+        raise RuntimeError("rope_kv_scatter: k_cache and v_cache must share strides")
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.dtype != torch.float32 or t.shape != (n, d) or t.stride(1) != 1:
+            raise RuntimeError(f"rope_kv_scatter: {name} must be fp32 [N, D] with unit column stride")
+    if cos.stride(0) != sin.stride(0):
+        raise RuntimeError("rope_kv_scatter: cos and sin must share strides")
+    if slots.dtype != torch.int64 or slots.shape != (n,):
+        raise RuntimeError("rope_kv_scatter: slots must be int64 [N]")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _last_dim_contiguous(f"rope_kv_scatter {name}", t)
+    if q_out is None:
+        q_out = torch.empty_like(q)
+    rc = lib().ir_rope_kv_scatter(
+        ptr(q), q.stride(0), q.stride(1), ptr(q_out), q_out.stride(0), q_out.stride(1), ptr(k), k.stride(0),
+        k.stride(1), ptr(v), v.stride(0), v.stride(1), ptr(cos), ptr(sin), cos.stride(0), ptr(k_cache),
+        ptr(v_cache), k_cache.stride(0), k_cache.stride(1), k_cache.shape[0], ptr(slots.contiguous()), n, hq,
+        k.shape[1], d, dtype_code(q.dtype), ptr(err_flags), stream_ptr(dev),
+    )
+    check(rc, "ir_rope_kv_scatter")
+    return q_out
+
+
 def paged_prefill(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -287,6 +338,7 @@ __all__ = [
     "paged_decode",
     "paged_attention_masked",
     "paged_prefill",
+    "rope_kv_scatter",
     "decode_workspace_bytes",
     "default_partition",
 ]

@@ -60,6 +60,49 @@ def paged_attention(
             f"paged_attention: q {tuple(q.shape)} inconsistent with k {tuple(k.shape)} and n_rep={n_rep}"
         )
     pool.write(layer_idx, k.reshape(-1, h_kv, d), v.reshape(-1, h_kv, d), paged.write_slots)
+    return _attend(q, paged, mask, layer_idx, scale)
+
+
+def rope_paged_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    paged,
+    mask: torch.Tensor | None,
+    layer_idx: int,
+    scale: float,
+    n_rep: int,
+) -> torch.Tensor:
+    """``apply_rotary_pos_emb`` + ``paged_attention`` with the rotation and the K/V
+    write fused into one kernel (``ir_rope_kv_scatter``).
+
+    Takes the pre-RoPE ``q``/``k`` of ``Attention.forward``
+    (``infrared/model/layers.py:158-164``) and the step's fp32 ``cos``/``sin``
+    ``[B, Sq, D]`` (``RotaryEmbedding`` output); the result is bit-identical to
+    rotating with the reference's ops and calling ``paged_attention``.
+    """
+    pool = paged.pool
+    h_kv, d = k.shape[-2], k.shape[-1]
+    b, sq, hq, dq = q.shape
+    if dq != d or hq != h_kv * n_rep:
+        raise RuntimeError(
+            f"rope_paged_attention: q {tuple(q.shape)} inconsistent with k {tuple(k.shape)} and n_rep={n_rep}"
+        )
+    q_rot = kernels.rope_kv_scatter(
+        q.reshape(b * sq, hq, d), k.reshape(b * sq, h_kv, d), v.reshape(b * sq, h_kv, d),
+        cos.reshape(b * sq, d), sin.reshape(b * sq, d), pool.k[layer_idx], pool.v[layer_idx],
+        paged.write_slots, err_flags=getattr(pool, "err_flags", None),
+    ).view(b, sq, hq, d)
+    return _attend(q_rot, paged, mask, layer_idx, scale)
+
+
+def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, scale: float) -> torch.Tensor:
+    """Attention over the pool (this step's K/V already written)."""
+    pool = paged.pool
+    b, sq, hq, d = q.shape
+    h_kv = pool.k.shape[-2]
     k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
     err = getattr(pool, "err_flags", None)
 

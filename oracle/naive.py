@@ -23,6 +23,8 @@ Restated functions and the reference lines they follow:
 - ``decode_reference`` (new) per-sequence decode over the block tables with no
   padding, in a chosen float dtype; equal to ``paged_attention_naive`` on
   the gather_slots/mask the engine builds (pinned in tests/test_oracle.py).
+- ``rotary_cos_sin``   infrared/model/layers.py:121-136 (RotaryEmbedding)
+- ``rotate_half`` / ``apply_rotary_pos_emb``  infrared/model/layers.py:72-89
 - ``prefill_reference`` (new) per-sequence causal attention of packed query
   chunks after a cached prefix, over the block tables; equal to
   ``paged_attention_naive`` on the prefill metadata of
@@ -65,6 +67,32 @@ def pool_gather(
     k = k_layer[flat].reshape(b, t, *k_layer.shape[1:])
     v = v_layer[flat].reshape(b, t, *v_layer.shape[1:])
     return k, v
+
+
+# --------------------------------------------------------------------- rotary embedding
+
+
+def rotary_cos_sin(positions: torch.Tensor, head_dim: int, theta: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 ``cos``/``sin`` ``[*positions.shape, head_dim]`` for absolute positions."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+    freqs = positions.to(torch.float32)[..., None] * inv_freq
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos(), emb.sin()
+
+
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    half = x.shape[-1] // 2
+    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+
+def apply_rotary_pos_emb(
+    q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``q``/``k`` ``[B, S, H, D]``, ``cos``/``sin`` ``[B, S, D]``; tables cast to the
+    activation dtype first, then ``x * cos + rotate_half(x) * sin`` in that dtype."""
+    cos = cos.unsqueeze(2).to(q.dtype)
+    sin = sin.unsqueeze(2).to(q.dtype)
+    return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
 
 
 # --------------------------------------------------------------------- math

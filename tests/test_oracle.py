@@ -223,6 +223,60 @@ def test_prefill_reference_closed_forms():
     assert np.abs(out[cu[1] : cu[2]].numpy() - ref).max() < 1e-5
 
 
+# ---------------------------------------------------------------- rotary embedding
+
+
+def test_rotary_tables_and_closed_form_rotation():
+    """RoPE is a rotation of each pair (x_i, x_{i+D/2}) by pos * theta^(-2i/D): checked
+    in fp64 against the fp32 restatement; position 0 is the identity (exactly)."""
+    d, theta = 64, 1_000_000.0
+    g = torch.Generator().manual_seed(21)
+    pos = torch.tensor([[0, 1, 7, 513, 4095]])
+    cos, sin = O.rotary_cos_sin(pos, d, theta)
+    x = torch.randn(1, 5, 3, d, generator=g)
+    q_rot, k_rot = O.apply_rotary_pos_emb(x, x.flip(2), cos, sin)
+    assert torch.equal(q_rot[0, 0], x[0, 0])  # cos 1, sin 0 at position 0
+    half = d // 2
+    inv = np.array([theta ** (-2.0 * i / d) for i in range(half)])
+    xn = x.double().numpy()
+    for si, p in enumerate(pos[0].tolist()):
+        ang = p * inv
+        c, s_ = np.cos(ang), np.sin(ang)
+        x1, x2 = xn[0, si, :, :half], xn[0, si, :, half:]
+        want = np.concatenate([x1 * c - x2 * s_, x2 * c + x1 * s_], axis=-1)
+        assert np.abs(q_rot[0, si].double().numpy() - want).max() < 2e-4 * max(1.0, p / 512)
+
+
+def test_rotary_relative_position_invariance():
+    """<rope(q, m), rope(k, n)> depends only on m - n."""
+    d, theta = 128, 10_000.0
+    g = torch.Generator().manual_seed(22)
+    q = torch.randn(1, 1, 1, d, generator=g).double()
+    k = torch.randn(1, 1, 1, d, generator=g).double()
+
+    def dot(m, n):
+        cm, sm = O.rotary_cos_sin(torch.tensor([[m]]), d, theta)
+        cn, sn = O.rotary_cos_sin(torch.tensor([[n]]), d, theta)
+        qm, _ = O.apply_rotary_pos_emb(q, q, cm.double(), sm.double())
+        kn, _ = O.apply_rotary_pos_emb(k, k, cn.double(), sn.double())
+        return float((qm * kn).sum())
+
+    assert abs(dot(10, 3) - dot(107, 100)) < 1e-3
+    assert abs(dot(10, 3) - dot(3, 10)) > 1e-3  # not symmetric in general
+
+
+def test_rotary_rejects_planted_sign_error(monkeypatch):
+    d = 32
+    pos = torch.tensor([[5]])
+    cos, sin = O.rotary_cos_sin(pos, d, 1e4)
+    x = torch.randn(1, 1, 1, d, generator=torch.Generator().manual_seed(23))
+    good, _ = O.apply_rotary_pos_emb(x, x, cos, sin)
+    with monkeypatch.context() as m:
+        m.setattr(O, "rotate_half", lambda t: torch.cat((t[..., d // 2 :], -t[..., : d // 2]), dim=-1))
+        bad, _ = O.apply_rotary_pos_emb(x, x, cos, sin)
+    assert (bad - good).abs().max() > 1e-2
+
+
 def test_naive_bf16_close_to_fp32():
     """The bf16 restatement (bf16 einsums, fp32 softmax) stays within 2e-2 of fp32."""
     q, k, v, bt, ctx, tables = _paged_decode_case(4, 2, 7, 128, 16, 64, 200, seed=3)
