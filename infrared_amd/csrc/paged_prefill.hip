@@ -22,8 +22,8 @@
 // 64-key tiles staged in LDS, double buffered: the next tile's global loads
 // are in flight (in registers) while the current one is in the math, and they
 // are written to the other LDS buffer afterwards.
-//   K tile : row-major [64 keys][D] (+16 bytes a row against bank conflicts);
-//   V tile : transposed [D][64 keys] (+8 bytes a row), written from pairs of
+//   K tile : row-major [64 keys][D] (+32 bytes a row against bank conflicts);
+//   V tile : transposed [D][64 keys] (+16 bytes a row), written from pairs of
 //            keys, so one d column of 4 consecutive keys is one 8-byte read.
 // Per tile a wavefront computes S^T = K . Q^T with 16x16x32 MFMA (rows = keys,
 // columns = its (token, head) pairs; Q^T stays in registers for the whole
@@ -76,8 +76,11 @@ struct PShape {
   static constexpr int COLS = NW * CT * 16;  // (token, head) columns per workgroup
   static constexpr int BN = 64;   // keys per tile
   static constexpr int NT = NW * 64;
-  static constexpr int KROW = D + 8;   // elements per K row in LDS
-  static constexpr int VROW = BN + 4;  // elements per V^T row in LDS
+  // LDS row pitches: gfx950 serves the 16-row MFMA operand reads without bank
+  // conflicts only with 32 extra bytes per K row and 16 per V^T row (8 and 16
+  // bytes still conflict two ways, measured with SQ_LDS_BANK_CONFLICT)
+  static constexpr int KROW = D + 16;  // elements per K row in LDS
+  static constexpr int VROW = BN + 8;  // elements per V^T row in LDS
   static constexpr int KCH = BN * D / 8;       // 16-byte K chunks per tile
   static constexpr int VPR = BN / 2 * D / 8;   // (key pair, 8 d) V chunks per tile
   static constexpr int KPT = (KCH + NT - 1) / NT;
