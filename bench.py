@@ -4,12 +4,20 @@ Workload (default): Qwen2.5-7B-shape paged decode — 64 sequences, 28 query /
 4 KV heads (GQA 7), head_dim 128, block 16, bf16, context U{512..4096}, block
 tables drawn from a random permutation of a pool 1.25x the blocks needed,
 q/K/V ~ N(0, 1) (synthetic: random values, no checkpoint). One step = one
-decode-attention call for the whole batch (one layer).
+decode-attention call for the whole batch (one layer). The default schedule is
+the planned one: ir_paged_decode_plan builds the balanced schedule of the
+batch's metadata once per decode step and every layer runs
+ir_paged_decode_planned on it, so the timed loop rebuilds a plan every
+``--layers`` (28) calls; ``--schedule fixed`` times ir_paged_decode's fixed
+split-KV partitions instead.
 
 Timing: W warm-up calls, then K calls captured in one hipGraph and replayed
 between two events on the launch stream, with torch.cuda.synchronize() on
 both sides. Calls rotate over R disjoint copies of the pool + block tables so
 consecutive calls do not hit K/V left in the 256 MB MALL by the previous one.
+``value`` is per call with the plan builds included; the roofline's
+``achieved`` is the attention kernel's own launches (a graph of K runs
+without plan builds).
 
 Other workloads (``--workload``): ``prefill`` -- 8 sequences x 512-token
 chunks after cached prefixes of up to 8192 tokens (pairs sharing prefix
@@ -52,6 +60,10 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--config", default=None, help="decode: qwen7b-bf16 (default) | qwen0.5b-fp32 | qwen7b-skewed")
     p.add_argument("--rotations", type=int, default=3)
     p.add_argument("--partition", type=int, default=0, help="split-KV partition tokens (0 = library default)")
+    p.add_argument("--schedule", choices=("planned", "fixed"), default="planned",
+                   help="decode: balanced plan + run (default) or fixed split-KV partitions")
+    p.add_argument("--layers", type=int, default=28,
+                   help="decode: calls per plan (layers of one decode step sharing its metadata)")
     p.add_argument("--cpu-iters", type=int, default=3, help="timed CPU-baseline iterations (0 = skip)")
     p.add_argument("--cpu-seqs", type=int, default=0, help="sequences in the CPU sample (0 = all)")
     p.add_argument("--check", action="store_true", help="also check the output against the oracle")
@@ -63,59 +75,98 @@ def _parse() -> argparse.Namespace:
     return p.parse_args()
 
 
+def _graph_ms(fn, steps: int) -> float:
+    """ms per call of ``steps`` calls of fn captured in one hipGraph, replayed
+    between events on the launch stream (after one warm replay)."""
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fn(0)
+    torch.cuda.current_stream().wait_stream(stream)
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    graph.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def _eager_ms(fn, steps: int) -> float:
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(steps):
+        fn(i)
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
 def _gpu_decode(case, args):
+    """Times the decode calls. Returns (info, eager_ms, call_ms, kernel_ms, outs):
+    call_ms per decode call (planned: one plan build every ``--layers`` calls,
+    as one decode step's layers share it), kernel_ms per launch of the dominant
+    (attention) kernel alone."""
     from infrared_amd import kernels
 
     cfg = case.config
     dev = case.q.device
     b, max_blocks = cfg.num_seqs, case.block_tables[0].shape[1]
-    part = args.partition or kernels.default_partition(b, cfg.num_kv_heads, max_blocks, cfg.block_size)
-    ws_bytes = kernels.decode_workspace_bytes(
-        b, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, max_blocks, cfg.block_size, part
-    )
-    ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    hq, hkv, bs = cfg.num_q_heads, cfg.num_kv_heads, cfg.block_size
+    rot = len(case.block_tables)
     outs = [torch.empty_like(case.q) for _ in case.block_tables]
+    planned = args.schedule == "planned" and kernels.decode_plan_bytes(b, hq, hkv, max_blocks, bs) > 0
+    info = {"schedule": "planned" if planned else "fixed"}
+    if planned:
+        plans = [kernels.decode_plan(bt, case.context_lens, hq, case.k_cache, bs) for bt in case.block_tables]
+        ws_bytes = kernels.planned_workspace_bytes(b, hq, hkv, cfg.head_dim)
+        ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
 
-    def call(i: int) -> None:
-        r = i % len(case.block_tables)
-        kernels.paged_decode(
-            case.q, case.k_cache, case.v_cache, case.block_tables[r], case.context_lens,
-            cfg.block_size, cfg.scale, out=outs[r], partition_tokens=part, workspace=ws,
-        )
+        def run(i: int) -> None:
+            r = i % rot
+            kernels.paged_decode_planned(case.q, case.k_cache, case.v_cache, plans[r], cfg.scale, out=outs[r],
+                                         workspace=ws)
+
+        def plan(i: int) -> None:
+            p = i % rot
+            kernels.decode_plan(case.block_tables[p], case.context_lens, hq, case.k_cache, bs, buf=plans[p].buf)
+
+        def call(i: int) -> None:
+            if i % args.layers == 0:
+                plan(i // args.layers)
+            run(i)
+
+        info.update({"layers_per_plan": args.layers, "plan_bytes": int(plans[0].buf.numel()),
+                     "workspace_bytes": ws_bytes})
+    else:
+        part = args.partition or kernels.default_partition(b, hkv, max_blocks, bs)
+        ws_bytes = kernels.decode_workspace_bytes(b, hq, hkv, cfg.head_dim, max_blocks, bs, part)
+        ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+
+        def call(i: int) -> None:
+            r = i % rot
+            kernels.paged_decode(case.q, case.k_cache, case.v_cache, case.block_tables[r], case.context_lens,
+                                 bs, cfg.scale, out=outs[r], partition_tokens=part, workspace=ws)
+
+        run = call
+        info.update({"partition_tokens": part, "workspace_bytes": ws_bytes})
 
     for i in range(args.warmup):
         call(i)
     torch.cuda.synchronize()
-
-    # eager (host-launched) timing, for reference
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for i in range(args.steps):
-        call(i)
-    e.record()
-    torch.cuda.synchronize()
-    eager_ms = s.elapsed_time(e) / args.steps
-
+    eager_ms = _eager_ms(call, args.steps)
     if args.mode == "eager":
-        return part, ws_bytes, eager_ms, eager_ms, outs
-    # graph-replayed timing: the K calls back to back on the device
-    graph = torch.cuda.CUDAGraph()
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        call(0)
-    torch.cuda.current_stream().wait_stream(stream)
-    with torch.cuda.graph(graph):
-        for i in range(args.steps):
-            call(i)
-    graph.replay()  # warm replay
-    torch.cuda.synchronize()
-    s.record()
-    graph.replay()
-    e.record()
-    torch.cuda.synchronize()
-    graph_ms = s.elapsed_time(e) / args.steps
-    return part, ws_bytes, eager_ms, graph_ms, outs
+        return info, eager_ms, eager_ms, eager_ms, outs
+    call_ms = _graph_ms(call, args.steps)
+    kernel_ms = _graph_ms(run, args.steps) if planned else call_ms
+    if planned:
+        info["plan_us"] = round(_graph_ms(plan, max(args.steps // 4, 8)) * 1e3, 2)
+    return info, eager_ms, call_ms, kernel_ms, outs
 
 
 def _cpu_baseline(case, args):
@@ -394,9 +445,10 @@ def main() -> int:
     case = make_decode_case(args.config, "cuda", rotations=args.rotations)
     cfg = case.config
     kv = case.kv_bytes
-    part, ws_bytes, eager_ms, graph_ms, outs = _gpu_decode(case, args)
+    info, eager_ms, graph_ms, kernel_ms, outs = _gpu_decode(case, args)
     us = graph_ms * 1e3
     gbps = kv / (graph_ms * 1e-3) / 1e9
+    kgbps = kv / (kernel_ms * 1e-3) / 1e9
     check = None
     if args.check:
         from oracle import naive as O
@@ -409,7 +461,7 @@ def main() -> int:
     if args.copy_calib_mib > 0:
         _copy_calibration(args.copy_calib_mib)
     cpu = _cpu_baseline(case, args) if args.cpu_iters > 0 else None
-    traffic, traffic_src = _traffic(f"decode_{args.config}")
+    traffic, traffic_src = _traffic(f"decode_{'planned_' if info['schedule'] == 'planned' else ''}{args.config}")
     esize = torch.tensor([], dtype=cfg.dtype).element_size()
     line = {
         "metric": METRIC,
@@ -434,19 +486,20 @@ def main() -> int:
             "sum_ctx": int(case.context_lens.long().sum()),
             "kv_bytes_per_call": kv,
             "rotations": args.rotations,
-            "partition_tokens": part,
-            "workspace_bytes": ws_bytes,
+            **info,
             "bytes_per_token": 2 * cfg.num_kv_heads * cfg.head_dim * esize,
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(gbps, 2),
+            "achieved": round(kgbps, 2),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
-            "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "frac": round(kgbps / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
             "traffic_source": traffic_src,
-            "timed": f"decode call, {args.mode} launches, events on the launch stream",
+            "kernel_us": round(kernel_ms * 1e3, 2),
+            "timed": (f"{'paged_decode_planned_kernel' if info['schedule'] == 'planned' else 'paged_decode_kernel'}"
+                      f" launches alone, {args.mode}, events on the launch stream"),
         },
         "cpu_baseline": cpu,
     }

@@ -159,6 +159,55 @@ int ir_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
                     int32_t* err_flags, ir_stream_t stream);
 
 /*
+ * Planned decode: the same attention as ir_paged_decode (one query token per
+ * sequence over block_tables / context_lens), on a work-balanced schedule that
+ * ir_paged_decode_plan builds once per batch of decode metadata and every
+ * layer's ir_paged_decode_planned reuses. Replaces the same reference seam as
+ * ir_paged_decode (infrared/model/triton_attention.py:110-129 via
+ * PagedKVPool/PagedContext, infrared/cache/paged_kv_cache.py:25-72); the
+ * plan/run split has no counterpart in the reference, whose metadata is also
+ * built once per step (infrared/engine/paged_engine.py:290-332) and shared by
+ * every layer.
+ *
+ * The call's 16-key tiles (per sequence, per KV head and group of <= 16 query
+ * heads) are cut into one equal slice per CU, so every CU reads the same
+ * number of keys whatever the spread of context lengths; sequences cut by a
+ * slice boundary are merged in the same launch (log-sum-exp of fp32
+ * partials, the last-arriving slice merges).
+ *
+ * ir_paged_decode_plan_bytes: bytes of plan for this shape, 0 when the shape
+ *   is not plannable (batch 1..1024, block_size a multiple of 16).
+ * ir_paged_decode_planned_workspace_bytes: bytes of workspace the run needs
+ *   (arrival counters + partials); zero-filled before first use, the run
+ *   leaves the counters at zero.
+ * ir_paged_decode_plan: writes the plan for (block_tables, context_lens) and a
+ *   pool with the given slot/head strides (elements) and dtype. Context
+ *   lengths outside [0, max_blocks * block_size] are clamped and flagged
+ *   (IR_ERR_CONTEXT_RANGE); block ids outside [0, num_blocks) are flagged
+ *   (IR_ERR_BLOCK_RANGE) and their keys masked, as in ir_paged_decode.
+ * ir_paged_decode_planned: runs one layer over the plan. Shapes and cache
+ *   strides must be those the plan was built for; q/out as in ir_paged_decode.
+ *   Calls sharing a workspace must be stream-ordered; a plan may be rebuilt
+ *   only after the runs that read it.
+ */
+int64_t ir_paged_decode_plan_bytes(int num_seqs, int num_q_heads, int num_kv_heads,
+                                   int max_blocks_per_seq, int block_size);
+int64_t ir_paged_decode_planned_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads,
+                                                int head_dim);
+int ir_paged_decode_plan(const int32_t* block_tables, int64_t bt_stride, int max_blocks_per_seq,
+                         const int32_t* context_lens, int num_seqs, int num_q_heads,
+                         int num_kv_heads, int block_size, int64_t num_blocks,
+                         int64_t cache_slot_stride, int64_t cache_head_stride, int dtype,
+                         void* plan, int64_t plan_bytes, int32_t* err_flags, ir_stream_t stream);
+int ir_paged_decode_planned(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
+                            const void* k_cache, const void* v_cache, int64_t cache_slot_stride,
+                            void* out, int64_t out_seq_stride, int64_t out_head_stride,
+                            int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                            int max_blocks_per_seq, int block_size, float scale, int dtype,
+                            const void* plan, void* workspace, int64_t workspace_bytes,
+                            int32_t* err_flags, ir_stream_t stream);
+
+/*
  * Paged attention over the reference's own per-forward metadata: per-key flat
  * slot ids plus an additive mask. This is the exact contract of
  * _paged_attention_triton / _paged_attention_naive

@@ -325,6 +325,7 @@ extern "C" int ir_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_he
   a.n_hg = (a.n_rep + 15) / 16;
   a.scale_log2 = scale * kLog2e;
   a.part_tokens = partition_tokens;
+  a.n_ups = num_kv_heads * a.n_hg;
   a.counters = nullptr;
   a.ws_o = nullptr;
   a.ws_ml = nullptr;

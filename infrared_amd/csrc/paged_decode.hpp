@@ -50,6 +50,7 @@ struct DecodeArgs {
   int num_seqs, num_q_heads, num_kv_heads, n_rep, n_hg;
   float scale_log2;
   int part_tokens, max_parts;
+  int n_ups;          // units per sequence: num_kv_heads * n_hg (planned schedule)
   int32_t* counters;  // [seq][kv_head][head group], zero at rest
   float* ws_o;        // [seq][q_head][part][D]
   float* ws_ml;       // [seq][q_head][part][2]

@@ -8,6 +8,8 @@ capture.
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import torch
 
 from infrared_amd._lib import check, dtype_code, lib, ptr, require_device, stream_ptr
@@ -184,6 +186,112 @@ def paged_decode(
         ptr(workspace) if need > 0 else None, need, ptr(err_flags), stream_ptr(dev),
     )
     check(rc, "ir_paged_decode")
+    return out
+
+
+@dataclass(frozen=True)
+class DecodePlan:
+    """A decode plan (``ir_paged_decode_plan``) and the shape it was built for.
+
+    ``buf`` holds the schedule of one batch of decode metadata; every layer of
+    the step runs on it with :func:`paged_decode_planned`. Rebuild it (same or
+    new buffer) when ``block_tables``/``context_lens`` change, after the runs
+    that read it.
+    """
+
+    buf: torch.Tensor
+    num_seqs: int
+    num_q_heads: int
+    num_kv_heads: int
+    max_blocks: int
+    block_size: int
+    num_blocks: int
+    slot_stride: int
+    head_stride: int
+    dtype: torch.dtype
+
+
+def decode_plan_bytes(num_seqs: int, num_q_heads: int, num_kv_heads: int, max_blocks: int, block_size: int) -> int:
+    """Plan bytes for this shape; 0 when it is not plannable (then use :func:`paged_decode`)."""
+    return int(lib().ir_paged_decode_plan_bytes(num_seqs, num_q_heads, num_kv_heads, max_blocks, block_size))
+
+
+def planned_workspace_bytes(num_seqs: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
+    return int(lib().ir_paged_decode_planned_workspace_bytes(num_seqs, num_q_heads, num_kv_heads, head_dim))
+
+
+def decode_plan(
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    num_q_heads: int,
+    k_cache: torch.Tensor,
+    block_size: int,
+    buf: torch.Tensor | None = None,
+    err_flags: torch.Tensor | None = None,
+) -> DecodePlan:
+    """Builds the balanced decode schedule of ``(block_tables, context_lens)``
+    for query heads ``num_q_heads`` over pool layers shaped like ``k_cache``
+    ``[num_slots, H_kv, D]`` (any layer: all share the strides)."""
+    dev = require_device(block_tables, context_lens, k_cache)
+    _cache_layer("decode_plan", k_cache)
+    _check_tables("decode_plan", block_tables, context_lens)
+    b, max_blocks = block_tables.shape
+    h_kv = k_cache.shape[1]
+    need = decode_plan_bytes(b, num_q_heads, h_kv, max_blocks, block_size)
+    if need <= 0:
+        raise RuntimeError(f"decode_plan: shape not plannable (batch {b}, block_size {block_size})")
+    if buf is None or buf.numel() < need:
+        buf = torch.empty(need, dtype=torch.uint8, device=dev)
+    if buf.dtype != torch.uint8 or buf.data_ptr() % 256:
+        raise RuntimeError("decode_plan: buf must be a 256-byte aligned uint8 tensor")
+    rc = lib().ir_paged_decode_plan(
+        ptr(block_tables), block_tables.stride(0), max_blocks, ptr(context_lens), b, num_q_heads, h_kv,
+        block_size, k_cache.shape[0] // block_size, k_cache.stride(0), k_cache.stride(1),
+        dtype_code(k_cache.dtype), ptr(buf), buf.numel(), ptr(err_flags), stream_ptr(dev),
+    )
+    check(rc, "ir_paged_decode_plan")
+    return DecodePlan(buf, b, num_q_heads, h_kv, max_blocks, block_size, k_cache.shape[0] // block_size,
+                      k_cache.stride(0), k_cache.stride(1), k_cache.dtype)
+
+
+def paged_decode_planned(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    plan: DecodePlan,
+    scale: float,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+    err_flags: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """:func:`paged_decode` over a plan: ``q`` ``[B, H_q, D]`` -> ``[B, H_q, D]``."""
+    dev = require_device(q, k_cache, v_cache, plan.buf)
+    _cache_layer("paged_decode_planned", k_cache)
+    if q.dim() != 3:
+        raise RuntimeError(f"paged_decode_planned: q must be [B, H_q, D], got {tuple(q.shape)}")
+    b, hq, d = q.shape
+    if (b, hq) != (plan.num_seqs, plan.num_q_heads) or k_cache.shape[1] != plan.num_kv_heads:
+        raise RuntimeError("paged_decode_planned: q / pool heads differ from the plan's")
+    if (k_cache.shape[0] // plan.block_size != plan.num_blocks or k_cache.stride(0) != plan.slot_stride
+            or k_cache.stride(1) != plan.head_stride or k_cache.dtype != plan.dtype):
+        raise RuntimeError("paged_decode_planned: pool layout differs from the plan's")
+    if v_cache.shape != k_cache.shape or v_cache.stride() != k_cache.stride():
+        raise RuntimeError("paged_decode_planned: v_cache must match k_cache's shape and strides")
+    if d != k_cache.shape[2] or q.dtype != k_cache.dtype:
+        raise RuntimeError("paged_decode_planned: q / pool shape or dtype mismatch")
+    _last_dim_contiguous("paged_decode_planned q", q)
+    if out is None:
+        out = torch.empty(b, hq, d, dtype=q.dtype, device=dev)
+    need = planned_workspace_bytes(b, hq, plan.num_kv_heads, d)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.zeros(need, dtype=torch.uint8, device=dev)
+    rc = lib().ir_paged_decode_planned(
+        ptr(q), q.stride(0), q.stride(1), ptr(k_cache), ptr(v_cache), k_cache.stride(0), ptr(out),
+        out.stride(0), out.stride(1), b, hq, plan.num_kv_heads, d, plan.max_blocks, plan.block_size,
+        float(scale), dtype_code(q.dtype), ptr(plan.buf), ptr(workspace), workspace.numel(), ptr(err_flags),
+        stream_ptr(dev),
+    )
+    check(rc, "ir_paged_decode_planned")
     return out
 
 

@@ -123,16 +123,30 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
             pool.block_size, scale, err_flags=err,
         ).view(b, sq, hq, d)
     elif paged.use_triton and block_tables is not None and context_lens is not None and sq == 1:
-        ws = None
-        if hasattr(pool, "workspace"):
-            need = kernels.decode_workspace_bytes(
-                b, hq, h_kv, d, block_tables.shape[1], pool.block_size
+        max_blocks = block_tables.shape[1]
+        plan_bytes = kernels.decode_plan_bytes(b, hq, h_kv, max_blocks, pool.block_size)
+        if plan_bytes > 0 and hasattr(pool, "plan_buffer"):
+            # balanced schedule: built by the step's first layer, reused by the rest
+            plan = paged.decode_plan
+            if plan is None:
+                plan = kernels.decode_plan(
+                    block_tables, context_lens, hq, k_layer, pool.block_size,
+                    buf=pool.plan_buffer(plan_bytes), err_flags=err,
+                )
+                paged.decode_plan = plan
+            ws = pool.workspace(kernels.planned_workspace_bytes(b, hq, h_kv, d))
+            out = kernels.paged_decode_planned(
+                q.reshape(b, hq, d), k_layer, v_layer, plan, scale, workspace=ws, err_flags=err
             )
-            ws = pool.workspace(need) if need > 0 else None
-        out = kernels.paged_decode(
-            q.reshape(b, hq, d), k_layer, v_layer, block_tables, context_lens,
-            pool.block_size, scale, workspace=ws, err_flags=err,
-        )
+        else:
+            ws = None
+            if hasattr(pool, "workspace"):
+                need = kernels.decode_workspace_bytes(b, hq, h_kv, d, max_blocks, pool.block_size)
+                ws = pool.workspace(need) if need > 0 else None
+            out = kernels.paged_decode(
+                q.reshape(b, hq, d), k_layer, v_layer, block_tables, context_lens,
+                pool.block_size, scale, workspace=ws, err_flags=err,
+            )
         out = out.view(b, 1, hq, d)
     else:
         if paged.gather_slots is None or mask is None:

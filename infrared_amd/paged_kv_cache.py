@@ -100,6 +100,7 @@ class PagedKVPool:
             raise ValueError(f"unknown pool layout {layout!r} (head_major, slot_major)")
         self.err_flags = torch.zeros(1, dtype=torch.int32, device=device)
         self._workspace: torch.Tensor | None = None
+        self._plan_buf: torch.Tensor | None = None
 
     # --- reference surface ------------------------------------------------
 
@@ -154,6 +155,14 @@ class PagedKVPool:
             self._workspace = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
         return self._workspace
 
+    def plan_buffer(self, nbytes: int) -> torch.Tensor:
+        """A cached device buffer of at least ``nbytes`` for the decode plan of
+        the current step (rebuilt by each step's first decode layer; steps are
+        stream-ordered). Grown outside hipGraph capture, like the workspace."""
+        if self._plan_buf is None or self._plan_buf.numel() < nbytes:
+            self._plan_buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+        return self._plan_buf
+
     def check_errors(self) -> None:
         """Synchronises, raises ``IndexError`` for any flagged range error, then clears the flags."""
         flags = int(self.err_flags.item())
@@ -181,6 +190,9 @@ class PagedContext:
     packed query tokens ``cu_seqlens_q`` ``[B + 1]`` int32 (sequence ``b`` owns
     packed rows ``cu[b]:cu[b+1]``), ``q_start`` ``[B]`` int32 (its cached
     prefix length) and ``max_q_len`` (host bound on the chunk sizes).
+    ``decode_plan`` caches the balanced decode schedule of ``block_tables`` /
+    ``context_lens``: the step's first decode layer builds it, the others reuse
+    it (a context is one step's metadata, shared by every layer).
     """
 
     pool: PagedKVPool
@@ -192,3 +204,4 @@ class PagedContext:
     cu_seqlens_q: torch.Tensor | None = None
     q_start: torch.Tensor | None = None
     max_q_len: int = 0
+    decode_plan: object | None = None
