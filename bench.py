@@ -4,12 +4,13 @@ Workload (default): Qwen2.5-7B-shape paged decode — 64 sequences, 28 query /
 4 KV heads (GQA 7), head_dim 128, block 16, bf16, context U{512..4096}, block
 tables drawn from a random permutation of a pool 1.25x the blocks needed,
 q/K/V ~ N(0, 1) (synthetic: random values, no checkpoint). One step = one
-decode-attention call for the whole batch (one layer). The default schedule is
-the planned one: ir_paged_decode_plan builds the balanced schedule of the
+decode-attention call for the whole batch (one layer). The schedule is the
+seam's: for a batch with at least one (sequence, KV head) unit per CU (C2) the
+planned one -- ir_paged_decode_plan builds the balanced schedule of the
 batch's metadata once per decode step and every layer runs
 ir_paged_decode_planned on it, so the timed loop rebuilds a plan every
-``--layers`` (28) calls; ``--schedule fixed`` times ir_paged_decode's fixed
-split-KV partitions instead.
+``--layers`` (28) calls -- otherwise ir_paged_decode's fixed split-KV
+partitions (``--schedule`` forces either).
 
 Timing: W warm-up calls, then K calls captured in one hipGraph and replayed
 between two events on the launch stream, with torch.cuda.synchronize() on
@@ -60,8 +61,9 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--config", default=None, help="decode: qwen7b-bf16 (default) | qwen0.5b-fp32 | qwen7b-skewed")
     p.add_argument("--rotations", type=int, default=3)
     p.add_argument("--partition", type=int, default=0, help="split-KV partition tokens (0 = library default)")
-    p.add_argument("--schedule", choices=("planned", "fixed"), default="planned",
-                   help="decode: balanced plan + run (default) or fixed split-KV partitions")
+    p.add_argument("--schedule", choices=("auto", "planned", "fixed"), default="auto",
+                   help="decode: the seam's choice (default: planned when the batch has a unit per CU), "
+                   "balanced plan + run, or fixed split-KV partitions")
     p.add_argument("--layers", type=int, default=28,
                    help="decode: calls per plan (layers of one decode step sharing its metadata)")
     p.add_argument("--cpu-iters", type=int, default=3, help="timed CPU-baseline iterations (0 = skip)")
@@ -120,17 +122,21 @@ def _gpu_decode(case, args):
     hq, hkv, bs = cfg.num_q_heads, cfg.num_kv_heads, cfg.block_size
     rot = len(case.block_tables)
     outs = [torch.empty_like(case.q) for _ in case.block_tables]
-    planned = args.schedule == "planned" and kernels.decode_plan_bytes(b, hq, hkv, max_blocks, bs) > 0
+    if args.schedule == "auto":
+        planned = kernels.decode_plan_pays(b, hq, hkv, max_blocks, bs, dev)
+    else:
+        planned = args.schedule == "planned" and kernels.decode_plan_bytes(b, hq, hkv, max_blocks, bs) > 0
     info = {"schedule": "planned" if planned else "fixed"}
     if planned:
         plans = [kernels.decode_plan(bt, case.context_lens, hq, case.k_cache, bs) for bt in case.block_tables]
         ws_bytes = kernels.planned_workspace_bytes(b, hq, hkv, cfg.head_dim)
-        ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        ctr = torch.zeros(kernels.decode_num_counters(b, hq, hkv), dtype=torch.int32, device=dev)
 
         def run(i: int) -> None:
             r = i % rot
             kernels.paged_decode_planned(case.q, case.k_cache, case.v_cache, plans[r], cfg.scale, out=outs[r],
-                                         workspace=ws)
+                                         workspace=ws, counters=ctr)
 
         def plan(i: int) -> None:
             p = i % rot
@@ -146,12 +152,13 @@ def _gpu_decode(case, args):
     else:
         part = args.partition or kernels.default_partition(b, hkv, max_blocks, bs)
         ws_bytes = kernels.decode_workspace_bytes(b, hq, hkv, cfg.head_dim, max_blocks, bs, part)
-        ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+        ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+        ctr = torch.zeros(kernels.decode_num_counters(b, hq, hkv), dtype=torch.int32, device=dev)
 
         def call(i: int) -> None:
             r = i % rot
             kernels.paged_decode(case.q, case.k_cache, case.v_cache, case.block_tables[r], case.context_lens,
-                                 bs, cfg.scale, out=outs[r], partition_tokens=part, workspace=ws)
+                                 bs, cfg.scale, out=outs[r], partition_tokens=part, workspace=ws, counters=ctr)
 
         run = call
         info.update({"partition_tokens": part, "workspace_bytes": ws_bytes})

@@ -112,16 +112,24 @@ int ir_paged_gather(const void* k_cache, const void* v_cache, int64_t cache_slot
 
 /*
  * Bytes of device workspace ir_paged_decode needs for this shape (0 when one
- * partition covers the longest context). The workspace holds the split-KV
- * arrival counters (one int32 per sequence x KV head x group of 16 query
- * heads) and the partials: unnormalised accumulators [num_seqs, num_q_heads,
- * parts, head_dim] and running max / sum [num_seqs, num_q_heads, parts, 2], fp32.
- * The caller zero-fills it once before first use; every call leaves the
- * counters at zero again. Calls sharing a workspace must be stream-ordered.
+ * partition covers the longest context): the split-KV partials, unnormalised
+ * accumulators [num_seqs, num_q_heads, parts, head_dim] and running max / sum
+ * [num_seqs, num_q_heads, parts, 2], fp32. Scratch: no initial contents.
+ * Calls sharing a workspace must be stream-ordered.
  */
 int64_t ir_paged_decode_workspace_size(int num_seqs, int num_q_heads, int num_kv_heads,
                                        int head_dim, int max_blocks_per_seq, int block_size,
                                        int partition_tokens);
+
+/*
+ * Arrival counters the split decode needs: one int32 per sequence x KV head x
+ * group of <= 16 query heads. The caller zero-fills the counters buffer once;
+ * every call (ir_paged_decode, ir_paged_decode_planned) leaves the counters it
+ * used at zero, so one counters buffer serves calls of any shape. Kept apart
+ * from the workspace because partial rows are scratch whose layout changes
+ * with the shape.
+ */
+int64_t ir_paged_decode_num_counters(int num_seqs, int num_q_heads, int num_kv_heads);
 
 /* The partition size (tokens) ir_paged_decode picks when partition_tokens == 0. */
 int ir_paged_decode_default_partition(int num_seqs, int num_kv_heads, int max_blocks_per_seq,
@@ -141,11 +149,11 @@ int ir_paged_decode_default_partition(int num_seqs, int num_kv_heads, int max_bl
  *   context_lens: [num_seqs] int32 (0 gives a zero output row).
  *   partition_tokens: split-KV partition length in tokens (multiple of 16,
  *                 at most 4096; 0 = ir_paged_decode_default_partition). A sequence longer
- *                 than one partition is split across workgroups whose partials
- *                 the last-arriving workgroup merges (log-sum-exp), all in one
- *                 launch.
- *   workspace:    >= ir_paged_decode_workspace_size(...) bytes, 256-byte
- *                 aligned, zero-filled before its first use.
+ *                 than one partition is split across workgroups whose partials a
+ *                 second launch merges with log-sum-exp weights.
+ *   counters:     >= ir_paged_decode_num_counters(...) int32, zero-filled before
+ *                 first use (required when a sequence can span partitions).
+ *   workspace:    >= ir_paged_decode_workspace_size(...) bytes, 256-byte aligned.
  * head_dim in {64, 128}; num_q_heads % num_kv_heads == 0; dtype f32/f16/bf16.
  */
 int ir_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
@@ -155,8 +163,9 @@ int ir_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
                     const int32_t* context_lens, void* out, int64_t out_seq_stride,
                     int64_t out_head_stride, int num_seqs, int num_q_heads,
                     int num_kv_heads, int head_dim, float scale, int dtype,
-                    int partition_tokens, void* workspace, int64_t workspace_bytes,
-                    int32_t* err_flags, ir_stream_t stream);
+                    int partition_tokens, int32_t* counters, int64_t num_counters,
+                    void* workspace, int64_t workspace_bytes, int32_t* err_flags,
+                    ir_stream_t stream);
 
 /*
  * Planned decode: the same attention as ir_paged_decode (one query token per
@@ -177,9 +186,10 @@ int ir_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
  *
  * ir_paged_decode_plan_bytes: bytes of plan for this shape, 0 when the shape
  *   is not plannable (batch 1..1024, block_size a multiple of 16).
- * ir_paged_decode_planned_workspace_bytes: bytes of workspace the run needs
- *   (arrival counters + partials); zero-filled before first use, the run
- *   leaves the counters at zero.
+ * ir_paged_decode_planned_workspace_bytes: bytes of workspace (fp32 partial
+ *   rows, scratch) the run needs; its arrival counters are
+ *   ir_paged_decode_num_counters(...) int32 of a zero-filled counters buffer,
+ *   which the run leaves at zero.
  * ir_paged_decode_plan: writes the plan for (block_tables, context_lens) and a
  *   pool with the given slot/head strides (elements) and dtype. Context
  *   lengths outside [0, max_blocks * block_size] are clamped and flagged
@@ -204,8 +214,9 @@ int ir_paged_decode_planned(const void* q, int64_t q_seq_stride, int64_t q_head_
                             void* out, int64_t out_seq_stride, int64_t out_head_stride,
                             int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                             int max_blocks_per_seq, int block_size, float scale, int dtype,
-                            const void* plan, void* workspace, int64_t workspace_bytes,
-                            int32_t* err_flags, ir_stream_t stream);
+                            const void* plan, int32_t* counters, int64_t num_counters,
+                            void* workspace, int64_t workspace_bytes, int32_t* err_flags,
+                            ir_stream_t stream);
 
 /*
  * Paged attention over the reference's own per-forward metadata: per-key flat

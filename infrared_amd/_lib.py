@@ -50,11 +50,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32],
     ),
     "ir_paged_decode_default_partition": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32]),
+    "ir_paged_decode_num_counters": (_c_i64, [_c_i32, _c_i32, _c_i32]),
     "ir_paged_decode": (
         _c_i32,
         [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i64, _c_i32,
          _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_f32, _c_i32, _c_i32,
-         _c_p, _c_i64, _c_p, _c_p],
+         _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p],
     ),
     "ir_paged_decode_plan_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "ir_paged_decode_planned_workspace_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32]),
@@ -66,7 +67,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ir_paged_decode_planned": (
         _c_i32,
         [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32,
-         _c_i32, _c_i32, _c_i32, _c_f32, _c_i32, _c_p, _c_p, _c_i64, _c_p, _c_p],
+         _c_i32, _c_i32, _c_i32, _c_f32, _c_i32, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p],
     ),
     "ir_paged_attention_masked": (
         _c_i32,

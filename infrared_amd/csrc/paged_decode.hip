@@ -6,8 +6,8 @@
 // LDS. A sequence that fits one partition writes its output directly. Longer
 // ones write fp32 partials that a second launch merges with log-sum-exp
 // weights (or, with IR_DECODE_MERGE=fused, the last workgroup of the unit to
-// finish -- found with an arrival counter in the workspace -- merges them and
-// resets the counter).
+// finish -- found with an arrival counter -- merges them and resets the
+// counter).
 #include <stdlib.h>
 #include <string.h>
 
@@ -162,18 +162,18 @@ int max_parts_for(int max_blocks, int bs, int part_tokens) {
 
 int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
-// Workspace layout: [counters: units int32][partial acc: rows x D fp32][max,sum: rows x 2 fp32],
-// each region 256-byte aligned.
+// Workspace layout: [partial acc: rows x D fp32][max,sum: rows x 2 fp32], each
+// region 256-byte aligned. The arrival counters live in their own buffer:
+// every call leaves them at zero, so one counters buffer may serve calls of
+// any shape, while partial rows are scratch that differs from call to call.
 struct WsLayout {
-  int64_t counters_bytes, acc_bytes, ml_bytes;
-  int64_t total() const { return counters_bytes + acc_bytes + ml_bytes; }
+  int64_t acc_bytes, ml_bytes;
+  int64_t total() const { return acc_bytes + ml_bytes; }
 };
 
-WsLayout ws_layout(int num_seqs, int num_q_heads, int num_kv_heads, int head_dim, int max_parts) {
-  const int n_hg = (num_q_heads / num_kv_heads + 15) / 16;
-  const int64_t units = (int64_t)num_seqs * num_kv_heads * n_hg;
+WsLayout ws_layout(int num_seqs, int num_q_heads, int head_dim, int max_parts) {
   const int64_t rows = (int64_t)num_seqs * num_q_heads * max_parts;
-  return WsLayout{align256(units * 4), align256(rows * head_dim * 4), align256(rows * 2 * 4)};
+  return WsLayout{align256(rows * head_dim * 4), align256(rows * 2 * 4)};
 }
 
 // Launch shape knobs, read once from the environment for tuning runs:
@@ -261,7 +261,12 @@ extern "C" int64_t ir_paged_decode_workspace_size(int num_seqs, int num_q_heads,
   if (num_q_heads % num_kv_heads) return 0;
   const int mp = max_parts_for(max_blocks_per_seq, block_size, partition_tokens);
   if (mp <= 1) return 0;
-  return ws_layout(num_seqs, num_q_heads, num_kv_heads, head_dim, mp).total();
+  return ws_layout(num_seqs, num_q_heads, head_dim, mp).total();
+}
+
+extern "C" int64_t ir_paged_decode_num_counters(int num_seqs, int num_q_heads, int num_kv_heads) {
+  if (num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return 0;
+  return (int64_t)num_seqs * num_kv_heads * ((num_q_heads / num_kv_heads + 15) / 16);
 }
 
 extern "C" int ir_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
@@ -271,8 +276,8 @@ extern "C" int ir_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_he
                                const int32_t* context_lens, void* out, int64_t out_seq_stride,
                                int64_t out_head_stride, int num_seqs, int num_q_heads, int num_kv_heads,
                                int head_dim, float scale, int dtype, int partition_tokens,
-                               void* workspace, int64_t workspace_bytes, int32_t* err_flags,
-                               ir_stream_t stream) {
+                               int32_t* counters, int64_t num_counters, void* workspace,
+                               int64_t workspace_bytes, int32_t* err_flags, ir_stream_t stream) {
   const int eb = dtype_bytes(dtype);
   IR_REQUIRE(eb > 0, "ir_paged_decode: unknown dtype %d", dtype);
   IR_REQUIRE(num_seqs >= 0 && num_q_heads > 0 && num_kv_heads > 0 && block_size > 0 &&
@@ -338,10 +343,14 @@ extern "C" int ir_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_he
     if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u))
       return fail(IR_EWORKSPACE, "ir_paged_decode: workspace of %lld bytes (256-byte aligned) required, got %lld",
                   (long long)need, (long long)workspace_bytes);
-    const WsLayout ly = ws_layout(num_seqs, num_q_heads, num_kv_heads, head_dim, a.max_parts);
-    a.counters = (int32_t*)workspace;
-    a.ws_o = (float*)((uint8_t*)workspace + ly.counters_bytes);
-    a.ws_ml = (float*)((uint8_t*)workspace + ly.counters_bytes + ly.acc_bytes);
+    const int64_t units = ir_paged_decode_num_counters(num_seqs, num_q_heads, num_kv_heads);
+    if (!counters || num_counters < units)
+      return fail(IR_EWORKSPACE, "ir_paged_decode: %lld arrival counters required, got %lld", (long long)units,
+                  (long long)num_counters);
+    const WsLayout ly = ws_layout(num_seqs, num_q_heads, head_dim, a.max_parts);
+    a.counters = counters;
+    a.ws_o = (float*)workspace;
+    a.ws_ml = (float*)((uint8_t*)workspace + ly.acc_bytes);
   }
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {

@@ -86,20 +86,20 @@ struct PlanArgs {
   int32_t* err;
 };
 
-// Workspace of the run: arrival counters [units] int32, then the partial rows
-// [(grid + units) x 16 heads] of D fp32 accumulators and (max, sum) pairs. A
-// slice g writes unit u's partial at row g + u: rows are unique because slices
-// and units are both increasing runs of the tile list, so a later slice never
-// meets an earlier unit.
+// Workspace of the run: the partial rows [(grid + units) x 16 heads] of D fp32
+// accumulators and (max, sum) pairs. A slice g writes unit u's partial at row
+// g + u: rows are unique because slices and units are both increasing runs of
+// the tile list, so a later slice never meets an earlier unit. The arrival
+// counters ([units] int32, zero at rest) are a separate buffer.
 struct PlannedWs {
-  int64_t counters_bytes, acc_bytes, ml_bytes;
-  int64_t total() const { return counters_bytes + acc_bytes + ml_bytes; }
+  int64_t acc_bytes, ml_bytes;
+  int64_t total() const { return acc_bytes + ml_bytes; }
 };
 
 PlannedWs planned_ws(int64_t units, int grid, int head_dim) {
   auto al = [](int64_t x) { return (x + 255) & ~(int64_t)255; };
   const int64_t rows = ((int64_t)grid + units) * 16;
-  return PlannedWs{al(units * 4), al(rows * head_dim * 4), al(rows * 2 * 4)};
+  return PlannedWs{al(rows * head_dim * 4), al(rows * 2 * 4)};
 }
 
 // floor(x / d) for 0 <= x < 2^30 and quotients below 2^22: a float
@@ -737,7 +737,8 @@ extern "C" int ir_paged_decode_planned(const void* q, int64_t q_seq_stride, int6
                                        const void* v_cache, int64_t cache_slot_stride, void* out,
                                        int64_t out_seq_stride, int64_t out_head_stride, int num_seqs,
                                        int num_q_heads, int num_kv_heads, int head_dim, int max_blocks_per_seq,
-                                       int block_size, float scale, int dtype, const void* plan, void* workspace,
+                                       int block_size, float scale, int dtype, const void* plan,
+                                       int32_t* counters, int64_t num_counters, void* workspace,
                                        int64_t workspace_bytes, int32_t* err_flags, ir_stream_t stream) {
   const int eb = dtype_bytes(dtype);
   IR_REQUIRE(eb > 0, "ir_paged_decode_planned: unknown dtype %d", dtype);
@@ -758,6 +759,10 @@ extern "C" int ir_paged_decode_planned(const void* q, int64_t q_seq_stride, int6
   if (!workspace || workspace_bytes < ws.total() || ((uintptr_t)workspace & 255u))
     return fail(IR_EWORKSPACE, "ir_paged_decode_planned: workspace of %lld bytes (256-byte aligned) required, got %lld",
                 (long long)ws.total(), (long long)workspace_bytes);
+  const int64_t units = (int64_t)num_seqs * num_kv_heads * n_hg;
+  if (!counters || num_counters < units)
+    return fail(IR_EWORKSPACE, "ir_paged_decode_planned: %lld arrival counters required, got %lld",
+                (long long)units, (long long)num_counters);
   DecodeArgs a;
   memset(&a, 0, sizeof(a));
   a.q = q;
@@ -777,9 +782,9 @@ extern "C" int ir_paged_decode_planned(const void* q, int64_t q_seq_stride, int6
   a.n_ups = num_kv_heads * n_hg;
   a.scale_log2 = scale * kLog2e;
   a.err = err_flags;
-  a.counters = (int32_t*)workspace;
-  a.ws_o = (float*)((uint8_t*)workspace + ws.counters_bytes);
-  a.ws_ml = (float*)((uint8_t*)workspace + ws.counters_bytes + ws.acc_bytes);
+  a.counters = counters;
+  a.ws_o = (float*)workspace;
+  a.ws_ml = (float*)((uint8_t*)workspace + ws.acc_bytes);
   const PlanLayout ly =
       plan_layout(num_seqs, grid, t_cap_of(num_seqs, a.n_ups, max_blocks_per_seq, block_size));
   const uint8_t* pl = (const uint8_t*)plan;

@@ -134,6 +134,19 @@ def decode_workspace_bytes(
     ))
 
 
+def decode_num_counters(num_seqs: int, num_q_heads: int, num_kv_heads: int) -> int:
+    """int32 arrival counters a split decode needs (zero at rest; one buffer serves every shape)."""
+    return int(lib().ir_paged_decode_num_counters(num_seqs, num_q_heads, num_kv_heads))
+
+
+def _counters_for(counters: torch.Tensor | None, n: int, dev) -> torch.Tensor:
+    if counters is None:
+        return torch.zeros(max(n, 1), dtype=torch.int32, device=dev)
+    if counters.dtype != torch.int32 or not counters.is_contiguous() or counters.numel() < n:
+        raise RuntimeError(f"decode counters must be a contiguous int32 tensor of >= {n} zeros")
+    return counters
+
+
 def default_partition(num_seqs: int, num_kv_heads: int, max_blocks: int, block_size: int) -> int:
     return int(lib().ir_paged_decode_default_partition(num_seqs, num_kv_heads, max_blocks, block_size))
 
@@ -150,13 +163,15 @@ def paged_decode(
     partition_tokens: int = 0,
     workspace: torch.Tensor | None = None,
     err_flags: torch.Tensor | None = None,
+    counters: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """GQA paged decode: ``q`` ``[B, H_q, D]`` -> ``[B, H_q, D]``.
 
     ``block_tables`` int32 ``[B, max_blocks]``, ``context_lens`` int32 ``[B]``.
-    ``workspace`` (uint8, 256-byte aligned, zero-filled before first use; the
-    kernel leaves its arrival counters at zero) is allocated when not given and
-    the longest possible context needs more than one partition.
+    ``workspace`` (uint8 scratch, 256-byte aligned) and ``counters`` (int32,
+    zero-filled before first use; every call leaves them at zero) are allocated
+    when not given and the longest possible context needs more than one
+    partition.
     """
     dev = require_device(q, k_cache, v_cache, block_tables, context_lens)
     _cache_layer("paged_decode", k_cache)
@@ -176,14 +191,19 @@ def paged_decode(
     if partition_tokens <= 0:
         partition_tokens = default_partition(b, h_kv, max_blocks, block_size)
     need = decode_workspace_bytes(b, hq, h_kv, d, max_blocks, block_size, partition_tokens)
-    if need > 0 and (workspace is None or workspace.numel() < need):
-        workspace = torch.zeros(need, dtype=torch.uint8, device=dev)
+    n_ctr = 0
+    if need > 0:
+        if workspace is None or workspace.numel() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        n_ctr = decode_num_counters(b, hq, h_kv)
+        counters = _counters_for(counters, n_ctr, dev)
     rc = lib().ir_paged_decode(
         ptr(q), q.stride(0), q.stride(1), ptr(k_cache), ptr(v_cache), k_cache.stride(0),
         k_cache.stride(1), k_cache.shape[0] // block_size, block_size, ptr(block_tables),
         block_tables.stride(0), max_blocks, ptr(context_lens), ptr(out), out.stride(0),
         out.stride(1), b, hq, h_kv, d, float(scale), dtype_code(q.dtype), partition_tokens,
-        ptr(workspace) if need > 0 else None, need, ptr(err_flags), stream_ptr(dev),
+        ptr(counters) if need > 0 else None, n_ctr, ptr(workspace) if need > 0 else None, need,
+        ptr(err_flags), stream_ptr(dev),
     )
     check(rc, "ir_paged_decode")
     return out
@@ -214,6 +234,27 @@ class DecodePlan:
 def decode_plan_bytes(num_seqs: int, num_q_heads: int, num_kv_heads: int, max_blocks: int, block_size: int) -> int:
     """Plan bytes for this shape; 0 when it is not plannable (then use :func:`paged_decode`)."""
     return int(lib().ir_paged_decode_plan_bytes(num_seqs, num_q_heads, num_kv_heads, max_blocks, block_size))
+
+
+_CU_COUNT: dict[int, int] = {}
+
+
+def decode_plan_pays(num_seqs: int, num_q_heads: int, num_kv_heads: int, max_blocks: int, block_size: int,
+                     device: torch.device | str | int | None = None) -> bool:
+    """Whether the planned schedule is the faster decode for this shape: it is
+    plannable and the batch has at least one unit (sequence x KV head x group
+    of <= 16 query heads) per CU. Smaller batches leave most slices idle and run
+    faster on :func:`paged_decode`'s fixed split-KV partitions (measured on
+    MI355X: 8 fp32 sequences 8.2 vs 11.5 us, 16 skewed long ones 35.8 vs
+    36.9 us; 64 x 4 KV heads 59.1 vs 54.3 us in favour of the plan)."""
+    if decode_plan_bytes(num_seqs, num_q_heads, num_kv_heads, max_blocks, block_size) <= 0:
+        return False
+    idx = torch.device(device if device is not None else "cuda").index
+    idx = torch.cuda.current_device() if idx is None else idx
+    if idx not in _CU_COUNT:
+        _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    units = num_seqs * num_kv_heads * ((num_q_heads // num_kv_heads + 15) // 16)
+    return units >= _CU_COUNT[idx]
 
 
 def planned_workspace_bytes(num_seqs: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
@@ -263,8 +304,11 @@ def paged_decode_planned(
     out: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
     err_flags: torch.Tensor | None = None,
+    counters: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """:func:`paged_decode` over a plan: ``q`` ``[B, H_q, D]`` -> ``[B, H_q, D]``."""
+    """:func:`paged_decode` over a plan: ``q`` ``[B, H_q, D]`` -> ``[B, H_q, D]``.
+    ``workspace`` (uint8 scratch) and ``counters`` (int32 zeros, left at zero)
+    are allocated when not given."""
     dev = require_device(q, k_cache, v_cache, plan.buf)
     _cache_layer("paged_decode_planned", k_cache)
     if q.dim() != 3:
@@ -284,12 +328,14 @@ def paged_decode_planned(
         out = torch.empty(b, hq, d, dtype=q.dtype, device=dev)
     need = planned_workspace_bytes(b, hq, plan.num_kv_heads, d)
     if workspace is None or workspace.numel() < need:
-        workspace = torch.zeros(need, dtype=torch.uint8, device=dev)
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    n_ctr = decode_num_counters(b, hq, plan.num_kv_heads)
+    counters = _counters_for(counters, n_ctr, dev)
     rc = lib().ir_paged_decode_planned(
         ptr(q), q.stride(0), q.stride(1), ptr(k_cache), ptr(v_cache), k_cache.stride(0), ptr(out),
         out.stride(0), out.stride(1), b, hq, plan.num_kv_heads, d, plan.max_blocks, plan.block_size,
-        float(scale), dtype_code(q.dtype), ptr(plan.buf), ptr(workspace), workspace.numel(), ptr(err_flags),
-        stream_ptr(dev),
+        float(scale), dtype_code(q.dtype), ptr(plan.buf), ptr(counters), n_ctr, ptr(workspace),
+        workspace.numel(), ptr(err_flags), stream_ptr(dev),
     )
     check(rc, "ir_paged_decode_planned")
     return out

@@ -10,7 +10,10 @@ metadata:
 
 1. ``ir_kv_scatter`` of the step's new K/V rows (decode tokens first, then the
    chunk tokens) into the pool at ``write_slots``;
-2. ``ir_paged_decode`` for the one-token decode rows over their block tables;
+2. the decode of the one-token rows over their block tables: on the balanced
+   plan that ``ir_paged_decode_plan`` builds once at the start of the step
+   (``ir_paged_decode_planned`` per layer) when the rows fill the device, else
+   ``ir_paged_decode``'s fixed split-KV partitions;
 3. ``ir_paged_prefill`` for the chunks (causal after their cached prefix).
 
 With ``overlap=True`` the decode (HBM-bound) and prefill (MFMA-bound) launches
@@ -152,19 +155,36 @@ class MixedStep:
         self.out_dec = torch.empty_like(inputs.q_dec)
         self.out_pre = torch.empty_like(inputs.q_pre)
         hq, d = inputs.q_dec.shape[2], inputs.q_dec.shape[3]
-        need = kernels.decode_workspace_bytes(
-            batch.dec_tables.shape[0], hq, pool.num_kv_heads, d, batch.dec_tables.shape[1], pool.block_size
-        )
-        self.workspace = torch.zeros(max(need, 256), dtype=torch.uint8, device=dev) if need > 0 else None
+        nd, max_blocks = batch.dec_tables.shape
+        self.planned = kernels.decode_plan_pays(nd, hq, pool.num_kv_heads, max_blocks, pool.block_size, dev)
+        if self.planned:
+            need = kernels.planned_workspace_bytes(nd, hq, pool.num_kv_heads, d)
+            self.plan_buf = torch.empty(
+                kernels.decode_plan_bytes(nd, hq, pool.num_kv_heads, max_blocks, pool.block_size),
+                dtype=torch.uint8, device=dev,
+            )
+        else:
+            need = kernels.decode_workspace_bytes(nd, hq, pool.num_kv_heads, d, max_blocks, pool.block_size)
+            self.plan_buf = None
+        self.plan: kernels.DecodePlan | None = None
+        self.workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=dev) if need > 0 else None
+        self.counters = torch.zeros(kernels.decode_num_counters(nd, hq, pool.num_kv_heads), dtype=torch.int32,
+                                    device=dev)
         self.err = torch.zeros(1, dtype=torch.int32, device=dev)
         self._side = torch.cuda.Stream(device=dev) if overlap else None
         self._graph: torch.cuda.CUDAGraph | None = None
 
     def _decode(self, layer: int) -> None:
         b, inp, pool = self.batch, self.inputs, self.pool
+        if self.planned:
+            kernels.paged_decode_planned(
+                inp.q_dec[layer], pool.k[layer], pool.v[layer], self.plan, self.scale, out=self.out_dec[layer],
+                workspace=self.workspace, err_flags=self.err, counters=self.counters,
+            )
+            return
         kernels.paged_decode(
             inp.q_dec[layer], pool.k[layer], pool.v[layer], b.dec_tables, b.dec_ctx, pool.block_size, self.scale,
-            out=self.out_dec[layer], workspace=self.workspace, err_flags=self.err,
+            out=self.out_dec[layer], workspace=self.workspace, err_flags=self.err, counters=self.counters,
         )
 
     def _prefill(self, layer: int) -> None:
@@ -189,6 +209,12 @@ class MixedStep:
         main.wait_stream(self._side)  # both are done before the next layer's scatter
 
     def eager(self) -> None:
+        if self.planned:  # one plan for the step's decode rows, shared by every layer
+            b = self.batch
+            self.plan = kernels.decode_plan(
+                b.dec_tables, b.dec_ctx, self.inputs.q_dec.shape[2], self.pool.k[0], self.pool.block_size,
+                buf=self.plan_buf, err_flags=self.err,
+            )
         for layer in range(self.pool.num_layers):
             self._layer(layer)
 

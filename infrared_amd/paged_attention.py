@@ -124,28 +124,32 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
         ).view(b, sq, hq, d)
     elif paged.use_triton and block_tables is not None and context_lens is not None and sq == 1:
         max_blocks = block_tables.shape[1]
-        plan_bytes = kernels.decode_plan_bytes(b, hq, h_kv, max_blocks, pool.block_size)
-        if plan_bytes > 0 and hasattr(pool, "plan_buffer"):
+        if hasattr(pool, "plan_buffer") and kernels.decode_plan_pays(b, hq, h_kv, max_blocks, pool.block_size,
+                                                                      q.device):
             # balanced schedule: built by the step's first layer, reused by the rest
             plan = paged.decode_plan
             if plan is None:
+                plan_bytes = kernels.decode_plan_bytes(b, hq, h_kv, max_blocks, pool.block_size)
                 plan = kernels.decode_plan(
                     block_tables, context_lens, hq, k_layer, pool.block_size,
                     buf=pool.plan_buffer(plan_bytes), err_flags=err,
                 )
                 paged.decode_plan = plan
             ws = pool.workspace(kernels.planned_workspace_bytes(b, hq, h_kv, d))
+            ctr = pool.decode_counters(kernels.decode_num_counters(b, hq, h_kv))
             out = kernels.paged_decode_planned(
-                q.reshape(b, hq, d), k_layer, v_layer, plan, scale, workspace=ws, err_flags=err
+                q.reshape(b, hq, d), k_layer, v_layer, plan, scale, workspace=ws, err_flags=err, counters=ctr
             )
         else:
-            ws = None
+            ws = ctr = None
             if hasattr(pool, "workspace"):
                 need = kernels.decode_workspace_bytes(b, hq, h_kv, d, max_blocks, pool.block_size)
-                ws = pool.workspace(need) if need > 0 else None
+                if need > 0:
+                    ws = pool.workspace(need)
+                    ctr = pool.decode_counters(kernels.decode_num_counters(b, hq, h_kv))
             out = kernels.paged_decode(
                 q.reshape(b, hq, d), k_layer, v_layer, block_tables, context_lens,
-                pool.block_size, scale, workspace=ws, err_flags=err,
+                pool.block_size, scale, workspace=ws, err_flags=err, counters=ctr,
             )
         out = out.view(b, 1, hq, d)
     else:

@@ -100,6 +100,7 @@ class PagedKVPool:
             raise ValueError(f"unknown pool layout {layout!r} (head_major, slot_major)")
         self.err_flags = torch.zeros(1, dtype=torch.int32, device=device)
         self._workspace: torch.Tensor | None = None
+        self._counters: torch.Tensor | None = None
         self._plan_buf: torch.Tensor | None = None
 
     # --- reference surface ------------------------------------------------
@@ -145,15 +146,23 @@ class PagedKVPool:
         return out
 
     def workspace(self, nbytes: int) -> torch.Tensor:
-        """A cached, zero-filled device buffer of at least ``nbytes`` (split-KV
-        counters and partials; the decode kernel leaves the counters at zero).
+        """A cached device buffer of at least ``nbytes`` for the decode kernels'
+        fp32 partial rows (scratch, any shape).
 
         Grow it outside hipGraph capture (the graph decoder's warm-up does) so a
         captured graph keeps pointing at live memory.
         """
         if self._workspace is None or self._workspace.numel() < nbytes:
-            self._workspace = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+            self._workspace = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
         return self._workspace
+
+    def decode_counters(self, n: int) -> torch.Tensor:
+        """A cached int32 buffer of at least ``n`` arrival counters, zero at rest:
+        every decode call leaves the counters it used at zero, so calls of any
+        batch shape share it. Grown (zero-filled) outside hipGraph capture."""
+        if self._counters is None or self._counters.numel() < n:
+            self._counters = torch.zeros(max(n, 64), dtype=torch.int32, device=self.device)
+        return self._counters
 
     def plan_buffer(self, nbytes: int) -> torch.Tensor:
         """A cached device buffer of at least ``nbytes`` for the decode plan of

@@ -56,15 +56,18 @@ def test_validation_errors_report_codes_and_messages():
     # unsupported head_dim
     rc = lib.ir_paged_decode(
         None, 0, 0, None, None, 0, 0, 1, 16, None, 0, 1, None, None, 0, 0, 1, 8, 2, 96, 1.0, 2, 0,
-        None, 0, None, None,
+        None, 0, None, 0, None, None,
     )
     assert rc == -2 and b"head_dim" in lib.ir_last_error()
     # heads not a multiple of kv heads
     rc = lib.ir_paged_decode(
         None, 0, 0, None, None, 0, 0, 1, 16, None, 0, 1, None, None, 0, 0, 1, 7, 2, 128, 1.0, 2, 0,
-        None, 0, None, None,
+        None, 0, None, 0, None, None,
     )
     assert rc == -1 and b"multiple" in lib.ir_last_error()
+    # a plan for a shape the plan does not take
+    rc = lib.ir_paged_decode_plan(None, 0, 16, None, 2000, 28, 4, 16, 100, 512, 128, 2, None, 0, None, None)
+    assert rc == -1 and b"plannable" in lib.ir_last_error()
     # null pointers with work to do
     rc = lib.ir_paged_attention_masked(
         None, 0, 0, 0, None, None, 0, 0, 10, None, 0, 0, None, 0, 0, 0, 2, None, 0, 0, 0, 1, 1, 4,
@@ -83,6 +86,23 @@ def test_decode_workspace_and_partition_helpers():
     ws = lib.ir_paged_decode_workspace_size(64, 28, 4, 128, 256, 16, 512)
     rows = 64 * 28 * 8
     assert ws >= rows * 128 * 4 + rows * 2 * 4
+    # counters: one per sequence x KV head x group of <= 16 query heads
+    assert lib.ir_paged_decode_num_counters(64, 28, 4) == 64 * 4
+    assert lib.ir_paged_decode_num_counters(8, 64, 2) == 8 * 2 * 2
+    assert lib.ir_paged_decode_num_counters(8, 28, 3) == 0  # not a GQA shape
+
+
+def test_decode_plan_helpers():
+    """The plan is offered for 1..1024 sequences with block sizes that are
+    multiples of 16, and its size covers one 8-byte fact per tile."""
+    lib = _lib.lib()
+    assert lib.ir_paged_decode_plan_bytes(0, 28, 4, 256, 16) == 0
+    assert lib.ir_paged_decode_plan_bytes(1025, 28, 4, 256, 16) == 0
+    assert lib.ir_paged_decode_plan_bytes(64, 28, 4, 256, 8) == 0
+    n = lib.ir_paged_decode_plan_bytes(64, 28, 4, 256, 16)
+    assert n >= 64 * 4 * 256 * 8  # tiles of the full table capacity, 8 bytes each
+    assert lib.ir_paged_decode_plan_bytes(64, 28, 4, 256, 32) >= 64 * 4 * 512 * 8
+    assert lib.ir_paged_decode_planned_workspace_bytes(64, 28, 4, 128) >= 256 * 16 * 128 * 4
 
 
 def test_no_product_module_imports_triton_or_the_oracle():

@@ -246,28 +246,32 @@ def test_decode_all_rows_empty():
 
 def test_decode_shared_workspace_across_different_splits():
     """The partial rows start as garbage (every int32 = 2) and are shared by calls
-    whose splits differ; each call matches the oracle and repeats bit for bit."""
+    whose splits and batch sizes differ, as are the arrival counters; each call
+    matches the oracle, repeats bit for bit and leaves the counters at zero."""
     case = make_decode_case(_MIX_CFG, DEV)
     cfg = case.config
     bt = case.block_tables[0]
     need = kernels.decode_workspace_bytes(8, 28, 4, 128, bt.shape[1], 16, 256)
     ws = torch.full((need // 4,), 2, dtype=torch.int32, device=DEV).view(torch.uint8)
-    ws[:256].zero_()  # arrival counters
+    ctr = torch.zeros(kernels.decode_num_counters(8, 28, 4), dtype=torch.int32, device=DEV)
     lens = [
         torch.tensor([5000, 5000, 5000, 5000, 5000, 5000, 5000, 5000], dtype=torch.int32),
         torch.tensor([0, 1, 5000, 0, 17, 4096, 0, 2048], dtype=torch.int32),
         torch.tensor([33, 0, 0, 0, 0, 0, 0, 4999], dtype=torch.int32),
+        torch.tensor([4000, 17, 5000], dtype=torch.int32),
     ]
     for cl in lens:
         cl = cl.to(DEV)
+        b = cl.shape[0]
         outs = [
-            kernels.paged_decode(case.q, case.k_cache, case.v_cache, bt, cl, 16, cfg.scale, partition_tokens=256,
-                                 workspace=ws)
+            kernels.paged_decode(case.q[:b], case.k_cache, case.v_cache, bt[:b], cl, 16, cfg.scale,
+                                 partition_tokens=256, workspace=ws, counters=ctr)
             for _ in range(2)
         ]
         torch.cuda.synchronize()
         assert torch.equal(outs[0], outs[1])
-        ref = O.decode_reference(case.q.cpu(), case.k_cache.cpu(), case.v_cache.cpu(), bt.cpu(), cl.cpu(), 16,
+        assert int(ctr.abs().sum()) == 0
+        ref = O.decode_reference(case.q[:b].cpu(), case.k_cache.cpu(), case.v_cache.cpu(), bt[:b].cpu(), cl.cpu(), 16,
                                  cfg.scale)
         assert (outs[0].float().cpu() - ref).abs().max().item() <= TOL[cfg.dtype]
 

@@ -14,6 +14,8 @@ from oracle import naive as O
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 SMALL = MixedConfig("mixed-small", 3, 12, 1, 300, 2, 64, 40, 28, 4, 128, 16, torch.bfloat16, seed=9)
+# 72 decode rows x 4 KV heads >= one unit per CU: the decode rows take the planned schedule
+WIDE = MixedConfig("mixed-wide", 2, 72, 1, 600, 1, 64, 40, 28, 4, 128, 16, torch.bfloat16, seed=10)
 
 
 def _oracle_step(cfg, pool_k, pool_v, batch, inputs):
@@ -30,12 +32,16 @@ def _oracle_step(cfg, pool_k, pool_v, batch, inputs):
     return outs
 
 
+@pytest.mark.parametrize("config,planned", [(SMALL, False), (WIDE, True)])
 @pytest.mark.parametrize("overlap", [False, True])
-def test_mixed_step_eager_matches_oracle_and_graph_replays(overlap):
-    cfg, pool, batch, inputs = make_mixed_case(SMALL, DEV)
+def test_mixed_step_eager_matches_oracle_and_graph_replays(overlap, config, planned):
+    """Both decode schedules inside the step: the fixed partitions (12 rows) and
+    the plan built once per step and captured with the layers (72 rows)."""
+    cfg, pool, batch, inputs = make_mixed_case(config, DEV)
     pk = [pool.k[i].cpu().clone() for i in range(cfg.num_layers)]
     pv = [pool.v[i].cpu().clone() for i in range(cfg.num_layers)]
     step = MixedStep(pool, batch, inputs, cfg.scale, overlap=overlap)
+    assert step.planned == planned
     step.eager()
     torch.cuda.synchronize()
     assert step.err.item() == 0

@@ -31,13 +31,12 @@ def _err():
     return torch.zeros(1, dtype=torch.int32, device=DEV)
 
 
-def _counters_zero(ws, case_or_shape) -> bool:
-    b, hq, hkv = case_or_shape
-    units = b * hkv * ((hq // hkv + 15) // 16)
-    return int(ws[: units * 4].view(torch.int32).abs().sum()) == 0
+def _garbage(nbytes: int) -> torch.Tensor:
+    """Scratch workspace whose every int32 reads 2 (partial rows start as garbage)."""
+    return torch.full(((nbytes + 3) // 4,), 2, dtype=torch.int32, device=DEV).view(torch.uint8)
 
 
-def _run_planned(case, bt=None, cl=None, err=None, ws=None, q=None, plan=None, scale=None):
+def _run_planned(case, bt=None, cl=None, err=None, ws=None, q=None, plan=None, scale=None, ctr=None):
     cfg = case.config
     scale = cfg.scale if scale is None else scale
     bt = case.block_tables[0] if bt is None else bt
@@ -46,10 +45,13 @@ def _run_planned(case, bt=None, cl=None, err=None, ws=None, q=None, plan=None, s
     if plan is None:
         plan = kernels.decode_plan(bt, cl, cfg.num_q_heads, case.k_cache, cfg.block_size, err_flags=err)
     if ws is None:
-        ws = torch.zeros(kernels.planned_workspace_bytes(cfg.num_seqs, cfg.num_q_heads, cfg.num_kv_heads,
-                                                         cfg.head_dim), dtype=torch.uint8, device=DEV)
-    out = kernels.paged_decode_planned(q, case.k_cache, case.v_cache, plan, scale, workspace=ws, err_flags=err)
-    return out, plan, ws
+        ws = _garbage(kernels.planned_workspace_bytes(cfg.num_seqs, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim))
+    if ctr is None:
+        ctr = torch.zeros(kernels.decode_num_counters(cfg.num_seqs, cfg.num_q_heads, cfg.num_kv_heads),
+                          dtype=torch.int32, device=DEV)
+    out = kernels.paged_decode_planned(q, case.k_cache, case.v_cache, plan, scale, workspace=ws, err_flags=err,
+                                       counters=ctr)
+    return out, plan, ctr
 
 
 def _check_planned(case, bt=None, cl=None):
@@ -57,10 +59,10 @@ def _check_planned(case, bt=None, cl=None):
     bt = case.block_tables[0] if bt is None else bt
     cl = case.context_lens if cl is None else cl
     err = _err()
-    out, _, ws = _run_planned(case, bt, cl, err)
+    out, _, ctr = _run_planned(case, bt, cl, err)
     torch.cuda.synchronize()
     assert err.item() == 0
-    assert _counters_zero(ws, (cfg.num_seqs, cfg.num_q_heads, cfg.num_kv_heads))
+    assert int(ctr.abs().sum()) == 0
     ref = O.decode_reference(case.q.cpu(), case.k_cache.cpu(), case.v_cache.cpu(), bt.cpu(), cl.cpu(),
                              cfg.block_size, cfg.scale, torch.float32)
     diff = (out.float().cpu() - ref).abs().max().item()
@@ -156,18 +158,36 @@ def test_planned_plan_shared_by_layers_and_calls():
     pool_k = torch.randn(3, *case.k_cache.shape, device=DEV).to(cfg.dtype)
     pool_v = torch.randn(3, *case.v_cache.shape, device=DEV).to(cfg.dtype)
     plan = kernels.decode_plan(bt, cl, cfg.num_q_heads, pool_k[0], 16)
-    need = kernels.planned_workspace_bytes(16, 28, 4, 128)
-    ws = torch.full((need // 4,), 2, dtype=torch.int32, device=DEV).view(torch.uint8)
-    ws[: 16 * 4 * 4].zero_()  # the arrival counters start at zero
+    ws = _garbage(kernels.planned_workspace_bytes(16, 28, 4, 128))
+    ctr = torch.zeros(kernels.decode_num_counters(16, 28, 4), dtype=torch.int32, device=DEV)
     for layer in range(3):
         q = torch.randn_like(case.q)
-        outs = [kernels.paged_decode_planned(q, pool_k[layer], pool_v[layer], plan, cfg.scale, workspace=ws)
-                for _ in range(2)]
+        outs = [kernels.paged_decode_planned(q, pool_k[layer], pool_v[layer], plan, cfg.scale, workspace=ws,
+                                             counters=ctr) for _ in range(2)]
         torch.cuda.synchronize()
         assert torch.equal(outs[0], outs[1])
-        assert _counters_zero(ws, (16, 28, 4))
+        assert int(ctr.abs().sum()) == 0
         ref = O.decode_reference(q.cpu(), pool_k[layer].cpu(), pool_v[layer].cpu(), bt.cpu(), cl.cpu(), 16, cfg.scale)
         assert (outs[0].float().cpu() - ref).abs().max().item() <= TOL[cfg.dtype]
+
+
+def test_planned_calls_of_different_batch_sizes_share_scratch_and_counters():
+    """Batches of 128, 109 and 128 sequences in turn on one scratch workspace
+    and one counters buffer (an engine's steps through one pool): a smaller
+    call's partial rows never land on a larger call's counters, every call
+    matches the oracle and the counters return to zero."""
+    cfg = DecodeConfig("p-shapes", 128, 28, 4, 128, 16, torch.bfloat16, "uniform", 1, 600, seed=31)
+    case = make_decode_case(cfg, DEV)
+    ws = _garbage(kernels.planned_workspace_bytes(128, 28, 4, 128))
+    ctr = torch.zeros(kernels.decode_num_counters(128, 28, 4), dtype=torch.int32, device=DEV)
+    for b in (128, 109, 128, 109):
+        bt, cl, q = case.block_tables[0][:b], case.context_lens[:b], case.q[:b]
+        plan = kernels.decode_plan(bt, cl, 28, case.k_cache, 16)
+        out = kernels.paged_decode_planned(q, case.k_cache, case.v_cache, plan, cfg.scale, workspace=ws, counters=ctr)
+        torch.cuda.synchronize()
+        assert int(ctr.abs().sum()) == 0
+        ref = O.decode_reference(q.cpu(), case.k_cache.cpu(), case.v_cache.cpu(), bt.cpu(), cl.cpu(), 16, cfg.scale)
+        assert (out.float().cpu() - ref).abs().max().item() <= TOL[cfg.dtype], f"batch {b}"
 
 
 def test_planned_flags_bad_block_ids_and_contexts():
@@ -225,14 +245,15 @@ def test_planned_graph_capture_replays_with_fresh_metadata():
     cl = case.context_lens.clone()
     q2 = torch.randn(2, *case.q.shape, device=DEV).to(cfg.dtype)
     plan_buf = torch.empty(kernels.decode_plan_bytes(12, 28, 4, bt.shape[1], 16), dtype=torch.uint8, device=DEV)
-    ws = torch.zeros(kernels.planned_workspace_bytes(12, 28, 4, 128), dtype=torch.uint8, device=DEV)
+    ws = _garbage(kernels.planned_workspace_bytes(12, 28, 4, 128))
+    ctr = torch.zeros(kernels.decode_num_counters(12, 28, 4), dtype=torch.int32, device=DEV)
     outs = torch.empty(2, *case.q.shape, dtype=cfg.dtype, device=DEV)
 
     def step():
         plan = kernels.decode_plan(bt, cl, 28, case.k_cache, 16, buf=plan_buf)
         for layer in range(2):
             kernels.paged_decode_planned(q2[layer], case.k_cache, case.v_cache, plan, cfg.scale, out=outs[layer],
-                                         workspace=ws)
+                                         workspace=ws, counters=ctr)
 
     step()  # warm-up outside capture
     torch.cuda.synchronize()
@@ -254,7 +275,7 @@ def test_planned_graph_capture_replays_with_fresh_metadata():
         torch.cuda.synchronize()
         for layer in range(2):
             assert torch.equal(got[layer], want[layer]), f"replay {it} layer {layer}"
-        assert _counters_zero(ws, (12, 28, 4))
+        assert int(ctr.abs().sum()) == 0
 
 
 def test_plannable_shapes_and_rejections():
@@ -274,30 +295,82 @@ def test_plannable_shapes_and_rejections():
 
 
 def test_seam_decode_builds_the_plan_once_per_context():
-    """Through ``paged_attention``: the first decode layer of a context builds
-    its plan, later layers reuse it; every layer matches the oracle."""
-    g = torch.Generator().manual_seed(13)
-    bs, h_kv, n_rep, d, b, layers = 16, 4, 7, 128, 20, 3
-    num_cached = torch.randint(0, 2000, (b,), generator=g).tolist()
-    perm = torch.randperm(4000, generator=g).tolist()
-    tables, off = [], 0
-    for nc in num_cached:
-        nb = metadata.blocks_for(nc + 1, bs)
-        tables.append(perm[off : off + nb])
-        off += nb
-    pool = PagedKVPool(layers, 4000, bs, h_kv, d, torch.bfloat16, device=DEV, strict=True)
+    """Through ``paged_attention``: a batch with a unit per CU takes the planned
+    schedule -- the first decode layer of a context builds its plan, later
+    layers reuse it -- and every layer matches the oracle; a small batch keeps
+    the fixed-partition kernel (no plan)."""
+    bs, h_kv, n_rep, d, layers = 16, 4, 7, 128, 3
+    for b, planned in ((80, True), (12, False)):
+        g = torch.Generator().manual_seed(13 + b)
+        num_cached = torch.randint(0, 700, (b,), generator=g).tolist()
+        nblk = [metadata.blocks_for(nc + 1, bs) for nc in num_cached]
+        perm = torch.randperm(sum(nblk) + 64, generator=g).tolist()
+        tables, off = [], 0
+        for nb in nblk:
+            tables.append(perm[off : off + nb])
+            off += nb
+        pool = PagedKVPool(layers, len(perm), bs, h_kv, d, torch.bfloat16, device=DEV, strict=True)
+        pool.k.normal_()
+        pool.v.normal_()
+        paged, mask = metadata.decode_context(pool, tables, num_cached)
+        assert isinstance(paged, PagedContext) and paged.decode_plan is None
+        assert kernels.decode_plan_pays(b, h_kv * n_rep, h_kv, paged.block_tables.shape[1], bs) == planned
+        plans = []
+        for layer in range(layers):
+            q = torch.randn(b, 1, h_kv * n_rep, d, device=DEV).bfloat16()
+            k = torch.randn(b, 1, h_kv, d, device=DEV).bfloat16()
+            v = torch.randn(b, 1, h_kv, d, device=DEV).bfloat16()
+            out = paged_attention(q, k, v, paged, mask, layer, d**-0.5, n_rep)
+            plans.append(paged.decode_plan)
+            ref = O.paged_attention_naive(q.float().cpu(), pool.k[layer].float().cpu(), pool.v[layer].float().cpu(),
+                                          paged.gather_slots.cpu(), mask.float().cpu(), d**-0.5, n_rep)
+            assert (out.float().cpu() - ref).abs().max().item() <= 2e-2
+        if planned:
+            assert plans[0] is not None and all(p is plans[0] for p in plans)
+        else:
+            assert all(p is None for p in plans)
+
+
+def test_seam_graph_decoder_replays_the_planned_step():
+    """HipGraphDecoder over a batch that fills the device (bucket 128 x 4 KV
+    heads): the captured step holds the plan build and two planned layers;
+    replays with new contexts equal the eager step at the same bucket bit for
+    bit and the tight (unpadded) eager step within the bf16 bar."""
+    from infrared_amd.hip_graph import HipGraphDecoder, build_decode_static_inputs, pick_bucket
+
+    bs, h_kv, n_rep, d, layers = 16, 4, 7, 128, 2
+    dtype = torch.bfloat16
+    pool = PagedKVPool(layers, 128 * 40, bs, h_kv, d, dtype, device=DEV)
     pool.k.normal_()
     pool.v.normal_()
-    paged, mask = metadata.decode_context(pool, tables, num_cached)
-    assert isinstance(paged, PagedContext) and paged.decode_plan is None
-    plans = []
-    for layer in range(layers):
-        q = torch.randn(b, 1, h_kv * n_rep, d, device=DEV).bfloat16()
-        k = torch.randn(b, 1, h_kv, d, device=DEV).bfloat16()
-        v = torch.randn(b, 1, h_kv, d, device=DEV).bfloat16()
-        out = paged_attention(q, k, v, paged, mask, layer, d**-0.5, n_rep)
-        plans.append(paged.decode_plan)
-        ref = O.paged_attention_naive(q.float().cpu(), pool.k[layer].float().cpu(), pool.v[layer].float().cpu(),
-                                      paged.gather_slots.cpu(), mask.float().cpu(), d**-0.5, n_rep)
-        assert (out.float().cpu() - ref).abs().max().item() <= 2e-2
-    assert plans[0] is not None and all(p is plans[0] for p in plans)
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    qkv = torch.randn(layers, 128, 1, h_kv * (n_rep + 2), d, generator=gen, device=DEV).to(dtype)
+
+    def step(buf, paged):
+        outs = []
+        ids = buf.ids[:, 0]
+        for layer in range(layers):
+            x = qkv[layer].index_select(0, ids)
+            q = x[:, :, : h_kv * n_rep].contiguous()
+            k = x[:, :, h_kv * n_rep : h_kv * (n_rep + 1)].contiguous()
+            v = x[:, :, h_kv * (n_rep + 1) :].contiguous()
+            outs.append(paged_attention(q, k, v, paged, buf.mask, layer, d**-0.5, n_rep))
+        return torch.stack(outs, dim=1)
+
+    dec = HipGraphDecoder(None, pool, max_num_seqs=128, t_max=640, block_size=bs, step_fn=step)
+    tables = [list(range(i * 40, i * 40 + 40)) for i in range(128)]
+    g = torch.Generator().manual_seed(6)
+    for it in range(3):
+        b = 100 + 9 * it
+        num_cached = torch.randint(0, 600, (b,), generator=g).tolist()
+        got = dec.decode(tables[:b], num_cached, list(range(b))).clone()
+        bucket = pick_bucket(b, dec.buckets)
+        assert bucket == 128 and kernels.decode_plan_pays(bucket, h_kv * n_rep, h_kv, 40, bs)
+        outs = []
+        for rows in (bucket, b):
+            inp = build_decode_static_inputs(tables[:b], num_cached, list(range(b)), rows, 640, bs, DEV, dtype)
+            paged = PagedContext(pool, inp.write_slots, inp.gather_slots, True, inp.block_tables, inp.context_lens)
+            outs.append(step(inp, paged)[:b])
+        torch.cuda.synchronize()
+        assert torch.equal(got, outs[0]), f"replay {it} differs from eager at bucket {bucket}"
+        assert (got.float() - outs[1].float()).abs().max().item() <= 2e-2, f"replay {it}: padded vs tight"
