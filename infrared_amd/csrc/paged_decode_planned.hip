@@ -490,9 +490,16 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     }
     const int cnt = min(kPlanRun, cnt_w - r0);
     const int last = cnt - 1;
+    // Issues the loads of tile i of the run. Past the run's end (the ring's
+    // last DEPTH issues, never computed) it reads the pool's first 16 rows
+    // instead, one shared tile that stays in L2, rather than re-reading the
+    // wavefront's last tile from HBM; the loop keeps its fixed shape, so the
+    // hardware wait counts stay exact.
     auto issue = [&](int i, Tile<DT, D>& tl, int& lb) -> uint32_t {
-      const uint32_t off = (uint32_t)__builtin_amdgcn_readlane((int)info_off, i);
-      const uint32_t meta = (uint32_t)__builtin_amdgcn_readlane((int)info_meta, i);
+      const int ii = i <= last ? i : last;
+      uint32_t off = (uint32_t)__builtin_amdgcn_readlane((int)info_off, ii);
+      const uint32_t meta = (uint32_t)__builtin_amdgcn_readlane((int)info_meta, ii);
+      if (i > last) off = 0u;
       issue_tile<DT, D>(kc, vc, off, lo_off, tl);
       lb = (int)(meta >> 5);
       const int valid = (int)(meta & 31u);
@@ -505,7 +512,7 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     uint32_t mk[DEPTH];
     int lb[DEPTH];
 #pragma unroll
-    for (int r = 0; r < DEPTH; ++r) mk[r] = issue(min(r, last), ring[r], lb[r]);
+    for (int r = 0; r < DEPTH; ++r) mk[r] = issue(r, ring[r], lb[r]);
     for (int i = 0; i < cnt; i += DEPTH) {
 #pragma unroll
       for (int r = 0; r < DEPTH; ++r) {
@@ -529,7 +536,7 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
           }
           compute_tile<DT, D>(ring[r], qr, mk[r], a.scale_log2, kstage[w], lane, st);
         }
-        mk[r] = issue(min(i + r + DEPTH, last), ring[r], lb[r]);
+        mk[r] = issue(i + r + DEPTH, ring[r], lb[r]);
       }
     }
   }
