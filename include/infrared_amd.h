@@ -149,8 +149,9 @@ int ir_paged_decode_default_partition(int num_seqs, int num_kv_heads, int max_bl
  *   context_lens: [num_seqs] int32 (0 gives a zero output row).
  *   partition_tokens: split-KV partition length in tokens (multiple of 16,
  *                 at most 4096; 0 = ir_paged_decode_default_partition). A sequence longer
- *                 than one partition is split across workgroups whose partials a
- *                 second launch merges with log-sum-exp weights.
+ *                 than one partition is split across workgroups; the last of them to
+ *                 finish (counted on `counters`) merges their fp32 partials with
+ *                 log-sum-exp weights.
  *   counters:     >= ir_paged_decode_num_counters(...) int32, zero-filled before
  *                 first use (required when a sequence can span partitions).
  *   workspace:    >= ir_paged_decode_workspace_size(...) bytes, 256-byte aligned.

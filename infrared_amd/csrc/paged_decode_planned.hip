@@ -442,7 +442,9 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
   const int whi = wlo + cnt_w;
   State<D> st;
   state_init(st);
-  int cur = -1, keep = -1;
+  // pend: a unit finished at the loop's end whose output is written last, so
+  // that no barrier of the end phase waits for its stores
+  int cur = -1, keep = -1, pend = -1;
 
   auto out_row = [&](const Lbl& x, int& h, int& nh) {
     const int hg = a.n_hg == 1 ? 0 : x.j - fdiv(x.j, a.n_hg) * a.n_hg;
@@ -468,6 +470,10 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     st.l = wave_sum_groups(st.l);
     const Lbl x = label(u);
     if (x.us >= wlo && x.ue <= whi) {
+      if (at_end) {
+        pend = u;
+        return;
+      }
       write_out(x);
     } else if (max(x.us, lo) < wlo) {
       slot_write<D>(sl.acc[w][c], sl.m[w], sl.l[w], st, g, c);
@@ -553,14 +559,19 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
       slot_read<D>(sl.acc[w2][c], g, acc2);
       fold_state(st, sl.m[w2][c], sl.l[w2][c], acc2);
     }
-    if (x.us >= lo && x.ue <= hi) write_out(x);
+    if (x.us >= lo && x.ue <= hi) pend = keep;
     else stage_partial(keep, keep == u_first ? 0 : 1);
   }
   __syncthreads();
 
-  // ---- 4. cross-workgroup partials, arrivals and the last arrival's merge
+  // ---- 4. cross-workgroup partials (16-byte device-scope stores), arrivals and
+  // the last arrival's merge
   const int U0 = s_stg[0], U1 = s_stg[1];
-  if (U0 < 0 && U1 < 0) return;
+  if (U0 < 0 && U1 < 0) {
+    if (pend >= 0) write_out(label(pend));
+    return;
+  }
+  const __amdgpu_buffer_rsrc_t r_o = dev_rsrc(a.ws_o), r_ml = dev_rsrc(a.ws_ml);
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int u = k == 0 ? U0 : U1;
@@ -571,15 +582,9 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     for (int it = tid; it < nh * (D / 4); it += NT) {
       const int hc = it / (D / 4);
       const int d0 = (it - hc * (D / 4)) * 4;
-      const int64_t rr = ((int64_t)grp + u) * 16 + hc;
-      float* wo = a.ws_o + rr * D + d0;
-      const f32x4 sv = *(const f32x4*)&stg.acc[k][hc][d0];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) store_dev(wo + q, sv[q]);
-      if (d0 == 0) {
-        store_dev(a.ws_ml + rr * 2 + 0, stg.m[k][hc]);
-        store_dev(a.ws_ml + rr * 2 + 1, stg.l[k][hc]);
-      }
+      const int rr = (grp + u) * 16 + hc;  // < 2^22 rows (plannable), so byte offsets fit int
+      store_dev4(r_o, (rr * D + d0) * 4, *(const f32x4*)&stg.acc[k][hc][d0]);
+      if (d0 == 0) store_dev2(r_ml, rr * 8, f32x2{stg.m[k][hc], stg.l[k][hc]});
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
@@ -609,40 +614,23 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     for (int it = tid; it < nh * (D / 4); it += NT) {
       const int hc = it / (D / 4);
       const int d0 = (it - hc * (D / 4)) * 4;
-      float M = kNegInf, Ls = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-      for (int p0 = 0; p0 < np; p0 += 4) {
-        float pm[4], pl[4], po[4][4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int pp = p0 + q < np ? p0 + q : np - 1;
-          const int64_t rr = ((int64_t)first + pp + u) * 16 + hc;
-          pm[q] = load_dev(a.ws_ml + rr * 2 + 0);
-          pl[q] = load_dev(a.ws_ml + rr * 2 + 1);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) po[q][e] = load_dev(a.ws_o + rr * D + d0 + e);
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (p0 + q >= np) continue;
-          const float Mn = fmaxf(M, pm[q]);
-          const float wa = fast_exp2(M - Mn), wb = fast_exp2(pm[q] - Mn);
-          Ls = wa * Ls + wb * pl[q];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = wa * o[e] + wb * po[q][e];
-          M = Mn;
-        }
-      }
+      float o[4], Ls;
+      lse_merge_dev<D>(r_o, r_ml, (first + u) * 16 + hc, 16, np, d0, o, Ls);
       const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
       store4<DT>((uint8_t*)a.out + ((int64_t)x.b * a.o_seq + (int64_t)(h0 + hc) * a.o_head + d0) * EB, o, inv);
     }
     if (tid == 0) __hip_atomic_store(a.counters + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  if (pend >= 0) write_out(label(pend));
 }
 
 template <int DT, int D>
 void launch_planned_dt_d(const DecodeArgs& a, const uint8_t* plan, const PlanLayout& ly, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((paged_decode_planned_kernel<DT, D, kPlanWaves, 2>), dim3(grid), dim3(kPlanWaves * 64), 0, s, a,
+  // One tile in flight per wavefront: at ~6.6 TB/s four wavefronts per CU keep
+  // HBM saturated with one tile each, and the shorter queues halve the latency
+  // of the end phase's round trips (two tiles in flight: 0.4 us slower per call
+  // on 64 sequences x 28/4 heads, contexts 512..4096).
+  hipLaunchKernelGGL((paged_decode_planned_kernel<DT, D, kPlanWaves, 1>), dim3(grid), dim3(kPlanWaves * 64), 0, s, a,
                      plan, ly);
 }
 
@@ -667,14 +655,16 @@ int64_t t_cap_of(int num_seqs, int n_ups, int max_blocks, int bs) {
 }
 
 // Shapes the plan takes: 16-token tiles inside one block, the prefix sums in
-// LDS, and tile-list indices (and (unit << 5)) in int32.
+// LDS, tile-list indices (and (unit << 5)) in int32, and fewer than 2^17 units,
+// so the partial rows ((#CUs + units) x 16 x head_dim fp32) sit below the 2 GiB
+// the device-scope buffer accesses address.
 bool plannable(int num_seqs, int num_q_heads, int num_kv_heads, int max_blocks, int bs) {
   if (num_seqs <= 0 || num_seqs > kPlanMaxSeqs || num_kv_heads <= 0 || num_q_heads <= 0 ||
       num_q_heads % num_kv_heads || bs <= 0 || bs % 16 != 0 || max_blocks < 0)
     return false;
   const int n_ups = num_kv_heads * n_hg_of(num_q_heads, num_kv_heads);
   return t_cap_of(num_seqs, n_ups, max_blocks, bs) < ((int64_t)1 << 30) &&
-         (int64_t)num_seqs * n_ups < ((int64_t)1 << 21);
+         (int64_t)num_seqs * n_ups < ((int64_t)1 << 17);
 }
 
 }  // namespace

@@ -244,6 +244,48 @@ def test_decode_all_rows_empty():
     assert out.float().abs().max().item() == 0.0
 
 
+_VARIANT_CHILD = r"""
+import sys, torch
+sys.path.insert(0, {root!r})
+from infrared_amd import kernels
+from infrared_amd.workloads import DecodeConfig, make_decode_case
+from oracle import naive as O
+for ctx, part in ((5000, 256), (777, 64), (4096, 0)):
+    cfg = DecodeConfig("variant", 8, 28, 4, 128, 16, torch.bfloat16, "uniform", 1, ctx, seed=ctx)
+    case = make_decode_case(cfg, "cuda")
+    bt = case.block_tables[0]
+    out = kernels.paged_decode(case.q, case.k_cache, case.v_cache, bt, case.context_lens, 16, cfg.scale,
+                               partition_tokens=part)
+    ref = O.decode_reference(case.q.cpu(), case.k_cache.cpu(), case.v_cache.cpu(), bt.cpu(),
+                             case.context_lens.cpu(), 16, cfg.scale, torch.float32)
+    diff = (out.float().cpu() - ref).abs().max().item()
+    print(ctx, part, diff, flush=True)
+    assert diff <= 2e-2, diff
+print("VARIANT OK")
+"""
+
+
+@pytest.mark.parametrize(
+    "env",
+    [{"IR_DECODE_MERGE": "kernel", "IR_DECODE_DEPTH": "2"}, {"IR_DECODE_DEPTH": "3", "IR_DECODE_WAVES": "8"}],
+    ids=["reduce-launch-depth2", "depth3-waves8"],
+)
+def test_decode_launch_variants(env):
+    """The tuning knobs' other launch shapes (a second merge launch, deeper load
+    rings, 8 wavefronts) keep the oracle's results on split and unsplit
+    sequences. The knobs are read once per process, so each runs in a child."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = subprocess.run(
+        [sys.executable, "-c", _VARIANT_CHILD.format(root=root)], env={**os.environ, **env},
+        capture_output=True, text=True, timeout=110, cwd=root,
+    )
+    assert res.returncode == 0 and "VARIANT OK" in res.stdout, res.stdout + res.stderr[-2000:]
+
+
 def test_decode_shared_workspace_across_different_splits():
     """The partial rows start as garbage (every int32 = 2) and are shared by calls
     whose splits and batch sizes differ, as are the arrival counters; each call
