@@ -155,6 +155,10 @@ __global__ __launch_bounds__(256) void paged_decode_reduce(DecodeArgs a) {
   merge_partials<DT, D, false>(a, seq, kvh * a.n_rep + hg * 16, nh, nparts, threadIdx.x, 256);
 }
 
+// (sequence, KV head) units that alone cover the 256 CUs: the default takes one
+// partition per unit from here on.
+constexpr int64_t kUnitsForCUs = 256;
+
 int max_parts_for(int max_blocks, int bs, int part_tokens) {
   const int64_t cap = (int64_t)max_blocks * bs;
   const int64_t p = (cap + part_tokens - 1) / part_tokens;
@@ -182,17 +186,22 @@ WsLayout ws_layout(int num_seqs, int num_q_heads, int head_dim, int max_parts) {
 // IR_DECODE_MERGE ("fused" (default): the last-arriving workgroup merges
 // split-KV partials, when the partial rows sit below 2 GiB; "kernel": a second
 // launch merges them) and IR_DECODE_DEPTH (tile loads a wavefront keeps in its
-// register ring, 1 (default), 2 or 3). Measured per call: 8 fp32 sequences of
-// <= 512 keys 8.2 us (kernel, 2) -> 7.35 us (fused, 1); 16 long-context bf16
-// sequences 35.9 -> 34.7 us.
+// register ring: 1, 2 or 3; by default 2 when the units alone cover the CUs,
+// else 1). With one workgroup per unit, contexts of unequal length leave the
+// call's tail to a few CUs, each of which then needs two tiles in flight per
+// wavefront (64 sequences of 512..4096 keys: 59 us at 2, 79 us at 1); split
+// small batches run faster with one, the shorter memory queues speeding up
+// their merges (8 fp32 sequences of <= 512 keys: 8.2 us with a second merge
+// launch and 2 -> 7.06 us fused with 1; 16 long-context bf16 sequences 35.9 ->
+// 33.6 us).
 struct LaunchKnobs {
   int waves = 4;
   bool fused = true;
-  int depth = 1;
+  int depth = 0;  // 0: by batch, as above
   LaunchKnobs() {
     if (const char* e = getenv("IR_DECODE_WAVES")) waves = atoi(e) == 8 ? 8 : 4;
     if (const char* e = getenv("IR_DECODE_MERGE")) fused = strcmp(e, "kernel") != 0;
-    if (const char* e = getenv("IR_DECODE_DEPTH")) depth = atoi(e) == 3 ? 3 : atoi(e) == 2 ? 2 : 1;
+    if (const char* e = getenv("IR_DECODE_DEPTH")) depth = atoi(e) == 3 ? 3 : atoi(e) == 2 ? 2 : atoi(e) == 1 ? 1 : 0;
   }
 };
 
@@ -220,12 +229,13 @@ void launch_depth(const DecodeArgs& a, int depth, bool fused, hipStream_t s) {
 template <int DT, int D>
 int launch_decode(const DecodeArgs& a, bool bs16, bool fused, hipStream_t s) {
   const LaunchKnobs& k = knobs();
+  const int depth = k.depth ? k.depth : ((int64_t)a.num_seqs * a.num_kv_heads >= kUnitsForCUs ? 2 : 1);
   if (bs16) {
-    if (k.waves == 8) launch_depth<DT, D, true, 8>(a, k.depth, fused, s);
-    else launch_depth<DT, D, true, 4>(a, k.depth, fused, s);
+    if (k.waves == 8) launch_depth<DT, D, true, 8>(a, depth, fused, s);
+    else launch_depth<DT, D, true, 4>(a, depth, fused, s);
   } else {
-    if (k.waves == 8) launch_depth<DT, D, false, 8>(a, k.depth, fused, s);
-    else launch_depth<DT, D, false, 4>(a, k.depth, fused, s);
+    if (k.waves == 8) launch_depth<DT, D, false, 8>(a, depth, fused, s);
+    else launch_depth<DT, D, false, 4>(a, depth, fused, s);
   }
   if (!fused && a.max_parts > 1)
     hipLaunchKernelGGL((paged_decode_reduce<DT, D>), dim3((unsigned)((int64_t)a.num_seqs * a.num_kv_heads * a.n_hg)),
@@ -247,7 +257,7 @@ extern "C" int ir_paged_decode_default_partition(int num_seqs, int num_kv_heads,
   // 1024 tokens (measured: 8 fp32 sequences of <= 512 keys run 28 % faster at
   // 128 than at 1024; 16 long-context sequences are fastest at 1024).
   const int64_t units = (int64_t)num_seqs * num_kv_heads;
-  if (units >= 256) return kMaxPartition;
+  if (units >= kUnitsForCUs) return kMaxPartition;
   const int64_t cap = (int64_t)max_blocks_per_seq * block_size;
   int64_t p = (units * cap / 64 + 15) / 16 * 16;
   if (p < 128) p = 128;

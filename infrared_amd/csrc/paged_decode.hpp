@@ -202,20 +202,31 @@ __device__ __forceinline__ void attend_tiles(const DecodeArgs& a, const int32_t*
       return load_tile<DT, D, BS16>(a, bt_row, bid, kc, vc, lo, t_begin + 16 * (w + NW * i), t_end, lane, tl, bad);
     };
     // Register ring of DEPTH tiles: while one tile is in the math, the next
-    // DEPTH-1 tiles' loads are in flight. The loop body is straight-line so
-    // the loads' wait counts stay exact: issues past the end re-read the last
-    // tile (still in L2) and a slot past the end is computed with an empty key
-    // mask, which changes nothing.
+    // DEPTH-1 tiles' loads are in flight.
     const int last = my_tiles - 1;
     Tile<DT, D> ring[DEPTH];
     uint32_t mk[DEPTH];
 #pragma unroll
     for (int r = 0; r < DEPTH; ++r) mk[r] = issue(min(r, last), ring[r]);
-    for (int i = 0; i < my_tiles; i += DEPTH) {
+    int i = 0;
+    // Steady state: every issue is a real tile, so the body is straight-line
+    // and the loads' wait counts are exact (a conditional issue here makes the
+    // compiler drain the ring every tile: 59 -> 67 us on 64 sequences).
+    for (; i + 2 * DEPTH <= my_tiles; i += DEPTH) {
+#pragma unroll
+      for (int r = 0; r < DEPTH; ++r) {
+        compute_tile<DT, D>(ring[r], qr, mk[r], a.scale_log2, kst, lane, st);
+        mk[r] = issue(i + r + DEPTH, ring[r]);
+      }
+    }
+    // The last tiles: nothing is issued past the end (the merge after the loop
+    // reuses the ring's registers and would wait for such loads); a slot past
+    // the end is computed with an empty key mask, which changes nothing.
+    for (; i < my_tiles; i += DEPTH) {
 #pragma unroll
       for (int r = 0; r < DEPTH; ++r) {
         compute_tile<DT, D>(ring[r], qr, i + r < my_tiles ? mk[r] : 0u, a.scale_log2, kst, lane, st);
-        mk[r] = issue(min(i + r + DEPTH, last), ring[r]);
+        if (i + r + DEPTH <= last) mk[r] = issue(i + r + DEPTH, ring[r]);
       }
     }
   }

@@ -497,16 +497,17 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     const int cnt = min(kPlanRun, cnt_w - r0);
     const int last = cnt - 1;
     // Issues the loads of tile i of the run. Past the run's end (the ring's
-    // last DEPTH issues, never computed) it reads the pool's first 16 rows
-    // instead, one shared tile that stays in L2, rather than re-reading the
-    // wavefront's last tile from HBM; the loop keeps its fixed shape, so the
-    // hardware wait counts stay exact.
+    // last DEPTH issues, never computed) it issues nothing: the end phase
+    // reuses the ring's registers, and a load still in flight into them would
+    // hold it up (padding loads cost 0.7 us per call this way). The branch is
+    // wave-uniform; with one tile in flight each tile's wait is a full drain
+    // anyway, so it costs nothing (a deeper ring would need the steady-state /
+    // tail split of attend_tiles).
     auto issue = [&](int i, Tile<DT, D>& tl, int& lb) -> uint32_t {
       const int ii = i <= last ? i : last;
-      uint32_t off = (uint32_t)__builtin_amdgcn_readlane((int)info_off, ii);
+      const uint32_t off = (uint32_t)__builtin_amdgcn_readlane((int)info_off, ii);
       const uint32_t meta = (uint32_t)__builtin_amdgcn_readlane((int)info_meta, ii);
-      if (i > last) off = 0u;
-      issue_tile<DT, D>(kc, vc, off, lo_off, tl);
+      if (i <= last) issue_tile<DT, D>(kc, vc, off, lo_off, tl);
       lb = (int)(meta >> 5);
       const int valid = (int)(meta & 31u);
       uint32_t m = 0;
