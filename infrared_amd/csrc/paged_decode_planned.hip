@@ -496,18 +496,16 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     }
     const int cnt = min(kPlanRun, cnt_w - r0);
     const int last = cnt - 1;
-    // Issues the loads of tile i of the run. Past the run's end (the ring's
-    // last DEPTH issues, never computed) it issues nothing: the end phase
-    // reuses the ring's registers, and a load still in flight into them would
-    // hold it up (padding loads cost 0.7 us per call this way). The branch is
-    // wave-uniform; with one tile in flight each tile's wait is a full drain
-    // anyway, so it costs nothing (a deeper ring would need the steady-state /
-    // tail split of attend_tiles).
-    auto issue = [&](int i, Tile<DT, D>& tl, int& lb) -> uint32_t {
-      const int ii = i <= last ? i : last;
+    // Issues the loads of tile i of the run (`real`: i is known to be a tile of
+    // the run). Past the run's end (the ring's last DEPTH issues, never
+    // computed) it issues nothing: the end phase reuses the ring's registers,
+    // and a load still in flight into them would hold it up (padding loads
+    // cost 0.7 us per call this way).
+    auto issue = [&](int i, Tile<DT, D>& tl, int& lb, bool real) -> uint32_t {
+      const int ii = real || i <= last ? i : last;
       const uint32_t off = (uint32_t)__builtin_amdgcn_readlane((int)info_off, ii);
       const uint32_t meta = (uint32_t)__builtin_amdgcn_readlane((int)info_meta, ii);
-      if (i <= last) issue_tile<DT, D>(kc, vc, off, lo_off, tl);
+      if (real || i <= last) issue_tile<DT, D>(kc, vc, off, lo_off, tl);
       lb = (int)(meta >> 5);
       const int valid = (int)(meta & 31u);
       uint32_t m = 0;
@@ -518,32 +516,45 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     Tile<DT, D> ring[DEPTH];
     uint32_t mk[DEPTH];
     int lb[DEPTH];
+    // Computes ring slot r, switching units (and queries) at a label change.
+    auto step = [&](int r) {
+      if (lb[r] != cur) {
+        if (cur >= 0) wave_finish(cur, false);
+        cur = lb[r];
+        if (q_lbl != cur) {
+          if (qn_lbl == cur) {
 #pragma unroll
-    for (int r = 0; r < DEPTH; ++r) mk[r] = issue(r, ring[r], lb[r]);
-    for (int i = 0; i < cnt; i += DEPTH) {
+            for (int k = 0; k < Sh::KDW; ++k) qr[k] = qn[k];
+          } else {
+            q_of(cur, qr);
+          }
+          q_lbl = cur;
+        }
+        if (cur + 1 <= ll && qn_lbl != cur + 1) {
+          q_of(cur + 1, qn);
+          qn_lbl = cur + 1;
+        }
+      }
+      compute_tile<DT, D>(ring[r], qr, mk[r], a.scale_log2, kstage[w], lane, st);
+    };
+#pragma unroll
+    for (int r = 0; r < DEPTH; ++r) mk[r] = issue(r, ring[r], lb[r], false);
+    int i = 0;
+    // Steady state: every issue is a real tile and the body has no branch
+    // around it (the branch cost 0.9 us per call on 64 sequences, even with
+    // one tile in flight); then the last DEPTH..2 DEPTH - 1 tiles.
+    for (; i + 2 * DEPTH <= cnt; i += DEPTH) {
 #pragma unroll
       for (int r = 0; r < DEPTH; ++r) {
-        if (i + r < cnt) {
-          if (lb[r] != cur) {
-            if (cur >= 0) wave_finish(cur, false);
-            cur = lb[r];
-            if (q_lbl != cur) {
-              if (qn_lbl == cur) {
+        step(r);
+        mk[r] = issue(i + r + DEPTH, ring[r], lb[r], true);
+      }
+    }
+    for (; i < cnt; i += DEPTH) {
 #pragma unroll
-                for (int k = 0; k < Sh::KDW; ++k) qr[k] = qn[k];
-              } else {
-                q_of(cur, qr);
-              }
-              q_lbl = cur;
-            }
-            if (cur + 1 <= ll && qn_lbl != cur + 1) {
-              q_of(cur + 1, qn);
-              qn_lbl = cur + 1;
-            }
-          }
-          compute_tile<DT, D>(ring[r], qr, mk[r], a.scale_log2, kstage[w], lane, st);
-        }
-        mk[r] = issue(i + r + DEPTH, ring[r], lb[r]);
+      for (int r = 0; r < DEPTH; ++r) {
+        if (i + r < cnt) step(r);
+        mk[r] = issue(i + r + DEPTH, ring[r], lb[r], false);
       }
     }
   }
