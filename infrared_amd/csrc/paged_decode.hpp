@@ -289,24 +289,33 @@ __device__ __forceinline__ f32x2 load_dev2(__amdgpu_buffer_rsrc_t r, int off) {
 // Log-sum-exp merge of n partial rows read at device scope, four rows' loads in
 // flight at a time: row p is row0 + p * step, its D fp32 accumulators at byte
 // (row * D) * 4 of r_o and its (max, sum) pair at byte row * 8 of r_ml. Gives
-// the unnormalised o[d0..d0+3] and the sum L. Rows with no key (max -inf) add
+// the unnormalised o[d0..d0+W) (W = 4 or 8) and the sum L. Rows with no key (max -inf) add
 // nothing: an exponent of -inf - -inf is NaN, which fmaxf turns into -1e30
 // (weight 0) without a branch (branches here measured 0.5 us per call slower).
-template <int D>
+template <int D, int W = 4>
 __device__ __forceinline__ void lse_merge_dev(__amdgpu_buffer_rsrc_t r_o, __amdgpu_buffer_rsrc_t r_ml, int row0,
-                                              int step, int n, int d0, float (&o)[4], float& L) {
+                                              int step, int n, int d0, float (&o)[W], float& L) {
+  static_assert(W == 4 || W == 8, "4 or 8 columns");
   float M = kNegInf;
   L = 0.f;
-  o[0] = o[1] = o[2] = o[3] = 0.f;
+#pragma unroll
+  for (int e = 0; e < W; ++e) o[e] = 0.f;
 #pragma unroll 1
   for (int p0 = 0; p0 < n; p0 += 4) {
     f32x2 ml[4];
-    f32x4 po[4];
+    float po[4][W];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int row = row0 + (p0 + q < n ? p0 + q : n - 1) * step;
       ml[q] = load_dev2(r_ml, row * 8);
-      po[q] = load_dev4(r_o, (row * D + d0) * 4);
+#pragma unroll
+      for (int h = 0; h < W; h += 4) {
+        const f32x4 v = load_dev4(r_o, (row * D + d0 + h) * 4);
+        po[q][h] = v[0];
+        po[q][h + 1] = v[1];
+        po[q][h + 2] = v[2];
+        po[q][h + 3] = v[3];
+      }
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -315,7 +324,7 @@ __device__ __forceinline__ void lse_merge_dev(__amdgpu_buffer_rsrc_t r_o, __amdg
       const float wa = fast_exp2(fmaxf(M - Mn, -1e30f)), wb = fast_exp2(fmaxf(ml[q][0] - Mn, -1e30f));
       L = wa * L + wb * ml[q][1];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = wa * o[e] + wb * po[q][e];
+      for (int e = 0; e < W; ++e) o[e] = wa * o[e] + wb * po[q][e];
       M = Mn;
     }
   }

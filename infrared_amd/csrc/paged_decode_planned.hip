@@ -613,26 +613,47 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     s_last[tid] = lst;
   }
   __syncthreads();
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int u = k == 0 ? U0 : U1;
-    if (u < 0 || !s_last[k]) continue;
-    const Lbl x = label(u);
-    const int first = x.us / R;
-    const int np = (x.ue - 1) / R - first + 1;
-    int h0, nh;
-    out_row(x, h0, nh);
-    h0 -= c;
-    for (int it = tid; it < nh * (D / 4); it += NT) {
-      const int hc = it / (D / 4);
-      const int d0 = (it - hc * (D / 4)) * 4;
-      float o[4], Ls;
-      lse_merge_dev<D>(r_o, r_ml, (first + u) * 16 + hc, 16, np, d0, o, Ls);
-      const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
-      store4<DT>((uint8_t*)a.out + ((int64_t)x.b * a.o_seq + (int64_t)(h0 + hc) * a.o_head + d0) * EB, o, inv);
-    }
-    if (tid == 0) __hip_atomic_store(a.counters + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Both units' merges in one pass, so their loads are in flight together (one
+  // after the other, the slices that end last -- which merge both -- took 2.15
+  // instead of 1.17 us): items of 8 columns of one head, U0's first.
+  constexpr int C8 = D / 8;
+  int n0 = 0, n1 = 0, b0 = 0, b1 = 0, h00 = 0, h01 = 0, f0r = 0, f1r = 0, np0 = 0, np1 = 0;
+  if (U0 >= 0 && s_last[0]) {
+    const Lbl x = label(U0);
+    int nh;
+    out_row(x, h00, nh);
+    h00 -= c;
+    n0 = nh * C8;
+    b0 = x.b;
+    f0r = (x.us / R + U0) * 16;
+    np0 = (x.ue - 1) / R - x.us / R + 1;
   }
+  if (U1 >= 0 && s_last[1]) {
+    const Lbl x = label(U1);
+    int nh;
+    out_row(x, h01, nh);
+    h01 -= c;
+    n1 = nh * C8;
+    b1 = x.b;
+    f1r = (x.us / R + U1) * 16;
+    np1 = (x.ue - 1) / R - x.us / R + 1;
+  }
+  for (int it = tid; it < n0 + n1; it += NT) {
+    const bool k1 = it >= n0;
+    const int j = k1 ? it - n0 : it;
+    const int hc = j / C8;
+    const int d0 = (j - hc * C8) * 8;
+    float o[8], Ls;
+    lse_merge_dev<D, 8>(r_o, r_ml, (k1 ? f1r : f0r) + hc, 16, k1 ? np1 : np0, d0, o, Ls);
+    const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+    uint8_t* dst = (uint8_t*)a.out +
+                   ((int64_t)(k1 ? b1 : b0) * a.o_seq + (int64_t)((k1 ? h01 : h00) + hc) * a.o_head + d0) * EB;
+    const float lo4[4] = {o[0], o[1], o[2], o[3]}, hi4[4] = {o[4], o[5], o[6], o[7]};
+    store4<DT>(dst, lo4, inv);
+    store4<DT>(dst + 4 * EB, hi4, inv);
+  }
+  if (tid == 0 && n0) __hip_atomic_store(a.counters + U0, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 1 && n1) __hip_atomic_store(a.counters + U1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (pend >= 0) write_out(label(pend));
 }
 
