@@ -242,19 +242,25 @@ _CU_COUNT: dict[int, int] = {}
 def decode_plan_pays(num_seqs: int, num_q_heads: int, num_kv_heads: int, max_blocks: int, block_size: int,
                      device: torch.device | str | int | None = None) -> bool:
     """Whether the planned schedule is the faster decode for this shape: it is
-    plannable and the batch has at least one unit (sequence x KV head x group
-    of <= 16 query heads) per CU. Smaller batches leave most slices idle and run
-    faster on :func:`paged_decode`'s fixed split-KV partitions (measured on
-    MI355X: 8 fp32 sequences 8.2 vs 11.5 us, 16 skewed long ones 35.8 vs
-    36.9 us; 64 x 4 KV heads 59.1 vs 54.3 us in favour of the plan)."""
+    plannable, and either the batch has a unit (sequence x KV head x group of
+    <= 16 query heads) per CU or its block tables can hold 16 tiles (256 keys)
+    per CU across the units. Below that the work is too small to spread: the
+    plan's per-call overhead outweighs the balance, and :func:`paged_decode`'s
+    fixed split-KV partitions win. Measured on MI355X (28 q / 4 kv heads, bf16,
+    per call): 64 sequences 57.2 (fixed) vs 49.7 us; 8 of 2k..32k keys 72.0 vs
+    55.0 us; 16 skewed long ones 33.4 vs 31.8 us; 16 of 16..1024 keys 16.3 vs
+    11.6 us; but 8 fp32 sequences of <= 512 keys 7.1 vs 10.5 us and 16 of <= 300
+    keys in tables of that width 7.9 vs 11.0 us."""
     if decode_plan_bytes(num_seqs, num_q_heads, num_kv_heads, max_blocks, block_size) <= 0:
         return False
     idx = torch.device(device if device is not None else "cuda").index
     idx = torch.cuda.current_device() if idx is None else idx
     if idx not in _CU_COUNT:
         _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    cus = _CU_COUNT[idx]
     units = num_seqs * num_kv_heads * ((num_q_heads // num_kv_heads + 15) // 16)
-    return units >= _CU_COUNT[idx]
+    tiles = units * ((max_blocks * block_size + 15) // 16)
+    return units >= cus or tiles >= 16 * cus
 
 
 def planned_workspace_bytes(num_seqs: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
