@@ -5,8 +5,9 @@ Workload (default): Qwen2.5-7B-shape paged decode — 64 sequences, 28 query /
 tables drawn from a random permutation of a pool 1.25x the blocks needed,
 q/K/V ~ N(0, 1) (synthetic: random values, no checkpoint). One step = one
 decode-attention call for the whole batch (one layer). The schedule is the
-seam's: for a batch with at least one (sequence, KV head) unit per CU (C2) the
-planned one -- ir_paged_decode_plan builds the balanced schedule of the
+seam's: for a batch with at least one (sequence, KV head) unit per CU, or
+block tables holding 16 tiles per CU (C2, C3), the planned one --
+ir_paged_decode_plan builds the balanced schedule of the
 batch's metadata once per decode step and every layer runs
 ir_paged_decode_planned on it, so the timed loop rebuilds a plan every
 ``--layers`` (28) calls -- otherwise ir_paged_decode's fixed split-KV
@@ -62,7 +63,7 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--rotations", type=int, default=3)
     p.add_argument("--partition", type=int, default=0, help="split-KV partition tokens (0 = library default)")
     p.add_argument("--schedule", choices=("auto", "planned", "fixed"), default="auto",
-                   help="decode: the seam's choice (default: planned when the batch has a unit per CU), "
+                   help="decode: the seam's choice (default: kernels.decode_plan_pays), "
                    "balanced plan + run, or fixed split-KV partitions")
     p.add_argument("--layers", type=int, default=28,
                    help="decode: calls per plan (layers of one decode step sharing its metadata)")
@@ -71,7 +72,8 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--check", action="store_true", help="also check the output against the oracle")
     p.add_argument("--mode", choices=("graph", "eager"), default="graph",
                    help="time a hipGraph replay of the K calls (default) or host-launched calls")
-    p.add_argument("--no-overlap", action="store_true", help="mixed: decode and prefill on one stream")
+    p.add_argument("--overlap", action="store_true",
+                   help="mixed: decode and prefill on two streams (default: one stream, measured faster)")
     p.add_argument("--copy-calib-mib", type=int, default=0,
                    help="after timing, run 10 device copies of this many MiB (counter calibration)")
     return p.parse_args()
@@ -282,7 +284,7 @@ def _bench_mixed(args) -> dict:
     from infrared_amd.mixed_step import MixedStep, make_mixed_case
 
     cfg, pool, batch, inputs = make_mixed_case("qwen7b-mixed", "cuda")
-    step = MixedStep(pool, batch, inputs, cfg.scale, overlap=not args.no_overlap)
+    step = MixedStep(pool, batch, inputs, cfg.scale, overlap=args.overlap)
     step.capture()
     for _ in range(max(1, args.warmup // 10)):
         step.replay()
@@ -335,7 +337,7 @@ def _bench_mixed(args) -> dict:
                    f"[{cfg.decode_ctx_lo},{cfg.decode_ctx_hi}], {cfg.num_prefill} x {cfg.chunk}-token chunks, "
                    f"{cfg.num_q_heads}q/{cfg.num_kv_heads}kv heads, head_dim {cfg.head_dim}, block {cfg.block_size}",
                    "decode_kv_bytes_per_step": dec_bytes, "prefill_flops_per_step": pre_flops,
-                   "scatter_bytes_per_step": scatter_bytes, "overlap_streams": not args.no_overlap,
+                   "scatter_bytes_per_step": scatter_bytes, "overlap_streams": args.overlap,
                    "replays": n},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,

@@ -11,12 +11,16 @@
 // infrared/engine/paged_engine.py:461-516 (a decode row is a sequence with one
 // query token at position context - 1).
 //
-// Work decomposition: one workgroup of 8 wavefronts (two per SIMD) per (query
-// block, KV head, sequence); heaviest query blocks (most keys) are dispatched
-// first. A query block is TQ = 256 / n_rep tokens, so the block's (token,
-// query head) pairs of the GQA group -- column j = token-in-block * n_rep +
-// head -- fill 256 columns almost exactly (7 heads: 36 tokens, 252 columns);
-// wavefront w owns columns 32w .. 32w+31 (two 16-column tiles). Every column
+// Work decomposition: one workgroup of NW wavefronts per (query block, KV
+// head, sequence); heaviest query blocks (most keys) are dispatched first. NW
+// is 8 (two per SIMD) unless that gives fewer workgroups than CUs; then 4 (one
+// per SIMD, up to 512 registers), twice the workgroups with half the columns
+// each, which shortens a small batch's critical path (4 x 256-token chunks:
+// 19.0 -> 16.6 us; a large one runs twice as long with 4). A query block is
+// TQ = 32 NW / n_rep tokens, so the block's (token, query head) pairs of the
+// GQA group -- column j = token-in-block * n_rep + head -- fill 32 NW columns
+// almost exactly (8 wavefronts, 7 heads: 36 tokens, 252 columns); wavefront w
+// owns columns 32w .. 32w+31 (two 16-column tiles). Every column
 // of a workgroup reads the same KV head, so each K/V element staged in LDS
 // feeds 32 columns per wavefront read. The workgroup walks the keys in
 // 64-key tiles staged in LDS, double buffered: the next tile's global loads
@@ -37,6 +41,8 @@
 // gathered history (infrared/model/triton_attention.py:110-129), streaming as
 // in infrared/model/triton_attention.py:135-177; probabilities are rounded to
 // the input dtype before the PV product, as softmax(...).to(q.dtype) does.
+#include <stdlib.h>
+
 #include <type_traits>
 
 #include "attn_tile.hpp"
@@ -65,13 +71,14 @@ struct PrefillArgs {
   void* out;
   int64_t o_tok, o_head;  // elements
   int num_q_heads, num_kv_heads, n_rep, tq;  // tq: query tokens per workgroup
+  int nw;                                    // wavefronts per workgroup (4 or 8)
   float scale_log2;
   int32_t* err;
 };
 
-template <int D>
+template <int D, int NW_ = 8>
 struct PShape {
-  static constexpr int NW = 8;    // wavefronts per workgroup (two per SIMD)
+  static constexpr int NW = NW_;  // wavefronts per workgroup (8: two per SIMD; 4: one)
   static constexpr int CT = 2;    // 16-column tiles per wavefront
   static constexpr int COLS = NW * CT * 16;  // (token, head) columns per workgroup
   static constexpr int BN = 64;   // keys per tile
@@ -91,10 +98,10 @@ struct PShape {
 
 // FAST: power-of-two block size and a pool layer small enough for 24-bit slot
 // and stride products (32-bit element offsets).
-template <int DT, int D, bool FAST>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+template <int DT, int D, bool FAST, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 2 : 1)))
 void paged_prefill_kernel(PrefillArgs a) {
-  typedef PShape<D> S;
+  typedef PShape<D, NW> S;
   constexpr int EB = 2;
   constexpr int CT = S::CT, BN = S::BN, NT = S::NT;
   __shared__ __attribute__((aligned(16))) uint16_t ks_lds[3][BN * S::KROW];
@@ -448,11 +455,19 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   const int64_t slots = a.num_blocks * a.bs;
   const bool fast = a.bs_shift >= 0 && slots < (1 << 23) && a.c_slot < (1 << 23) &&
                     (slots * a.c_slot + a.c_head * a.num_kv_heads) < ((int64_t)1 << 31);
-  const dim3 block(PShape<D>::NT);
-  if (fast)
-    hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true>), dim3((unsigned)grid), block, 0, s, a);
-  else
-    hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false>), dim3((unsigned)grid), block, 0, s, a);
+  if (a.nw == 4) {
+    const dim3 block(PShape<D, 4>::NT);
+    if (fast)
+      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 4>), dim3((unsigned)grid), block, 0, s, a);
+    else
+      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 4>), dim3((unsigned)grid), block, 0, s, a);
+  } else {
+    const dim3 block(PShape<D, 8>::NT);
+    if (fast)
+      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8>), dim3((unsigned)grid), block, 0, s, a);
+    else
+      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8>), dim3((unsigned)grid), block, 0, s, a);
+  }
   return check_launch("ir_paged_prefill");
 }
 
@@ -511,7 +526,18 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
   a.num_seqs = num_seqs;
   a.total_q = total_q;
   a.n_rep = num_q_heads / num_kv_heads;
-  a.tq = PShape<128>::COLS / a.n_rep;
+  // Workgroups of 8 wavefronts (256 query columns) unless that leaves CUs
+  // idle: then 4 (128 columns), twice the workgroups, half the work each.
+  // IR_PREFILL_WAVES (4 or 8) forces one for tuning runs.
+  {
+    const int tq8 = PShape<128, 8>::COLS / a.n_rep;
+    const int64_t wgs8 = (int64_t)((max_q_len + tq8 - 1) / tq8) * num_kv_heads * num_seqs;
+    const char* e = getenv("IR_PREFILL_WAVES");
+    // (4 wavefronts hold at most 128 query heads per KV head)
+    const bool four = a.n_rep <= PShape<128, 4>::COLS && (e ? atoi(e) == 4 : wgs8 < 256);
+    a.nw = four ? 4 : 8;
+    a.tq = (four ? PShape<128, 4>::COLS : PShape<128, 8>::COLS) / a.n_rep;
+  }
   a.n_qblocks = (max_q_len + a.tq - 1) / a.tq;
   a.out = out;
   a.o_tok = out_tok_stride;

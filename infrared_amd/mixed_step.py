@@ -16,10 +16,14 @@ metadata:
    ``ir_paged_decode``'s fixed split-KV partitions;
 3. ``ir_paged_prefill`` for the chunks (causal after their cached prefix).
 
-With ``overlap=True`` the decode (HBM-bound) and prefill (MFMA-bound) launches
-of a layer run on two streams that fork after the scatter and join before the
-next layer's scatter; captured, they become parallel graph branches. Both
-streams have the default priority.
+By default the three run on one stream. With ``overlap=True`` the decode
+(HBM-bound) and prefill (MFMA-bound) launches of a layer run on two streams
+that fork after the scatter and join before the next layer's scatter;
+captured, they become parallel graph branches (both streams at the default
+priority). That measured slower on MI355X (203 vs 190 us per layer at
+224 decode rows + 4 x 256-token chunks): the planned decode runs one
+workgroup per CU, and the prefill's workgroups (110 KB of LDS each) hold CUs
+that those slices then wait for.
 
 The per-layer projections around attention are not part of this path; the
 caller supplies each layer's q and new K/V (``MixedInputs``).
@@ -148,7 +152,7 @@ class MixedStep:
     """
 
     def __init__(self, pool: PagedKVPool, batch: MixedBatch, inputs: MixedInputs, scale: float, *,
-                 overlap: bool = True) -> None:
+                 overlap: bool = False) -> None:
         self.pool, self.batch, self.inputs, self.scale = pool, batch, inputs, scale
         self.overlap = overlap
         dev = pool.device

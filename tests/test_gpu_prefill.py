@@ -81,6 +81,17 @@ def test_prefill_shape_sweep(dtype, h_q, h_kv, d, bs, layout):
     _check(case)
 
 
+def test_prefill_workgroup_sizes_agree():
+    """Small batches run 4-wavefront workgroups (128 query columns), large ones
+    8 (256; the full-size test above): a 2-sequence batch on 4, and 160 query
+    heads per KV head, which 4 wavefronts cannot hold, on 8 -- both match the
+    oracle."""
+    small = PrefillConfig("pf-small", 2, 0, 28, 4, 128, 16, torch.bfloat16, 0, seed=21)
+    _check(make_prefill_case(small, DEV, prefixes=[0, 300], q_lens=[256, 77]))
+    wide = PrefillConfig("pf-wide-group", 2, 0, 160, 1, 64, 16, torch.bfloat16, 0, seed=22)
+    _check(make_prefill_case(wide, DEV, prefixes=[40, 0], q_lens=[5, 3]))
+
+
 def test_prefill_block_id_cache_reload():
     """Block size 1 and a 2600-token context: the workgroup's staged block ids
     (1024 at a time) are refilled mid-walk."""
