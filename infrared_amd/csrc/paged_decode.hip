@@ -252,15 +252,15 @@ extern "C" int ir_paged_decode_default_partition(int num_seqs, int num_kv_heads,
                                                  int block_size) {
   // One partition per (sequence, KV head) when those units alone cover the
   // 256 CUs: no split-KV merge, fewest per-workgroup prologues. Smaller
-  // batches split their keys so the table capacity spreads over about 64
-  // workgroups or more, in partitions of 128 (two tiles per wavefront) to
-  // 1024 tokens (measured: 8 fp32 sequences of <= 512 keys run 28 % faster at
-  // 128 than at 1024; 16 long-context sequences are fastest at 1024).
+  // batches split their keys so the table capacity spreads over about 128
+  // workgroups or more, in partitions of 64 (one tile per wavefront) to 1024
+  // tokens (measured: 8 fp32 sequences of <= 512 keys 6.85 us at 64, 7.25 us
+  // at 128, 10.4 us at 512; 16 long-context sequences are fastest at 1024).
   const int64_t units = (int64_t)num_seqs * num_kv_heads;
   if (units >= kUnitsForCUs) return kMaxPartition;
   const int64_t cap = (int64_t)max_blocks_per_seq * block_size;
-  int64_t p = (units * cap / 64 + 15) / 16 * 16;
-  if (p < 128) p = 128;
+  int64_t p = (units * cap / 128 + 15) / 16 * 16;
+  if (p < 64) p = 64;
   if (p > 1024) p = 1024;
   return (int)p;
 }

@@ -286,13 +286,13 @@ __device__ __forceinline__ f32x2 load_dev2(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCacheSc1);
 }
 
-// Log-sum-exp merge of n partial rows read at device scope, four rows' loads in
+// Log-sum-exp merge of n partial rows read at device scope, NB rows' loads in
 // flight at a time: row p is row0 + p * step, its D fp32 accumulators at byte
 // (row * D) * 4 of r_o and its (max, sum) pair at byte row * 8 of r_ml. Gives
 // the unnormalised o[d0..d0+W) (W = 4 or 8) and the sum L. Rows with no key (max -inf) add
 // nothing: an exponent of -inf - -inf is NaN, which fmaxf turns into -1e30
 // (weight 0) without a branch (branches here measured 0.5 us per call slower).
-template <int D, int W = 4>
+template <int D, int W = 4, int NB = 4>
 __device__ __forceinline__ void lse_merge_dev(__amdgpu_buffer_rsrc_t r_o, __amdgpu_buffer_rsrc_t r_ml, int row0,
                                               int step, int n, int d0, float (&o)[W], float& L) {
   static_assert(W == 4 || W == 8, "4 or 8 columns");
@@ -301,11 +301,11 @@ __device__ __forceinline__ void lse_merge_dev(__amdgpu_buffer_rsrc_t r_o, __amdg
 #pragma unroll
   for (int e = 0; e < W; ++e) o[e] = 0.f;
 #pragma unroll 1
-  for (int p0 = 0; p0 < n; p0 += 4) {
-    f32x2 ml[4];
-    float po[4][W];
+  for (int p0 = 0; p0 < n; p0 += NB) {
+    f32x2 ml[NB];
+    float po[NB][W];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < NB; ++q) {
       const int row = row0 + (p0 + q < n ? p0 + q : n - 1) * step;
       ml[q] = load_dev2(r_ml, row * 8);
 #pragma unroll
@@ -318,7 +318,7 @@ __device__ __forceinline__ void lse_merge_dev(__amdgpu_buffer_rsrc_t r_o, __amdg
       }
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < NB; ++q) {
       if (p0 + q >= n) continue;
       const float Mn = fmaxf(M, ml[q][0]);
       const float wa = fast_exp2(fmaxf(M - Mn, -1e30f)), wb = fast_exp2(fmaxf(ml[q][0] - Mn, -1e30f));
