@@ -286,12 +286,15 @@ __device__ __forceinline__ f32x2 load_dev2(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCacheSc1);
 }
 
-// Log-sum-exp merge of n partial rows read at device scope, NB rows' loads in
-// flight at a time: row p is row0 + p * step, its D fp32 accumulators at byte
-// (row * D) * 4 of r_o and its (max, sum) pair at byte row * 8 of r_ml. Gives
-// the unnormalised o[d0..d0+W) (W = 4 or 8) and the sum L. Rows with no key (max -inf) add
-// nothing: an exponent of -inf - -inf is NaN, which fmaxf turns into -1e30
-// (weight 0) without a branch (branches here measured 0.5 us per call slower).
+// Log-sum-exp merge of n partial rows read at device scope, up to NB rows'
+// loads in flight at a time (only rows that exist are read): row p is row0 +
+// p * step, its D fp32 accumulators at byte (row * D) * 4 of r_o and its
+// (max, sum) pair at byte row * 8 of r_ml. Gives the unnormalised
+// o[d0..d0+W) (W = 4 or 8) and the sum L. The arithmetic order depends on n
+// alone, so merges of the same rows are bit-identical whoever runs them. Rows
+// with no key (max -inf) add nothing: an exponent of -inf - -inf is NaN, which
+// fmaxf turns into -1e30 (weight 0) without a branch (branches here measured
+// 0.5 us per call slower).
 template <int D, int W = 4, int NB = 4>
 __device__ __forceinline__ void lse_merge_dev(__amdgpu_buffer_rsrc_t r_o, __amdgpu_buffer_rsrc_t r_ml, int row0,
                                               int step, int n, int d0, float (&o)[W], float& L) {
@@ -306,7 +309,8 @@ __device__ __forceinline__ void lse_merge_dev(__amdgpu_buffer_rsrc_t r_o, __amdg
     float po[NB][W];
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
-      const int row = row0 + (p0 + q < n ? p0 + q : n - 1) * step;
+      if (q > 0 && p0 + q >= n) continue;  // the batch's first row always exists
+      const int row = row0 + (p0 + q) * step;
       ml[q] = load_dev2(r_ml, row * 8);
 #pragma unroll
       for (int h = 0; h < W; h += 4) {

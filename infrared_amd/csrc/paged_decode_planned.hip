@@ -644,7 +644,7 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     const int hc = j / C8;
     const int d0 = (j - hc * C8) * 8;
     float o[8], Ls;
-    lse_merge_dev<D, 8>(r_o, r_ml, (k1 ? f1r : f0r) + hc, 16, k1 ? np1 : np0, d0, o, Ls);
+    lse_merge_dev<D, 8, 8>(r_o, r_ml, (k1 ? f1r : f0r) + hc, 16, k1 ? np1 : np0, d0, o, Ls);
     const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
     uint8_t* dst = (uint8_t*)a.out +
                    ((int64_t)(k1 ? b1 : b0) * a.o_seq + (int64_t)((k1 ? h01 : h00) + hc) * a.o_head + d0) * EB;
