@@ -368,6 +368,8 @@ def _bench_rope(args) -> dict:
         kernels.rope_kv_scatter(q, k, v, cos, sin, kc, vc, slots, q_out=q_out)
 
     ms = _time_graph(call, args) if args.mode == "graph" else _time_eager(call, args)
+    if args.copy_calib_mib > 0:
+        _copy_calibration(args.copy_calib_mib)
     nbytes = (2 * n * hq * d + 4 * n * hkv * d) * 2 + 2 * n * d * 4 + n * 8
     gbps = nbytes / (ms * 1e-3) / 1e9
     return {

@@ -16,10 +16,24 @@
 // round to nearest even). In fp32 the same three operations run unfused (no
 // multiply-add contraction), so results are bit-identical to the reference.
 //
-// Work: one lane per (token, row, 8-element chunk of the first half); it also
-// handles the matching 8 elements of the second half, which is what rotate_half
-// pairs them with. Rows of a token: num_q_heads q rows, then num_kv_heads k
-// rows, then num_kv_heads v rows.
+// Work: one workgroup per token, a 2-D block of (head_dim/16 chunks) x (rows);
+// lane (c, r) takes 8-element chunk c of the first half of row r and the
+// matching 8 elements of the second half, which is what rotate_half pairs them
+// with. Rows of a token: num_q_heads q rows, then num_kv_heads k rows, then
+// num_kv_heads v rows (v is copied as is). The token's cos/sin rows are
+// rounded once per wavefront into that wavefront's LDS (1 KB at head_dim 128)
+// instead of being reloaded and rerounded by every lane; the row loads are
+// issued before the tables are waited on, and lanes past the last row load a
+// real row so no branch separates the loads. Row offsets are 24-bit products
+// when every stride allows it. Measured on MI355X for 1,248 tokens of 28 q /
+// 4 kv heads, head_dim 128, bf16, head-major pool (24.3 MB): 4.9 us per call,
+// against 3.8 us for the same accesses with no tables or rotation and 11.3 us
+// for one lane per (token, row, chunk) with software rounding; several tokens
+// per workgroup, one wavefront per workgroup, q and k/v in separate
+// workgroups, and two rows per lane all measured slower.
+#include <algorithm>
+#include <type_traits>
+
 #include "common.hpp"
 #include "status.hpp"
 
@@ -70,10 +84,6 @@ struct Chunk8 {
       }
     }
   }
-  __device__ __forceinline__ static void copy(const uint8_t* src, uint8_t* dst) {
-    *(u32x4*)dst = *(const u32x4*)src;
-    if constexpr (DT == IR_DTYPE_F32) *(u32x4*)(dst + 16) = *(const u32x4*)(src + 16);
-  }
   __device__ __forceinline__ static void store(uint8_t* p, const float (&x)[8]) {
     if constexpr (DT == IR_DTYPE_F32) {
       *(f32x4*)p = f32x4{x[0], x[1], x[2], x[3]};
@@ -83,80 +93,157 @@ struct Chunk8 {
       *(u32x4*)p = u32x4{E::pack2(x[0], x[1]), E::pack2(x[2], x[3]), E::pack2(x[4], x[5]), E::pack2(x[6], x[7])};
     }
   }
-  // value rounded to the dtype (identity for fp32)
-  __device__ __forceinline__ static float round(float f) {
-    if constexpr (DT == IR_DTYPE_F32) return f;
-    else return Elem<DT>::to_f32(Elem<DT>::from_f32(f));
+  struct Raw {
+    u32x4 w[EB / 2];
+  };
+  __device__ __forceinline__ static void raw_load(const uint8_t* p, Raw& r) {
+#pragma unroll
+    for (int i = 0; i < EB / 2; ++i) r.w[i] = *(const u32x4*)(p + 16 * i);
+  }
+  __device__ __forceinline__ static void raw_store(uint8_t* p, const Raw& r) {
+#pragma unroll
+    for (int i = 0; i < EB / 2; ++i) *(u32x4*)(p + 16 * i) = r.w[i];
+  }
+  __device__ __forceinline__ static void unpack(const Raw& r, float (&x)[8]) {
+    if constexpr (DT == IR_DTYPE_F32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[i] = __uint_as_float(r.w[0][i]);
+        x[4 + i] = __uint_as_float(r.w[1][i]);
+      }
+    } else {
+      using E = Elem<DT>;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[2 * i] = E::lo(r.w[0][i]);
+        x[2 * i + 1] = E::hi(r.w[0][i]);
+      }
+    }
+  }
+  // each value rounded to the dtype, to nearest even, two per conversion
+  // instruction (identity for fp32)
+  __device__ __forceinline__ static void round8(float (&x)[8]) {
+    if constexpr (DT != IR_DTYPE_F32) {
+      using E = Elem<DT>;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w = E::pack2(x[2 * i], x[2 * i + 1]);
+        x[2 * i] = E::lo(w);
+        x[2 * i + 1] = E::hi(w);
+      }
+    }
   }
 };
 
-template <int DT>
-__global__ __launch_bounds__(256) void rope_kv_scatter_kernel(RopeArgs a) {
+template <int DT, bool WIDE>
+__global__ __launch_bounds__(1024) void rope_kv_scatter_kernel(RopeArgs a) {
 #pragma clang fp contract(off)
   typedef Chunk8<DT> C;
-  const int half = a.head_dim / 2;
-  const int chunks = half / 8;
-  const int rows = a.num_q_heads + 2 * a.num_kv_heads;
-  const int64_t per_tok = (int64_t)rows * chunks;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= a.n_tokens * per_tok) return;
-  const int64_t tok = idx / per_tok;
-  const int rem = (int)(idx - tok * per_tok);
-  const int row = rem / chunks;
-  const int i0 = (rem - row * chunks) * 8;  // first-half element index
-  const int64_t off1 = (int64_t)i0 * C::EB, off2 = (int64_t)(i0 + half) * C::EB;
-
-  const bool is_q = row < a.num_q_heads;
-  const bool is_k = !is_q && row < a.num_q_heads + a.num_kv_heads;
-  int64_t slot = 0;
-  if (!is_q) {
-    slot = a.slots[tok];
-    if (slot < 0) return;  // padding sentinel
-    if (slot >= a.num_slots) {
-      flag_error(a.err, IR_ERR_SLOT_RANGE);
-      return;
-    }
+  typedef typename std::conditional<WIDE, int64_t, uint32_t>::type Off;
+  extern __shared__ float tab[];  // per wavefront: [cos | sin], head_dim each, rounded to the dtype
+  const int D = a.head_dim, half = D / 2;
+  const int nq = a.num_q_heads, nkv = a.num_kv_heads;
+  const int rows = nq + 2 * nkv;
+  const int64_t tok = blockIdx.x;
+  const int ci = threadIdx.x;  // 8-element chunk of the first half
+  const int row = blockIdx.y * blockDim.y + threadIdx.y;
+  const int tid = threadIdx.y * blockDim.x + threadIdx.x;
+  const int lane = tid & 63;
+  const int i0 = ci * 8;
+  const int off1 = i0 * C::EB, off2 = (i0 + half) * C::EB;
+  // lanes past the last row load a real row (the last) and store nothing
+  const bool in = row < rows;
+  const int rr = in ? row : rows - 1;
+  const bool is_q = rr < nq, is_v = rr >= nq + nkv;
+  const int h = is_q ? rr : (is_v ? rr - nq - nkv : rr - nq);  // head within q, k or v
+  auto mul = [](int r, int64_t stride) -> Off {
+    if constexpr (WIDE) return (int64_t)r * stride;
+    else return __umul24((uint32_t)r, (uint32_t)stride);
+  };
+  // the wavefront's own copy of the token's tables, rounded once: one 16-byte
+  // load of each table per lane covers head_dim <= 256 (clamped, no branch, so
+  // the row loads below go out before the tables are waited on)
+  const float* cs = a.cos + tok * a.cs_tok;
+  const float* sn = a.sin + tok * a.cs_tok;
+  float* wt = tab + (tid >> 6) * 2 * D;
+  const int t0 = min(lane, D / 4 - 1);
+  const f32x4 c4 = *(const f32x4*)(cs + 4 * t0), s4 = *(const f32x4*)(sn + 4 * t0);
+  // the row's loads: none needs the slot; selects, not branches
+  const uint8_t* src = (is_q ? a.q + tok * a.q_tok : is_v ? a.v + tok * a.v_tok : a.k + tok * a.k_tok) +
+                       mul(h, is_q ? a.q_head : is_v ? a.v_head : a.k_head);
+  const Off doff = mul(h, is_q ? a.qo_head : a.c_head);  // row offset in q_out or in the slot
+  typename C::Raw r1, r2;
+  C::raw_load(src + off1, r1);
+  C::raw_load(src + off2, r2);
+  {
+    float t[8] = {c4[0], c4[1], c4[2], c4[3], s4[0], s4[1], s4[2], s4[3]};
+    C::round8(t);
+    // lanes past the table rewrite the last piece with the same values
+    *(f32x4*)(wt + 4 * t0) = f32x4{t[0], t[1], t[2], t[3]};
+    *(f32x4*)(wt + D + 4 * t0) = f32x4{t[4], t[5], t[6], t[7]};
   }
-  if (!is_q && !is_k) {  // v row: plain copy into the slot
-    const int h = row - a.num_q_heads - a.num_kv_heads;
-    const uint8_t* src = a.v + tok * a.v_tok + h * a.v_head;
-    uint8_t* dst = a.vc + slot * a.c_slot + h * a.c_head;
-    C::copy(src + off1, dst + off1);
-    C::copy(src + off2, dst + off2);
+  // a workgroup's last wavefront may be partial: its live lanes cover the rest
+  const int live = min(64, (int)(blockDim.x * blockDim.y) - (tid & ~63));
+  for (int i = lane + live; i < D / 4; i += live) {  // head_dim above 256
+    const f32x4 c8 = *(const f32x4*)(cs + 4 * i), s8 = *(const f32x4*)(sn + 4 * i);
+    float t[8] = {c8[0], c8[1], c8[2], c8[3], s8[0], s8[1], s8[2], s8[3]};
+    C::round8(t);
+    *(f32x4*)(wt + 4 * i) = f32x4{t[0], t[1], t[2], t[3]};
+    *(f32x4*)(wt + D + 4 * i) = f32x4{t[4], t[5], t[6], t[7]};
+  }
+  const int64_t slot = a.slots[tok];
+  // a negative slot is the padding sentinel (no K/V write); past the pool is flagged
+  const bool kv_ok = slot >= 0 && slot < a.num_slots;
+  if (slot >= a.num_slots && tid == 0 && blockIdx.y == 0) flag_error(a.err, IR_ERR_SLOT_RANGE);
+  // one wavefront's LDS accesses complete in order; the wait and the code
+  // motion barrier keep the reads below the writes
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  if (!in || (!is_q && !kv_ok)) return;
+  uint8_t* dst = (is_q ? a.qo + tok * a.qo_tok : (is_v ? a.vc : a.kc) + slot * a.c_slot) + doff;
+  if (is_v) {
+    C::raw_store(dst + off1, r1);
+    C::raw_store(dst + off2, r2);
     return;
   }
-  const uint8_t* src;
-  uint8_t* dst;
-  if (is_q) {
-    src = a.q + tok * a.q_tok + row * a.q_head;
-    dst = a.qo + tok * a.qo_tok + row * a.qo_head;
-  } else {
-    const int h = row - a.num_q_heads;
-    src = a.k + tok * a.k_tok + h * a.k_head;
-    dst = a.kc + slot * a.c_slot + h * a.c_head;
-  }
+  float c1[8], c2[8], s1[8], s2[8];
+  Chunk8<IR_DTYPE_F32>::load((const uint8_t*)(wt + i0), c1);
+  Chunk8<IR_DTYPE_F32>::load((const uint8_t*)(wt + i0 + half), c2);
+  Chunk8<IR_DTYPE_F32>::load((const uint8_t*)(wt + D + i0), s1);
+  Chunk8<IR_DTYPE_F32>::load((const uint8_t*)(wt + D + i0 + half), s2);
   float x1[8], x2[8];
-  C::load(src + off1, x1);
-  C::load(src + off2, x2);
-  // the 8 cos / sin values of each half, 16-byte loads
-  float cv1[8], cv2[8], sv1[8], sv2[8];
-  Chunk8<IR_DTYPE_F32>::load((const uint8_t*)(a.cos + tok * a.cs_tok + i0), cv1);
-  Chunk8<IR_DTYPE_F32>::load((const uint8_t*)(a.cos + tok * a.cs_tok + i0 + half), cv2);
-  Chunk8<IR_DTYPE_F32>::load((const uint8_t*)(a.sin + tok * a.cs_tok + i0), sv1);
-  Chunk8<IR_DTYPE_F32>::load((const uint8_t*)(a.sin + tok * a.cs_tok + i0 + half), sv2);
+  C::unpack(r1, x1);
+  C::unpack(r2, x2);
+  // first half: x1 * cos + (-x2) * sin; second half: x2 * cos + x1 * sin;
+  // each product rounded to the dtype, the sums rounded by the store
+  float a1[8], b1[8], a2[8], b2[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    a1[e] = x1[e] * c1[e];
+    b1[e] = -x2[e] * s1[e];
+    a2[e] = x2[e] * c2[e];
+    b2[e] = x1[e] * s2[e];
+  }
+  C::round8(a1);
+  C::round8(b1);
+  C::round8(a2);
+  C::round8(b2);
   float o1[8], o2[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float c1 = C::round(cv1[e]), s1 = C::round(sv1[e]);
-    const float c2 = C::round(cv2[e]), s2 = C::round(sv2[e]);
-    // first half: x1 * cos + (-x2) * sin; second half: x2 * cos + x1 * sin
-    const float a1 = C::round(x1[e] * c1), b1 = C::round(-x2[e] * s1);
-    const float a2 = C::round(x2[e] * c2), b2 = C::round(x1[e] * s2);
-    o1[e] = C::round(a1 + b1);
-    o2[e] = C::round(a2 + b2);
+    o1[e] = a1[e] + b1[e];
+    o2[e] = a2[e] + b2[e];
   }
   C::store(dst + off1, o1);
   C::store(dst + off2, o2);
+}
+
+template <int DT>
+void launch_rope(bool wide, dim3 grid, dim3 block, size_t lds, hipStream_t s, const RopeArgs& a) {
+  if (wide)
+    hipLaunchKernelGGL((rope_kv_scatter_kernel<DT, true>), grid, block, lds, s, a);
+  else
+    hipLaunchKernelGGL((rope_kv_scatter_kernel<DT, false>), grid, block, lds, s, a);
 }
 
 }  // namespace
@@ -217,15 +304,26 @@ extern "C" int ir_rope_kv_scatter(const void* q, int64_t q_tok_stride, int64_t q
   a.num_kv_heads = num_kv_heads;
   a.head_dim = head_dim;
   a.err = err_flags;
-  const int64_t total = n_tokens * (int64_t)(num_q_heads + 2 * num_kv_heads) * (head_dim / 16);
-  IR_REQUIRE((total + 255) / 256 <= 0x7fffffff, "ir_rope_kv_scatter: too many tokens");
-  const dim3 grid((unsigned)((total + 255) / 256));
+  IR_REQUIRE(n_tokens <= 0x7fffffff, "ir_rope_kv_scatter: too many tokens");
+  IR_REQUIRE(head_dim <= 1024, "ir_rope_kv_scatter: head_dim above 1024");
+  const int rows = num_q_heads + 2 * num_kv_heads, chunks = head_dim / 16;
+  // rows per workgroup: the token's rows, at most 1,024 lanes and 64 KB of tables
+  const int max_waves = std::min(16, 8192 / head_dim);
+  const int rpb = std::min(rows, std::max(1, max_waves * 64 / chunks));
+  const int waves = (rpb * chunks + 63) / 64;
+  const dim3 grid((unsigned)n_tokens, (unsigned)((rows + rpb - 1) / rpb)), block((unsigned)chunks, (unsigned)rpb);
+  const size_t lds = (size_t)waves * 2 * head_dim * 4;
+  // 24-bit row offsets when every head stride and row offset allows it; the
+  // 64-bit variant otherwise (a head-major pool of over 64 Ki slots at
+  // head_dim 128 in bf16 has a 16 MiB head stride)
+  const int64_t ms = std::max({a.q_head, a.qo_head, a.k_head, a.v_head, a.c_head});
+  const bool wide = ms >= (1 << 24) || ms * rows >= ((int64_t)1 << 31);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == IR_DTYPE_BF16)
-    hipLaunchKernelGGL(rope_kv_scatter_kernel<IR_DTYPE_BF16>, grid, dim3(256), 0, s, a);
+    launch_rope<IR_DTYPE_BF16>(wide, grid, block, lds, s, a);
   else if (dtype == IR_DTYPE_F16)
-    hipLaunchKernelGGL(rope_kv_scatter_kernel<IR_DTYPE_F16>, grid, dim3(256), 0, s, a);
+    launch_rope<IR_DTYPE_F16>(wide, grid, block, lds, s, a);
   else
-    hipLaunchKernelGGL(rope_kv_scatter_kernel<IR_DTYPE_F32>, grid, dim3(256), 0, s, a);
+    launch_rope<IR_DTYPE_F32>(wide, grid, block, lds, s, a);
   return check_launch("ir_rope_kv_scatter");
 }

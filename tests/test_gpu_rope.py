@@ -32,7 +32,7 @@ def _case(dtype, n, hq, hkv, d, num_slots, layout, seed):
 
 @pytest.mark.parametrize("layout", ["head_major", "slot_major"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("hq,hkv,d", [(28, 4, 128), (14, 2, 64), (8, 8, 16)])
+@pytest.mark.parametrize("hq,hkv,d", [(28, 4, 128), (14, 2, 64), (8, 8, 16), (6, 2, 80), (4, 2, 512), (0, 3, 32), (9, 1, 128)])
 def test_rope_scatter_bit_exact(dtype, hq, hkv, d, layout):
     n, num_slots = 77, 300
     q, k, v, base, cos, sin, slots = _case(dtype, n, hq, hkv, d, num_slots, layout, seed=hq + d)
@@ -47,6 +47,24 @@ def test_rope_scatter_bit_exact(dtype, hq, hkv, d, layout):
     O.pool_write(kr, vr, k_ref[0], v.cpu(), slots)
     assert torch.equal(q_out.cpu(), q_ref[0])
     assert torch.equal(kc.cpu(), kr) and torch.equal(vc.cpu(), vr)
+
+
+def test_rope_scatter_wide_pool_offsets():
+    """A head-major pool whose head stride is 32 MiB (row offsets past 24 bits)."""
+    n, hq, hkv, d, num_slots = 300, 12, 4, 128, 1 << 17
+    q, k, v, _, cos, sin, _ = _case(torch.bfloat16, n, hq, hkv, d, 8, "slot_major", seed=17)
+    kc = torch.zeros(hkv, num_slots, d, dtype=torch.bfloat16, device=DEV).permute(1, 0, 2)
+    vc = torch.zeros(hkv, num_slots, d, dtype=torch.bfloat16, device=DEV).permute(1, 0, 2)
+    slots = torch.randperm(num_slots, generator=torch.Generator().manual_seed(18))[:n]
+    slots[:4] = torch.tensor([0, num_slots - 1, 1, num_slots - 2])
+    q_out = kernels.rope_kv_scatter(q, k, v, cos.to(DEV), sin.to(DEV), kc, vc, slots.to(DEV))
+    torch.cuda.synchronize()
+    q_ref, k_ref = O.apply_rotary_pos_emb(q.cpu()[None], k.cpu()[None], cos[None], sin[None])
+    assert torch.equal(q_out.cpu(), q_ref[0])
+    assert torch.equal(kc[slots.to(DEV)].cpu(), k_ref[0]) and torch.equal(vc[slots.to(DEV)].cpu(), v.cpu())
+    written = torch.zeros(num_slots, dtype=torch.bool)
+    written[slots] = True
+    assert int(kc[(~written).to(DEV)].abs().sum()) == 0 and int(vc[(~written).to(DEV)].abs().sum()) == 0
 
 
 def test_rope_scatter_in_place_skip_and_flag():
