@@ -231,10 +231,22 @@ def _bench_prefill(args) -> dict:
     case = make_prefill_case("qwen7b-prefill", "cuda", rotations=args.rotations)
     cfg = case.config
     out = torch.empty_like(case.q)
+    total_q, max_blocks = case.q.shape[0], case.block_tables[0].shape[1]
+    # heaviest-first work order (the seam's choice unless --schedule forces it),
+    # rebuilt every --layers calls as an engine step would
+    ordered = args.schedule == "planned" or (args.schedule == "auto" and kernels.prefill_order_pays(
+        cfg.num_seqs, cfg.chunk, cfg.num_q_heads, cfg.num_kv_heads))
+    order_buf = torch.empty(max(1, kernels.prefill_order_len(cfg.num_seqs, cfg.chunk, cfg.num_q_heads,
+                                                             cfg.num_kv_heads)), dtype=torch.int32, device="cuda")
+    order = [None]
 
     def call(i: int) -> None:
+        if ordered and i % args.layers == 0:
+            order[0] = kernels.prefill_order(case.cu_seqlens_q, case.q_start, total_q, cfg.chunk, max_blocks,
+                                             cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, buf=order_buf)
         kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[i % len(case.block_tables)],
-                              case.cu_seqlens_q, case.q_start, cfg.chunk, cfg.block_size, cfg.scale, out=out)
+                              case.cu_seqlens_q, case.q_start, cfg.chunk, cfg.block_size, cfg.scale, out=out,
+                              order=order[0])
 
     ms = _time_graph(call, args) if args.mode == "graph" else _time_eager(call, args)
     if args.copy_calib_mib > 0:
@@ -271,7 +283,9 @@ def _bench_prefill(args) -> dict:
         "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"{cfg.name}: {cfg.num_seqs} chunks of {cfg.chunk} after prefixes {case.prefixes}, "
                    f"{cfg.num_q_heads}q/{cfg.num_kv_heads}kv heads, head_dim {cfg.head_dim}, block {cfg.block_size}",
-                   "flops_per_call": case.flops, "kv_bytes_per_call": case.kv_bytes, "rotations": args.rotations},
+                   "flops_per_call": case.flops, "kv_bytes_per_call": case.kv_bytes, "rotations": args.rotations,
+                   "schedule": "heaviest-first order" if ordered else "default order",
+                   "layers_per_order": args.layers if ordered else None},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": _traffic("prefill_qwen7b-prefill")[0],
                      "timed": f"prefill call, {args.mode} launches, events on the launch stream"},

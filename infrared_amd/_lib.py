@@ -85,7 +85,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_i32,
         [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i64, _c_i32,
          _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_f32,
-         _c_i32, _c_p, _c_p],
+         _c_i32, _c_p, _c_i64, _c_p, _c_p],
+    ),
+    "ir_paged_prefill_order_len": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32]),
+    "ir_paged_prefill_order": (
+        _c_i32,
+        [_c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p],
     ),
 }
 

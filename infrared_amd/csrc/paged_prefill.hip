@@ -74,6 +74,7 @@ struct PrefillArgs {
   int nw;                                    // wavefronts per workgroup (4 or 8)
   float scale_log2;
   int32_t* err;
+  const int32_t* order;  // [num_seqs * n_qblocks] items (seq * n_qblocks + block), or null
 };
 
 template <int D, int NW_ = 8>
@@ -112,16 +113,28 @@ void paged_prefill_kernel(PrefillArgs a) {
   const int lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
   const int TQ = a.tq;
 
-  // ---- which (query block, KV head, sequence): heaviest first
-  const int per_tb = a.num_kv_heads * a.num_seqs;
-  const int tb = a.n_qblocks - 1 - (int)(blockIdx.x / per_tb);
-  const int rest = (int)(blockIdx.x % per_tb);
-  const int seq = rest % a.num_seqs;
-  const int kvh = rest / a.num_seqs;
+  // ---- which (query block, KV head, sequence): item order[i / H_kv] of the
+  // heaviest-first order when one is given, else the last query blocks (most
+  // keys within a sequence) first
+  int tb, seq, kvh;
+  if (a.order) {
+    const int k = (int)(blockIdx.x / a.num_kv_heads);
+    kvh = (int)(blockIdx.x - (unsigned)k * a.num_kv_heads);
+    const int item = a.order[k];
+    if (item < 0 || item >= a.num_seqs * a.n_qblocks) return;
+    seq = item / a.n_qblocks;
+    tb = item - seq * a.n_qblocks;
+  } else {
+    const int per_tb = a.num_kv_heads * a.num_seqs;
+    tb = a.n_qblocks - 1 - (int)(blockIdx.x / per_tb);
+    const int rest = (int)(blockIdx.x % per_tb);
+    seq = rest % a.num_seqs;
+    kvh = rest / a.num_seqs;
+  }
 
   int q_lo = a.cu_q[seq];
   int q_len = a.cu_q[seq + 1] - q_lo;
-  if (q_lo < 0 || q_len < 0 || q_lo + q_len > a.total_q) {
+  if (q_lo < 0 || q_len < 0 || (int64_t)q_lo + q_len > a.total_q) {
     if (tid == 0 && tb == 0 && kvh == 0) flag_error(a.err, IR_ERR_CONTEXT_RANGE);
     return;
   }
@@ -131,7 +144,7 @@ void paged_prefill_kernel(PrefillArgs a) {
   const int cap = a.max_blocks * a.bs;
   if (p0 < 0 || (int64_t)p0 + q_len > cap) {
     if (tid == 0 && tb == 0 && kvh == 0) flag_error(a.err, IR_ERR_CONTEXT_RANGE);
-    p0 = p0 < 0 ? 0 : p0;
+    p0 = p0 < 0 ? 0 : min(p0, cap);  // keeps p0 + q_len within int range
   }
   // keys this block needs: up to its last query's position, within the table
   const int kmax = min(cap, p0 + min(q_len, tq0 + TQ));
@@ -445,6 +458,111 @@ void paged_prefill_kernel(PrefillArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- work order
+//
+// The dispatcher hands workgroup i to the first CU with room, in index order,
+// so issuing the heaviest items first is the longest-processing-time rule: on
+// a chunked prefill whose items outnumber the CUs (8 chunks of 512 tokens
+// after prefixes of 2.5k-4k keys: 480 workgroups, 1 per CU) the busiest CU's
+// share drops from 1.26x to 1.06x of the mean (tile counts, simulated). The
+// order is built once per step (all layers share the metadata) by one
+// workgroup: every (sequence, query block) item is weighed by the 64-key tiles
+// its workgroup walks, and a counting sort over kOrderBuckets equal-width
+// weight ranges writes the items heaviest range first; items with no query
+// rows go last as -1. Workgroups write disjoint outputs, so the order (ties
+// land in any order) never changes a result bit.
+
+constexpr int kOrderThreads = 1024;
+constexpr int kOrderBuckets = 2048;
+
+struct OrderArgs {
+  const int32_t* cu_q;
+  const int32_t* q_start;
+  int num_seqs, total_q, n_qblocks, tq, cap;  // cap: keys the block tables hold
+  int32_t* order;                             // [num_seqs * n_qblocks]
+};
+
+// 64-key tiles the workgroups of item (seq * n_qblocks + block) walk, following
+// paged_prefill_kernel's bounds; -1 when they return without work (an item
+// that only flags bad metadata weighs 0).
+__device__ int prefill_item_weight(const OrderArgs& a, int item) {
+  const int seq = item / a.n_qblocks, tb = item - seq * a.n_qblocks;
+  const int q_lo = a.cu_q[seq], q_len = a.cu_q[seq + 1] - q_lo;
+  if (q_lo < 0 || q_len < 0 || (int64_t)q_lo + q_len > a.total_q) return tb == 0 ? 0 : -1;
+  const int tq0 = tb * a.tq;
+  if (tq0 >= q_len) return -1;
+  const int p0 = max(0, min(a.q_start[seq], a.cap));
+  const int64_t kmax = min((int64_t)a.cap, (int64_t)p0 + min(q_len, tq0 + a.tq));
+  return (int)((kmax + 63) / 64);
+}
+
+__global__ __launch_bounds__(kOrderThreads) void prefill_order_kernel(OrderArgs a) {
+  __shared__ int start[kOrderBuckets + 1];  // bucket kOrderBuckets: items without work
+  __shared__ int wave_max[kOrderThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int n = a.num_seqs * a.n_qblocks;
+
+  int wmax = 0;
+  for (int i = tid; i < n; i += kOrderThreads) wmax = max(wmax, prefill_item_weight(a, i));
+  for (int o = 32; o > 0; o >>= 1) wmax = max(wmax, __shfl_xor(wmax, o));
+  if (lane == 0) wave_max[tid >> 6] = wmax;
+  for (int i = tid; i <= kOrderBuckets; i += kOrderThreads) start[i] = 0;
+  __syncthreads();
+  wmax = 0;
+  for (int i = 0; i < kOrderThreads / 64; ++i) wmax = max(wmax, wave_max[i]);
+  // bucket 0 holds the heaviest weights
+  auto bucket = [&](int wt) {
+    return wt < 0 ? kOrderBuckets : (int)((int64_t)(wmax - wt) * kOrderBuckets / ((int64_t)wmax + 1));
+  };
+  for (int i = tid; i < n; i += kOrderThreads) atomicAdd(&start[bucket(prefill_item_weight(a, i))], 1);
+  __syncthreads();
+  // exclusive scan of the counts by the first wavefront: lane l owns a run of
+  // consecutive buckets
+  if (tid < 64) {
+    constexpr int kRun = (kOrderBuckets + 1 + 63) / 64;
+    const int lo = lane * kRun, hi = min(lo + kRun, kOrderBuckets + 1);
+    int sum = 0;
+    for (int i = lo; i < hi; ++i) sum += start[i];
+    int incl = sum;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o);
+      if (lane >= o) incl += y;
+    }
+    int run = incl - sum;
+    for (int i = lo; i < hi; ++i) {
+      const int cnt = start[i];
+      start[i] = run;
+      run += cnt;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += kOrderThreads) {
+    const int wt = prefill_item_weight(a, i);
+    const int pos = atomicAdd(&start[bucket(wt)], 1);
+    a.order[pos] = wt < 0 ? -1 : i;
+  }
+}
+
+// Workgroup shape of a prefill call: 8 wavefronts (256 query columns) unless
+// that leaves CUs idle, then 4 (128 columns), twice the workgroups with half
+// the work each. IR_PREFILL_WAVES (4 or 8) forces one for tuning runs.
+struct PrefillGeometry {
+  int nw, tq, n_qblocks;
+};
+
+PrefillGeometry prefill_geometry(int max_q_len, int n_rep, int num_kv_heads, int num_seqs) {
+  const int tq8 = PShape<128, 8>::COLS / n_rep;
+  const int64_t wgs8 = (int64_t)((max_q_len + tq8 - 1) / tq8) * num_kv_heads * num_seqs;
+  const char* e = getenv("IR_PREFILL_WAVES");
+  // (4 wavefronts hold at most 128 query heads per KV head)
+  const bool four = n_rep <= PShape<128, 4>::COLS && (e ? atoi(e) == 4 : wgs8 < 256);
+  PrefillGeometry g;
+  g.nw = four ? 4 : 8;
+  g.tq = (four ? PShape<128, 4>::COLS : PShape<128, 8>::COLS) / n_rep;
+  g.n_qblocks = (max_q_len + g.tq - 1) / g.tq;
+  return g;
+}
+
 template <int DT, int D>
 int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   const int64_t grid = (int64_t)a.n_qblocks * a.num_kv_heads * a.num_seqs;
@@ -482,7 +600,8 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
                                 int max_blocks_per_seq, const int32_t* cu_seqlens_q, const int32_t* q_start,
                                 int num_seqs, int total_q, int max_q_len, void* out, int64_t out_tok_stride,
                                 int64_t out_head_stride, int num_q_heads, int num_kv_heads, int head_dim, float scale,
-                                int dtype, int32_t* err_flags, ir_stream_t stream) {
+                                int dtype, const int32_t* order, int64_t order_len, int32_t* err_flags,
+                                ir_stream_t stream) {
   IR_REQUIRE(dtype == IR_DTYPE_BF16 || dtype == IR_DTYPE_F16 || dtype == IR_DTYPE_F32,
              "ir_paged_prefill: unknown dtype %d", dtype);
   if (dtype == IR_DTYPE_F32)
@@ -526,19 +645,17 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
   a.num_seqs = num_seqs;
   a.total_q = total_q;
   a.n_rep = num_q_heads / num_kv_heads;
-  // Workgroups of 8 wavefronts (256 query columns) unless that leaves CUs
-  // idle: then 4 (128 columns), twice the workgroups, half the work each.
-  // IR_PREFILL_WAVES (4 or 8) forces one for tuning runs.
-  {
-    const int tq8 = PShape<128, 8>::COLS / a.n_rep;
-    const int64_t wgs8 = (int64_t)((max_q_len + tq8 - 1) / tq8) * num_kv_heads * num_seqs;
-    const char* e = getenv("IR_PREFILL_WAVES");
-    // (4 wavefronts hold at most 128 query heads per KV head)
-    const bool four = a.n_rep <= PShape<128, 4>::COLS && (e ? atoi(e) == 4 : wgs8 < 256);
-    a.nw = four ? 4 : 8;
-    a.tq = (four ? PShape<128, 4>::COLS : PShape<128, 8>::COLS) / a.n_rep;
-  }
-  a.n_qblocks = (max_q_len + a.tq - 1) / a.tq;
+  const PrefillGeometry geo = prefill_geometry(max_q_len, a.n_rep, num_kv_heads, num_seqs);
+  a.nw = geo.nw;
+  a.tq = geo.tq;
+  a.n_qblocks = geo.n_qblocks;
+  const int64_t n_items = (int64_t)num_seqs * a.n_qblocks;
+  IR_REQUIRE(n_items <= 0x7fffffff, "ir_paged_prefill: %lld work items", (long long)n_items);
+  IR_REQUIRE(!order || order_len == n_items,
+             "ir_paged_prefill: order holds %lld items, this call has %lld (build it with ir_paged_prefill_order "
+             "for the same metadata and shapes)",
+             (long long)order_len, (long long)n_items);
+  a.order = order;
   a.out = out;
   a.o_tok = out_tok_stride;
   a.o_head = out_head_stride;
@@ -550,4 +667,43 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
   if (dtype == IR_DTYPE_BF16)
     return head_dim == 128 ? launch_prefill<IR_DTYPE_BF16, 128>(a, s) : launch_prefill<IR_DTYPE_BF16, 64>(a, s);
   return head_dim == 128 ? launch_prefill<IR_DTYPE_F16, 128>(a, s) : launch_prefill<IR_DTYPE_F16, 64>(a, s);
+}
+
+extern "C" int64_t ir_paged_prefill_order_len(int num_seqs, int max_q_len, int num_q_heads, int num_kv_heads) {
+  if (num_seqs <= 0 || max_q_len <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
+    return 0;
+  const PrefillGeometry geo = prefill_geometry(max_q_len, num_q_heads / num_kv_heads, num_kv_heads, num_seqs);
+  return (int64_t)num_seqs * geo.n_qblocks;
+}
+
+extern "C" int ir_paged_prefill_order(const int32_t* cu_seqlens_q, const int32_t* q_start, int num_seqs,
+                                      int total_q, int max_q_len, int max_blocks_per_seq, int block_size,
+                                      int num_q_heads, int num_kv_heads, int32_t* order, int64_t order_len,
+                                      ir_stream_t stream) {
+  IR_REQUIRE(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && num_q_heads > 0 && num_kv_heads > 0 &&
+                 block_size > 0 && max_blocks_per_seq >= 0,
+             "ir_paged_prefill_order: bad sizes");
+  IR_REQUIRE(num_q_heads % num_kv_heads == 0, "ir_paged_prefill_order: num_q_heads %d not a multiple of num_kv_heads %d",
+             num_q_heads, num_kv_heads);
+  IR_REQUIRE((int64_t)max_blocks_per_seq * block_size <= (int64_t)1 << 30,
+             "ir_paged_prefill_order: block tables of %d x %d tokens exceed 2^30 keys", max_blocks_per_seq,
+             block_size);
+  const int64_t need = ir_paged_prefill_order_len(num_seqs, max_q_len, num_q_heads, num_kv_heads);
+  IR_REQUIRE(order_len == need, "ir_paged_prefill_order: order holds %lld items, this call has %lld",
+             (long long)order_len, (long long)need);
+  IR_REQUIRE(need <= 0x7fffffff, "ir_paged_prefill_order: %lld work items", (long long)need);
+  if (need == 0) return ok();
+  IR_REQUIRE(cu_seqlens_q && q_start && order, "ir_paged_prefill_order: null pointer");
+  const PrefillGeometry geo = prefill_geometry(max_q_len, num_q_heads / num_kv_heads, num_kv_heads, num_seqs);
+  OrderArgs a;
+  a.cu_q = cu_seqlens_q;
+  a.q_start = q_start;
+  a.num_seqs = num_seqs;
+  a.total_q = total_q;
+  a.n_qblocks = geo.n_qblocks;
+  a.tq = geo.tq;
+  a.cap = max_blocks_per_seq * block_size;
+  a.order = order;
+  hipLaunchKernelGGL(prefill_order_kernel, dim3(1), dim3(kOrderThreads), 0, (hipStream_t)stream, a);
+  return check_launch("ir_paged_prefill_order");
 }

@@ -441,6 +441,60 @@ def rope_kv_scatter(
     return q_out
 
 
+def prefill_order_len(num_seqs: int, max_q_len: int, num_q_heads: int, num_kv_heads: int) -> int:
+    """int32 items of a prefill work order for these shapes (0: nothing to order)."""
+    return int(lib().ir_paged_prefill_order_len(num_seqs, max_q_len, num_q_heads, num_kv_heads))
+
+
+def prefill_order_pays(num_seqs: int, max_q_len: int, num_q_heads: int, num_kv_heads: int,
+                       device: torch.device | str | int | None = None) -> bool:
+    """Whether a heaviest-first order can shorten the call: its workgroups
+    (one per CU at a time) outnumber the CUs, so the dispatch order decides
+    which CU finishes last. Below that every workgroup starts at once."""
+    n_items = prefill_order_len(num_seqs, max_q_len, num_q_heads, num_kv_heads)
+    if n_items <= 0:
+        return False
+    idx = torch.device(device if device is not None else "cuda").index
+    idx = torch.cuda.current_device() if idx is None else idx
+    if idx not in _CU_COUNT:
+        _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return n_items * num_kv_heads > _CU_COUNT[idx]
+
+
+def prefill_order(
+    cu_seqlens_q: torch.Tensor,
+    q_start: torch.Tensor,
+    total_q: int,
+    max_q_len: int,
+    max_blocks: int,
+    block_size: int,
+    num_q_heads: int,
+    num_kv_heads: int,
+    buf: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Heaviest-first work order of a prefill call's (sequence, query block)
+    items, built on the device (``ir_paged_prefill_order``); pass it to every
+    layer's :func:`paged_prefill` over the same metadata. ``buf`` (int32) is
+    reused when large enough."""
+    dev = require_device(cu_seqlens_q, q_start)
+    b = q_start.shape[0]
+    for name, t, n in (("cu_seqlens_q", cu_seqlens_q, b + 1), ("q_start", q_start, b)):
+        if t.dtype != torch.int32 or t.shape != (n,) or not t.is_contiguous():
+            raise RuntimeError(f"prefill_order: {name} must be contiguous int32 [{n}]")
+    n = prefill_order_len(b, max_q_len, num_q_heads, num_kv_heads)
+    if buf is None or buf.numel() < n:
+        buf = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    if buf.dtype != torch.int32 or not buf.is_contiguous():
+        raise RuntimeError("prefill_order: buf must be a contiguous int32 tensor")
+    order = buf[:n]
+    rc = lib().ir_paged_prefill_order(
+        ptr(cu_seqlens_q), ptr(q_start), b, int(total_q), int(max_q_len), int(max_blocks), int(block_size),
+        num_q_heads, num_kv_heads, ptr(order), n, stream_ptr(dev),
+    )
+    check(rc, "ir_paged_prefill_order")
+    return order
+
+
 def paged_prefill(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -453,6 +507,7 @@ def paged_prefill(
     scale: float,
     out: torch.Tensor | None = None,
     err_flags: torch.Tensor | None = None,
+    order: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Causal paged attention for packed query chunks: ``q`` ``[total_q, H_q, D]``.
 
@@ -460,6 +515,7 @@ def paged_prefill(
     ``[B+1]``); its query ``i`` is at position ``q_start[b] + i`` (int32 ``[B]``)
     and attends keys ``0..q_start[b]+i`` through ``block_tables[b]``. ``max_q_len``
     bounds the per-sequence query counts (host value, sizes the grid).
+    ``order``: the :func:`prefill_order` of this metadata (schedule only).
     """
     dev = require_device(q, k_cache, v_cache, block_tables, cu_seqlens_q, q_start)
     _cache_layer("paged_prefill", k_cache)
@@ -478,14 +534,18 @@ def paged_prefill(
         if t.dtype != torch.int32 or t.shape != (n,) or not t.is_contiguous():
             raise RuntimeError(f"paged_prefill: {name} must be contiguous int32 [{n}]")
     _last_dim_contiguous("paged_prefill q", q)
+    if order is not None:
+        require_device(q, order)
+        if order.dtype != torch.int32 or order.dim() != 1 or not order.is_contiguous():
+            raise RuntimeError("paged_prefill: order must be a contiguous int32 vector")
     if out is None:
         out = torch.empty(total_q, hq, d, dtype=q.dtype, device=dev)
     rc = lib().ir_paged_prefill(
         ptr(q), q.stride(0), q.stride(1), ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
         k_cache.shape[0] // block_size, block_size, ptr(block_tables), block_tables.stride(0),
         block_tables.shape[1], ptr(cu_seqlens_q), ptr(q_start), b, total_q, int(max_q_len), ptr(out),
-        out.stride(0), out.stride(1), hq, h_kv, d, float(scale), dtype_code(q.dtype), ptr(err_flags),
-        stream_ptr(dev),
+        out.stride(0), out.stride(1), hq, h_kv, d, float(scale), dtype_code(q.dtype), ptr(order),
+        0 if order is None else order.numel(), ptr(err_flags), stream_ptr(dev),
     )
     check(rc, "ir_paged_prefill")
     return out
@@ -498,6 +558,9 @@ __all__ = [
     "paged_decode",
     "paged_attention_masked",
     "paged_prefill",
+    "prefill_order",
+    "prefill_order_len",
+    "prefill_order_pays",
     "rope_kv_scatter",
     "decode_workspace_bytes",
     "default_partition",

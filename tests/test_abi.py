@@ -105,6 +105,22 @@ def test_decode_plan_helpers():
     assert lib.ir_paged_decode_planned_workspace_bytes(64, 28, 4, 128) >= 256 * 16 * 128 * 4
 
 
+def test_prefill_order_helpers():
+    """A prefill work order holds one item per (sequence, query block): 8 chunks
+    of 512 tokens at 28 / 4 heads run 256-column workgroups (36 tokens of 7
+    heads, 15 blocks each); 2 chunks would leave CUs idle, so they run
+    128-column ones (18 tokens, 29 blocks). A wrong length is refused."""
+    lib = _lib.lib()
+    assert lib.ir_paged_prefill_order_len(8, 512, 28, 4) == 8 * 15
+    assert lib.ir_paged_prefill_order_len(2, 512, 28, 4) == 2 * 29
+    assert lib.ir_paged_prefill_order_len(0, 512, 28, 4) == 0
+    assert lib.ir_paged_prefill_order_len(8, 512, 28, 3) == 0
+    rc = lib.ir_paged_prefill_order(None, None, 8, 4096, 512, 600, 16, 28, 4, None, 7, None)
+    assert rc == -1 and b"order holds" in lib.ir_last_error()
+    rc = lib.ir_paged_prefill_order(None, None, 8, 4096, 512, 600, 16, 28, 4, None, 120, None)
+    assert rc == -1 and b"null" in lib.ir_last_error()
+
+
 def test_no_product_module_imports_triton_or_the_oracle():
     pkg = os.path.join(ROOT, "infrared_amd")
     for name in os.listdir(pkg):

@@ -150,3 +150,94 @@ def test_prefill_fp32_is_refused():
     qs = torch.tensor([3, 4], dtype=torch.int32, device=DEV)
     with pytest.raises(RuntimeError, match="fp32"):
         kernels.paged_prefill(q, case.k_cache, case.v_cache, case.block_tables[0], cu, qs, 1, 16, 0.125)
+
+
+def _host_weights(case, tq, n_qblocks):
+    """Key tiles (64 keys) each (sequence, query block) item walks, -1 for items
+    without query rows: the bounds the prefill kernel applies, from the host
+    copy of the metadata."""
+    cap = case.block_tables[0].shape[1] * case.config.block_size
+    cu = case.cu_seqlens_q.cpu().tolist()
+    qs = case.q_start.cpu().tolist()
+    w = []
+    for b in range(len(qs)):
+        q_len = cu[b + 1] - cu[b]
+        for tb in range(n_qblocks):
+            if tb * tq >= q_len:
+                w.append(-1)
+                continue
+            p0 = max(0, min(qs[b], cap))
+            kmax = min(cap, p0 + min(q_len, (tb + 1) * tq))
+            w.append((kmax + 63) // 64)
+    return w
+
+
+@pytest.mark.parametrize("prefixes,q_lens", [
+    (None, None),  # the full 8 x 512-token workload (8-wavefront workgroups)
+    ([0, 37, 512, 1000, 3, 3, 0, 5], [1, 31, 100, 512, 0, 9, 64, 33]),  # ragged, one empty chunk
+    ([0, 300], [256, 77]),  # 4-wavefront workgroups
+])
+def test_prefill_order_is_a_heaviest_first_permutation(prefixes, q_lens):
+    """The device-built order lists every item with work exactly once, heaviest
+    first (non-increasing key-tile counts: the weights here are below the
+    order's 2048 buckets, so the order is exact), then -1 for the items
+    without query rows."""
+    cfg = PrefillConfig("pf-order", 8 if prefixes is None else len(prefixes), 512, 28, 4, 128, 16,
+                        torch.bfloat16, 512, seed=4)
+    case = make_prefill_case(cfg, DEV, prefixes=prefixes, q_lens=q_lens)
+    b, max_q = len(case.q_lens), max(case.q_lens)
+    n = kernels.prefill_order_len(b, max_q, 28, 4)
+    # query tokens per workgroup: 256 columns of 7 heads, or 128 when 256-column
+    # workgroups would number fewer than the CUs
+    four = -(-max_q // (256 // 7)) * 4 * b < 256
+    tq = (128 if four else 256) // 7
+    n_qblocks = -(-max_q // tq)
+    assert n == b * n_qblocks
+    order = kernels.prefill_order(case.cu_seqlens_q, case.q_start, case.q.shape[0], max_q,
+                                  case.block_tables[0].shape[1], 16, 28, 4).cpu().tolist()
+    w = _host_weights(case, tq, n_qblocks)
+    busy = [i for i in range(n) if w[i] >= 0]
+    assert sorted(i for i in order if i >= 0) == busy
+    assert order[len(busy):] == [-1] * (n - len(busy))
+    ws = [w[i] for i in order[: len(busy)]]
+    assert ws == sorted(ws, reverse=True)
+
+
+def test_prefill_order_changes_no_result_bit():
+    """The same calls with and without the heaviest-first order: identical
+    outputs and error flags (full workload, ragged chunks, a packed mixed step,
+    bad block ids)."""
+    cases = [
+        make_prefill_case("qwen7b-prefill", DEV),
+        make_prefill_case("qwen7b-prefill", DEV, prefixes=[0, 37, 512, 1000, 3, 3, 0, 5],
+                          q_lens=[1, 31, 100, 512, 0, 9, 64, 33]),
+        make_prefill_case(PrefillConfig("pf-mixed-o", 8, 0, 28, 4, 128, 16, torch.bfloat16, 0, seed=21), DEV,
+                          prefixes=[700, 1500, 99, 2047, 16, 3000, 0, 256], q_lens=[1, 1, 1, 1, 1, 1, 256, 200]),
+    ]
+    for i, case in enumerate(cases):
+        cfg = case.config
+        bt = case.block_tables[0].clone()
+        if i == 1:
+            bt[3, 5] = case.pool_blocks + 3  # a bad block id inside sequence 3's keys
+        b, max_q = len(case.q_lens), max(case.q_lens)
+        order = kernels.prefill_order(case.cu_seqlens_q, case.q_start, case.q.shape[0], max_q, bt.shape[1],
+                                      cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads)
+        outs, errs = [], []
+        for o in (None, order):
+            err = torch.zeros(1, dtype=torch.int32, device=DEV)
+            outs.append(kernels.paged_prefill(case.q, case.k_cache, case.v_cache, bt, case.cu_seqlens_q,
+                                              case.q_start, max_q, cfg.block_size, cfg.scale, err_flags=err,
+                                              order=o))
+            errs.append(err)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], outs[1]), cfg.name
+        assert errs[0].item() == errs[1].item() == (ERR_BLOCK_RANGE if i == 1 else 0)
+
+
+def test_prefill_order_length_is_checked():
+    case = make_prefill_case("qwen7b-prefill", DEV)
+    cfg = case.config
+    wrong = torch.full((7,), -1, dtype=torch.int32, device=DEV)
+    with pytest.raises(RuntimeError, match="order holds"):
+        kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[0], case.cu_seqlens_q,
+                              case.q_start, cfg.chunk, cfg.block_size, cfg.scale, order=wrong)
