@@ -77,10 +77,10 @@ struct PrefillArgs {
   const int32_t* order;  // [num_seqs * n_qblocks] items (seq * n_qblocks + block), or null
 };
 
-template <int D, int NW_ = 8>
+template <int D, int NW_ = 8, int CT_ = 2>
 struct PShape {
   static constexpr int NW = NW_;  // wavefronts per workgroup (8: two per SIMD; 4: one)
-  static constexpr int CT = 2;    // 16-column tiles per wavefront
+  static constexpr int CT = CT_;  // 16-column tiles per wavefront
   static constexpr int COLS = NW * CT * 16;  // (token, head) columns per workgroup
   static constexpr int BN = 64;   // keys per tile
   static constexpr int NT = NW * 64;
@@ -99,10 +99,10 @@ struct PShape {
 
 // FAST: power-of-two block size and a pool layer small enough for 24-bit slot
 // and stride products (32-bit element offsets).
-template <int DT, int D, bool FAST, int NW>
+template <int DT, int D, bool FAST, int NW, int CTW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 2 : 1)))
 void paged_prefill_kernel(PrefillArgs a) {
-  typedef PShape<D, NW> S;
+  typedef PShape<D, NW, CTW> S;
   constexpr int EB = 2;
   constexpr int CT = S::CT, BN = S::BN, NT = S::NT;
   __shared__ __attribute__((aligned(16))) uint16_t ks_lds[3][BN * S::KROW];
@@ -214,6 +214,10 @@ void paged_prefill_kernel(PrefillArgs a) {
 
   u32x4 kreg[S::KPT];
   u32x4 vreg[S::VPT][2];
+  // whether each load in flight reads a usable key: applied when the tile is
+  // stored (zero_unless), not when it is loaded, so the loads stay in flight
+  // through the next tile's math instead of being waited for at once
+  bool kuse[S::KPT], vuse[S::VPT][2];
   // Global loads of key tile kb into registers (whole workgroup, uniform call).
   auto load_regs = [&](int kb) {
     const int k0 = kb * BN;
@@ -227,7 +231,8 @@ void paged_prefill_kernel(PrefillArgs a) {
         const int key = q / (D / 8), part = q % (D / 8);
         bool use;
         const int64_t sl = slot_of(k0 + key, use);
-        kreg[i] = zero_unless(*(const u32x4*)(kc + sl + part * 8), use);
+        kreg[i] = *(const u32x4*)(kc + sl + part * 8);
+        kuse[i] = use;
       }
     }
 #pragma unroll
@@ -237,8 +242,10 @@ void paged_prefill_kernel(PrefillArgs a) {
         const int pr = v % (BN / 2), part = v / (BN / 2);
         bool u0, u1;
         const int64_t s0 = slot_of(k0 + 2 * pr, u0), s1 = slot_of(k0 + 2 * pr + 1, u1);
-        vreg[i][0] = zero_unless(*(const u32x4*)(vc + s0 + part * 8), u0);
-        vreg[i][1] = zero_unless(*(const u32x4*)(vc + s1 + part * 8), u1);
+        vreg[i][0] = *(const u32x4*)(vc + s0 + part * 8);
+        vreg[i][1] = *(const u32x4*)(vc + s1 + part * 8);
+        vuse[i][0] = u0;
+        vuse[i][1] = u1;
       }
     }
   };
@@ -249,7 +256,7 @@ void paged_prefill_kernel(PrefillArgs a) {
       const int q = tid + NT * i;
       if (q < S::KCH) {
         const int key = q / (D / 8), part = q % (D / 8);
-        *(u32x4*)&ks_lds[buf][key * S::KROW + part * 8] = kreg[i];
+        *(u32x4*)&ks_lds[buf][key * S::KROW + part * 8] = zero_unless(kreg[i], kuse[i]);
       }
     }
 #pragma unroll
@@ -257,7 +264,7 @@ void paged_prefill_kernel(PrefillArgs a) {
       const int v = tid + NT * i;
       if (v < S::VPR) {
         const int pr = v % (BN / 2), part = v / (BN / 2);
-        const u32x4 x0 = vreg[i][0], x1 = vreg[i][1];
+        const u32x4 x0 = zero_unless(vreg[i][0], vuse[i][0]), x1 = zero_unless(vreg[i][1], vuse[i][1]);
         uint16_t* dst = &vt_lds[buf][part * 8 * S::VROW + 2 * pr];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -576,15 +583,15 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   if (a.nw == 4) {
     const dim3 block(PShape<D, 4>::NT);
     if (fast)
-      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 4>), dim3((unsigned)grid), block, 0, s, a);
+      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 4, 2>), dim3((unsigned)grid), block, 0, s, a);
     else
-      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 4>), dim3((unsigned)grid), block, 0, s, a);
+      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 4, 2>), dim3((unsigned)grid), block, 0, s, a);
   } else {
     const dim3 block(PShape<D, 8>::NT);
     if (fast)
-      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8>), dim3((unsigned)grid), block, 0, s, a);
+      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 2>), dim3((unsigned)grid), block, 0, s, a);
     else
-      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8>), dim3((unsigned)grid), block, 0, s, a);
+      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 2>), dim3((unsigned)grid), block, 0, s, a);
   }
   return check_launch("ir_paged_prefill");
 }
