@@ -112,6 +112,22 @@ __device__ __forceinline__ f32x4 mfma_k32<IR_DTYPE_F16>(u32x4 a, u32x4 b, f32x4 
                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// acc + lo + hi of a dword holding two 16-bit elements (one v_dot2c against
+// packed 1.0s, fp32 accumulation).
+template <int DT>
+__device__ __forceinline__ float sum2(uint32_t w, float acc);
+
+template <>
+__device__ __forceinline__ float sum2<IR_DTYPE_BF16>(uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, 0x3f803f80u),
+                                         acc, false);
+}
+
+template <>
+__device__ __forceinline__ float sum2<IR_DTYPE_F16>(uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), __builtin_bit_cast(f16x2, 0x3c003c00u), acc, false);
+}
+
 // 16x16x16, 16-bit inputs: 4 elements (2 dwords) of A and B per lane.
 template <int DT>
 __device__ __forceinline__ f32x4 mfma_k16(u32x2 a, u32x2 b, f32x4 c);

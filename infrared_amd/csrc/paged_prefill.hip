@@ -52,6 +52,11 @@ namespace ir {
 namespace {
 
 constexpr int kBtCache = 1024;  // block ids staged in LDS per workgroup
+#ifndef IR_PREFILL_AHEAD
+#define IR_PREFILL_AHEAD 2
+#endif
+// MFMA steps between an LDS operand read and its use
+constexpr int kOperandAhead = IR_PREFILL_AHEAD;
 
 struct PrefillArgs {
   const void* q;
@@ -99,7 +104,7 @@ struct PShape {
 
 // FAST: power-of-two block size and a pool layer small enough for 24-bit slot
 // and stride products (32-bit element offsets).
-template <int DT, int D, bool FAST, int NW, int CTW>
+template <int DT, int D, bool FAST, int NW, int CTW, bool PP>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 2 : 1)))
 void paged_prefill_kernel(PrefillArgs a) {
   typedef PShape<D, NW, CTW> S;
@@ -151,30 +156,37 @@ void paged_prefill_kernel(PrefillArgs a) {
   const int nkb = kmax > 0 && a.num_blocks > 0 ? (kmax + BN - 1) / BN : 0;
 
   // columns of this lane: tile ct holds column j = 32 w + 16 ct + c, i.e.
-  // token tq0 + j / n_rep, query head kvh * n_rep + j % n_rep
-  int col_tok[CT], col_head[CT];
-  bool col_ok[CT];
-#pragma unroll
-  for (int ct = 0; ct < CT; ++ct) {
+  // token tq0 + j / n_rep, query head kvh * n_rep + j % n_rep (recomputed for
+  // the output store rather than kept live through the key walk)
+  struct Col {
+    int tok, head;
+    bool ok;
+  };
+  auto column = [&](int ct) {
     const int j = w * (CT * 16) + ct * 16 + c;
     const int t = j / a.n_rep;
-    col_tok[ct] = tq0 + t;
-    col_head[ct] = kvh * a.n_rep + (j - t * a.n_rep);
-    col_ok[ct] = t < TQ && tq0 + t < q_len;
-  }
+    return Col{tq0 + t, kvh * a.n_rep + (j - t * a.n_rep), t < TQ && tq0 + t < q_len};
+  };
   const int32_t* bt_row = a.bt + (int64_t)seq * a.bt_stride;
   const uint16_t* kc = (const uint16_t*)a.kc + (int64_t)kvh * a.c_head;
   const uint16_t* vc = (const uint16_t*)a.vc + (int64_t)kvh * a.c_head;
 
-  // ---- Q^T operands: lane (g, c) holds d = 32 ks + 8 g .. +7 of its column
+  // ---- Q^T operands: lane (g, c) holds d = 32 ks + 8 g .. +7 of its column,
+  // multiplied by scale * log2(e) and rounded back to the input dtype, so the
+  // score MFMA yields base-2 exponents directly
   u32x4 qreg[CT][S::KS];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
-    const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)(q_lo + (col_ok[ct] ? col_tok[ct] : 0)) * a.q_tok +
-                           (int64_t)(col_ok[ct] ? col_head[ct] : 0) * a.q_head;
+    const Col col = column(ct);
+    const uint16_t* qrow = (const uint16_t*)a.q + (int64_t)(q_lo + (col.ok ? col.tok : 0)) * a.q_tok +
+                           (int64_t)(col.ok ? col.head : 0) * a.q_head;
 #pragma unroll
-    for (int ks = 0; ks < S::KS; ++ks)
-      qreg[ct][ks] = col_ok[ct] ? *(const u32x4*)(qrow + ks * 32 + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+    for (int ks = 0; ks < S::KS; ++ks) {
+      const u32x4 x = col.ok ? *(const u32x4*)(qrow + ks * 32 + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        qreg[ct][ks][e] = Elem<DT>::pack2(Elem<DT>::lo(x[e]) * a.scale_log2, Elem<DT>::hi(x[e]) * a.scale_log2);
+    }
   }
 
   // ---- block-id cache: ids [bt_base, bt_base + kBtCache) of this sequence
@@ -223,7 +235,10 @@ void paged_prefill_kernel(PrefillArgs a) {
     const int k0 = kb * BN;
     const int k_last = min(k0 + BN, kmax) - 1;
     const int last_blk = FAST ? k_last >> a.bs_shift : k_last / a.bs;
-    if (last_blk >= bt_base + kBtCache) fill_bt(FAST ? k0 >> a.bs_shift : k0 / a.bs);
+    // (the ping-pong schedule runs only on tables the cache holds whole: its
+    // wave groups never meet at the same barrier for a refill)
+    if constexpr (!PP)
+      if (last_blk >= bt_base + kBtCache) fill_bt(FAST ? k0 >> a.bs_shift : k0 / a.bs);
 #pragma unroll
     for (int i = 0; i < S::KPT; ++i) {
       const int q = tid + NT * i;
@@ -276,12 +291,15 @@ void paged_prefill_kernel(PrefillArgs a) {
     }
   };
 
-  // ---- online softmax state, per column tile: lane owns column c of it
-  f32x4 acc[CT][S::DTL];
-  float m[CT], l[CT];
+  // ---- online softmax state, per column tile: lane owns column c of it.
+  // negm[ct] holds -m (the running base-2 max, 0 before the first tile) in
+  // all four slots: it is the accumulator a tile's score MFMAs start from, so
+  // the scores arrive as s - m and need only the exponential.
+  f32x4 acc[CT][S::DTL], negm[CT];
+  float l[CT];
 #pragma unroll
   for (int qt = 0; qt < CT; ++qt) {
-    m[qt] = -__FLT_MAX__;
+    negm[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     l[qt] = 0.f;
 #pragma unroll
     for (int dt = 0; dt < S::DTL; ++dt) acc[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -289,7 +307,7 @@ void paged_prefill_kernel(PrefillArgs a) {
   const int qpos0 = p0 + tq0;  // position of the block's first query
   int col_lim[CT];             // last key each column may see
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct) col_lim[ct] = min(p0 + col_tok[ct], kmax - 1);
+  for (int ct = 0; ct < CT; ++ct) col_lim[ct] = min(p0 + column(ct).tok, kmax - 1);
 
   // S^T += K . Q^T for key tile kt (< 4), k-step ks (< KS) of the tile staged
   // at kb_lds.
@@ -305,16 +323,18 @@ void paged_prefill_kernel(PrefillArgs a) {
       for (int kt = 0; kt < 4; ++kt) x[ct][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
   };
 
-  // One key tile kb, software pipelined: the raw scores `cur` of tile kb are
-  // ready; while their exponentials run on the VALU, the scores `nxt` of tile
-  // kb + 1 (already staged) are computed on the MFMA pipe (NX), then
-  // O^T += V^T . P^T for tile kb. Scores stay raw (scale > 0 keeps the max
-  // where it is); the base-2 scale is folded into the exponent:
-  // p = exp2(s * scale_log2 - m).
+  // One key tile kb, software pipelined: the scores `cur` of tile kb (base 2,
+  // less the max m they were started from) are ready; while their
+  // exponentials run on the VALU, the scores `nxt` of tile kb + 1 (already
+  // staged) are computed on the MFMA pipe (NX), then O^T += V^T . P^T for tile
+  // kb. The first tile sets m to its own max; later ones move it only when
+  // their max exceeds it by more than kRescaleSlack, and only those tiles
+  // subtract the change from their scores.
   auto step = [&](auto nx_tag, int kb, f32x4 (&cur)[CT][4], f32x4 (&nxt)[CT][4]) {
     constexpr bool NX = decltype(nx_tag)::value;
     using E = Elem<DT>;
     const int k0 = kb * BN;
+    const bool first = kb == 0;
     // only tiles that cross the causal diagonal or the last key are masked
     if (!(k0 + BN - 1 <= qpos0 && k0 + BN <= kmax)) {
 #pragma unroll
@@ -331,23 +351,29 @@ void paged_prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
         mx = fmaxf(mx, fmaxf(fmaxf(cur[ct][kt][0], cur[ct][kt][1]), fmaxf(cur[ct][kt][2], cur[ct][kt][3])));
-      mx = wave_max_groups_swap(mx) * a.scale_log2;
-      const bool grow = mx > m[ct] + kRescaleSlack;
+      mx = wave_max_groups_swap(mx);  // relative to m; finite on the first tile (key 0 is always visible)
+      const bool grow = first || mx > kRescaleSlack;
       if (__any(grow)) {
-        const float m_new = grow ? mx : m[ct];
-        const float alpha = fast_exp2(m[ct] - m_new);
-        l[ct] *= alpha;
+        const float d = grow ? mx : 0.f;  // the max moves up by d
+        if (!first) {
+          const float alpha = fast_exp2(-d);
+          l[ct] *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < S::DTL; ++dt) acc[ct][dt] *= alpha;
-        m[ct] = m_new;
+          for (int dt = 0; dt < S::DTL; ++dt) acc[ct][dt] *= alpha;
+        }
+        negm[ct] -= d;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) cur[ct][kt] -= d;
       }
     }
     // next tile's scores (MFMA) interleaved with this tile's exponentials (VALU)
     const uint16_t* kn = ks_lds[(kb + 1) % 3];
-    if constexpr (NX) zero_s(nxt);
-    float ls[CT];
+    if constexpr (NX) {
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) ls[ct] = 0.f;
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) nxt[ct][kt] = negm[ct];
+    }
     // NQK = 4 * KS score MFMA steps, SPS of this lane's CT * 16 scores each.
     // Program order is kept step by step (sched_barrier): each step's K operand
     // was read one step earlier, its MFMAs go to the matrix pipe and the
@@ -356,12 +382,14 @@ void paged_prefill_kernel(PrefillArgs a) {
     auto k_operand = [&](int t) {
       return *(const u32x4*)&kn[((t % 4) * 16 + c) * S::KROW + (t / 4) * 32 + 8 * g];
     };
-    u32x4 ka_next = NX ? k_operand(0) : u32x4{0u, 0u, 0u, 0u};
+    u32x4 kring[kOperandAhead];
+#pragma unroll
+    for (int t = 0; t < kOperandAhead; ++t) kring[t] = NX ? k_operand(t) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int t = 0; t < NQK; ++t) {
       if constexpr (NX) {
-        const u32x4 ka = ka_next;
-        if (t + 1 < NQK) ka_next = k_operand(t + 1);
+        const u32x4 ka = kring[t % kOperandAhead];
+        if (t + kOperandAhead < NQK) kring[t % kOperandAhead] = k_operand(t + kOperandAhead);
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) nxt[ct][t % 4] = mfma_k32<DT>(ka, qreg[ct][t / 4], nxt[ct][t % 4]);
       }
@@ -369,9 +397,7 @@ void paged_prefill_kernel(PrefillArgs a) {
       for (int j = 0; j < SPS; ++j) {
         const int i = t * SPS + j;
         const int ct = i / 16, kt = (i % 16) / 4, r = i % 4;
-        const float pv = fast_exp2(__builtin_fmaf(cur[ct][kt][r], a.scale_log2, -m[ct]));
-        ls[ct] += pv;
-        cur[ct][kt][r] = pv;
+        cur[ct][kt][r] = fast_exp2(cur[ct][kt][r]);
       }
       // (no scheduling barrier)
     }
@@ -380,13 +406,17 @@ void paged_prefill_kernel(PrefillArgs a) {
     u32x4 pb[CT][2];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-      l[ct] += ls[ct];
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
+      for (int st = 0; st < 2; ++st) {
         pb[ct][st] = u32x4{E::pack2(cur[ct][2 * st][0], cur[ct][2 * st][1]),
                            E::pack2(cur[ct][2 * st][2], cur[ct][2 * st][3]),
                            E::pack2(cur[ct][2 * st + 1][0], cur[ct][2 * st + 1][1]),
                            E::pack2(cur[ct][2 * st + 1][2], cur[ct][2 * st + 1][3])};
+        // the running sum adds the rounded probabilities the PV product uses,
+        // two per instruction
+#pragma unroll
+        for (int e = 0; e < 4; ++e) l[ct] = sum2<DT>(pb[ct][st][e], l[ct]);
+      }
     }
     // O^T += V^T . P^T; V^T operand: d row c of the tile, the same key slots
     // (operands read one step ahead)
@@ -397,11 +427,13 @@ void paged_prefill_kernel(PrefillArgs a) {
       const u32x2 hi = *(const u32x2*)(row + 16 + 4 * g);
       return u32x4{lo[0], lo[1], hi[0], hi[1]};
     };
-    u32x4 va_next = v_operand(0);
+    u32x4 vring[kOperandAhead];
+#pragma unroll
+    for (int t = 0; t < kOperandAhead; ++t) vring[t] = v_operand(t);
 #pragma unroll
     for (int t = 0; t < 2 * S::DTL; ++t) {
-      const u32x4 va = va_next;
-      if (t + 1 < 2 * S::DTL) va_next = v_operand(t + 1);
+      const u32x4 va = vring[t % kOperandAhead];
+      if (t + kOperandAhead < 2 * S::DTL) vring[t % kOperandAhead] = v_operand(t + kOperandAhead);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
         acc[ct][t % S::DTL] = mfma_k32<DT>(va, pb[ct][t / S::DTL], acc[ct][t % S::DTL]);
@@ -416,7 +448,164 @@ void paged_prefill_kernel(PrefillArgs a) {
     if (kb + 3 < nkb) load_regs(kb + 3);
     __syncthreads();
   };
-  if (nkb > 0) {
+  if constexpr (PP) {
+    // ---- ping-pong schedule (8 wavefronts, two per SIMD). Each wavefront's
+    // iteration i is a matrix half -- the scores of tile i and the PV product
+    // of tile i - 1, 64 MFMAs -- and a vector half -- tile i's softmax, one
+    // tile's LDS store and the next tile's global loads. Waves 4..7 start one
+    // barrier later than waves 0..3, so on every SIMD one wavefront runs its
+    // matrix half while the other runs its vector half (in lockstep the two
+    // pipes mostly took turns). Barrier intervals: the leading group's halves
+    // of iteration i are intervals 2i and 2i + 1, the following group's
+    // 2i + 1 and 2i + 2. Tile t is read (K) in intervals 2t, 2t + 1 and (V)
+    // 2t + 2, 2t + 3, so the leaders store their part of it in interval
+    // 2t - 1 (iteration t - 1) and the followers in 2t - 2 (iteration t - 2);
+    // the next tile for its buffer (t + 3) is first stored in interval
+    // 2t + 4: a 3-deep ring suffices. Each wavefront keeps one tile's global
+    // loads in flight, issued an iteration before their store.
+    const bool lead = w < NW / 2;
+    const int ahead = lead ? 1 : 2;  // the tile a wavefront stores in iteration i is i + ahead
+    f32x4 sc[CT][4];                 // scores of the tile in flight through the iteration
+    u32x4 pb[CT][2];                 // probabilities of the previous tile (PV operand)
+    using E = Elem<DT>;
+    constexpr int NQK = 4 * S::KS, NPV = 2 * S::DTL;
+    // matrix half: S(i) = K(i) . Q^T starting from -m (QK), O^T += V^T(i-1) . P^T(i-1) (PV)
+    auto matrix_half = [&](auto qk_tag, auto pv_tag, int i) {
+      constexpr bool QK = decltype(qk_tag)::value, PVH = decltype(pv_tag)::value;
+      const uint16_t* kb_lds = ks_lds[i % 3];
+      const uint16_t* vb_lds = vt_lds[(i + 2) % 3];
+      auto k_operand = [&](int t) {
+        return *(const u32x4*)&kb_lds[((t % 4) * 16 + c) * S::KROW + (t / 4) * 32 + 8 * g];
+      };
+      auto v_operand = [&](int t) {
+        const uint16_t* row = vb_lds + ((t % S::DTL) * 16 + c) * S::VROW + (t / S::DTL) * 32;
+        const u32x2 lo = *(const u32x2*)(row + 4 * g);
+        const u32x2 hi = *(const u32x2*)(row + 16 + 4 * g);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      };
+      if constexpr (QK) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt) sc[ct][kt] = negm[ct];
+      }
+      constexpr int NT_ = NQK > NPV ? NQK : NPV;
+      u32x4 kring[kOperandAhead], vring[kOperandAhead];
+#pragma unroll
+      for (int t = 0; t < kOperandAhead; ++t) {
+        if constexpr (QK) kring[t] = k_operand(t);
+        if constexpr (PVH) vring[t] = v_operand(t);
+      }
+#pragma unroll
+      for (int t = 0; t < NT_; ++t) {
+        if constexpr (QK) {
+          if (t < NQK) {
+            const u32x4 ka = kring[t % kOperandAhead];
+            if (t + kOperandAhead < NQK) kring[t % kOperandAhead] = k_operand(t + kOperandAhead);
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) sc[ct][t % 4] = mfma_k32<DT>(ka, qreg[ct][t / 4], sc[ct][t % 4]);
+          }
+        }
+        if constexpr (PVH) {
+          if (t < NPV) {
+            const u32x4 va = vring[t % kOperandAhead];
+            if (t + kOperandAhead < NPV) vring[t % kOperandAhead] = v_operand(t + kOperandAhead);
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+              acc[ct][t % S::DTL] = mfma_k32<DT>(va, pb[ct][t / S::DTL], acc[ct][t % S::DTL]);
+          }
+        }
+        // keep the steps in program order: hoisting every operand read to
+        // the top would hold all of them in registers at once
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    // vector half: tile i's mask, running max (the first tile sets it; later
+    // ones move it past kRescaleSlack only), exponentials, P^T and the sums
+    auto vector_half = [&](int i) {
+      const int k0 = i * BN;
+      if (!(k0 + BN - 1 <= qpos0 && k0 + BN <= kmax)) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (k0 + kt * 16 + 4 * g + r > col_lim[ct]) sc[ct][kt][r] = kNegInf;
+      }
+      const bool first = i == 0;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        float mx = kNegInf;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+          mx = fmaxf(mx, fmaxf(fmaxf(sc[ct][kt][0], sc[ct][kt][1]), fmaxf(sc[ct][kt][2], sc[ct][kt][3])));
+        mx = wave_max_groups_swap(mx);
+        const bool grow = first || mx > kRescaleSlack;
+        if (__any(grow)) {
+          const float d = grow ? mx : 0.f;
+          if (!first) {
+            const float alpha = fast_exp2(-d);
+            l[ct] *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < S::DTL; ++dt) acc[ct][dt] *= alpha;
+          }
+          negm[ct] -= d;
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt) sc[ct][kt] -= d;
+        }
+      }
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[ct][kt][r] = fast_exp2(sc[ct][kt][r]);
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          pb[ct][st] = u32x4{E::pack2(sc[ct][2 * st][0], sc[ct][2 * st][1]),
+                             E::pack2(sc[ct][2 * st][2], sc[ct][2 * st][3]),
+                             E::pack2(sc[ct][2 * st + 1][0], sc[ct][2 * st + 1][1]),
+                             E::pack2(sc[ct][2 * st + 1][2], sc[ct][2 * st + 1][3])};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) l[ct] = sum2<DT>(pb[ct][st][e], l[ct]);
+        }
+      }
+    };
+    if (nkb > 0) {
+      fill_bt(0);
+      load_regs(0);
+      store_regs(0);
+      if (!lead && nkb > 1) {
+        load_regs(1);
+        store_regs(1);
+      }
+      if (ahead < nkb) load_regs(ahead);
+      __syncthreads();
+      if (!lead) __syncthreads();  // the followers start half an iteration later
+      auto vector_and_memory = [&](int i) {
+        const int st = i + ahead;
+        if (st < nkb) store_regs(st % 3);
+        if (st + 1 < nkb) load_regs(st + 1);
+        vector_half(i);
+      };
+      // iteration 0 has no PV product, iteration nkb no scores: peeled
+      matrix_half(std::true_type{}, std::false_type{}, 0);
+      __syncthreads();
+      vector_and_memory(0);
+      __syncthreads();
+      for (int i = 1; i < nkb; ++i) {
+        matrix_half(std::true_type{}, std::true_type{}, i);
+        __syncthreads();
+        vector_and_memory(i);
+        __syncthreads();
+      }
+      matrix_half(std::false_type{}, std::true_type{}, nkb);
+      __syncthreads();
+      __syncthreads();
+      if (lead) __syncthreads();  // as many barriers as the followers
+    }
+  } else if (nkb > 0) {
     fill_bt(0);
     load_regs(0);
     store_regs(0);
@@ -454,9 +643,9 @@ void paged_prefill_kernel(PrefillArgs a) {
   for (int qt = 0; qt < CT; ++qt) {
     const float lsum = wave_sum_groups_swap(l[qt]);
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    if (!col_ok[qt]) continue;
-    uint8_t* orow =
-        (uint8_t*)a.out + ((int64_t)(q_lo + col_tok[qt]) * a.o_tok + (int64_t)col_head[qt] * a.o_head) * EB;
+    const Col col = column(qt);
+    if (!col.ok) continue;
+    uint8_t* orow = (uint8_t*)a.out + ((int64_t)(q_lo + col.tok) * a.o_tok + (int64_t)col.head * a.o_head) * EB;
 #pragma unroll
     for (int dt = 0; dt < S::DTL; ++dt) {
       const float o[4] = {acc[qt][dt][0], acc[qt][dt][1], acc[qt][dt][2], acc[qt][dt][3]};
@@ -580,18 +769,28 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   const int64_t slots = a.num_blocks * a.bs;
   const bool fast = a.bs_shift >= 0 && slots < (1 << 23) && a.c_slot < (1 << 23) &&
                     (slots * a.c_slot + a.c_head * a.num_kv_heads) < ((int64_t)1 << 31);
+  // ping-pong schedule for 8-wavefront workgroups whose block tables fit the
+  // block-id cache whole (IR_PREFILL_PINGPONG=0 turns it off for comparisons)
+  const char* e = getenv("IR_PREFILL_PINGPONG");
+  const bool pp = a.nw == 8 && a.max_blocks <= kBtCache && !(e && atoi(e) == 0);
   if (a.nw == 4) {
     const dim3 block(PShape<D, 4>::NT);
     if (fast)
-      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 4, 2>), dim3((unsigned)grid), block, 0, s, a);
+      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 4, 2, false>), dim3((unsigned)grid), block, 0, s, a);
     else
-      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 4, 2>), dim3((unsigned)grid), block, 0, s, a);
+      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 4, 2, false>), dim3((unsigned)grid), block, 0, s, a);
+  } else if (pp) {
+    const dim3 block(PShape<D, 8>::NT);
+    if (fast)
+      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 2, true>), dim3((unsigned)grid), block, 0, s, a);
+    else
+      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 2, true>), dim3((unsigned)grid), block, 0, s, a);
   } else {
     const dim3 block(PShape<D, 8>::NT);
     if (fast)
-      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 2>), dim3((unsigned)grid), block, 0, s, a);
+      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 2, false>), dim3((unsigned)grid), block, 0, s, a);
     else
-      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 2>), dim3((unsigned)grid), block, 0, s, a);
+      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 2, false>), dim3((unsigned)grid), block, 0, s, a);
   }
   return check_launch("ir_paged_prefill");
 }

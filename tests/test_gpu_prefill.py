@@ -241,3 +241,27 @@ def test_prefill_order_length_is_checked():
     with pytest.raises(RuntimeError, match="order holds"):
         kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[0], case.cu_seqlens_q,
                               case.q_start, cfg.chunk, cfg.block_size, cfg.scale, order=wrong)
+
+
+@pytest.mark.parametrize("name,prefixes,q_lens", [
+    ("qwen7b-prefill", None, None),
+    ("qwen7b-prefill", [0, 37, 512, 1000, 3, 3, 0, 5], [1, 31, 100, 512, 0, 9, 64, 33]),
+])
+def test_prefill_ping_pong_schedule_matches_lockstep_bit_for_bit(name, prefixes, q_lens, monkeypatch):
+    """The 8-wavefront kernel's ping-pong schedule (waves 4..7 half an
+    iteration behind 0..3) does the same arithmetic in the same order as the
+    lockstep schedule (IR_PREFILL_PINGPONG=0): identical outputs, and both
+    within the bar of the oracle."""
+    case = make_prefill_case(name, DEV, prefixes=prefixes, q_lens=q_lens)
+    outs = []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("IR_PREFILL_PINGPONG", flag)
+        outs.append(_run(case))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    cfg = case.config
+    ref = O.prefill_reference(
+        case.q.cpu(), case.k_cache.cpu(), case.v_cache.cpu(), case.block_tables[0].cpu(),
+        case.cu_seqlens_q.cpu(), case.q_start.cpu(), cfg.block_size, cfg.scale,
+    )
+    assert (outs[0].float().cpu() - ref).abs().max().item() <= TOL
