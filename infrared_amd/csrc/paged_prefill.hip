@@ -12,7 +12,9 @@
 // query token at position context - 1).
 //
 // Work decomposition: one workgroup of NW wavefronts per (query block, KV
-// head, sequence); heaviest query blocks (most keys) are dispatched first. NW
+// head, sequence), dispatched heaviest first: in the order
+// ir_paged_prefill_order builds once per step (all sequences' items by key
+// tiles), or else a sequence's last query blocks first. NW
 // is 8 (two per SIMD) unless that gives fewer workgroups than CUs; then 4 (one
 // per SIMD, up to 512 registers), twice the workgroups with half the columns
 // each, which shortens a small batch's critical path (4 x 256-token chunks:
@@ -23,9 +25,12 @@
 // owns columns 32w .. 32w+31 (two 16-column tiles). Every column
 // of a workgroup reads the same KV head, so each K/V element staged in LDS
 // feeds 32 columns per wavefront read. The workgroup walks the keys in
-// 64-key tiles staged in LDS, double buffered: the next tile's global loads
-// are in flight (in registers) while the current one is in the math, and they
-// are written to the other LDS buffer afterwards.
+// 64-key tiles staged in a 3-deep LDS ring: a later tile's global loads are
+// in flight (in registers) while the current one is in the math, and are
+// written to its LDS buffer a tile later. 8-wavefront workgroups run a
+// ping-pong schedule (waves 4..7 half an iteration behind 0..3, so each SIMD
+// overlaps one wave's MFMAs with the other's softmax); 4-wavefront ones and
+// long block tables run in lockstep, one barrier per tile.
 //   K tile : row-major [64 keys][D] (+32 bytes a row against bank conflicts);
 //   V tile : transposed [D][64 keys] (+16 bytes a row), written from pairs of
 //            keys, so one d column of 4 consecutive keys is one 8-byte read.
