@@ -112,6 +112,19 @@ __device__ __forceinline__ f32x4 mfma_k32<IR_DTYPE_F16>(u32x4 a, u32x4 b, f32x4 
                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// gfx950 LDS transpose read of 16-bit elements (ds_read_b64_tr_b16): within
+// each group of 16 lanes, lane 4a + b receives element b of the 4-element
+// (8-byte) pieces addressed by lanes a, a + 4, a + 8 and a + 12, in that order
+// (measured lane layout). p must point into LDS, 8-byte aligned.
+// Takes an LDS-address-space pointer: offsets computed in that space fold
+// into the instruction (a generic pointer costs a cast per read).
+typedef __attribute__((address_space(3))) const uint16_t lds_u16;
+__device__ __forceinline__ u32x2 lds_read_tr16(lds_u16* p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+  return __builtin_bit_cast(u32x2, v);
+}
+
 // acc + lo + hi of a dword holding two 16-bit elements (one v_dot2c against
 // packed 1.0s, fp32 accumulation).
 template <int DT>

@@ -27,13 +27,14 @@
 // feeds 32 columns per wavefront read. The workgroup walks the keys in
 // 64-key tiles staged in a 3-deep LDS ring: a later tile's global loads are
 // in flight (in registers) while the current one is in the math, and are
-// written to its LDS buffer a tile later. 8-wavefront workgroups run a
-// ping-pong schedule (waves 4..7 half an iteration behind 0..3, so each SIMD
-// overlaps one wave's MFMAs with the other's softmax); 4-wavefront ones and
-// long block tables run in lockstep, one barrier per tile.
-//   K tile : row-major [64 keys][D] (+32 bytes a row against bank conflicts);
-//   V tile : transposed [D][64 keys] (+16 bytes a row), written from pairs of
-//            keys, so one d column of 4 consecutive keys is one 8-byte read.
+// written to its LDS buffer a tile later. The workgroup runs in lockstep,
+// one barrier per tile; 8-wavefront workgroups can instead run a ping-pong
+// schedule (waves 4..7 half an iteration behind 0..3, so each SIMD overlaps
+// one wave's MFMAs with the other's softmax), selected by
+// IR_PREFILL_PINGPONG=1.
+//   K and V tiles: row-major [64 keys][D] (+32 bytes a row against bank
+//   conflicts), loaded and stored alike (a thread's K and V pieces share the
+//   key's slot); the PV product reads V^T with gfx950's transpose read.
 // Per tile a wavefront computes S^T = K . Q^T with 16x16x32 MFMA (rows = keys,
 // columns = its (token, head) pairs; Q^T stays in registers for the whole
 // walk), the online softmax in base 2 down each column (a lane owns one
@@ -58,7 +59,7 @@ namespace {
 
 constexpr int kBtCache = 1024;  // block ids staged in LDS per workgroup
 #ifndef IR_PREFILL_AHEAD
-#define IR_PREFILL_AHEAD 2
+#define IR_PREFILL_AHEAD 1
 #endif
 // MFMA steps between an LDS operand read and its use
 constexpr int kOperandAhead = IR_PREFILL_AHEAD;
@@ -98,11 +99,8 @@ struct PShape {
   // conflicts only with 32 extra bytes per K row and 16 per V^T row (8 and 16
   // bytes still conflict two ways, measured with SQ_LDS_BANK_CONFLICT)
   static constexpr int KROW = D + 16;  // elements per K row in LDS
-  static constexpr int VROW = BN + 8;  // elements per V^T row in LDS
   static constexpr int KCH = BN * D / 8;       // 16-byte K chunks per tile
-  static constexpr int VPR = BN / 2 * D / 8;   // (key pair, 8 d) V chunks per tile
   static constexpr int KPT = (KCH + NT - 1) / NT;
-  static constexpr int VPT = (VPR + NT - 1) / NT;
   static constexpr int KS = D / 32;   // k-steps of S^T = K . Q^T
   static constexpr int DTL = D / 16;  // d tiles of O^T
 };
@@ -116,7 +114,7 @@ void paged_prefill_kernel(PrefillArgs a) {
   constexpr int EB = 2;
   constexpr int CT = S::CT, BN = S::BN, NT = S::NT;
   __shared__ __attribute__((aligned(16))) uint16_t ks_lds[3][BN * S::KROW];
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[3][D * S::VROW];
+  __shared__ __attribute__((aligned(16))) uint16_t vs_lds[3][BN * S::KROW];
   __shared__ int32_t bt_lds[kBtCache];
 
   const int tid = threadIdx.x;
@@ -229,12 +227,13 @@ void paged_prefill_kernel(PrefillArgs a) {
     return u32x4{keep ? x[0] : 0u, keep ? x[1] : 0u, keep ? x[2] : 0u, keep ? x[3] : 0u};
   };
 
-  u32x4 kreg[S::KPT];
-  u32x4 vreg[S::VPT][2];
+  // K and V of a key share its slot: each thread loads the same 16-byte
+  // piece of both
+  u32x4 kreg[S::KPT], vreg[S::KPT];
   // whether each load in flight reads a usable key: applied when the tile is
   // stored (zero_unless), not when it is loaded, so the loads stay in flight
   // through the next tile's math instead of being waited for at once
-  bool kuse[S::KPT], vuse[S::VPT][2];
+  bool kuse[S::KPT];
   // Global loads of key tile kb into registers (whole workgroup, uniform call).
   auto load_regs = [&](int kb) {
     const int k0 = kb * BN;
@@ -252,24 +251,13 @@ void paged_prefill_kernel(PrefillArgs a) {
         bool use;
         const int64_t sl = slot_of(k0 + key, use);
         kreg[i] = *(const u32x4*)(kc + sl + part * 8);
+        vreg[i] = *(const u32x4*)(vc + sl + part * 8);
         kuse[i] = use;
       }
     }
-#pragma unroll
-    for (int i = 0; i < S::VPT; ++i) {
-      const int v = tid + NT * i;
-      if (S::VPR % NT == 0 || v < S::VPR) {
-        const int pr = v % (BN / 2), part = v / (BN / 2);
-        bool u0, u1;
-        const int64_t s0 = slot_of(k0 + 2 * pr, u0), s1 = slot_of(k0 + 2 * pr + 1, u1);
-        vreg[i][0] = *(const u32x4*)(vc + s0 + part * 8);
-        vreg[i][1] = *(const u32x4*)(vc + s1 + part * 8);
-        vuse[i][0] = u0;
-        vuse[i][1] = u1;
-      }
-    }
   };
-  // Registers -> LDS buffer `buf` (K row-major, V transposed).
+  // Registers -> LDS buffer `buf`: K and V tiles both row-major [64 keys][D]
+  // (+32 bytes a row).
   auto store_regs = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < S::KPT; ++i) {
@@ -277,23 +265,24 @@ void paged_prefill_kernel(PrefillArgs a) {
       if (q < S::KCH) {
         const int key = q / (D / 8), part = q % (D / 8);
         *(u32x4*)&ks_lds[buf][key * S::KROW + part * 8] = zero_unless(kreg[i], kuse[i]);
+        *(u32x4*)&vs_lds[buf][key * S::KROW + part * 8] = zero_unless(vreg[i], kuse[i]);
       }
     }
-#pragma unroll
-    for (int i = 0; i < S::VPT; ++i) {
-      const int v = tid + NT * i;
-      if (v < S::VPR) {
-        const int pr = v % (BN / 2), part = v / (BN / 2);
-        const u32x4 x0 = zero_unless(vreg[i][0], vuse[i][0]), x1 = zero_unless(vreg[i][1], vuse[i][1]);
-        uint16_t* dst = &vt_lds[buf][part * 8 * S::VROW + 2 * pr];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // element 2e / 2e+1 of both keys -> (key 2pr, key 2pr+1) pairs
-          *(uint32_t*)(dst + (2 * e) * S::VROW) = __builtin_amdgcn_perm(x1[e], x0[e], 0x05040100u);
-          *(uint32_t*)(dst + (2 * e + 1) * S::VROW) = __builtin_amdgcn_perm(x1[e], x0[e], 0x07060302u);
-        }
-      }
-    }
+  };
+  // V^T operand of PV step t (d tile t % DTL, 32-key step t / DTL) from the
+  // row-major V tile at vb: lane (g, c) needs V[32 st + 4 g + e][16 dt + c]
+  // (k-slots 0..3) and V[32 st + 16 + 4 g + e][..] (4..7), e = 0..3: the
+  // columns of 4 consecutive rows. gfx950's transpose read returns, to lane
+  // 4a + b of each 16-lane group, element b of the 4-element pieces that lanes
+  // a, a + 4, a + 8, a + 12 address, so lane c points at row key0 + c / 4,
+  // columns 16 dt + 4 (c % 4) .. +3, and gets its column of rows key0 .. +3.
+  auto v_operand_tr = [&](const uint16_t* vb, int t) {
+    const int dt = t % S::DTL, st = t / S::DTL;
+    const int v_lane = (4 * g + (c >> 2)) * S::KROW + 4 * (c & 3);
+    lds_u16* p = (lds_u16*)vb + v_lane + 32 * st * S::KROW + 16 * dt;
+    const u32x2 lo = lds_read_tr16(p);
+    const u32x2 hi = lds_read_tr16(p + 16 * S::KROW);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
   };
 
   // ---- online softmax state, per column tile: lane owns column c of it.
@@ -425,12 +414,9 @@ void paged_prefill_kernel(PrefillArgs a) {
     }
     // O^T += V^T . P^T; V^T operand: d row c of the tile, the same key slots
     // (operands read one step ahead)
-    const uint16_t* vb_lds = vt_lds[kb % 3];
+    const uint16_t* vb_lds = vs_lds[kb % 3];
     auto v_operand = [&](int t) {
-      const uint16_t* row = vb_lds + ((t % S::DTL) * 16 + c) * S::VROW + (t / S::DTL) * 32;
-      const u32x2 lo = *(const u32x2*)(row + 4 * g);
-      const u32x2 hi = *(const u32x2*)(row + 16 + 4 * g);
-      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      return v_operand_tr(vb_lds, t);
     };
     u32x4 vring[kOperandAhead];
 #pragma unroll
@@ -478,15 +464,12 @@ void paged_prefill_kernel(PrefillArgs a) {
     auto matrix_half = [&](auto qk_tag, auto pv_tag, int i) {
       constexpr bool QK = decltype(qk_tag)::value, PVH = decltype(pv_tag)::value;
       const uint16_t* kb_lds = ks_lds[i % 3];
-      const uint16_t* vb_lds = vt_lds[(i + 2) % 3];
+      const uint16_t* vb_lds = vs_lds[(i + 2) % 3];
       auto k_operand = [&](int t) {
         return *(const u32x4*)&kb_lds[((t % 4) * 16 + c) * S::KROW + (t / 4) * 32 + 8 * g];
       };
       auto v_operand = [&](int t) {
-        const uint16_t* row = vb_lds + ((t % S::DTL) * 16 + c) * S::VROW + (t / S::DTL) * 32;
-        const u32x2 lo = *(const u32x2*)(row + 4 * g);
-        const u32x2 hi = *(const u32x2*)(row + 16 + 4 * g);
-        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+        return v_operand_tr(vb_lds, t);
       };
       if constexpr (QK) {
 #pragma unroll
@@ -774,10 +757,13 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   const int64_t slots = a.num_blocks * a.bs;
   const bool fast = a.bs_shift >= 0 && slots < (1 << 23) && a.c_slot < (1 << 23) &&
                     (slots * a.c_slot + a.c_head * a.num_kv_heads) < ((int64_t)1 << 31);
-  // ping-pong schedule for 8-wavefront workgroups whose block tables fit the
-  // block-id cache whole (IR_PREFILL_PINGPONG=0 turns it off for comparisons)
+  // ping-pong schedule on request (IR_PREFILL_PINGPONG=1), for 8-wavefront
+  // workgroups whose block tables fit the block-id cache whole. Measured on
+  // the 8 x 512-token workload: ahead of lockstep while V went through a
+  // register transpose (235 vs 257 us), behind it with row-major V and
+  // transpose reads (242 vs 225 us), so lockstep is the default.
   const char* e = getenv("IR_PREFILL_PINGPONG");
-  const bool pp = a.nw == 8 && a.max_blocks <= kBtCache && !(e && atoi(e) == 0);
+  const bool pp = a.nw == 8 && a.max_blocks <= kBtCache && e && atoi(e) == 1;
   if (a.nw == 4) {
     const dim3 block(PShape<D, 4>::NT);
     if (fast)
