@@ -3,9 +3,11 @@ model (random weights, head_dim 64 so the HIP block-table kernels engage).
 
 The flows are the ones the reference engine drives the seam with
 (infrared/engine/paged_engine.py: prefill with a cached prefix :194-207,
-batched decode :290-332, packed mixed prefill+decode steps :461-516): whole
-and chunked prefill, prefix-cache block reuse, greedy decode, and a mixed step
-that packs one sequence's decode with another's prefill chunk. At every step
+batched decode :290-332, packed mixed prefill+decode steps :461-516,
+recompute preemption :553-600): whole and chunked prefill, prefix-cache block
+reuse, greedy decode, a mixed step that packs one sequence's decode with
+another's prefill chunk, and eviction + recompute of a sequence whose new
+blocks still hold another's K/V. At every step
 the logits are compared with a full recompute of the sequence by the oracle
 (contiguous causal attention over all tokens, fp32, the reference's model
 math of infrared/model/layers.py:79-118 and :158-180), so paging, block
@@ -88,6 +90,11 @@ class Blocks:
     def grow(self, table: list[int], length: int) -> None:
         while len(table) * BS < length:
             table.append(self.free.pop())
+
+    def release(self, table: list[int]) -> None:
+        """Returns a table's blocks; the next grows reuse them first (LIFO)."""
+        self.free.extend(reversed(table))
+        table.clear()
 
 
 def _step(model, pool, seqs):
@@ -207,3 +214,69 @@ def test_mixed_step_packs_decode_with_prefill_chunk():
     logits = _step(model, pool, [(a_tok[29:], ta, 29), (b_tok[20:], tb, 20)])
     _check(model, logits[:1], a_tok, slice(29, None))
     _check(model, logits[1:], b_tok, slice(20, None))
+
+
+def test_recompute_preemption_then_resume():
+    """Recompute preemption as the reference engine does it
+    (infrared/engine/paged_engine.py:553-600): two sequences decode in a 7-block
+    pool; when the newest needs a block and none is free it is evicted (blocks
+    freed), the other decodes on and finishes, then the evicted one re-prefills
+    its whole history -- prompt and generated tokens -- in chunks into blocks the
+    first one left (holding its stale K/V) and decodes on. Every step's logits
+    match the full recompute, so nothing of the old blocks or tables leaks."""
+    model = TinyModel(10)
+    pool = PagedKVPool(L, 7, BS, HKV, D, torch.bfloat16, device=DEV, strict=True)
+    blocks = Blocks(7, seed=11)
+    g = torch.Generator().manual_seed(12)
+    a = torch.randint(0, VOCAB, (40,), generator=g).tolist()
+    b = torch.randint(0, VOCAB, (30,), generator=g).tolist()
+    ta: list[int] = []
+    tb: list[int] = []
+    blocks.grow(ta, len(a))
+    blocks.grow(tb, len(b))
+    logits = _step(model, pool, [(a, ta, 0), (b, tb, 0)])
+    _check(model, logits[: len(a)], a, slice(0, None))
+    _check(model, logits[len(a) :], b, slice(0, None))
+
+    def greedy(tokens):
+        return int(model.reference_logits(tokens)[-1].argmax())
+
+    a.append(greedy(a))
+    b.append(greedy(b))
+    running = {"a": (a, ta), "b": (b, tb)}
+    old_tb = None
+    for _ in range(20):
+        # a block for each running sequence's new token; when the pool is dry
+        # the newest running sequence (b) is preempted
+        for name in list(running):
+            tok, tab = running[name]
+            if len(tab) * BS >= len(tok):
+                continue
+            if not blocks.free:
+                old_tb = list(tb)
+                blocks.release(tb)
+                del running["b"]
+                if name == "b":
+                    continue
+            blocks.grow(tab, len(tok))
+        seqs = list(running.values())
+        got = _decode(model, pool, [t for t, _ in seqs], [t for _, t in seqs], blocks)
+        for i, (tok, _) in enumerate(seqs):
+            _check(model, got[i : i + 1], tok, slice(-1, None))
+            tok.append(greedy(tok))
+    assert old_tb is not None and "b" not in running, "the pool never ran dry"
+    # a finishes; b recomputes the K/V of its whole history (all but the token
+    # it feeds next) in chunks, into a's freed blocks, then decodes on
+    blocks.release(ta)
+    hist = len(b) - 1
+    done = 0
+    for n in (16, 20, hist - 36):
+        blocks.grow(tb, done + n)
+        logits = _step(model, pool, [(b[done : done + n], tb, done)])
+        _check(model, logits, b[: done + n], slice(done, None))
+        done += n
+    assert tb != old_tb[: len(tb)]
+    for _ in range(8):
+        got = _decode(model, pool, [b], [tb], blocks)
+        _check(model, got, b, slice(-1, None))
+        b.append(greedy(b))
