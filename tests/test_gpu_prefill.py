@@ -68,6 +68,10 @@ _SWEEP = [
     (torch.bfloat16, 24, 2, 64, 4),  # 12 heads per KV head: two head groups of 8
     (torch.float16, 28, 4, 128, 1),
     (torch.float16, 12, 3, 64, 8),
+    # block sizes that are not powers of two take the general addressing path
+    # (64-bit slot offsets, a division per key instead of shifts)
+    (torch.bfloat16, 28, 4, 128, 12),
+    (torch.float16, 8, 2, 64, 24),
 ]
 
 
@@ -246,6 +250,9 @@ def test_prefill_order_length_is_checked():
 @pytest.mark.parametrize("name,prefixes,q_lens", [
     ("qwen7b-prefill", None, None),
     ("qwen7b-prefill", [0, 37, 512, 1000, 3, 3, 0, 5], [1, 31, 100, 512, 0, 9, 64, 33]),
+    # fp16, head_dim 64, a 12-token block (general addressing path), 8-wavefront workgroups
+    (PrefillConfig("pf-pp-f16", 8, 0, 32, 8, 64, 12, torch.float16, 0, seed=31),
+     [0, 100, 7, 300, 12, 0, 50, 1], [300, 256, 290, 200, 310, 280, 260, 299]),
 ])
 def test_prefill_ping_pong_schedule_matches_lockstep_bit_for_bit(name, prefixes, q_lens, monkeypatch):
     """The 8-wavefront kernel's ping-pong schedule (waves 4..7 half an
