@@ -64,9 +64,10 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--partition", type=int, default=0, help="split-KV partition tokens (0 = library default)")
     p.add_argument("--schedule", choices=("auto", "planned", "fixed"), default="auto",
                    help="decode: the seam's choice (default: kernels.decode_plan_pays), "
-                   "balanced plan + run, or fixed split-KV partitions")
+                   "balanced plan + run, or fixed split-KV partitions; prefill: the seam's choice "
+                   "(kernels.prefill_order_pays), the heaviest-first work order, or the default order")
     p.add_argument("--layers", type=int, default=28,
-                   help="decode: calls per plan (layers of one decode step sharing its metadata)")
+                   help="calls per decode plan / prefill order (layers of one step sharing its metadata)")
     p.add_argument("--cpu-iters", type=int, default=3, help="timed CPU-baseline iterations (0 = skip)")
     p.add_argument("--cpu-seqs", type=int, default=0, help="sequences in the CPU sample (0 = all)")
     p.add_argument("--check", action="store_true", help="also check the output against the oracle")
