@@ -272,3 +272,39 @@ def test_prefill_ping_pong_schedule_matches_lockstep_bit_for_bit(name, prefixes,
         case.cu_seqlens_q.cpu(), case.q_start.cpu(), cfg.block_size, cfg.scale,
     )
     assert (outs[0].float().cpu() - ref).abs().max().item() <= TOL
+
+
+def test_prefill_order_and_kernel_replay_in_a_hip_graph():
+    """A step's order build and prefill captured in one hipGraph: each of three
+    replays -- with eager work clearing the output and scribbling over the order
+    buffer in between -- equals the eager, unordered call bit for bit."""
+    case = make_prefill_case("qwen7b-prefill", DEV)
+    cfg = case.config
+    b, max_q = len(case.q_lens), max(case.q_lens)
+    eager = _run(case)
+    out = torch.empty_like(case.q)
+    buf = torch.empty(kernels.prefill_order_len(b, max_q, cfg.num_q_heads, cfg.num_kv_heads), dtype=torch.int32,
+                      device=DEV)
+
+    def call():
+        order = kernels.prefill_order(case.cu_seqlens_q, case.q_start, case.q.shape[0], max_q,
+                                      case.block_tables[0].shape[1], cfg.block_size, cfg.num_q_heads,
+                                      cfg.num_kv_heads, buf=buf)
+        kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[0], case.cu_seqlens_q,
+                              case.q_start, max_q, cfg.block_size, cfg.scale, out=out, order=order)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for _ in range(3):
+        out.zero_()
+        buf.fill_(-7)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
