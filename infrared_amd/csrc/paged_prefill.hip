@@ -61,7 +61,8 @@ constexpr int kBtCache = 1024;  // block ids staged in LDS per workgroup
 #ifndef IR_PREFILL_AHEAD
 #define IR_PREFILL_AHEAD 1
 #endif
-// MFMA steps between an LDS operand read and its use
+// MFMA steps between an LDS operand read and its use (2 measured the same as
+// 1 on the 8 x 512-token workload, with more register pressure)
 constexpr int kOperandAhead = IR_PREFILL_AHEAD;
 
 struct PrefillArgs {
