@@ -17,6 +17,10 @@ Timing: W warm-up calls, then K calls captured in one hipGraph and replayed
 between two events on the launch stream, with torch.cuda.synchronize() on
 both sides. Calls rotate over R disjoint copies of the pool + block tables so
 consecutive calls do not hit K/V left in the 256 MB MALL by the previous one.
+``roofline.peak`` is the published MI355X figure (8 TB/s HBM, 2.5 PFLOP/s dense
+bf16 MFMA) and ``frac`` is taken against it; ``roofline.measured_peak`` is the
+same roof measured on the device after the timing (a 1 GiB device copy, or an
+8192^3 bf16 matmul through torch's BLAS), reported beside it.
 ``value`` is per call with the plan builds included; the roofline's
 ``achieved`` is the attention kernel's own launches (a graph of K runs
 without plan builds).
@@ -288,6 +292,7 @@ def _bench_prefill(args) -> dict:
                    "schedule": "heaviest-first order" if ordered else "default order",
                    "layers_per_order": args.layers if ordered else None},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "measured_peak": _measured_peak("mfma"),
                      "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": _traffic("prefill_qwen7b-prefill")[0],
                      "timed": f"prefill call, {args.mode} launches, events on the launch stream"},
         "cpu_baseline": cpu,
@@ -355,6 +360,7 @@ def _bench_mixed(args) -> dict:
                    "scatter_bytes_per_step": scatter_bytes, "overlap_streams": args.overlap,
                    "replays": n},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "measured_peak": _measured_peak("hbm"),
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                      "timed": "whole step (decode KV bytes / step time: scatter and prefill time included)"},
         "cpu_baseline": cpu,
@@ -394,10 +400,37 @@ def _bench_rope(args) -> dict:
         "config": {"workload": "one mixed-step layer: rotate q (in/out) and k, write k/v into a head-major pool",
                    "bytes_per_call": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "measured_peak": _measured_peak("hbm"),
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                      "timed": f"rope+scatter call, {args.mode} launches, events on the launch stream"},
         "cpu_baseline": None,
     }
+
+
+def _measured_peak(bound: str) -> dict:
+    """The roof the kernel is held against, measured on this device beside the
+    published figure: a 1 GiB device-to-device copy (read + write bytes / time)
+    for HBM-bound kernels, an 8192^3 bf16 matmul through torch's BLAS for
+    MFMA-bound ones. Events around 10 runs after 3 warm-ups."""
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if bound == "hbm":
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        run, work, unit, how = (lambda: dst.copy_(src)), 2 * src.numel() / 1e9, "GB/s", "1 GiB device copy"
+    else:
+        n = 8192
+        x = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+        y = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+        run, work, unit, how = (lambda: x @ y), 2 * n**3 / 1e12, "TFLOP/s", "8192^3 bf16 matmul (torch BLAS)"
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(10):
+        run()
+    e.record()
+    torch.cuda.synchronize()
+    return {"value": round(work / (s.elapsed_time(e) / 10 * 1e-3), 1), "unit": unit, "how": how}
 
 
 def _time_eager(call, args) -> float:
@@ -519,6 +552,7 @@ def main() -> int:
             "bound": "hbm",
             "achieved": round(kgbps, 2),
             "peak": HBM_PEAK_GBPS,
+            "measured_peak": _measured_peak("hbm"),
             "unit": "GB/s",
             "frac": round(kgbps / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
