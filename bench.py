@@ -72,7 +72,7 @@ def _parse() -> argparse.Namespace:
                    "(kernels.prefill_order_pays), the heaviest-first work order, or the default order")
     p.add_argument("--layers", type=int, default=28,
                    help="calls per decode plan / prefill order (layers of one step sharing its metadata)")
-    p.add_argument("--cpu-iters", type=int, default=3, help="timed CPU-baseline iterations (0 = skip)")
+    p.add_argument("--cpu-iters", type=int, default=5, help="timed CPU-baseline iterations (0 = skip)")
     p.add_argument("--cpu-seqs", type=int, default=0, help="sequences in the CPU sample (0 = all)")
     p.add_argument("--check", action="store_true", help="also check the output against the oracle")
     p.add_argument("--mode", choices=("graph", "eager"), default="graph",
@@ -84,9 +84,18 @@ def _parse() -> argparse.Namespace:
     return p.parse_args()
 
 
-def _graph_ms(fn, steps: int) -> float:
-    """ms per call of ``steps`` calls of fn captured in one hipGraph, replayed
-    between events on the launch stream (after one warm replay)."""
+WARM_MS = 50.0  # GPU time of graph replays before the timed ones
+TIMED_REPLAYS = 7  # timed replays; the median is reported
+_REPLAY_STATS: dict[str, dict] = {}
+
+
+def _graph_ms(fn, steps: int, tag: str = "call") -> float:
+    """ms per call of ``steps`` calls of fn captured in one hipGraph.
+
+    The graph is replayed until at least ``WARM_MS`` of GPU time has passed
+    (clocks and caches reach their steady state), then ``TIMED_REPLAYS``
+    replays are timed one by one between events on the launch stream; the
+    median per-call time is returned and the spread kept under ``tag``."""
     graph = torch.cuda.CUDAGraph()
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
@@ -96,14 +105,31 @@ def _graph_ms(fn, steps: int) -> float:
     with torch.cuda.graph(graph):
         for i in range(steps):
             fn(i)
-    graph.replay()
-    torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    graph.replay()
-    e.record()
-    torch.cuda.synchronize()
-    return s.elapsed_time(e) / steps
+    warm_ms, warm_replays = 0.0, 0
+    while warm_ms < WARM_MS and warm_replays < 100000:
+        s.record()
+        graph.replay()
+        e.record()
+        torch.cuda.synchronize()
+        warm_ms += s.elapsed_time(e)
+        warm_replays += 1
+    per_call = []
+    for _ in range(TIMED_REPLAYS):
+        s.record()
+        graph.replay()
+        e.record()
+        torch.cuda.synchronize()
+        per_call.append(s.elapsed_time(e) / steps)
+    _REPLAY_STATS[tag] = {
+        "timed_replays": TIMED_REPLAYS,
+        "calls_per_replay": steps,
+        "warm_replays": warm_replays,
+        "warm_ms": round(warm_ms, 2),
+        "min_us": round(min(per_call) * 1e3, 3),
+        "max_us": round(max(per_call) * 1e3, 3),
+    }
+    return statistics.median(per_call)
 
 
 def _eager_ms(fn, steps: int) -> float:
@@ -176,14 +202,49 @@ def _gpu_decode(case, args):
     eager_ms = _eager_ms(call, args.steps)
     if args.mode == "eager":
         return info, eager_ms, eager_ms, eager_ms, outs
-    call_ms = _graph_ms(call, args.steps)
-    kernel_ms = _graph_ms(run, args.steps) if planned else call_ms
+    call_ms = _graph_ms(call, args.steps, "call")
+    kernel_ms = _graph_ms(run, args.steps, "kernel") if planned else call_ms
     if planned:
-        info["plan_us"] = round(_graph_ms(plan, max(args.steps // 4, 8)) * 1e3, 2)
+        info["plan_us"] = round(_graph_ms(plan, max(args.steps // 4, 8), "plan") * 1e3, 2)
     return info, eager_ms, call_ms, kernel_ms, outs
 
 
+def _cpu_host() -> dict:
+    """Host facts for the CPU baseline: the threads torch uses (the box's CPU
+    share: OMP_NUM_THREADS), the CPUs the OS reports and the CPU model."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    return {"cores": torch.get_num_threads(), "host_cpus": os.cpu_count(), "affinity_cpus": affinity,
+            "cpu_model": model}
+
+
+def _cpu_median(fn, iters: int) -> tuple[float, float, float]:
+    """(median, min, max) seconds of ``iters`` timed calls of fn after one warm-up."""
+    fn()
+    times = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), min(times), max(times)
+
+
 def _cpu_baseline(case, args):
+    """The reference's naive-gather fallback (the oracle's restatement of
+    gather -> repeat_kv -> masked softmax, in the workload dtype) on the host
+    cores over the same inputs. ``executed_bytes``: the padded, repeated K/V the
+    naive path's two einsums read (B * T_max * H_q * D * 2 tensors)."""
     from oracle import naive as O
 
     cfg = case.config
@@ -196,24 +257,25 @@ def _cpu_baseline(case, args):
     mask = O.decode_mask(ctx, t_max, cfg.dtype)
     q = case.q[:n, None].cpu()
     kc, vc = case.k_cache.cpu(), case.v_cache.cpu()
-    threads = torch.get_num_threads()
-    O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, cfg.n_rep)  # warm-up
-    times = []
-    for _ in range(args.cpu_iters):
-        t0 = time.perf_counter()
-        O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, cfg.n_rep)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
+    host = _cpu_host()
+    t, t_lo, t_hi = _cpu_median(lambda: O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, cfg.n_rep),
+                                args.cpu_iters)
     esize = torch.tensor([], dtype=cfg.dtype).element_size()
     kv = sum(ctx) * 2 * cfg.num_kv_heads * cfg.head_dim * esize
+    executed = n * t_max * cfg.num_q_heads * cfg.head_dim * esize * 2
     return {
         "value": round(kv / t / 1e9, 4),
         "unit": "GB/s",
         "us_per_call": round(t * 1e6, 1),
-        "cores": threads,
+        "min_us": round(t_lo * 1e6, 1),
+        "max_us": round(t_hi * 1e6, 1),
+        **host,
         "kind": "port",
-        "sample": f"{n} of {cfg.num_seqs} sequences (sum ctx {sum(ctx)}), naive gather+repeat_kv+"
-        f"masked softmax in {str(cfg.dtype).replace('torch.', '')}, median of {args.cpu_iters} "
+        "algorithmic_bytes": kv,
+        "executed_bytes": executed,
+        "executed_over_algorithmic": round(executed / kv, 2),
+        "sample": f"{n} of {cfg.num_seqs} sequences (sum ctx {sum(ctx)}, padded to {t_max}), naive gather+"
+        f"repeat_kv+masked softmax in {str(cfg.dtype).replace('torch.', '')}, median of {args.cpu_iters} "
         "after 1 warm-up, torch CPU",
     }
 
@@ -269,16 +331,14 @@ def _bench_prefill(args) -> dict:
         mask = O.attention_mask([0], pre, n, pre + n, cfg.dtype)
         q = case.q[None, :n].cpu()
         kc, vc = case.k_cache.cpu(), case.v_cache.cpu()
-        O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, cfg.n_rep)
-        times = []
-        for _ in range(args.cpu_iters):
-            t0 = time.perf_counter()
-            O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, cfg.n_rep)
-            times.append(time.perf_counter() - t0)
-        t = statistics.median(times)
+        t, t_lo, t_hi = _cpu_median(lambda: O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, cfg.n_rep),
+                                    args.cpu_iters)
         fl = 4 * cfg.num_q_heads * cfg.head_dim * (n * pre + n * (n + 1) // 2)
-        cpu = {"value": round(fl / t / 1e12, 6), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-               "kind": "port",
+        # the naive path computes every (query, key) pair of the padded score matrix
+        fl_exec = 4 * cfg.num_q_heads * cfg.head_dim * n * (pre + n)
+        cpu = {"value": round(fl / t / 1e12, 6), "unit": "TFLOP/s", "us_per_call": round(t * 1e6, 1),
+               "min_us": round(t_lo * 1e6, 1), "max_us": round(t_hi * 1e6, 1), **_cpu_host(), "kind": "port",
+               "algorithmic_flops": fl, "executed_flops": fl_exec,
                "sample": f"sequence 0 only ({n} queries after a {pre}-token prefix), naive gather+repeat_kv+masked "
                f"softmax in bf16, median of {args.cpu_iters} after 1 warm-up, torch CPU"}
     return {
@@ -306,17 +366,26 @@ def _bench_mixed(args) -> dict:
     cfg, pool, batch, inputs = make_mixed_case("qwen7b-mixed", "cuda")
     step = MixedStep(pool, batch, inputs, cfg.scale, overlap=args.overlap)
     step.capture()
-    for _ in range(max(1, args.warmup // 10)):
-        step.replay()
-    torch.cuda.synchronize()
-    n = max(1, args.steps // 20)
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(n):
+    warm_ms, warm = 0.0, 0
+    while warm_ms < WARM_MS and warm < 1000:
+        s.record()
         step.replay()
-    e.record()
-    torch.cuda.synchronize()
-    ms = s.elapsed_time(e) / n
+        e.record()
+        torch.cuda.synchronize()
+        warm_ms += s.elapsed_time(e)
+        warm += 1
+    n = max(TIMED_REPLAYS, args.steps // 20)
+    per = []
+    for _ in range(n):
+        s.record()
+        step.replay()
+        e.record()
+        torch.cuda.synchronize()
+        per.append(s.elapsed_time(e))
+    ms = statistics.median(per)
+    _REPLAY_STATS["step"] = {"timed_replays": n, "warm_replays": warm, "warm_ms": round(warm_ms, 2),
+                             "min_us": round(min(per) * 1e3, 2), "max_us": round(max(per) * 1e3, 2)}
     esize = 2
     dec_bytes = int(batch.dec_ctx.long().sum()) * 2 * cfg.num_kv_heads * cfg.head_dim * esize * cfg.num_layers
     pairs = cfg.num_prefill * (cfg.chunk * cfg.prefix + cfg.chunk * (cfg.chunk + 1) // 2)
@@ -337,17 +406,17 @@ def _bench_mixed(args) -> dict:
         mask = O.decode_mask(ctx, t_max, cfg.dtype)
         q = inputs.q_dec[0, :nd, None].cpu()
         kc, vc = pool.k[0].cpu(), pool.v[0].cpu()
-        O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, cfg.num_q_heads // cfg.num_kv_heads)
-        times = []
-        for _ in range(args.cpu_iters):
-            t0 = time.perf_counter()
-            O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, cfg.num_q_heads // cfg.num_kv_heads)
-            times.append(time.perf_counter() - t0)
-        t = statistics.median(times)
+        n_rep = cfg.num_q_heads // cfg.num_kv_heads
+        t, t_lo, t_hi = _cpu_median(lambda: O.paged_attention_naive(q, kc, vc, gs, mask, cfg.scale, n_rep),
+                                    args.cpu_iters)
         kvb = sum(ctx) * 2 * cfg.num_kv_heads * cfg.head_dim * esize
-        cpu = {"value": round(kvb / t / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
-               "sample": f"{nd} of {cfg.num_decode} decode rows of one layer (prefill and scatter not included), "
-               f"naive gather+repeat_kv+masked softmax in bf16, median of {args.cpu_iters}, torch CPU"}
+        executed = nd * t_max * cfg.num_q_heads * cfg.head_dim * esize * 2
+        cpu = {"value": round(kvb / t / 1e9, 4), "unit": "GB/s", "us_per_call": round(t * 1e6, 1),
+               "min_us": round(t_lo * 1e6, 1), "max_us": round(t_hi * 1e6, 1), **_cpu_host(), "kind": "port",
+               "algorithmic_bytes": kvb, "executed_bytes": executed,
+               "sample": f"{nd} of {cfg.num_decode} decode rows of one layer (prefill and scatter not included; "
+               f"x{cfg.num_layers} layers is an extrapolation), naive gather+repeat_kv+masked softmax in bf16, "
+               f"median of {args.cpu_iters} after 1 warm-up, torch CPU"}
     return {
         "metric": "mixed engine step us per 28-layer hipGraph replay (224 decode rows + 4 x 256-token prefill chunks)",
         "value": round(ms * 1e3, 2), "unit": "us/step", "us_per_layer": round(ms * 1e3 / cfg.num_layers, 2),
@@ -409,28 +478,41 @@ def _bench_rope(args) -> dict:
 
 def _measured_peak(bound: str) -> dict:
     """The roof the kernel is held against, measured on this device beside the
-    published figure: a 1 GiB device-to-device copy (read + write bytes / time)
-    for HBM-bound kernels, an 8192^3 bf16 matmul through torch's BLAS for
-    MFMA-bound ones. Events around 10 runs after 3 warm-ups."""
+    published figure. HBM-bound kernels: a read-only stream of 4 GiB with the
+    decode kernels' load form (``ir_hbm_read``: non-temporal 16-byte loads,
+    ``value``) and a 1 GiB device-to-device copy (read + write bytes). MFMA-bound
+    ones: an 8192^3 bf16 matmul through torch's BLAS. Events around 10 runs
+    after 3 warm-ups; the buffers exceed the 256 MB MALL."""
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def rate(run, work):
+        for _ in range(3):
+            run()
+        torch.cuda.synchronize()
+        s.record()
+        for _ in range(10):
+            run()
+        e.record()
+        torch.cuda.synchronize()
+        return round(work / (s.elapsed_time(e) / 10 * 1e-3), 1)
+
     if bound == "hbm":
+        from infrared_amd import kernels
+
+        src = torch.empty(4 << 30, dtype=torch.uint8, device="cuda")
+        sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+        read = rate(lambda: kernels.hbm_read(src, sink), src.numel() / 1e9)
+        del src
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
-        run, work, unit, how = (lambda: dst.copy_(src)), 2 * src.numel() / 1e9, "GB/s", "1 GiB device copy"
-    else:
-        n = 8192
-        x = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
-        y = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
-        run, work, unit, how = (lambda: x @ y), 2 * n**3 / 1e12, "TFLOP/s", "8192^3 bf16 matmul (torch BLAS)"
-    for _ in range(3):
-        run()
-    torch.cuda.synchronize()
-    s.record()
-    for _ in range(10):
-        run()
-    e.record()
-    torch.cuda.synchronize()
-    return {"value": round(work / (s.elapsed_time(e) / 10 * 1e-3), 1), "unit": unit, "how": how}
+        copy = rate(lambda: dst.copy_(src), 2 * src.numel() / 1e9)
+        del src, dst
+        return {"value": read, "unit": "GB/s", "how": "4 GiB read-only stream (ir_hbm_read, non-temporal 16 B loads)",
+                "copy": copy, "copy_how": "1 GiB device copy, read + write bytes"}
+    n = 8192
+    x = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    y = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    return {"value": rate(lambda: x @ y, 2 * n**3 / 1e12), "unit": "TFLOP/s", "how": "8192^3 bf16 matmul (torch BLAS)"}
 
 
 def _time_eager(call, args) -> float:
@@ -456,29 +538,13 @@ def _copy_calibration(mib: int) -> None:
     torch.cuda.synchronize()
 
 
-def _time_graph(call, args) -> float:
-    """ms per call: warm-up, then K calls captured in one hipGraph and replayed
-    between events on the launch stream."""
+def _time_graph(call, args, tag: str = "call") -> float:
+    """ms per call: W warm-up calls, then K calls captured in one hipGraph,
+    warmed and timed as in :func:`_graph_ms`."""
     for i in range(args.warmup):
         call(i)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        call(0)
-    torch.cuda.current_stream().wait_stream(stream)
-    with torch.cuda.graph(graph):
-        for i in range(args.steps):
-            call(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    graph.replay()
-    e.record()
-    torch.cuda.synchronize()
-    return s.elapsed_time(e) / args.steps
+    return _graph_ms(call, args.steps, tag)
 
 
 def main() -> int:
@@ -495,7 +561,7 @@ def main() -> int:
         return 2
     if args.workload != "decode":
         line = {"prefill": _bench_prefill, "mixed": _bench_mixed, "rope": _bench_rope}[args.workload](args)
-        line.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup})
+        line.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "timing": dict(_REPLAY_STATS)})
         print(json.dumps(line), flush=True)
         return 0
     from infrared_amd.workloads import make_decode_case
@@ -563,6 +629,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
     }
+    line["timing"] = dict(_REPLAY_STATS)
     if check is not None:
         line["max_abs_err_vs_fp32_oracle"] = check
     print(json.dumps(line), flush=True)

@@ -327,6 +327,19 @@ int ir_rope_kv_scatter(const void* q, int64_t q_tok_stride, int64_t q_head_strid
                        int num_kv_heads, int head_dim, int dtype, int32_t* err_flags,
                        ir_stream_t stream);
 
+/*
+ * Read-only HBM streaming roof (a measurement utility; no counterpart in the
+ * reference, which publishes no bandwidth figure): reads `bytes` of `src` with
+ * the decode kernels' load form (non-temporal 16-byte loads, 1 KiB contiguous
+ * per wavefront instruction) and discards them. Timing a call gives the read
+ * bandwidth the decode's achieved KV GB/s is held against.
+ * ir_hbm_read_granule: `bytes` must be a positive multiple of this.
+ * ir_hbm_read: `sink` is one uint32 the kernel may write (a value no caller
+ * should rely on); workgroups 0 = 8 per CU.
+ */
+int64_t ir_hbm_read_granule(void);
+int ir_hbm_read(const void* src, int64_t bytes, uint32_t* sink, int workgroups, ir_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -87,6 +87,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_f32,
          _c_i32, _c_p, _c_i64, _c_p, _c_p],
     ),
+    "ir_hbm_read_granule": (_c_i64, []),
+    "ir_hbm_read": (_c_i32, [_c_p, _c_i64, _c_p, _c_i32, _c_p]),
     "ir_paged_prefill_order_len": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32]),
     "ir_paged_prefill_order": (
         _c_i32,

@@ -667,19 +667,6 @@ void launch_planned_dt_d(const DecodeArgs& a, const uint8_t* plan, const PlanLay
                      plan, ly);
 }
 
-// CUs of the current device (the grid of both kernels), cached per device.
-int device_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;
-  }
-  return cache[dev];
-}
-
 int n_hg_of(int num_q_heads, int num_kv_heads) { return (num_q_heads / num_kv_heads + 15) / 16; }
 
 // Upper bound on the tile list for a table capacity.

@@ -148,6 +148,9 @@ void paged_prefill_kernel(PrefillArgs a) {
     return;
   }
   const int tq0 = tb * TQ;
+  // a chunk longer than the host's max_q_len has rows no workgroup covers
+  if (tb == a.n_qblocks - 1 && kvh == 0 && tid == 0 && q_len > a.n_qblocks * TQ)
+    flag_error(a.err, IR_ERR_CONTEXT_RANGE);
   if (tq0 >= q_len) return;
   int p0 = a.q_start[seq];
   const int cap = a.max_blocks * a.bs;
@@ -728,9 +731,25 @@ __global__ __launch_bounds__(kOrderThreads) void prefill_order_kernel(OrderArgs 
   }
 }
 
+// Tuning knobs, read once per process: IR_PREFILL_WAVES (4 or 8) forces the
+// workgroup shape, IR_PREFILL_PINGPONG=1 selects the ping-pong schedule.
+struct PrefillKnobs {
+  int waves = 0;  // 0: by grid size
+  bool pingpong = false;
+  PrefillKnobs() {
+    if (const char* e = getenv("IR_PREFILL_WAVES")) waves = atoi(e) == 4 ? 4 : 8;
+    if (const char* e = getenv("IR_PREFILL_PINGPONG")) pingpong = atoi(e) == 1;
+  }
+};
+
+const PrefillKnobs& prefill_knobs() {
+  static const PrefillKnobs k;
+  return k;
+}
+
 // Workgroup shape of a prefill call: 8 wavefronts (256 query columns) unless
 // that leaves CUs idle, then 4 (128 columns), twice the workgroups with half
-// the work each. IR_PREFILL_WAVES (4 or 8) forces one for tuning runs.
+// the work each.
 struct PrefillGeometry {
   int nw, tq, n_qblocks;
 };
@@ -738,9 +757,9 @@ struct PrefillGeometry {
 PrefillGeometry prefill_geometry(int max_q_len, int n_rep, int num_kv_heads, int num_seqs) {
   const int tq8 = PShape<128, 8>::COLS / n_rep;
   const int64_t wgs8 = (int64_t)((max_q_len + tq8 - 1) / tq8) * num_kv_heads * num_seqs;
-  const char* e = getenv("IR_PREFILL_WAVES");
+  const int forced = prefill_knobs().waves;
   // (4 wavefronts hold at most 128 query heads per KV head)
-  const bool four = n_rep <= PShape<128, 4>::COLS && (e ? atoi(e) == 4 : wgs8 < 256);
+  const bool four = n_rep <= PShape<128, 4>::COLS && (forced ? forced == 4 : wgs8 < device_cus());
   PrefillGeometry g;
   g.nw = four ? 4 : 8;
   g.tq = (four ? PShape<128, 4>::COLS : PShape<128, 8>::COLS) / n_rep;
@@ -763,8 +782,7 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   // the 8 x 512-token workload: ahead of lockstep while V went through a
   // register transpose (235 vs 257 us), behind it with row-major V and
   // transpose reads (242 vs 225 us), so lockstep is the default.
-  const char* e = getenv("IR_PREFILL_PINGPONG");
-  const bool pp = a.nw == 8 && a.max_blocks <= kBtCache && e && atoi(e) == 1;
+  const bool pp = a.nw == 8 && a.max_blocks <= kBtCache && prefill_knobs().pingpong;
   if (a.nw == 4) {
     const dim3 block(PShape<D, 4>::NT);
     if (fast)

@@ -18,6 +18,9 @@ int ok();
 // Maps the result of the preceding launches to IR_OK / IR_ELAUNCH.
 int check_launch(const char* what);
 
+// CUs of the current device, cached per device (256 if the runtime cannot say).
+int device_cus();
+
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 inline int dtype_bytes(int dtype) {

@@ -13,10 +13,13 @@ Same API as the reference module:
 
 PyTorch-ROCm's ``torch.cuda.CUDAGraph`` is a hipGraph; the HIP kernels are
 launched on torch's current stream, so they are captured as graph kernel
-nodes. They neither synchronise nor allocate, and the split-KV workspace is
-grown during warm-up (outside capture) so every replay sees the same memory.
-The kernel reads only ``context_lens[b]`` keys per row, so a replay costs the
-real context, not ``t_max``.
+nodes. They neither synchronise nor allocate. The pool's decode buffers
+(split-KV workspace, arrival counters, plan buffer) are grown during a
+bucket's warm-up, outside capture; a larger bucket captured later may grow
+them again, which replaces the pool's tensors, so every captured graph keeps
+references to the buffers it was captured with and its replays stay on that
+live memory. The kernel reads only ``context_lens[b]`` keys per row, so a
+replay costs the real context, not ``t_max``.
 """
 
 from __future__ import annotations
@@ -116,6 +119,8 @@ class _Captured:
     graph: torch.cuda.CUDAGraph
     buf: DecodeInputs
     out: torch.Tensor
+    # the pool buffers the graph's kernels address (kept alive for its replays)
+    pool_buffers: tuple
 
 
 class HipGraphDecoder:
@@ -209,4 +214,5 @@ class HipGraphDecoder:
             out = self._forward(buf)
         if self._mempool is None:
             self._mempool = graph.pool()
-        self._graphs[bucket] = _Captured(graph=graph, buf=buf, out=out)
+        held = tuple(getattr(self.pool, n, None) for n in ("_workspace", "_counters", "_plan_buf"))
+        self._graphs[bucket] = _Captured(graph=graph, buf=buf, out=out, pool_buffers=held)

@@ -551,6 +551,23 @@ def paged_prefill(
     return out
 
 
+def hbm_read(src: torch.Tensor, sink: torch.Tensor, workgroups: int = 0) -> None:
+    """Reads all of ``src`` (contiguous, a multiple of :func:`hbm_read_granule`
+    bytes) with the decode kernels' load form and discards it: timing it gives
+    the device's read-only HBM roof. ``sink``: an int32 tensor of >= 1 element."""
+    dev = require_device(src, sink)
+    nbytes = src.numel() * src.element_size()
+    if not src.is_contiguous() or nbytes % hbm_read_granule():
+        raise RuntimeError(f"hbm_read: src must be contiguous and a multiple of {hbm_read_granule()} bytes")
+    if sink.dtype != torch.int32 or sink.numel() < 1:
+        raise RuntimeError("hbm_read: sink must be an int32 tensor")
+    check(lib().ir_hbm_read(ptr(src), nbytes, ptr(sink), int(workgroups), stream_ptr(dev)), "ir_hbm_read")
+
+
+def hbm_read_granule() -> int:
+    return int(lib().ir_hbm_read_granule())
+
+
 __all__ = [
     "kv_scatter",
     "gather_slots",

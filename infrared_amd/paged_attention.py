@@ -137,15 +137,18 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
         max_blocks = block_tables.shape[1]
         if hasattr(pool, "plan_buffer") and kernels.decode_plan_pays(b, hq, h_kv, max_blocks, pool.block_size,
                                                                       q.device):
-            # balanced schedule: built by the step's first layer, reused by the rest
+            # balanced schedule: built by the step's first layer, reused by the
+            # rest -- unless another context's plan has since taken the pool's
+            # plan buffer (two decode contexts run interleaved), then rebuilt
             plan = paged.decode_plan
-            if plan is None:
+            if plan is None or getattr(pool, "plan_owner", plan) is not plan:
                 plan_bytes = kernels.decode_plan_bytes(b, hq, h_kv, max_blocks, pool.block_size)
                 plan = kernels.decode_plan(
                     block_tables, context_lens, hq, k_layer, pool.block_size,
                     buf=pool.plan_buffer(plan_bytes), err_flags=err,
                 )
                 paged.decode_plan = plan
+                pool.plan_owner = plan
             ws = pool.workspace(kernels.planned_workspace_bytes(b, hq, h_kv, d))
             ctr = pool.decode_counters(kernels.decode_num_counters(b, hq, h_kv))
             out = kernels.paged_decode_planned(

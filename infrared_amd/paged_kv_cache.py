@@ -102,6 +102,9 @@ class PagedKVPool:
         self._workspace: torch.Tensor | None = None
         self._counters: torch.Tensor | None = None
         self._plan_buf: torch.Tensor | None = None
+        # the decode plan whose schedule plan_buffer() holds now: a context
+        # whose cached plan is not this one was overwritten and rebuilds it
+        self.plan_owner: object | None = None
 
     # --- reference surface ------------------------------------------------
 
@@ -149,8 +152,9 @@ class PagedKVPool:
         """A cached device buffer of at least ``nbytes`` for the decode kernels'
         fp32 partial rows (scratch, any shape).
 
-        Grow it outside hipGraph capture (the graph decoder's warm-up does) so a
-        captured graph keeps pointing at live memory.
+        Grow it outside hipGraph capture (the graph decoder's warm-up does).
+        Growing replaces the tensor: a graph captured on the old one must hold a
+        reference to it (the graph decoder does) to keep its memory alive.
         """
         if self._workspace is None or self._workspace.numel() < nbytes:
             self._workspace = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)

@@ -62,3 +62,51 @@ def test_mixed_step_eager_matches_oracle_and_graph_replays(overlap, config, plan
         # eager work between replays
         torch.cuda.synchronize()
     assert step.err.item() == 0
+
+
+def test_mixed_step_full_shape():
+    """The benchmark's mixed step at its own shape: 28 layers, 224 decode rows
+    (context U{256..4096}), 4 x 256-token chunks. Every layer's scatter equals
+    torch's index_put on a copy of the pool taken before the step (the whole
+    layer, bit for bit); decode rows and chunks match the oracle on three
+    layers (a row subset of the decode); the captured step replays bit for bit."""
+    cfg, pool, batch, inputs = make_mixed_case("qwen7b-mixed", DEV)
+    assert (cfg.num_layers, cfg.num_decode, cfg.num_prefill, cfg.chunk) == (28, 224, 4, 256)
+    layers = (0, 13, 27)
+    rows = list(range(0, cfg.num_decode, 14))  # 16 decode rows
+    before_k = pool.k.clone()
+    before_v = pool.v.clone()
+    step = MixedStep(pool, batch, inputs, cfg.scale)
+    assert step.planned
+    step.eager()
+    torch.cuda.synchronize()
+    assert step.err.item() == 0
+    slots = batch.write_slots
+    for layer in range(cfg.num_layers):
+        before_k[layer].index_put_((slots,), inputs.k_new[layer])
+        before_v[layer].index_put_((slots,), inputs.v_new[layer])
+        assert torch.equal(pool.k[layer], before_k[layer]), f"layer {layer}: K scatter differs from index_put"
+        assert torch.equal(pool.v[layer], before_v[layer]), f"layer {layer}: V scatter differs from index_put"
+    del before_k, before_v
+    torch.cuda.empty_cache()
+    for layer in layers:
+        kc, vc = pool.k[layer].cpu(), pool.v[layer].cpu()
+        dec = O.decode_reference(inputs.q_dec[layer].cpu(), kc, vc, batch.dec_tables.cpu(), batch.dec_ctx.cpu(),
+                                 cfg.block_size, cfg.scale, seqs=rows)
+        err = (step.out_dec[layer].float().cpu()[rows] - dec[rows]).abs().max().item()
+        assert err <= 2e-2, f"layer {layer}: decode max-abs error {err}"
+        pre = O.prefill_reference(inputs.q_pre[layer].cpu(), kc, vc, batch.pre_tables.cpu(), batch.cu_seqlens_q.cpu(),
+                                  batch.q_start.cpu(), cfg.block_size, cfg.scale)
+        err = (step.out_pre[layer].float().cpu() - pre).abs().max().item()
+        assert err <= 2e-2, f"layer {layer}: prefill max-abs error {err}"
+    eager_dec, eager_pre = step.out_dec.clone(), step.out_pre.clone()
+    step.capture()
+    for _ in range(2):
+        step.out_dec.zero_()
+        step.out_pre.zero_()
+        step.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(step.out_dec, eager_dec) and torch.equal(step.out_pre, eager_pre)
+    assert step.err.item() == 0
+    del step, pool, inputs
+    torch.cuda.empty_cache()

@@ -247,31 +247,72 @@ def test_prefill_order_length_is_checked():
                               case.q_start, cfg.chunk, cfg.block_size, cfg.scale, order=wrong)
 
 
-@pytest.mark.parametrize("name,prefixes,q_lens", [
-    ("qwen7b-prefill", None, None),
-    ("qwen7b-prefill", [0, 37, 512, 1000, 3, 3, 0, 5], [1, 31, 100, 512, 0, 9, 64, 33]),
+_PP_CASES = {
+    "c4": ("qwen7b-prefill", None, None),
+    "ragged": ("qwen7b-prefill", [0, 37, 512, 1000, 3, 3, 0, 5], [1, 31, 100, 512, 0, 9, 64, 33]),
     # fp16, head_dim 64, a 12-token block (general addressing path), 8-wavefront workgroups
-    (PrefillConfig("pf-pp-f16", 8, 0, 32, 8, 64, 12, torch.float16, 0, seed=31),
-     [0, 100, 7, 300, 12, 0, 50, 1], [300, 256, 290, 200, 310, 280, 260, 299]),
-])
-def test_prefill_ping_pong_schedule_matches_lockstep_bit_for_bit(name, prefixes, q_lens, monkeypatch):
+    "f16-bs12": (PrefillConfig("pf-pp-f16", 8, 0, 32, 8, 64, 12, torch.float16, 0, seed=31),
+                 [0, 100, 7, 300, 12, 0, 50, 1], [300, 256, 290, 200, 310, 280, 260, 299]),
+}
+
+_PP_CHILD = r"""
+import sys, torch
+sys.path.insert(0, {root!r})
+sys.path.insert(0, {tests!r})
+from test_gpu_prefill import _PP_CASES, _run
+from infrared_amd.workloads import make_prefill_case
+name, prefixes, q_lens = _PP_CASES[{key!r}]
+out = _run(make_prefill_case(name, "cuda", prefixes=prefixes, q_lens=q_lens))
+torch.cuda.synchronize()
+torch.save(out.cpu(), {path!r})
+print("PINGPONG OK")
+"""
+
+
+@pytest.mark.parametrize("key", list(_PP_CASES))
+def test_prefill_ping_pong_schedule_matches_lockstep_bit_for_bit(key, tmp_path):
     """The 8-wavefront kernel's ping-pong schedule (waves 4..7 half an
     iteration behind 0..3) does the same arithmetic in the same order as the
-    lockstep schedule (IR_PREFILL_PINGPONG=0): identical outputs, and both
-    within the bar of the oracle."""
+    lockstep schedule: identical outputs, and both within the bar of the
+    oracle. The schedule knob is read once per process, so the ping-pong run
+    is a child process (IR_PREFILL_PINGPONG=1) on the same seeded case."""
+    import os
+    import subprocess
+    import sys
+
+    name, prefixes, q_lens = _PP_CASES[key]
+    tests = os.path.dirname(os.path.abspath(__file__))
+    path = str(tmp_path / "pp.pt")
+    res = subprocess.run(
+        [sys.executable, "-c", _PP_CHILD.format(root=os.path.dirname(tests), tests=tests, key=key, path=path)],
+        env={**os.environ, "IR_PREFILL_PINGPONG": "1"}, capture_output=True, text=True, timeout=110,
+    )
+    assert res.returncode == 0 and "PINGPONG OK" in res.stdout, res.stdout + res.stderr[-2000:]
     case = make_prefill_case(name, DEV, prefixes=prefixes, q_lens=q_lens)
-    outs = []
-    for flag in ("1", "0"):
-        monkeypatch.setenv("IR_PREFILL_PINGPONG", flag)
-        outs.append(_run(case))
-    torch.cuda.synchronize()
-    assert torch.equal(outs[0], outs[1])
+    lockstep = _run(case).cpu()
+    pingpong = torch.load(path, weights_only=True)
+    assert torch.equal(pingpong, lockstep)
     cfg = case.config
     ref = O.prefill_reference(
         case.q.cpu(), case.k_cache.cpu(), case.v_cache.cpu(), case.block_tables[0].cpu(),
         case.cu_seqlens_q.cpu(), case.q_start.cpu(), cfg.block_size, cfg.scale,
     )
-    assert (outs[0].float().cpu() - ref).abs().max().item() <= TOL
+    assert (lockstep.float() - ref).abs().max().item() <= TOL
+
+
+def test_prefill_flags_understated_max_q_len():
+    """A chunk longer than the host's max_q_len bound has rows no workgroup
+    covers: the call flags IR_ERR_CONTEXT_RANGE instead of leaving them silently
+    unwritten; with the true bound the same call is clean."""
+    case = make_prefill_case("qwen7b-prefill", DEV, prefixes=[0, 64, 0, 0, 0, 0, 0, 0],
+                             q_lens=[300, 40, 8, 8, 8, 8, 8, 8])
+    cfg = case.config
+    for max_q, flagged in ((100, True), (300, False)):
+        err = torch.zeros(1, dtype=torch.int32, device=DEV)
+        kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[0], case.cu_seqlens_q,
+                              case.q_start, max_q, cfg.block_size, cfg.scale, err_flags=err)
+        torch.cuda.synchronize()
+        assert bool(err.item() & ERR_CONTEXT_RANGE) == flagged, (max_q, err.item())
 
 
 def test_prefill_order_and_kernel_replay_in_a_hip_graph():

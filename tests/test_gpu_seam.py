@@ -218,3 +218,55 @@ def test_hip_graph_decode_replay_matches_eager():
         torch.cuda.synchronize()
         assert torch.equal(got, outs[0]), f"replay {it} differs from eager at bucket {bucket}"
         assert (got.float() - outs[1].float()).abs().max().item() <= 2e-2, f"replay {it}: padded vs tight"
+
+
+def test_hip_graph_smaller_bucket_after_buffer_growth():
+    """A bucket captured first keeps replaying correctly after a larger bucket's
+    warm-up has grown (replaced) the pool's workspace, counters and plan
+    buffer: the first graph still addresses the buffers it was captured with.
+    The freed sizes are then handed out again, filled with ones (a counter
+    read from them would skip merges), before the small bucket replays."""
+    bs, h_kv, n_rep, d, layers, t_max = 16, 4, 7, 128, 2, 4096
+    dtype = torch.bfloat16
+    nblk = t_max // bs
+    pool = PagedKVPool(layers, 64 * nblk, bs, h_kv, d, dtype, device=DEV)
+    pool.k.normal_()
+    pool.v.normal_()
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    qkv = torch.randn(layers, 64, 1, h_kv * (n_rep + 2), d, generator=gen, device=DEV).to(dtype)
+
+    def step(buf, paged):
+        outs = []
+        ids = buf.ids[:, 0]
+        for layer in range(layers):
+            x = qkv[layer].index_select(0, ids)
+            q = x[:, :, : h_kv * n_rep].contiguous()
+            k = x[:, :, h_kv * n_rep : h_kv * (n_rep + 1)].contiguous()
+            v = x[:, :, h_kv * (n_rep + 1) :].contiguous()
+            outs.append(paged_attention(q, k, v, paged, buf.mask, layer, d**-0.5, n_rep))
+        return torch.stack(outs, dim=1)
+
+    dec = HipGraphDecoder(None, pool, max_num_seqs=64, t_max=t_max, block_size=bs, step_fn=step)
+    tables = [list(range(i * nblk, (i + 1) * nblk)) for i in range(64)]
+    rng = torch.Generator().manual_seed(11)
+
+    def eager(b, num_cached):
+        bucket = pick_bucket(b, dec.buckets)
+        inp = build_decode_static_inputs(tables[:b], num_cached, list(range(b)), bucket, t_max, bs, DEV, dtype)
+        paged = PagedContext(pool, inp.write_slots, inp.gather_slots, True, inp.block_tables, inp.context_lens)
+        return step(inp, paged)[:b]
+
+    small = [int(x) for x in torch.randint(1000, 4000, (4,), generator=rng)]
+    dec.decode(tables[:4], small, list(range(4)))
+    sizes = [t.numel() for t in (pool._workspace, pool._counters, pool._plan_buf)]
+    large = [int(x) for x in torch.randint(1000, 4000, (64,), generator=rng)]
+    dec.decode(tables[:64], large, list(range(64)))
+    assert [t.numel() for t in (pool._workspace, pool._counters, pool._plan_buf)] != sizes, "no buffer grew"
+    filler = [torch.ones(n // 4 + 1, dtype=torch.int32, device=DEV) for n in sizes for _ in range(4)]
+    for it in range(3):
+        small = [c + 1 for c in small]
+        got = dec.decode(tables[:4], small, list(range(4))).clone()
+        ref = eager(4, small)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"bucket-4 replay {it} after growth differs from eager"
+    assert all(int(f.min()) == 1 and int(f.max()) == 1 for f in filler), "a replay wrote into freed memory"
