@@ -169,6 +169,28 @@ int ir_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
                     ir_stream_t stream);
 
 /*
+ * ir_paged_decode without a caller workspace, for callers that cannot
+ * allocate device memory (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference: it is
+ * ir_paged_decode with the same arguments, minus counters and workspace, whose
+ * split-KV arrival counters and fp32 partial rows live in a 16 MiB device array
+ * inside the library (64 KiB of counters, the rest partial rows), held by
+ * every GPU the library runs on until the process ends. A call whose
+ * ir_paged_decode_workspace_size exceeds 16 MiB - 64 KiB, or that needs more
+ * than 16,384 counters, returns IR_EWORKSPACE. All calls on one GPU share that
+ * array: calls that overlap on one GPU (other streams, concurrent graph
+ * replays) race; calls ordered on one stream do not. Allocates nothing.
+ */
+int ir_paged_decode_noalloc(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
+                            const void* k_cache, const void* v_cache, int64_t cache_slot_stride,
+                            int64_t cache_head_stride, int64_t num_blocks, int block_size,
+                            const int32_t* block_tables, int64_t bt_stride, int max_blocks_per_seq,
+                            const int32_t* context_lens, void* out, int64_t out_seq_stride,
+                            int64_t out_head_stride, int num_seqs, int num_q_heads, int num_kv_heads,
+                            int head_dim, float scale, int dtype, int partition_tokens,
+                            int32_t* err_flags, ir_stream_t stream);
+
+/*
  * Planned decode: the same attention as ir_paged_decode (one query token per
  * sequence over block_tables / context_lens), on a work-balanced schedule that
  * ir_paged_decode_plan builds once per batch of decode metadata and every

@@ -57,6 +57,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_f32, _c_i32, _c_i32,
          _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p],
     ),
+    "ir_paged_decode_noalloc": (
+        _c_i32,
+        [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i64, _c_i32,
+         _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_f32, _c_i32, _c_i32,
+         _c_p, _c_p],
+    ),
     "ir_paged_decode_plan_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "ir_paged_decode_planned_workspace_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32]),
     "ir_paged_decode_plan": (

@@ -1,0 +1,79 @@
+"""ir_paged_decode_noalloc (through the C ABI) against ir_paged_decode on the
+same inputs: the same kernels on the library's own scratch array instead of a
+caller workspace, so the outputs must be identical bit for bit -- on two calls
+in a row, the second with a smaller input (fewer sequences, shorter
+contexts), then the first shape again (the counters the calls share must be
+back at zero). A shape whose partial rows exceed the array is refused before
+any device work."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from infrared_amd import kernels
+from infrared_amd._lib import check, dtype_code, lib, ptr, stream_ptr
+from infrared_amd.workloads import DecodeConfig, make_decode_case
+from oracle import naive as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+IR_EWORKSPACE = -3
+
+LONG = DecodeConfig("na-long", 8, 28, 4, 128, 16, torch.bfloat16, "uniform", 3000, 20000, seed=41)
+SHORT = DecodeConfig("na-short", 3, 28, 4, 128, 16, torch.bfloat16, "uniform", 100, 3000, seed=42)
+
+
+def _noalloc(case, out, err, partition=0):
+    cfg = case.config
+    q, kc, vc, bt = case.q, case.k_cache, case.v_cache, case.block_tables[0]
+    return lib().ir_paged_decode_noalloc(
+        ptr(q), q.stride(0), q.stride(1), ptr(kc), ptr(vc), kc.stride(0), kc.stride(1),
+        kc.shape[0] // cfg.block_size, cfg.block_size, ptr(bt), bt.stride(0), bt.shape[1], ptr(case.context_lens),
+        ptr(out), out.stride(0), out.stride(1), cfg.num_seqs, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim,
+        float(cfg.scale), dtype_code(q.dtype), partition, ptr(err), stream_ptr(q.device),
+    )
+
+
+def _both(case):
+    cfg = case.config
+    bt = case.block_tables[0]
+    part = kernels.default_partition(cfg.num_seqs, cfg.num_kv_heads, bt.shape[1], cfg.block_size)
+    assert kernels.decode_workspace_bytes(cfg.num_seqs, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim,
+                                          bt.shape[1], cfg.block_size, part) > 0, "shape must split"
+    ref = kernels.paged_decode(case.q, case.k_cache, case.v_cache, bt, case.context_lens, cfg.block_size, cfg.scale,
+                               partition_tokens=part)
+    out = torch.full_like(case.q, 7.0)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    check(_noalloc(case, out, err), "ir_paged_decode_noalloc")
+    torch.cuda.synchronize()
+    assert err.item() == 0
+    return ref, out
+
+
+def test_noalloc_decode_matches_the_workspace_decode():
+    long_case = make_decode_case(LONG, DEV)
+    short_case = make_decode_case(SHORT, DEV)
+    outs = []
+    for case in (long_case, short_case, long_case):
+        ref, out = _both(case)
+        assert torch.equal(out, ref), f"{case.config.name}: no-alloc decode differs from ir_paged_decode"
+        outs.append(out)
+    out = outs[1]
+    cfg = SHORT
+    expect = O.decode_reference(short_case.q.cpu(), short_case.k_cache.cpu(), short_case.v_cache.cpu(),
+                                short_case.block_tables[0].cpu(), short_case.context_lens.cpu(), cfg.block_size,
+                                cfg.scale)
+    assert (out.float().cpu() - expect).abs().max().item() <= 2e-2
+
+
+def test_noalloc_decode_refuses_shapes_beyond_its_scratch():
+    """1024 sequences of 32k keys split into 1024-token partitions need far more
+    than the 16 MiB array: refused with IR_EWORKSPACE and a message naming the
+    limit (sizes are checked before any pointer is used)."""
+    rc = lib().ir_paged_decode_noalloc(
+        None, 0, 0, None, None, 0, 0, 0, 16, None, 2048, 2048, None, None, 0, 0, 1024, 28, 4, 128,
+        0.088, 2, 1024, None, None,
+    )
+    assert rc == IR_EWORKSPACE
+    assert "no-alloc scratch holds" in lib().ir_last_error().decode()
