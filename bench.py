@@ -69,9 +69,9 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--schedule", choices=("auto", "planned", "fixed"), default="auto",
                    help="decode: the seam's choice (default: kernels.decode_plan_pays), "
                    "balanced plan + run, or fixed split-KV partitions; prefill: the seam's choice "
-                   "(kernels.prefill_order_pays), the heaviest-first work order, or the default order")
+                   "(kernels.prefill_plan_pays), the work plan, or none")
     p.add_argument("--layers", type=int, default=28,
-                   help="calls per decode plan / prefill order (layers of one step sharing its metadata)")
+                   help="calls per decode / prefill plan (layers of one step sharing its metadata)")
     p.add_argument("--cpu-iters", type=int, default=5, help="timed CPU-baseline iterations (0 = skip)")
     p.add_argument("--cpu-seqs", type=int, default=0, help="sequences in the CPU sample (0 = all)")
     p.add_argument("--check", action="store_true", help="also check the output against the oracle")
@@ -299,21 +299,23 @@ def _bench_prefill(args) -> dict:
     cfg = case.config
     out = torch.empty_like(case.q)
     total_q, max_blocks = case.q.shape[0], case.block_tables[0].shape[1]
-    # heaviest-first work order (the seam's choice unless --schedule forces it),
-    # rebuilt every --layers calls as an engine step would
-    ordered = args.schedule == "planned" or (args.schedule == "auto" and kernels.prefill_order_pays(
+    # the work plan (the seam's choice unless --schedule forces it), rebuilt
+    # every --layers calls as an engine step would
+    planned = args.schedule == "planned" or (args.schedule == "auto" and kernels.prefill_plan_pays(
         cfg.num_seqs, cfg.chunk, cfg.num_q_heads, cfg.num_kv_heads))
-    order_buf = torch.empty(max(1, kernels.prefill_order_len(cfg.num_seqs, cfg.chunk, cfg.num_q_heads,
-                                                             cfg.num_kv_heads)), dtype=torch.int32, device="cuda")
-    order = [None]
+    plan_buf = torch.empty(max(256, kernels.prefill_plan_bytes(cfg.num_seqs, cfg.chunk, cfg.num_q_heads,
+                                                               cfg.num_kv_heads, cfg.head_dim)),
+                           dtype=torch.uint8, device="cuda")
+    plan = [None]
 
     def call(i: int) -> None:
-        if ordered and i % args.layers == 0:
-            order[0] = kernels.prefill_order(case.cu_seqlens_q, case.q_start, total_q, cfg.chunk, max_blocks,
-                                             cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, buf=order_buf)
+        if planned and i % args.layers == 0:
+            plan[0] = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, total_q, cfg.chunk, max_blocks,
+                                           cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim,
+                                           buf=plan_buf)
         kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[i % len(case.block_tables)],
                               case.cu_seqlens_q, case.q_start, cfg.chunk, cfg.block_size, cfg.scale, out=out,
-                              order=order[0])
+                              plan=plan[0])
 
     ms = _time_graph(call, args) if args.mode == "graph" else _time_eager(call, args)
     if args.copy_calib_mib > 0:
@@ -349,8 +351,8 @@ def _bench_prefill(args) -> dict:
         "config": {"workload": f"{cfg.name}: {cfg.num_seqs} chunks of {cfg.chunk} after prefixes {case.prefixes}, "
                    f"{cfg.num_q_heads}q/{cfg.num_kv_heads}kv heads, head_dim {cfg.head_dim}, block {cfg.block_size}",
                    "flops_per_call": case.flops, "kv_bytes_per_call": case.kv_bytes, "rotations": args.rotations,
-                   "schedule": "heaviest-first order" if ordered else "default order",
-                   "layers_per_order": args.layers if ordered else None},
+                   "schedule": "work plan (heaviest first, heavy items cut)" if planned else "unplanned",
+                   "layers_per_plan": args.layers if planned else None},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "measured_peak": _measured_peak("mfma"),
                      "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": _traffic("prefill_qwen7b-prefill")[0],

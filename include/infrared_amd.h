@@ -284,11 +284,17 @@ int ir_paged_attention_masked(const void* q, int64_t q_b_stride, int64_t q_s_str
  *   q, out:       [total_q, num_q_heads, head_dim] (strides token, head in elements).
  *   cu_seqlens_q: [num_seqs + 1] int32, non-decreasing, cu_seqlens_q[num_seqs] <= total_q.
  *   q_start:      [num_seqs] int32, tokens already cached (the first query's position).
- *   max_q_len:    upper bound of the per-sequence query counts (sizes the grid).
- *   order:        null, or the work order ir_paged_prefill_order wrote for this call's
- *                 cu_seqlens_q / q_start and shapes (order_len int32 items): workgroups
- *                 then run the heaviest (sequence, query block) items first. It changes
- *                 the schedule only, never a result bit.
+ *   max_q_len:    upper bound of the per-sequence query counts (sizes the grid; a chunk
+ *                 longer than it sets IR_ERR_CONTEXT_RANGE and its rows past the bound
+ *                 are not written).
+ *   plan:         null, or the plan ir_paged_prefill_plan wrote for this call's
+ *                 cu_seqlens_q / q_start and shapes (plan_bytes as sized by
+ *                 ir_paged_prefill_plan_bytes): workgroups then run the heaviest work
+ *                 first, and items heavier than the mean load of a workgroup slot are cut
+ *                 into key-range pieces merged in the same launch. The plan also holds
+ *                 the pieces' arrival counters and partial rows, so calls on one plan
+ *                 must be stream-ordered. Results agree with the unplanned call within
+ *                 fp32 rounding of the merge (identical when nothing is cut).
  * Keys q_start[b] + q_len_b beyond the table (max_blocks_per_seq * block_size) set
  * IR_ERR_CONTEXT_RANGE and are clamped; a bad block id sets IR_ERR_BLOCK_RANGE and
  * that block's keys read as zeros. head_dim in {64, 128}; dtype bf16 or f16 (fp32 returns
@@ -301,27 +307,29 @@ int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
                      const int32_t* cu_seqlens_q, const int32_t* q_start, int num_seqs,
                      int total_q, int max_q_len, void* out, int64_t out_tok_stride,
                      int64_t out_head_stride, int num_q_heads, int num_kv_heads, int head_dim,
-                     float scale, int dtype, const int32_t* order, int64_t order_len,
+                     float scale, int dtype, void* plan, int64_t plan_bytes,
                      int32_t* err_flags, ir_stream_t stream);
 
 /*
- * Heaviest-first work order for ir_paged_prefill, built on the device from the
- * call's metadata (no host synchronisation, so it can be captured). Like the
- * decode plan it has no counterpart in the reference, which builds a step's
- * prefill metadata once (infrared/engine/paged_engine.py:194-207, :461-516) and
- * shares it across layers; so is this order: build it once per step, pass it to
- * every layer's ir_paged_prefill.
- * ir_paged_prefill_order_len: int32 items of the order for these shapes (0 when
- *   there is nothing to order).
- * ir_paged_prefill_order: writes the order (one workgroup; a counting sort of the
- *   (sequence, query block) items by the key tiles they walk). Arguments as for
- *   ir_paged_prefill; order_len must equal ir_paged_prefill_order_len(...).
+ * Work plan for ir_paged_prefill, built on the device from the call's metadata
+ * (no host synchronisation, so it can be captured). Like the decode plan it
+ * has no counterpart in the reference, which builds a step's prefill metadata
+ * once (infrared/engine/paged_engine.py:194-207, :461-516) and shares it across
+ * layers; so is this plan: build it once per step, pass it to every layer's
+ * ir_paged_prefill.
+ * ir_paged_prefill_plan_bytes: bytes of plan for these shapes (0 when there is
+ *   nothing to plan).
+ * ir_paged_prefill_plan: writes the plan (one workgroup: weighs every (sequence,
+ *   query block) item by the key tiles it walks, cuts the heaviest, sorts the
+ *   pieces heaviest first, clears the arrival counters). Arguments as for
+ *   ir_paged_prefill.
  */
-int64_t ir_paged_prefill_order_len(int num_seqs, int max_q_len, int num_q_heads, int num_kv_heads);
-int ir_paged_prefill_order(const int32_t* cu_seqlens_q, const int32_t* q_start, int num_seqs,
-                           int total_q, int max_q_len, int max_blocks_per_seq, int block_size,
-                           int num_q_heads, int num_kv_heads, int32_t* order, int64_t order_len,
-                           ir_stream_t stream);
+int64_t ir_paged_prefill_plan_bytes(int num_seqs, int max_q_len, int num_q_heads, int num_kv_heads,
+                                    int head_dim);
+int ir_paged_prefill_plan(const int32_t* cu_seqlens_q, const int32_t* q_start, int num_seqs,
+                          int total_q, int max_q_len, int max_blocks_per_seq, int block_size,
+                          int num_q_heads, int num_kv_heads, int head_dim, void* plan,
+                          int64_t plan_bytes, ir_stream_t stream);
 
 /*
  * Fused rotary embedding + KV-slot scatter. Replaces, per layer,

@@ -95,10 +95,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "ir_hbm_read_granule": (_c_i64, []),
     "ir_hbm_read": (_c_i32, [_c_p, _c_i64, _c_p, _c_i32, _c_p]),
-    "ir_paged_prefill_order_len": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32]),
-    "ir_paged_prefill_order": (
+    "ir_paged_prefill_plan_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
+    "ir_paged_prefill_plan": (
         _c_i32,
-        [_c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p],
+        [_c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p],
     ),
 }
 

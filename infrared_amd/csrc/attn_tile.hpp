@@ -342,6 +342,83 @@ __device__ __forceinline__ void merge_column(const MergeSmem<NW, D>& sm, int hc,
   }
 }
 
+// ---------------------------------------------------------------- device-scope partial rows
+//
+// Device-scope accesses for split-KV partials: written through to the device
+// coherence point and read back from it, so one workgroup can merge what
+// workgroups on other XCDs wrote without a cache-wide fence. They are buffer
+// loads/stores with the sc1 cache policy (the bits an agent-scope relaxed
+// atomic load/store carries), 8 or 16 bytes wide, through a resource over
+// `base` at byte offsets below 2 GiB: a partial row moves in a quarter of the
+// requests 4-byte atomics would take, and under a saturated memory system each
+// request is a long round trip (16-byte accesses took the planned decode's end
+// phase from 5.9 to ~4 us).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* base) {
+  // dword3 0x00020000: DATA_FORMAT 32, the raw-buffer setting of this family
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, 0x7fffffff, 0x00020000);
+}
+constexpr int kCacheSc1 = 16;  // cache-policy operand of the buffer builtins: sc1
+__device__ __forceinline__ void store_dev4(__amdgpu_buffer_rsrc_t r, int off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kCacheSc1);
+}
+__device__ __forceinline__ void store_dev2(__amdgpu_buffer_rsrc_t r, int off, f32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, kCacheSc1);
+}
+__device__ __forceinline__ f32x4 load_dev4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCacheSc1);
+}
+__device__ __forceinline__ f32x2 load_dev2(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCacheSc1);
+}
+
+// Log-sum-exp merge of n partial rows read at device scope, up to NB rows'
+// loads in flight at a time (only rows that exist are read): row p is row0 +
+// p * step, its D fp32 accumulators at byte (row * D) * 4 of r_o and its
+// (max, sum) pair at byte row * 8 of r_ml. Gives the unnormalised
+// o[d0..d0+W) (W = 4 or 8) and the sum L. The arithmetic order depends on n
+// alone, so merges of the same rows are bit-identical whoever runs them. Rows
+// with no key (max -inf) add nothing: an exponent of -inf - -inf is NaN, which
+// fmaxf turns into -1e30 (weight 0) without a branch (branches here measured
+// 0.5 us per call slower).
+template <int D, int W = 4, int NB = 4>
+__device__ __forceinline__ void lse_merge_dev(__amdgpu_buffer_rsrc_t r_o, __amdgpu_buffer_rsrc_t r_ml, int row0,
+                                              int step, int n, int d0, float (&o)[W], float& L) {
+  static_assert(W == 4 || W == 8, "4 or 8 columns");
+  float M = kNegInf;
+  L = 0.f;
+#pragma unroll
+  for (int e = 0; e < W; ++e) o[e] = 0.f;
+#pragma unroll 1
+  for (int p0 = 0; p0 < n; p0 += NB) {
+    f32x2 ml[NB];
+    float po[NB][W];
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      if (q > 0 && p0 + q >= n) continue;  // the batch's first row always exists
+      const int row = row0 + (p0 + q) * step;
+      ml[q] = load_dev2(r_ml, row * 8);
+#pragma unroll
+      for (int h = 0; h < W; h += 4) {
+        const f32x4 v = load_dev4(r_o, (row * D + d0 + h) * 4);
+        po[q][h] = v[0];
+        po[q][h + 1] = v[1];
+        po[q][h + 2] = v[2];
+        po[q][h + 3] = v[3];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      if (p0 + q >= n) continue;
+      const float Mn = fmaxf(M, ml[q][0]);
+      const float wa = fast_exp2(fmaxf(M - Mn, -1e30f)), wb = fast_exp2(fmaxf(ml[q][0] - Mn, -1e30f));
+      L = wa * L + wb * ml[q][1];
+#pragma unroll
+      for (int e = 0; e < W; ++e) o[e] = wa * o[e] + wb * po[q][e];
+      M = Mn;
+    }
+  }
+}
+
 template <int DT>
 __device__ __forceinline__ void store4(uint8_t* dst, const float (&o)[4], float scale) {
   if constexpr (DT == IR_DTYPE_F32) {

@@ -11,27 +11,35 @@
 // infrared/engine/paged_engine.py:461-516 (a decode row is a sequence with one
 // query token at position context - 1).
 //
-// Work decomposition: one workgroup of NW wavefronts per (query block, KV
-// head, sequence), dispatched heaviest first: in the order
-// ir_paged_prefill_order builds once per step (all sequences' items by key
-// tiles), or else a sequence's last query blocks first. NW
-// is 8 (two per SIMD) unless that gives fewer workgroups than CUs; then 4 (one
-// per SIMD, up to 512 registers), twice the workgroups with half the columns
-// each, which shortens a small batch's critical path (4 x 256-token chunks:
-// 19.0 -> 16.6 us; a large one runs twice as long with 4). A query block is
-// TQ = 32 NW / n_rep tokens, so the block's (token, query head) pairs of the
-// GQA group -- column j = token-in-block * n_rep + head -- fill 32 NW columns
-// almost exactly (8 wavefronts, 7 heads: 36 tokens, 252 columns); wavefront w
-// owns columns 32w .. 32w+31 (two 16-column tiles). Every column
-// of a workgroup reads the same KV head, so each K/V element staged in LDS
-// feeds 32 columns per wavefront read. The workgroup walks the keys in
-// 64-key tiles staged in a 3-deep LDS ring: a later tile's global loads are
-// in flight (in registers) while the current one is in the math, and are
-// written to its LDS buffer a tile later. The workgroup runs in lockstep,
-// one barrier per tile; 8-wavefront workgroups can instead run a ping-pong
-// schedule (waves 4..7 half an iteration behind 0..3, so each SIMD overlaps
-// one wave's MFMAs with the other's softmax), selected by
-// IR_PREFILL_PINGPONG=1.
+// Work decomposition: an item is a (sequence, query block); each runs as one
+// workgroup of NW wavefronts per KV head. A query block is TQ = 32 NW / n_rep
+// tokens, so the block's (token, query head) pairs of the GQA group -- column
+// j = token-in-block * n_rep + head -- fill 32 NW columns almost exactly (4
+// wavefronts, 7 heads: 18 tokens, 126 columns); wavefront w owns columns
+// 32w .. 32w+31 (two 16-column tiles). Every column of a workgroup reads the
+// same KV head, so each K/V element staged in LDS feeds 32 columns per
+// wavefront read. The workgroup walks the keys in 64-key tiles staged in an
+// LDS ring, one barrier per tile.
+//
+// Shapes (host choice): 4-wavefront workgroups on a 2-deep ring, one tile at
+// a time (~78 KB of LDS, <= 256 registers): two share a CU, and their waves,
+// bound by no common barrier, fill each other's MFMA and VALU gaps -- the
+// default for batches that fill the CUs twice over. Smaller batches take
+// 4-wavefront workgroups on a 3-deep ring whose next tile's scores run beside
+// the current tile's exponentials (one per CU, up to 512 registers: the
+// shortest critical path when the CUs are not full). 8-wavefront lockstep
+// workgroups (256 columns) are kept for comparison (IR_PREFILL_WAVES=8).
+//
+// Plan (ir_paged_prefill_plan, built on the device once per step, shared by
+// every layer): the items in heaviest-first order -- the dispatcher places
+// workgroups in index order, so that is the longest-processing-time rule --
+// with the key range of any item heavier than the mean load of a workgroup
+// slot cut into pieces, each its own workgroup. A piece attends its share of
+// the item's key tiles and writes fp32 partial rows (max, sum, unnormalised
+// output) into the plan; the last piece of the item to arrive (an arrival
+// counter in the plan) merges them with log-sum-exp weights in part order and
+// writes the output. Without a plan, a sequence's last query blocks go first
+// and nothing is cut.
 //   K and V tiles: row-major [64 keys][D] (+32 bytes a row against bank
 //   conflicts), loaded and stored alike (a thread's K and V pieces share the
 //   key's slot); the PV product reads V^T with gfx950's transpose read.
@@ -48,6 +56,7 @@
 // in infrared/model/triton_attention.py:135-177; probabilities are rounded to
 // the input dtype before the PV product, as softmax(...).to(q.dtype) does.
 #include <stdlib.h>
+#include <string.h>
 
 #include <type_traits>
 
@@ -86,7 +95,13 @@ struct PrefillArgs {
   int nw;                                    // wavefronts per workgroup (4 or 8)
   float scale_log2;
   int32_t* err;
-  const int32_t* order;  // [num_seqs * n_qblocks] items (seq * n_qblocks + block), or null
+  // plan (or nulls): items[k] = (item, piece), item = seq * n_qblocks + block
+  // (-1: none), piece = nparts | part << 8 | first piece index << 16
+  const int2* items;
+  int32_t* counters;  // one per (cut item, KV head), zero at rest
+  float* ws_o;        // partial rows [piece][kv head][column][D]
+  float* ws_ml;       // (max, sum) of each partial row
+  int64_t n_items_grid;  // workgroups of a planned call: plan entries x H_kv
 };
 
 template <int D, int NW_ = 8, int CT_ = 2>
@@ -108,31 +123,40 @@ struct PShape {
 
 // FAST: power-of-two block size and a pool layer small enough for 24-bit slot
 // and stride products (32-bit element offsets).
-template <int DT, int D, bool FAST, int NW, int CTW, bool PP>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 2 : 1)))
+// SCHED: kLockstep (3-deep ring, next tile's scores beside this tile's
+// exponentials) or kRing2 (2-deep ring, one tile at a time: ~78 KB of LDS
+// and <= 256 registers, so two 4-wavefront workgroups share a CU).
+constexpr int kLockstep = 0, kRing2 = 2;
+
+template <int DT, int D, bool FAST, int NW, int CTW, int SCHED>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 8 || SCHED == kRing2 ? 2 : 1)))
 void paged_prefill_kernel(PrefillArgs a) {
   typedef PShape<D, NW, CTW> S;
   constexpr int EB = 2;
   constexpr int CT = S::CT, BN = S::BN, NT = S::NT;
-  __shared__ __attribute__((aligned(16))) uint16_t ks_lds[3][BN * S::KROW];
-  __shared__ __attribute__((aligned(16))) uint16_t vs_lds[3][BN * S::KROW];
+  constexpr int RING = SCHED == kRing2 ? 2 : 3;
+  __shared__ __attribute__((aligned(16))) uint16_t ks_lds[RING][BN * S::KROW];
+  __shared__ __attribute__((aligned(16))) uint16_t vs_lds[RING][BN * S::KROW];
   __shared__ int32_t bt_lds[kBtCache];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
   const int TQ = a.tq;
 
-  // ---- which (query block, KV head, sequence): item order[i / H_kv] of the
-  // heaviest-first order when one is given, else the last query blocks (most
-  // keys within a sequence) first
-  int tb, seq, kvh;
-  if (a.order) {
+  // ---- which (query block, KV head, sequence) and which piece of its keys:
+  // plan entry i / H_kv when a plan is given, else the last query blocks (most
+  // keys within a sequence) first, uncut
+  int tb, seq, kvh, nparts = 1, part = 0, pbase = 0;
+  if (a.items) {
     const int k = (int)(blockIdx.x / a.num_kv_heads);
     kvh = (int)(blockIdx.x - (unsigned)k * a.num_kv_heads);
-    const int item = a.order[k];
-    if (item < 0 || item >= a.num_seqs * a.n_qblocks) return;
-    seq = item / a.n_qblocks;
-    tb = item - seq * a.n_qblocks;
+    const int2 e = a.items[k];
+    if (e.x < 0 || e.x >= a.num_seqs * a.n_qblocks) return;
+    seq = e.x / a.n_qblocks;
+    tb = e.x - seq * a.n_qblocks;
+    nparts = max(e.y & 0xff, 1);
+    part = min((e.y >> 8) & 0xff, nparts - 1);
+    pbase = (int)((uint32_t)e.y >> 16);
   } else {
     const int per_tb = a.num_kv_heads * a.num_seqs;
     tb = a.n_qblocks - 1 - (int)(blockIdx.x / per_tb);
@@ -158,9 +182,12 @@ void paged_prefill_kernel(PrefillArgs a) {
     if (tid == 0 && tb == 0 && kvh == 0) flag_error(a.err, IR_ERR_CONTEXT_RANGE);
     p0 = p0 < 0 ? 0 : min(p0, cap);  // keeps p0 + q_len within int range
   }
-  // keys this block needs: up to its last query's position, within the table
+  // keys this block needs: up to its last query's position, within the table;
+  // this piece walks key tiles [t_lo, t_hi) of them
   const int kmax = min(cap, p0 + min(q_len, tq0 + TQ));
   const int nkb = kmax > 0 && a.num_blocks > 0 ? (kmax + BN - 1) / BN : 0;
+  const int t_lo = (int)((int64_t)part * nkb / nparts);
+  const int t_hi = (int)((int64_t)(part + 1) * nkb / nparts);
 
   // columns of this lane: tile ct holds column j = 32 w + 16 ct + c, i.e.
   // token tq0 + j / n_rep, query head kvh * n_rep + j % n_rep (recomputed for
@@ -243,10 +270,7 @@ void paged_prefill_kernel(PrefillArgs a) {
     const int k0 = kb * BN;
     const int k_last = min(k0 + BN, kmax) - 1;
     const int last_blk = FAST ? k_last >> a.bs_shift : k_last / a.bs;
-    // (the ping-pong schedule runs only on tables the cache holds whole: its
-    // wave groups never meet at the same barrier for a refill)
-    if constexpr (!PP)
-      if (last_blk >= bt_base + kBtCache) fill_bt(FAST ? k0 >> a.bs_shift : k0 / a.bs);
+    if (last_blk >= bt_base + kBtCache) fill_bt(FAST ? k0 >> a.bs_shift : k0 / a.bs);
 #pragma unroll
     for (int i = 0; i < S::KPT; ++i) {
       const int q = tid + NT * i;
@@ -332,7 +356,7 @@ void paged_prefill_kernel(PrefillArgs a) {
     constexpr bool NX = decltype(nx_tag)::value;
     using E = Elem<DT>;
     const int k0 = kb * BN;
-    const bool first = kb == 0;
+    const bool first = kb == t_lo;
     // only tiles that cross the causal diagonal or the last key are masked
     if (!(k0 + BN - 1 <= qpos0 && k0 + BN <= kmax)) {
 #pragma unroll
@@ -365,7 +389,7 @@ void paged_prefill_kernel(PrefillArgs a) {
       }
     }
     // next tile's scores (MFMA) interleaved with this tile's exponentials (VALU)
-    const uint16_t* kn = ks_lds[(kb + 1) % 3];
+    const uint16_t* kn = ks_lds[(kb + 1) % RING];
     if constexpr (NX) {
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
@@ -418,7 +442,7 @@ void paged_prefill_kernel(PrefillArgs a) {
     }
     // O^T += V^T . P^T; V^T operand: d row c of the tile, the same key slots
     // (operands read one step ahead)
-    const uint16_t* vb_lds = vs_lds[kb % 3];
+    const uint16_t* vb_lds = vs_lds[kb % RING];
     auto v_operand = [&](int t) {
       return v_operand_tr(vb_lds, t);
     };
@@ -435,191 +459,62 @@ void paged_prefill_kernel(PrefillArgs a) {
     }
   };
 
-  // ---- walk the key tiles through a 3-deep LDS ring: tile kb (V) and tile
-  // kb + 1 (K) are read while tile kb + 2 is written from registers and tile
-  // kb + 3 is in flight from global memory
-  auto tail = [&](int kb) {
-    if (kb + 2 < nkb) store_regs((kb + 2) % 3);
-    if (kb + 3 < nkb) load_regs(kb + 3);
-    __syncthreads();
-  };
-  if constexpr (PP) {
-    // ---- ping-pong schedule (8 wavefronts, two per SIMD). Each wavefront's
-    // iteration i is a matrix half -- the scores of tile i and the PV product
-    // of tile i - 1, 64 MFMAs -- and a vector half -- tile i's softmax, one
-    // tile's LDS store and the next tile's global loads. Waves 4..7 start one
-    // barrier later than waves 0..3, so on every SIMD one wavefront runs its
-    // matrix half while the other runs its vector half (in lockstep the two
-    // pipes mostly took turns). Barrier intervals: the leading group's halves
-    // of iteration i are intervals 2i and 2i + 1, the following group's
-    // 2i + 1 and 2i + 2. Tile t is read (K) in intervals 2t, 2t + 1 and (V)
-    // 2t + 2, 2t + 3, so the leaders store their part of it in interval
-    // 2t - 1 (iteration t - 1) and the followers in 2t - 2 (iteration t - 2);
-    // the next tile for its buffer (t + 3) is first stored in interval
-    // 2t + 4: a 3-deep ring suffices. Each wavefront keeps one tile's global
-    // loads in flight, issued an iteration before their store.
-    const bool lead = w < NW / 2;
-    const int ahead = lead ? 1 : 2;  // the tile a wavefront stores in iteration i is i + ahead
-    f32x4 sc[CT][4];                 // scores of the tile in flight through the iteration
-    u32x4 pb[CT][2];                 // probabilities of the previous tile (PV operand)
-    using E = Elem<DT>;
-    constexpr int NQK = 4 * S::KS, NPV = 2 * S::DTL;
-    // matrix half: S(i) = K(i) . Q^T starting from -m (QK), O^T += V^T(i-1) . P^T(i-1) (PV)
-    auto matrix_half = [&](auto qk_tag, auto pv_tag, int i) {
-      constexpr bool QK = decltype(qk_tag)::value, PVH = decltype(pv_tag)::value;
-      const uint16_t* kb_lds = ks_lds[i % 3];
-      const uint16_t* vb_lds = vs_lds[(i + 2) % 3];
-      auto k_operand = [&](int t) {
-        return *(const u32x4*)&kb_lds[((t % 4) * 16 + c) * S::KROW + (t / 4) * 32 + 8 * g];
-      };
-      auto v_operand = [&](int t) {
-        return v_operand_tr(vb_lds, t);
-      };
-      if constexpr (QK) {
+  // ---- walk key tiles [t_lo, t_hi)
+  if constexpr (SCHED == kRing2) {
+    // one tile per step: its scores (from -m), softmax and PV product read
+    // buffer kb % 2 while tile kb + 1 is written to the other buffer from the
+    // registers its loads filled a step earlier and tile kb + 2's loads go
+    // out
+    if (t_lo < t_hi) {
+      fill_bt(FAST ? (t_lo * BN) >> a.bs_shift : (t_lo * BN) / a.bs);
+      load_regs(t_lo);
+      store_regs(t_lo & 1);
+      if (t_lo + 1 < t_hi) load_regs(t_lo + 1);
+      __syncthreads();
+      f32x4 sc[CT][4];
+      for (int kb = t_lo; kb < t_hi; ++kb) {
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
           for (int kt = 0; kt < 4; ++kt) sc[ct][kt] = negm[ct];
-      }
-      constexpr int NT_ = NQK > NPV ? NQK : NPV;
-      u32x4 kring[kOperandAhead], vring[kOperandAhead];
 #pragma unroll
-      for (int t = 0; t < kOperandAhead; ++t) {
-        if constexpr (QK) kring[t] = k_operand(t);
-        if constexpr (PVH) vring[t] = v_operand(t);
-      }
-#pragma unroll
-      for (int t = 0; t < NT_; ++t) {
-        if constexpr (QK) {
-          if (t < NQK) {
-            const u32x4 ka = kring[t % kOperandAhead];
-            if (t + kOperandAhead < NQK) kring[t % kOperandAhead] = k_operand(t + kOperandAhead);
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) sc[ct][t % 4] = mfma_k32<DT>(ka, qreg[ct][t / 4], sc[ct][t % 4]);
-          }
-        }
-        if constexpr (PVH) {
-          if (t < NPV) {
-            const u32x4 va = vring[t % kOperandAhead];
-            if (t + kOperandAhead < NPV) vring[t % kOperandAhead] = v_operand(t + kOperandAhead);
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct)
-              acc[ct][t % S::DTL] = mfma_k32<DT>(va, pb[ct][t / S::DTL], acc[ct][t % S::DTL]);
-          }
-        }
-        // keep the steps in program order: hoisting every operand read to
-        // the top would hold all of them in registers at once
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    };
-    // vector half: tile i's mask, running max (the first tile sets it; later
-    // ones move it past kRescaleSlack only), exponentials, P^T and the sums
-    auto vector_half = [&](int i) {
-      const int k0 = i * BN;
-      if (!(k0 + BN - 1 <= qpos0 && k0 + BN <= kmax)) {
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-          for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              if (k0 + kt * 16 + 4 * g + r > col_lim[ct]) sc[ct][kt][r] = kNegInf;
-      }
-      const bool first = i == 0;
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        float mx = kNegInf;
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-          mx = fmaxf(mx, fmaxf(fmaxf(sc[ct][kt][0], sc[ct][kt][1]), fmaxf(sc[ct][kt][2], sc[ct][kt][3])));
-        mx = wave_max_groups_swap(mx);
-        const bool grow = first || mx > kRescaleSlack;
-        if (__any(grow)) {
-          const float d = grow ? mx : 0.f;
-          if (!first) {
-            const float alpha = fast_exp2(-d);
-            l[ct] *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < S::DTL; ++dt) acc[ct][dt] *= alpha;
-          }
-          negm[ct] -= d;
-#pragma unroll
-          for (int kt = 0; kt < 4; ++kt) sc[ct][kt] -= d;
-        }
-      }
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) sc[ct][kt][r] = fast_exp2(sc[ct][kt][r]);
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          pb[ct][st] = u32x4{E::pack2(sc[ct][2 * st][0], sc[ct][2 * st][1]),
-                             E::pack2(sc[ct][2 * st][2], sc[ct][2 * st][3]),
-                             E::pack2(sc[ct][2 * st + 1][0], sc[ct][2 * st + 1][1]),
-                             E::pack2(sc[ct][2 * st + 1][2], sc[ct][2 * st + 1][3])};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) l[ct] = sum2<DT>(pb[ct][st][e], l[ct]);
-        }
-      }
-    };
-    if (nkb > 0) {
-      fill_bt(0);
-      load_regs(0);
-      store_regs(0);
-      if (!lead && nkb > 1) {
-        load_regs(1);
-        store_regs(1);
-      }
-      if (ahead < nkb) load_regs(ahead);
-      __syncthreads();
-      if (!lead) __syncthreads();  // the followers start half an iteration later
-      auto vector_and_memory = [&](int i) {
-        const int st = i + ahead;
-        if (st < nkb) store_regs(st % 3);
-        if (st + 1 < nkb) load_regs(st + 1);
-        vector_half(i);
-      };
-      // iteration 0 has no PV product, iteration nkb no scores: peeled
-      matrix_half(std::true_type{}, std::false_type{}, 0);
-      __syncthreads();
-      vector_and_memory(0);
-      __syncthreads();
-      for (int i = 1; i < nkb; ++i) {
-        matrix_half(std::true_type{}, std::true_type{}, i);
-        __syncthreads();
-        vector_and_memory(i);
+        for (int t = 0; t < 4 * S::KS; ++t) qk_step(ks_lds[kb & 1], t % 4, t / 4, sc);
+        step(std::false_type{}, kb, sc, sc);
+        if (kb + 1 < t_hi) store_regs((kb + 1) & 1);
+        if (kb + 2 < t_hi) load_regs(kb + 2);
         __syncthreads();
       }
-      matrix_half(std::false_type{}, std::true_type{}, nkb);
-      __syncthreads();
-      __syncthreads();
-      if (lead) __syncthreads();  // as many barriers as the followers
     }
-  } else if (nkb > 0) {
-    fill_bt(0);
-    load_regs(0);
-    store_regs(0);
-    if (nkb > 1) {
-      load_regs(1);
-      store_regs(1);
+  } else if (t_lo < t_hi) {
+    // 3-deep ring: tile kb (V) and tile kb + 1 (K) are read while tile kb + 2
+    // is written from registers and tile kb + 3 is in flight
+    auto tail = [&](int kb) {
+      if (kb + 2 < t_hi) store_regs((kb + 2) % 3);
+      if (kb + 3 < t_hi) load_regs(kb + 3);
+      __syncthreads();
+    };
+    fill_bt(FAST ? (t_lo * BN) >> a.bs_shift : (t_lo * BN) / a.bs);
+    load_regs(t_lo);
+    store_regs(t_lo % 3);
+    if (t_lo + 1 < t_hi) {
+      load_regs(t_lo + 1);
+      store_regs((t_lo + 1) % 3);
     }
-    if (nkb > 2) load_regs(2);
+    if (t_lo + 2 < t_hi) load_regs(t_lo + 2);
     __syncthreads();
     f32x4 sa[CT][4], sb[CT][4];
     zero_s(sa);
 #pragma unroll
-    for (int t = 0; t < 4 * S::KS; ++t) qk_step(ks_lds[0], t % 4, t / 4, sa);
-    int kb = 0;
+    for (int t = 0; t < 4 * S::KS; ++t) qk_step(ks_lds[t_lo % 3], t % 4, t / 4, sa);
+    int kb = t_lo;
     // two tiles per trip so the score buffers swap roles without copies
-    for (; kb + 2 < nkb; kb += 2) {
+    for (; kb + 2 < t_hi; kb += 2) {
       step(std::true_type{}, kb, sa, sb);
       tail(kb);
       step(std::true_type{}, kb + 1, sb, sa);
       tail(kb + 1);
     }
-    if (kb + 1 < nkb) {
+    if (kb + 1 < t_hi) {
       step(std::true_type{}, kb, sa, sb);
       tail(kb);
       step(std::false_type{}, kb + 1, sb, sa);
@@ -629,51 +524,154 @@ void paged_prefill_kernel(PrefillArgs a) {
   }
   if (bad) flag_error(a.err, IR_ERR_BLOCK_RANGE);
 
-  // ---- normalise and store: lane (g, c) register r of d tile dt = output
-  // d = 16 dt + 4 g + r of column c
+  if (nparts == 1) {
+    // ---- normalise and store: lane (g, c) register r of d tile dt = output
+    // d = 16 dt + 4 g + r of column c
+#pragma unroll
+    for (int qt = 0; qt < CT; ++qt) {
+      const float lsum = wave_sum_groups_swap(l[qt]);
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      const Col col = column(qt);
+      if (!col.ok) continue;
+      uint8_t* orow = (uint8_t*)a.out + ((int64_t)(q_lo + col.tok) * a.o_tok + (int64_t)col.head * a.o_head) * EB;
+#pragma unroll
+      for (int dt = 0; dt < S::DTL; ++dt) {
+        const float o[4] = {acc[qt][dt][0], acc[qt][dt][1], acc[qt][dt][2], acc[qt][dt][3]};
+        store4<DT>(orow + (dt * 16 + 4 * g) * EB, o, inv);
+      }
+    }
+    return;
+  }
+
+  // ---- a piece of a cut item: publish this piece's partial rows (device
+  // scope), count its arrival; the last piece to arrive merges them all in
+  // part order (the same arithmetic whichever piece arrives last), its own
+  // part from registers and the others loaded for exactly the (column, d)
+  // elements each lane holds, every load of a part in flight together
+  constexpr int COLS = S::COLS;
+  const __amdgpu_buffer_rsrc_t r_o = dev_rsrc(a.ws_o), r_ml = dev_rsrc(a.ws_ml);
+  const int row_step = a.num_kv_heads * COLS;  // rows between parts of one item
+  const int row_base = (pbase * a.num_kv_heads + kvh) * COLS;  // part 0, column 0
+  float lsum[CT];
 #pragma unroll
   for (int qt = 0; qt < CT; ++qt) {
-    const float lsum = wave_sum_groups_swap(l[qt]);
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    lsum[qt] = wave_sum_groups_swap(l[qt]);
+    const int row = row_base + part * row_step + w * (CT * 16) + qt * 16 + c;
+#pragma unroll
+    for (int dt = 0; dt < S::DTL; ++dt) store_dev4(r_o, (row * D + dt * 16 + 4 * g) * 4, acc[qt][dt]);
+    if (g == 0) store_dev2(r_ml, row * 8, f32x2{-negm[qt][0], lsum[qt]});
+  }
+  __shared__ int s_last;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  int32_t* ctr = a.counters + pbase * a.num_kv_heads + kvh;
+  if (tid == 0) {
+    const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == nparts - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  f32x4 o_run[CT][S::DTL];
+  float m_run[CT], l_run[CT];
+#pragma unroll
+  for (int qt = 0; qt < CT; ++qt) {
+    m_run[qt] = kNegInf;
+    l_run[qt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < S::DTL; ++dt) o_run[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int p = 0; p < nparts; ++p) {
+    f32x4 op[CT][S::DTL];
+    float mp[CT], lp[CT];
+    if (p == part) {
+#pragma unroll
+      for (int qt = 0; qt < CT; ++qt) {
+        mp[qt] = -negm[qt][0];
+        lp[qt] = lsum[qt];
+#pragma unroll
+        for (int dt = 0; dt < S::DTL; ++dt) op[qt][dt] = acc[qt][dt];
+      }
+    } else {
+#pragma unroll
+      for (int qt = 0; qt < CT; ++qt) {
+        const int row = row_base + p * row_step + w * (CT * 16) + qt * 16 + c;
+        const f32x2 ml = load_dev2(r_ml, row * 8);
+        mp[qt] = ml[0];
+        lp[qt] = ml[1];
+#pragma unroll
+        for (int dt = 0; dt < S::DTL; ++dt) op[qt][dt] = load_dev4(r_o, (row * D + dt * 16 + 4 * g) * 4);
+      }
+    }
+#pragma unroll
+    for (int qt = 0; qt < CT; ++qt) {
+      // a part without keys has max -inf: its weight is exp2(-inf) = 0, and
+      // fmaxf keeps an (-inf) - (-inf) exponent from becoming NaN
+      const float mn = fmaxf(m_run[qt], mp[qt]);
+      const float wa = fast_exp2(fmaxf(m_run[qt] - mn, -1e30f)), wb = fast_exp2(fmaxf(mp[qt] - mn, -1e30f));
+      l_run[qt] = wa * l_run[qt] + wb * lp[qt];
+#pragma unroll
+      for (int dt = 0; dt < S::DTL; ++dt) o_run[qt][dt] = wa * o_run[qt][dt] + wb * op[qt][dt];
+      m_run[qt] = mn;
+    }
+  }
+#pragma unroll
+  for (int qt = 0; qt < CT; ++qt) {
+    const float inv = l_run[qt] > 0.f ? 1.f / l_run[qt] : 0.f;
     const Col col = column(qt);
     if (!col.ok) continue;
     uint8_t* orow = (uint8_t*)a.out + ((int64_t)(q_lo + col.tok) * a.o_tok + (int64_t)col.head * a.o_head) * EB;
 #pragma unroll
     for (int dt = 0; dt < S::DTL; ++dt) {
-      const float o[4] = {acc[qt][dt][0], acc[qt][dt][1], acc[qt][dt][2], acc[qt][dt][3]};
+      const float o[4] = {o_run[qt][dt][0], o_run[qt][dt][1], o_run[qt][dt][2], o_run[qt][dt][3]};
       store4<DT>(orow + (dt * 16 + 4 * g) * EB, o, inv);
     }
   }
+  if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ---------------------------------------------------------------- work order
+// ---------------------------------------------------------------- plan
 //
 // The dispatcher hands workgroup i to the first CU with room, in index order,
-// so issuing the heaviest items first is the longest-processing-time rule: on
-// a chunked prefill whose items outnumber the CUs (8 chunks of 512 tokens
-// after prefixes of 2.5k-4k keys: 480 workgroups, 1 per CU) the busiest CU's
-// share drops from 1.26x to 1.06x of the mean (tile counts, simulated). The
-// order is built once per step (all layers share the metadata) by one
-// workgroup: every (sequence, query block) item is weighed by the 64-key tiles
-// its workgroup walks, and a counting sort over kOrderBuckets equal-width
-// weight ranges writes the items heaviest range first; items with no query
-// rows go last as -1. Workgroups write disjoint outputs, so the order (ties
-// land in any order) never changes a result bit.
+// so issuing the heaviest work first is the longest-processing-time rule. But
+// an order cannot shorten the heaviest item itself, which bounds the call when
+// one sequence's prefix is much longer than the rest. The plan therefore cuts
+// every item heavier than 1.5x the mean load of a workgroup slot (and than
+// kMinPieceTiles) into pieces of at most that threshold, at most kMaxParts per
+// item and at most the plan's piece capacity in all (the smallest threshold
+// that fits it, found by bisection), then counting-sorts the pieces by weight
+// over kPlanBuckets ranges, heaviest first; items without query rows go last
+// as -1. Measured on 8 chunks of 512 tokens after prefixes of U{0..8192} keys
+// (per-workgroup timestamps): a workgroup costs ~7 us plus ~2.2 us per 64-key
+// tile while sharing its CU, and cutting at the mean (the longest item, 99
+// tiles, against a mean of 75) made the call 10% slower -- the pieces' fixed
+// costs and merges outweighed a tail the heaviest-first order had mostly
+// filled -- so only items well above the mean are cut. One workgroup builds it once per step (every layer shares the
+// metadata) and clears the arrival counters. Each thread owns a contiguous
+// run of items, so the pieces' partial-row indices come from a deterministic
+// scan; only the position of equal-weight pieces in the order varies, which
+// changes the schedule, never a result bit.
 
-constexpr int kOrderThreads = 1024;
-constexpr int kOrderBuckets = 2048;
+constexpr int kPlanThreads = 1024;
+constexpr int kPlanBuckets = 2048;
+constexpr int kMaxParts = 16;      // pieces per item (8-bit field)
+constexpr int kMinPieceTiles = 8;  // items of at most this many key tiles are never cut
+constexpr int kPlanWeightCache = 8192;  // items whose weights the plan keeps in LDS
 
-struct OrderArgs {
+struct PlanArgs {
   const int32_t* cu_q;
   const int32_t* q_start;
   int num_seqs, total_q, n_qblocks, tq, cap;  // cap: keys the block tables hold
-  int32_t* order;                             // [num_seqs * n_qblocks]
+  int num_kv_heads, slots, cap_pieces;        // slots: workgroups resident on the device at once
+  int entries;
+  int2* items;        // [entries]
+  int32_t* counters;  // [cap_pieces * num_kv_heads]
 };
 
 // 64-key tiles the workgroups of item (seq * n_qblocks + block) walk, following
 // paged_prefill_kernel's bounds; -1 when they return without work (an item
 // that only flags bad metadata weighs 0).
-__device__ int prefill_item_weight(const OrderArgs& a, int item) {
+__device__ int prefill_item_weight(const PlanArgs& a, int item) {
   const int seq = item / a.n_qblocks, tb = item - seq * a.n_qblocks;
   const int q_lo = a.cu_q[seq], q_len = a.cu_q[seq + 1] - q_lo;
   if (q_lo < 0 || q_len < 0 || (int64_t)q_lo + q_len > a.total_q) return tb == 0 ? 0 : -1;
@@ -684,61 +682,150 @@ __device__ int prefill_item_weight(const OrderArgs& a, int item) {
   return (int)((kmax + 63) / 64);
 }
 
-__global__ __launch_bounds__(kOrderThreads) void prefill_order_kernel(OrderArgs a) {
-  __shared__ int start[kOrderBuckets + 1];  // bucket kOrderBuckets: items without work
-  __shared__ int wave_max[kOrderThreads / 64];
+__device__ __forceinline__ int pieces_of(int w, int T) {
+  return w > T ? min(kMaxParts, (w + T - 1) / T) : (w >= 0 ? 1 : 0);
+}
+
+// Block-wide sum / max over kPlanThreads threads (every thread gets the result).
+__device__ int64_t plan_sum(int64_t x, int64_t* red) {
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  int64_t t = 0;
+  for (int i = 0; i < kPlanThreads / 64; ++i) t += red[i];
+  return t;
+}
+
+__device__ int64_t plan_max(int64_t x, int64_t* red) {
+  for (int o = 32; o > 0; o >>= 1) x = max(x, (int64_t)__shfl_xor(x, o));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  int64_t t = red[0];
+  for (int i = 1; i < kPlanThreads / 64; ++i) t = max(t, red[i]);
+  return t;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PlanArgs a) {
+  __shared__ int start[kPlanBuckets + 1];
+  __shared__ int64_t red[kPlanThreads / 64];
+  __shared__ int run_base[kPlanThreads];
+  __shared__ int w_cache[kPlanWeightCache];
   const int tid = threadIdx.x, lane = tid & 63;
   const int n = a.num_seqs * a.n_qblocks;
+  const int per = (n + kPlanThreads - 1) / kPlanThreads;
+  const int i_lo = min(n, tid * per), i_hi = min(n, i_lo + per);
+  // the items' weights are read from global metadata once when they fit LDS
+  const bool cached = n <= kPlanWeightCache;
+  auto weight = [&](int i) { return cached ? w_cache[i] : prefill_item_weight(a, i); };
 
-  int wmax = 0;
-  for (int i = tid; i < n; i += kOrderThreads) wmax = max(wmax, prefill_item_weight(a, i));
-  for (int o = 32; o > 0; o >>= 1) wmax = max(wmax, __shfl_xor(wmax, o));
-  if (lane == 0) wave_max[tid >> 6] = wmax;
-  for (int i = tid; i <= kOrderBuckets; i += kOrderThreads) start[i] = 0;
+  int64_t tot = 0, wm = 0;
+  for (int i = i_lo; i < i_hi; ++i) {
+    const int w = prefill_item_weight(a, i);
+    if (cached) w_cache[i] = w;
+    tot += max(w, 0);
+    wm = max(wm, (int64_t)w);
+  }
+  const int64_t total = plan_sum(tot, red);
+  const int wmax = (int)plan_max(wm, red);
+  // the cut threshold: the mean load of a workgroup slot, raised until the
+  // pieces of the cut items fit the plan's capacity
+  int lo = (int)max((int64_t)kMinPieceTiles, (total * a.num_kv_heads * 3 + 2 * a.slots - 1) / (2 * a.slots));
+  int hi = max(lo, wmax);
+  while (lo < hi) {
+    const int mid = lo + (hi - lo) / 2;
+    int64_t cnt = 0;
+    for (int i = i_lo; i < i_hi; ++i) {
+      const int w = weight(i);
+      if (w > mid) cnt += pieces_of(w, mid);
+    }
+    if (plan_sum(cnt, red) <= a.cap_pieces) hi = mid;
+    else lo = mid + 1;
+  }
+  const int T = lo;
+
+  // first partial-row piece of each cut item: exclusive scan over the runs
+  int mine = 0;
+  for (int i = i_lo; i < i_hi; ++i) {
+    const int np = pieces_of(weight(i), T);
+    if (np > 1) mine += np;
+  }
+  run_base[tid] = mine;
+  for (int i = tid; i <= kPlanBuckets; i += kPlanThreads) start[i] = 0;
   __syncthreads();
-  wmax = 0;
-  for (int i = 0; i < kOrderThreads / 64; ++i) wmax = max(wmax, wave_max[i]);
-  // bucket 0 holds the heaviest weights
-  auto bucket = [&](int wt) {
-    return wt < 0 ? kOrderBuckets : (int)((int64_t)(wmax - wt) * kOrderBuckets / ((int64_t)wmax + 1));
-  };
-  for (int i = tid; i < n; i += kOrderThreads) atomicAdd(&start[bucket(prefill_item_weight(a, i))], 1);
-  __syncthreads();
-  // exclusive scan of the counts by the first wavefront: lane l owns a run of
-  // consecutive buckets
-  if (tid < 64) {
-    constexpr int kRun = (kOrderBuckets + 1 + 63) / 64;
-    const int lo = lane * kRun, hi = min(lo + kRun, kOrderBuckets + 1);
+  if (tid < 64) {  // scan of the 1024 run totals by one wavefront
+    constexpr int kRun = kPlanThreads / 64;
     int sum = 0;
-    for (int i = lo; i < hi; ++i) sum += start[i];
+    for (int k = 0; k < kRun; ++k) sum += run_base[lane * kRun + k];
     int incl = sum;
     for (int o = 1; o < 64; o <<= 1) {
       const int y = __shfl_up(incl, o);
       if (lane >= o) incl += y;
     }
-    int run = incl - sum;
-    for (int i = lo; i < hi; ++i) {
-      const int cnt = start[i];
-      start[i] = run;
-      run += cnt;
+    int r = incl - sum;
+    for (int k = 0; k < kRun; ++k) {
+      const int v = run_base[lane * kRun + k];
+      run_base[lane * kRun + k] = r;
+      r += v;
     }
   }
   __syncthreads();
-  for (int i = tid; i < n; i += kOrderThreads) {
-    const int wt = prefill_item_weight(a, i);
-    const int pos = atomicAdd(&start[bucket(wt)], 1);
-    a.order[pos] = wt < 0 ? -1 : i;
+
+  // bucket 0 holds the heaviest pieces
+  auto bucket = [&](int pw) { return (int)((int64_t)(wmax - pw) * kPlanBuckets / ((int64_t)wmax + 1)); };
+  for (int i = i_lo; i < i_hi; ++i) {
+    const int w = weight(i);
+    const int np = pieces_of(w, T);
+    if (np > 0) atomicAdd(&start[bucket((w + np - 1) / np)], np);
   }
+  __syncthreads();
+  if (tid < 64) {  // exclusive scan of the bucket counts; start[kPlanBuckets] = pieces in all
+    constexpr int kRun = (kPlanBuckets + 1 + 63) / 64;
+    const int b_lo = lane * kRun, b_hi = min(b_lo + kRun, kPlanBuckets + 1);
+    int sum = 0;
+    for (int i = b_lo; i < b_hi; ++i) sum += start[i];
+    int incl = sum;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o);
+      if (lane >= o) incl += y;
+    }
+    int r = incl - sum;
+    for (int i = b_lo; i < b_hi; ++i) {
+      const int cnt = start[i];
+      start[i] = r;
+      r += cnt;
+    }
+  }
+  __syncthreads();
+  const int used = start[kPlanBuckets];
+  __syncthreads();
+  int pb = run_base[tid];
+  for (int i = i_lo; i < i_hi; ++i) {
+    const int w = weight(i);
+    const int np = pieces_of(w, T);
+    if (np == 0) continue;
+    const int pos = atomicAdd(&start[bucket((w + np - 1) / np)], np);
+    for (int p = 0; p < np; ++p)
+      a.items[pos + p] = np > 1 ? make_int2(i, np | (p << 8) | (pb << 16)) : make_int2(i, 1);
+    if (np > 1) pb += np;
+  }
+  for (int k = used + tid; k < a.entries; k += kPlanThreads) a.items[k] = make_int2(-1, 0);
+  for (int k = tid; k < a.cap_pieces * a.num_kv_heads; k += kPlanThreads) a.counters[k] = 0;
 }
 
 // Tuning knobs, read once per process: IR_PREFILL_WAVES (4 or 8) forces the
-// workgroup shape, IR_PREFILL_PINGPONG=1 selects the ping-pong schedule.
+// workgroup size, IR_PREFILL_RING2 (1 or 0) forces or forbids the 2-deep ring
+// for 4-wavefront workgroups, IR_PREFILL_CUTS=0 keeps the plan from cutting
+// items (order only).
 struct PrefillKnobs {
-  int waves = 0;  // 0: by grid size
-  bool pingpong = false;
+  int waves = 0;   // 0: 4, or 8 when 4 cannot hold a token's query heads
+  int ring2 = -1;  // -1: by grid size
+  bool cuts = true;
   PrefillKnobs() {
-    if (const char* e = getenv("IR_PREFILL_WAVES")) waves = atoi(e) == 4 ? 4 : 8;
-    if (const char* e = getenv("IR_PREFILL_PINGPONG")) pingpong = atoi(e) == 1;
+    if (const char* e = getenv("IR_PREFILL_WAVES")) waves = atoi(e) == 8 ? 8 : 4;
+    if (const char* e = getenv("IR_PREFILL_RING2")) ring2 = atoi(e) == 1 ? 1 : 0;
+    if (const char* e = getenv("IR_PREFILL_CUTS")) cuts = atoi(e) != 0;
   }
 };
 
@@ -747,29 +834,54 @@ const PrefillKnobs& prefill_knobs() {
   return k;
 }
 
-// Workgroup shape of a prefill call: 8 wavefronts (256 query columns) unless
-// that leaves CUs idle, then 4 (128 columns), twice the workgroups with half
-// the work each.
+// Workgroup shape and schedule of a prefill call, from its shapes alone (the
+// plan and every layer's call agree on it): 4 wavefronts (128 query columns)
+// on the 2-deep ring when the call has workgroups for two per CU, else on the
+// 3-deep ring; 8 wavefronts (256 columns) when a token's query heads need more
+// than 128 columns or on request. `slots`: workgroups resident at once.
 struct PrefillGeometry {
-  int nw, tq, n_qblocks;
+  int nw, tq, n_qblocks, sched, slots;
 };
 
 PrefillGeometry prefill_geometry(int max_q_len, int n_rep, int num_kv_heads, int num_seqs) {
-  const int tq8 = PShape<128, 8>::COLS / n_rep;
-  const int64_t wgs8 = (int64_t)((max_q_len + tq8 - 1) / tq8) * num_kv_heads * num_seqs;
-  const int forced = prefill_knobs().waves;
-  // (4 wavefronts hold at most 128 query heads per KV head)
-  const bool four = n_rep <= PShape<128, 4>::COLS && (forced ? forced == 4 : wgs8 < device_cus());
+  const PrefillKnobs& k = prefill_knobs();
   PrefillGeometry g;
-  g.nw = four ? 4 : 8;
-  g.tq = (four ? PShape<128, 4>::COLS : PShape<128, 8>::COLS) / n_rep;
+  g.nw = (n_rep > PShape<128, 4>::COLS || k.waves == 8) ? 8 : 4;
+  g.tq = (g.nw == 4 ? PShape<128, 4>::COLS : PShape<128, 8>::COLS) / n_rep;
   g.n_qblocks = (max_q_len + g.tq - 1) / g.tq;
+  const int cus = device_cus();
+  const int64_t wgs = (int64_t)g.n_qblocks * num_kv_heads * num_seqs;
+  const bool ring2 = g.nw == 4 && (k.ring2 >= 0 ? k.ring2 == 1 : wgs >= 2 * (int64_t)cus);
+  g.sched = ring2 ? kRing2 : kLockstep;
+  g.slots = ring2 ? 2 * cus : cus;
   return g;
 }
 
+int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+// Plan layout: items [entries] int2, counters [cap_pieces * H_kv] int32,
+// (max, sum) [cap_pieces * H_kv * cols] fp32 x 2, partial outputs [.. * D] fp32.
+struct PlanLayout {
+  int64_t entries, cap_pieces, cols;
+  int64_t off_ctr, off_ml, off_o, total;
+};
+
+PlanLayout plan_layout(const PrefillGeometry& g, int num_seqs, int num_kv_heads, int head_dim) {
+  PlanLayout l;
+  l.cols = 32 * g.nw;
+  l.cap_pieces = (g.slots + num_kv_heads - 1) / num_kv_heads;
+  l.entries = (int64_t)num_seqs * g.n_qblocks + l.cap_pieces;
+  l.off_ctr = align256(l.entries * 8);
+  const int64_t rows = l.cap_pieces * num_kv_heads * l.cols;
+  l.off_ml = l.off_ctr + align256(l.cap_pieces * num_kv_heads * 4);
+  l.off_o = l.off_ml + align256(rows * 8);
+  l.total = l.off_o + align256(rows * head_dim * 4);
+  return l;
+}
+
 template <int DT, int D>
-int launch_prefill(const PrefillArgs& a, hipStream_t s) {
-  const int64_t grid = (int64_t)a.n_qblocks * a.num_kv_heads * a.num_seqs;
+int launch_prefill(const PrefillArgs& a, int sched, hipStream_t s) {
+  const int64_t grid = a.items ? a.n_items_grid : (int64_t)a.n_qblocks * a.num_kv_heads * a.num_seqs;
   if (grid <= 0) return ok();
   if (grid > 0x7fffffff) return fail(IR_EINVAL, "ir_paged_prefill: grid of %lld workgroups too large", (long long)grid);
   // fast addressing: slot and stride below 2^23 (24-bit products) and every
@@ -777,30 +889,20 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
   const int64_t slots = a.num_blocks * a.bs;
   const bool fast = a.bs_shift >= 0 && slots < (1 << 23) && a.c_slot < (1 << 23) &&
                     (slots * a.c_slot + a.c_head * a.num_kv_heads) < ((int64_t)1 << 31);
-  // ping-pong schedule on request (IR_PREFILL_PINGPONG=1), for 8-wavefront
-  // workgroups whose block tables fit the block-id cache whole. Measured on
-  // the 8 x 512-token workload: ahead of lockstep while V went through a
-  // register transpose (235 vs 257 us), behind it with row-major V and
-  // transpose reads (242 vs 225 us), so lockstep is the default.
-  const bool pp = a.nw == 8 && a.max_blocks <= kBtCache && prefill_knobs().pingpong;
+  const dim3 g((unsigned)grid);
   if (a.nw == 4) {
     const dim3 block(PShape<D, 4>::NT);
-    if (fast)
-      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 4, 2, false>), dim3((unsigned)grid), block, 0, s, a);
-    else
-      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 4, 2, false>), dim3((unsigned)grid), block, 0, s, a);
-  } else if (pp) {
-    const dim3 block(PShape<D, 8>::NT);
-    if (fast)
-      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 2, true>), dim3((unsigned)grid), block, 0, s, a);
-    else
-      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 2, true>), dim3((unsigned)grid), block, 0, s, a);
+    if (sched == kRing2) {
+      if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 4, 2, kRing2>), g, block, 0, s, a);
+      else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 4, 2, kRing2>), g, block, 0, s, a);
+    } else {
+      if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 4, 2, kLockstep>), g, block, 0, s, a);
+      else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 4, 2, kLockstep>), g, block, 0, s, a);
+    }
   } else {
     const dim3 block(PShape<D, 8>::NT);
-    if (fast)
-      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 2, false>), dim3((unsigned)grid), block, 0, s, a);
-    else
-      hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 2, false>), dim3((unsigned)grid), block, 0, s, a);
+    if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 2, kLockstep>), g, block, 0, s, a);
+    else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 2, kLockstep>), g, block, 0, s, a);
   }
   return check_launch("ir_paged_prefill");
 }
@@ -810,14 +912,22 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
 
 using namespace ir;
 
+extern "C" int64_t ir_paged_prefill_plan_bytes(int num_seqs, int max_q_len, int num_q_heads, int num_kv_heads,
+                                               int head_dim) {
+  if (num_seqs <= 0 || max_q_len <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads ||
+      num_q_heads / num_kv_heads > 256 || (head_dim != 64 && head_dim != 128))
+    return 0;
+  const PrefillGeometry geo = prefill_geometry(max_q_len, num_q_heads / num_kv_heads, num_kv_heads, num_seqs);
+  return plan_layout(geo, num_seqs, num_kv_heads, head_dim).total;
+}
+
 extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_head_stride, const void* k_cache,
                                 const void* v_cache, int64_t cache_slot_stride, int64_t cache_head_stride,
                                 int64_t num_blocks, int block_size, const int32_t* block_tables, int64_t bt_stride,
                                 int max_blocks_per_seq, const int32_t* cu_seqlens_q, const int32_t* q_start,
                                 int num_seqs, int total_q, int max_q_len, void* out, int64_t out_tok_stride,
                                 int64_t out_head_stride, int num_q_heads, int num_kv_heads, int head_dim, float scale,
-                                int dtype, const int32_t* order, int64_t order_len, int32_t* err_flags,
-                                ir_stream_t stream) {
+                                int dtype, void* plan, int64_t plan_bytes, int32_t* err_flags, ir_stream_t stream) {
   IR_REQUIRE(dtype == IR_DTYPE_BF16 || dtype == IR_DTYPE_F16 || dtype == IR_DTYPE_F32,
              "ir_paged_prefill: unknown dtype %d", dtype);
   if (dtype == IR_DTYPE_F32)
@@ -842,6 +952,7 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
                  (cache_head_stride * 2) % 16 == 0 && (out_tok_stride * 2) % 8 == 0 && (out_head_stride * 2) % 8 == 0,
              "ir_paged_prefill: q/cache strides must be multiples of 16 bytes, out strides of 8 bytes");
   PrefillArgs a;
+  memset(&a, 0, sizeof(a));
   a.q = q;
   a.q_tok = q_tok_stride;
   a.q_head = q_head_stride;
@@ -867,11 +978,19 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
   a.n_qblocks = geo.n_qblocks;
   const int64_t n_items = (int64_t)num_seqs * a.n_qblocks;
   IR_REQUIRE(n_items <= 0x7fffffff, "ir_paged_prefill: %lld work items", (long long)n_items);
-  IR_REQUIRE(!order || order_len == n_items,
-             "ir_paged_prefill: order holds %lld items, this call has %lld (build it with ir_paged_prefill_order "
-             "for the same metadata and shapes)",
-             (long long)order_len, (long long)n_items);
-  a.order = order;
+  if (plan) {
+    const PlanLayout ly = plan_layout(geo, num_seqs, num_kv_heads, head_dim);
+    IR_REQUIRE(plan_bytes >= ly.total && ((uintptr_t)plan & 255u) == 0,
+               "ir_paged_prefill: plan of %lld bytes (256-byte aligned) required, got %lld (build it with "
+               "ir_paged_prefill_plan for the same metadata and shapes)",
+               (long long)ly.total, (long long)plan_bytes);
+    uint8_t* pl = (uint8_t*)plan;
+    a.items = (const int2*)pl;
+    a.counters = (int32_t*)(pl + ly.off_ctr);
+    a.ws_ml = (float*)(pl + ly.off_ml);
+    a.ws_o = (float*)(pl + ly.off_o);
+    a.n_items_grid = ly.entries * num_kv_heads;
+  }
   a.out = out;
   a.o_tok = out_tok_stride;
   a.o_head = out_head_stride;
@@ -881,45 +1000,50 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
   a.err = err_flags;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == IR_DTYPE_BF16)
-    return head_dim == 128 ? launch_prefill<IR_DTYPE_BF16, 128>(a, s) : launch_prefill<IR_DTYPE_BF16, 64>(a, s);
-  return head_dim == 128 ? launch_prefill<IR_DTYPE_F16, 128>(a, s) : launch_prefill<IR_DTYPE_F16, 64>(a, s);
+    return head_dim == 128 ? launch_prefill<IR_DTYPE_BF16, 128>(a, geo.sched, s)
+                           : launch_prefill<IR_DTYPE_BF16, 64>(a, geo.sched, s);
+  return head_dim == 128 ? launch_prefill<IR_DTYPE_F16, 128>(a, geo.sched, s)
+                         : launch_prefill<IR_DTYPE_F16, 64>(a, geo.sched, s);
 }
 
-extern "C" int64_t ir_paged_prefill_order_len(int num_seqs, int max_q_len, int num_q_heads, int num_kv_heads) {
-  if (num_seqs <= 0 || max_q_len <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
-    return 0;
-  const PrefillGeometry geo = prefill_geometry(max_q_len, num_q_heads / num_kv_heads, num_kv_heads, num_seqs);
-  return (int64_t)num_seqs * geo.n_qblocks;
-}
-
-extern "C" int ir_paged_prefill_order(const int32_t* cu_seqlens_q, const int32_t* q_start, int num_seqs,
-                                      int total_q, int max_q_len, int max_blocks_per_seq, int block_size,
-                                      int num_q_heads, int num_kv_heads, int32_t* order, int64_t order_len,
-                                      ir_stream_t stream) {
+extern "C" int ir_paged_prefill_plan(const int32_t* cu_seqlens_q, const int32_t* q_start, int num_seqs, int total_q,
+                                     int max_q_len, int max_blocks_per_seq, int block_size, int num_q_heads,
+                                     int num_kv_heads, int head_dim, void* plan, int64_t plan_bytes,
+                                     ir_stream_t stream) {
   IR_REQUIRE(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && num_q_heads > 0 && num_kv_heads > 0 &&
                  block_size > 0 && max_blocks_per_seq >= 0,
-             "ir_paged_prefill_order: bad sizes");
-  IR_REQUIRE(num_q_heads % num_kv_heads == 0, "ir_paged_prefill_order: num_q_heads %d not a multiple of num_kv_heads %d",
+             "ir_paged_prefill_plan: bad sizes");
+  IR_REQUIRE(num_q_heads % num_kv_heads == 0, "ir_paged_prefill_plan: num_q_heads %d not a multiple of num_kv_heads %d",
              num_q_heads, num_kv_heads);
   IR_REQUIRE((int64_t)max_blocks_per_seq * block_size <= (int64_t)1 << 30,
-             "ir_paged_prefill_order: block tables of %d x %d tokens exceed 2^30 keys", max_blocks_per_seq,
+             "ir_paged_prefill_plan: block tables of %d x %d tokens exceed 2^30 keys", max_blocks_per_seq,
              block_size);
-  const int64_t need = ir_paged_prefill_order_len(num_seqs, max_q_len, num_q_heads, num_kv_heads);
-  IR_REQUIRE(order_len == need, "ir_paged_prefill_order: order holds %lld items, this call has %lld",
-             (long long)order_len, (long long)need);
-  IR_REQUIRE(need <= 0x7fffffff, "ir_paged_prefill_order: %lld work items", (long long)need);
-  if (need == 0) return ok();
-  IR_REQUIRE(cu_seqlens_q && q_start && order, "ir_paged_prefill_order: null pointer");
+  const int64_t need = ir_paged_prefill_plan_bytes(num_seqs, max_q_len, num_q_heads, num_kv_heads, head_dim);
+  if (need == 0) return ok();  // nothing to plan
+  IR_REQUIRE(plan && plan_bytes >= need && ((uintptr_t)plan & 255u) == 0,
+             "ir_paged_prefill_plan: plan of %lld bytes (256-byte aligned) required, got %lld", (long long)need,
+             (long long)plan_bytes);
+  IR_REQUIRE(cu_seqlens_q && q_start, "ir_paged_prefill_plan: null pointer");
   const PrefillGeometry geo = prefill_geometry(max_q_len, num_q_heads / num_kv_heads, num_kv_heads, num_seqs);
-  OrderArgs a;
-  a.cu_q = cu_seqlens_q;
-  a.q_start = q_start;
-  a.num_seqs = num_seqs;
-  a.total_q = total_q;
-  a.n_qblocks = geo.n_qblocks;
-  a.tq = geo.tq;
-  a.cap = max_blocks_per_seq * block_size;
-  a.order = order;
-  hipLaunchKernelGGL(prefill_order_kernel, dim3(1), dim3(kOrderThreads), 0, (hipStream_t)stream, a);
-  return check_launch("ir_paged_prefill_order");
+  const PlanLayout ly = plan_layout(geo, num_seqs, num_kv_heads, head_dim);
+  IR_REQUIRE(ly.entries <= 0x7fffffff && ly.cap_pieces < 65536 &&
+                 ly.cap_pieces * num_kv_heads * ly.cols * head_dim * 4 < ((int64_t)1 << 31),
+             "ir_paged_prefill_plan: plan too large for this shape");
+  PlanArgs p;
+  p.cu_q = cu_seqlens_q;
+  p.q_start = q_start;
+  p.num_seqs = num_seqs;
+  p.total_q = total_q;
+  p.n_qblocks = geo.n_qblocks;
+  p.tq = geo.tq;
+  p.cap = max_blocks_per_seq * block_size;
+  p.num_kv_heads = num_kv_heads;
+  p.slots = geo.slots;
+  p.cap_pieces = prefill_knobs().cuts ? (int)ly.cap_pieces : 0;
+  p.entries = (int)ly.entries;
+  uint8_t* pl = (uint8_t*)plan;
+  p.items = (int2*)pl;
+  p.counters = (int32_t*)(pl + ly.off_ctr);
+  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, p);
+  return check_launch("ir_paged_prefill_plan");
 }

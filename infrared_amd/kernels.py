@@ -441,27 +441,45 @@ def rope_kv_scatter(
     return q_out
 
 
-def prefill_order_len(num_seqs: int, max_q_len: int, num_q_heads: int, num_kv_heads: int) -> int:
-    """int32 items of a prefill work order for these shapes (0: nothing to order)."""
-    return int(lib().ir_paged_prefill_order_len(num_seqs, max_q_len, num_q_heads, num_kv_heads))
+@dataclass(frozen=True)
+class PrefillPlan:
+    """A prefill work plan (``ir_paged_prefill_plan``) and the shape it was built
+    for. ``buf`` holds the heaviest-first pieces of one step's prefill metadata
+    plus their arrival counters and partial rows; every layer of the step runs
+    on it with :func:`paged_prefill` (stream-ordered: the runs write into it).
+    Rebuild it when ``cu_seqlens_q``/``q_start`` change."""
+
+    buf: torch.Tensor
+    num_seqs: int
+    max_q_len: int
+    num_q_heads: int
+    num_kv_heads: int
+    head_dim: int
 
 
-def prefill_order_pays(num_seqs: int, max_q_len: int, num_q_heads: int, num_kv_heads: int,
-                       device: torch.device | str | int | None = None) -> bool:
-    """Whether a heaviest-first order can shorten the call: its workgroups
-    (one per CU at a time) outnumber the CUs, so the dispatch order decides
-    which CU finishes last. Below that every workgroup starts at once."""
-    n_items = prefill_order_len(num_seqs, max_q_len, num_q_heads, num_kv_heads)
-    if n_items <= 0:
+def prefill_plan_bytes(num_seqs: int, max_q_len: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
+    """Bytes of a prefill plan for these shapes (0: nothing to plan)."""
+    return int(lib().ir_paged_prefill_plan_bytes(num_seqs, max_q_len, num_q_heads, num_kv_heads, head_dim))
+
+
+def prefill_plan_pays(num_seqs: int, max_q_len: int, num_q_heads: int, num_kv_heads: int,
+                      device: torch.device | str | int | None = None) -> bool:
+    """Whether a plan can shorten the call: its workgroups outnumber the CUs,
+    so the dispatch order -- and cutting the heaviest items -- decides which
+    CU finishes last. Below that every workgroup starts at once. (Items are
+    (sequence, block of 128 // n_rep query tokens), 4-wavefront workgroups.)"""
+    if num_seqs <= 0 or max_q_len <= 0 or num_kv_heads <= 0 or num_q_heads % num_kv_heads:
         return False
+    n_rep = num_q_heads // num_kv_heads
+    tq = (128 if n_rep <= 128 else 256) // n_rep
     idx = torch.device(device if device is not None else "cuda").index
     idx = torch.cuda.current_device() if idx is None else idx
     if idx not in _CU_COUNT:
         _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
-    return n_items * num_kv_heads > _CU_COUNT[idx]
+    return num_seqs * -(-max_q_len // tq) * num_kv_heads > _CU_COUNT[idx]
 
 
-def prefill_order(
+def prefill_plan(
     cu_seqlens_q: torch.Tensor,
     q_start: torch.Tensor,
     total_q: int,
@@ -470,29 +488,31 @@ def prefill_order(
     block_size: int,
     num_q_heads: int,
     num_kv_heads: int,
+    head_dim: int,
     buf: torch.Tensor | None = None,
-) -> torch.Tensor:
-    """Heaviest-first work order of a prefill call's (sequence, query block)
-    items, built on the device (``ir_paged_prefill_order``); pass it to every
-    layer's :func:`paged_prefill` over the same metadata. ``buf`` (int32) is
-    reused when large enough."""
+) -> PrefillPlan:
+    """Work plan of a prefill call's (sequence, query block) items, built on
+    the device (``ir_paged_prefill_plan``); pass it to every layer's
+    :func:`paged_prefill` over the same metadata. ``buf`` (uint8, 256-byte
+    aligned) is reused when large enough."""
     dev = require_device(cu_seqlens_q, q_start)
     b = q_start.shape[0]
     for name, t, n in (("cu_seqlens_q", cu_seqlens_q, b + 1), ("q_start", q_start, b)):
         if t.dtype != torch.int32 or t.shape != (n,) or not t.is_contiguous():
-            raise RuntimeError(f"prefill_order: {name} must be contiguous int32 [{n}]")
-    n = prefill_order_len(b, max_q_len, num_q_heads, num_kv_heads)
+            raise RuntimeError(f"prefill_plan: {name} must be contiguous int32 [{n}]")
+    n = prefill_plan_bytes(b, max_q_len, num_q_heads, num_kv_heads, head_dim)
+    if n <= 0:
+        raise RuntimeError("prefill_plan: nothing to plan for these shapes")
     if buf is None or buf.numel() < n:
-        buf = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
-    if buf.dtype != torch.int32 or not buf.is_contiguous():
-        raise RuntimeError("prefill_order: buf must be a contiguous int32 tensor")
-    order = buf[:n]
-    rc = lib().ir_paged_prefill_order(
+        buf = torch.empty(n, dtype=torch.uint8, device=dev)
+    if buf.dtype != torch.uint8 or buf.data_ptr() % 256:
+        raise RuntimeError("prefill_plan: buf must be a 256-byte aligned uint8 tensor")
+    rc = lib().ir_paged_prefill_plan(
         ptr(cu_seqlens_q), ptr(q_start), b, int(total_q), int(max_q_len), int(max_blocks), int(block_size),
-        num_q_heads, num_kv_heads, ptr(order), n, stream_ptr(dev),
+        num_q_heads, num_kv_heads, head_dim, ptr(buf), buf.numel(), stream_ptr(dev),
     )
-    check(rc, "ir_paged_prefill_order")
-    return order
+    check(rc, "ir_paged_prefill_plan")
+    return PrefillPlan(buf, b, int(max_q_len), num_q_heads, num_kv_heads, head_dim)
 
 
 def paged_prefill(
@@ -507,7 +527,7 @@ def paged_prefill(
     scale: float,
     out: torch.Tensor | None = None,
     err_flags: torch.Tensor | None = None,
-    order: torch.Tensor | None = None,
+    plan: PrefillPlan | None = None,
 ) -> torch.Tensor:
     """Causal paged attention for packed query chunks: ``q`` ``[total_q, H_q, D]``.
 
@@ -515,7 +535,8 @@ def paged_prefill(
     ``[B+1]``); its query ``i`` is at position ``q_start[b] + i`` (int32 ``[B]``)
     and attends keys ``0..q_start[b]+i`` through ``block_tables[b]``. ``max_q_len``
     bounds the per-sequence query counts (host value, sizes the grid).
-    ``order``: the :func:`prefill_order` of this metadata (schedule only).
+    ``plan``: the :func:`prefill_plan` of this metadata and shapes (heaviest
+    work first, the heaviest items cut into merged key-range pieces).
     """
     dev = require_device(q, k_cache, v_cache, block_tables, cu_seqlens_q, q_start)
     _cache_layer("paged_prefill", k_cache)
@@ -534,18 +555,20 @@ def paged_prefill(
         if t.dtype != torch.int32 or t.shape != (n,) or not t.is_contiguous():
             raise RuntimeError(f"paged_prefill: {name} must be contiguous int32 [{n}]")
     _last_dim_contiguous("paged_prefill q", q)
-    if order is not None:
-        require_device(q, order)
-        if order.dtype != torch.int32 or order.dim() != 1 or not order.is_contiguous():
-            raise RuntimeError("paged_prefill: order must be a contiguous int32 vector")
+    if plan is not None:
+        require_device(q, plan.buf)
+        if (plan.num_seqs, plan.max_q_len, plan.num_q_heads, plan.num_kv_heads, plan.head_dim) != (
+                b, int(max_q_len), hq, h_kv, d):
+            raise RuntimeError("paged_prefill: the plan was built for other shapes")
     if out is None:
         out = torch.empty(total_q, hq, d, dtype=q.dtype, device=dev)
     rc = lib().ir_paged_prefill(
         ptr(q), q.stride(0), q.stride(1), ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
         k_cache.shape[0] // block_size, block_size, ptr(block_tables), block_tables.stride(0),
         block_tables.shape[1], ptr(cu_seqlens_q), ptr(q_start), b, total_q, int(max_q_len), ptr(out),
-        out.stride(0), out.stride(1), hq, h_kv, d, float(scale), dtype_code(q.dtype), ptr(order),
-        0 if order is None else order.numel(), ptr(err_flags), stream_ptr(dev),
+        out.stride(0), out.stride(1), hq, h_kv, d, float(scale), dtype_code(q.dtype),
+        None if plan is None else ptr(plan.buf), 0 if plan is None else plan.buf.numel(), ptr(err_flags),
+        stream_ptr(dev),
     )
     check(rc, "ir_paged_prefill")
     return out
@@ -575,9 +598,10 @@ __all__ = [
     "paged_decode",
     "paged_attention_masked",
     "paged_prefill",
-    "prefill_order",
-    "prefill_order_len",
-    "prefill_order_pays",
+    "PrefillPlan",
+    "prefill_plan",
+    "prefill_plan_bytes",
+    "prefill_plan_pays",
     "rope_kv_scatter",
     "decode_workspace_bytes",
     "default_partition",

@@ -172,10 +172,10 @@ class MixedStep:
             self.plan_buf = None
         self.plan: kernels.DecodePlan | None = None
         npre = batch.q_start.shape[0]
-        self.ordered = kernels.prefill_order_pays(npre, batch.max_q_len, hq, pool.num_kv_heads, dev)
-        self.order_buf = (torch.empty(kernels.prefill_order_len(npre, batch.max_q_len, hq, pool.num_kv_heads),
-                                      dtype=torch.int32, device=dev) if self.ordered else None)
-        self.order: torch.Tensor | None = None
+        self.ordered = kernels.prefill_plan_pays(npre, batch.max_q_len, hq, pool.num_kv_heads, dev)
+        self.plan_pre_buf = (torch.empty(kernels.prefill_plan_bytes(npre, batch.max_q_len, hq, pool.num_kv_heads, d),
+                                         dtype=torch.uint8, device=dev) if self.ordered else None)
+        self.plan_pre: kernels.PrefillPlan | None = None
         self.workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=dev) if need > 0 else None
         self.counters = torch.zeros(kernels.decode_num_counters(nd, hq, pool.num_kv_heads), dtype=torch.int32,
                                     device=dev)
@@ -200,7 +200,7 @@ class MixedStep:
         b, inp, pool = self.batch, self.inputs, self.pool
         kernels.paged_prefill(
             inp.q_pre[layer], pool.k[layer], pool.v[layer], b.pre_tables, b.cu_seqlens_q, b.q_start, b.max_q_len,
-            pool.block_size, self.scale, out=self.out_pre[layer], err_flags=self.err, order=self.order,
+            pool.block_size, self.scale, out=self.out_pre[layer], err_flags=self.err, plan=self.plan_pre,
         )
 
     def _layer(self, layer: int) -> None:
@@ -224,11 +224,12 @@ class MixedStep:
                 b.dec_tables, b.dec_ctx, self.inputs.q_dec.shape[2], self.pool.k[0], self.pool.block_size,
                 buf=self.plan_buf, err_flags=self.err,
             )
-        if self.ordered:  # one prefill work order per step, shared by every layer
+        if self.ordered:  # one prefill work plan per step, shared by every layer
             b = self.batch
-            self.order = kernels.prefill_order(
+            self.plan_pre = kernels.prefill_plan(
                 b.cu_seqlens_q, b.q_start, self.inputs.q_pre.shape[1], b.max_q_len, b.pre_tables.shape[1],
-                self.pool.block_size, self.inputs.q_pre.shape[2], self.pool.num_kv_heads, buf=self.order_buf,
+                self.pool.block_size, self.inputs.q_pre.shape[2], self.pool.num_kv_heads,
+                self.inputs.q_pre.shape[3], buf=self.plan_pre_buf,
             )
         for layer in range(self.pool.num_layers):
             self._layer(layer)

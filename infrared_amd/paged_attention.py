@@ -119,19 +119,19 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
     ):
         max_q = getattr(paged, "max_q_len", 0) or b * sq
         nseq = q_start.shape[0]
-        # heaviest-first order: built by the step's first layer, reused by the rest
-        order = getattr(paged, "prefill_order", None)
-        if order is None and kernels.prefill_order_pays(nseq, max_q, hq, h_kv, q.device):
-            order = kernels.prefill_order(
-                cu_seqlens_q, q_start, b * sq, max_q, block_tables.shape[1], pool.block_size, hq, h_kv
+        # work plan: built by the step's first layer, reused by the rest
+        plan = getattr(paged, "prefill_plan", None)
+        if plan is None and kernels.prefill_plan_pays(nseq, max_q, hq, h_kv, q.device):
+            plan = kernels.prefill_plan(
+                cu_seqlens_q, q_start, b * sq, max_q, block_tables.shape[1], pool.block_size, hq, h_kv, d
             )
             try:
-                paged.prefill_order = order
+                paged.prefill_plan = plan
             except AttributeError:  # a context object without the field keeps none
                 pass
         out = kernels.paged_prefill(
             q.reshape(b * sq, hq, d), k_layer, v_layer, block_tables, cu_seqlens_q, q_start, max_q,
-            pool.block_size, scale, err_flags=err, order=order,
+            pool.block_size, scale, err_flags=err, plan=plan,
         ).view(b, sq, hq, d)
     elif paged.use_triton and block_tables is not None and context_lens is not None and sq == 1:
         max_blocks = block_tables.shape[1]

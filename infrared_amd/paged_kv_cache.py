@@ -204,7 +204,7 @@ class PagedContext:
     packed rows ``cu[b]:cu[b+1]``), ``q_start`` ``[B]`` int32 (its cached
     prefix length) and ``max_q_len`` (host bound on the chunk sizes).
     ``decode_plan`` caches the balanced decode schedule of ``block_tables`` /
-    ``context_lens``, ``prefill_order`` the heaviest-first work order of a
+    ``context_lens``, ``prefill_plan`` the heaviest-first work plan of a
     prefill step: the step's first layer builds them, the others reuse them (a
     context is one step's metadata, shared by every layer).
     """
@@ -219,4 +219,4 @@ class PagedContext:
     q_start: torch.Tensor | None = None
     max_q_len: int = 0
     decode_plan: object | None = None
-    prefill_order: torch.Tensor | None = None
+    prefill_plan: object | None = None

@@ -12,10 +12,10 @@ Decode workloads (one query token per sequence):
 Prefill workload (``make_prefill_case``):
 
 - ``qwen7b-prefill``: 8 sequences, each a 512-token chunk after a cached
-  prefix of 16 * U{0..512} tokens (0..8192); sequences 2i and 2i+1 share the
-  prefix length and the prefix's block ids (prefix caching shares full
-  blocks), 28 q / 4 kv heads, head_dim 128, block 16, bf16, pool 1.25x the
-  distinct blocks needed.
+  prefix of U{0..8192} tokens drawn per sequence; sequences 2i and 2i+1 share
+  the block ids of the full blocks of their common prefix (prefix caching
+  shares full blocks; a partial last block stays private), 28 q / 4 kv heads,
+  head_dim 128, block 16, bf16, pool 1.25x the distinct blocks needed.
 
 Each sequence's block table is a consecutive chunk of one random permutation
 of the pool's block ids (non-contiguous physical blocks). q and the whole K/V
@@ -171,7 +171,7 @@ class PrefillConfig:
     head_dim: int
     block_size: int
     dtype: torch.dtype
-    prefix_blocks_max: int  # prefix = block_size * U{0..prefix_blocks_max}
+    prefix_max: int  # cached prefix = U{0..prefix_max} tokens, per sequence
     seed: int = 0
 
     @property
@@ -184,7 +184,7 @@ class PrefillConfig:
 
 
 PREFILL_CONFIGS: dict[str, PrefillConfig] = {
-    "qwen7b-prefill": PrefillConfig("qwen7b-prefill", 8, 512, 28, 4, 128, 16, torch.bfloat16, 512, seed=4),
+    "qwen7b-prefill": PrefillConfig("qwen7b-prefill", 8, 512, 28, 4, 128, 16, torch.bfloat16, 8192, seed=4),
 }
 
 
@@ -238,8 +238,7 @@ def make_prefill_case(
     gen = torch.Generator().manual_seed(seed)
     bs, b = cfg.block_size, cfg.num_seqs
     if prefixes is None:
-        pairs = torch.randint(0, cfg.prefix_blocks_max + 1, ((b + 1) // 2,), generator=gen)
-        prefixes = [int(pairs[i // 2]) * bs for i in range(b)]
+        prefixes = [int(x) for x in torch.randint(0, cfg.prefix_max + 1, (b,), generator=gen)]
     q_lens = [cfg.chunk] * b if q_lens is None else list(q_lens)
     if len(prefixes) != b or len(q_lens) != b:
         raise ValueError("prefixes / q_lens must have one entry per sequence")

@@ -105,19 +105,35 @@ def test_decode_plan_helpers():
     assert lib.ir_paged_decode_planned_workspace_bytes(64, 28, 4, 128) >= 256 * 16 * 128 * 4
 
 
-def test_prefill_order_helpers():
-    """A prefill work order holds one item per (sequence, query block): 8 chunks
-    of 512 tokens at 28 / 4 heads run 256-column workgroups (36 tokens of 7
-    heads, 15 blocks each); 2 chunks would leave CUs idle, so they run
-    128-column ones (18 tokens, 29 blocks). A wrong length is refused."""
+def _plan_bytes(num_seqs, max_q, n_rep, h_kv, d, cus=256):
+    """The plan layout the header documents, restated: 4-wavefront workgroups of
+    128 // n_rep query tokens (two per CU when the call has workgroups for
+    that), one entry per item plus the piece capacity (one piece per KV head of
+    every workgroup slot), the counters, and (max, sum) + D fp32 per partial
+    row of 128 columns; each region 256-byte aligned."""
+    a = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    tq = 128 // n_rep
+    nqb = -(-max_q // tq)
+    slots = 2 * cus if nqb * h_kv * num_seqs >= 2 * cus else cus
+    cap = -(-slots // h_kv)
+    rows = cap * h_kv * 128
+    return a((num_seqs * nqb + cap) * 8) + a(cap * h_kv * 4) + a(rows * 8) + a(rows * d * 4)
+
+
+def test_prefill_plan_helpers():
+    """A prefill plan's size follows its documented layout (8 chunks of 512
+    tokens at 28 / 4 heads: 29 blocks of 18 tokens each, two workgroups per CU;
+    2 chunks: one per CU), nothing is planned for empty or invalid shapes, and a
+    short plan buffer or a null pointer is refused before any device work."""
     lib = _lib.lib()
-    assert lib.ir_paged_prefill_order_len(8, 512, 28, 4) == 8 * 15
-    assert lib.ir_paged_prefill_order_len(2, 512, 28, 4) == 2 * 29
-    assert lib.ir_paged_prefill_order_len(0, 512, 28, 4) == 0
-    assert lib.ir_paged_prefill_order_len(8, 512, 28, 3) == 0
-    rc = lib.ir_paged_prefill_order(None, None, 8, 4096, 512, 600, 16, 28, 4, None, 7, None)
-    assert rc == -1 and b"order holds" in lib.ir_last_error()
-    rc = lib.ir_paged_prefill_order(None, None, 8, 4096, 512, 600, 16, 28, 4, None, 120, None)
+    assert lib.ir_paged_prefill_plan_bytes(8, 512, 28, 4, 128) == _plan_bytes(8, 512, 7, 4, 128)
+    assert lib.ir_paged_prefill_plan_bytes(2, 512, 28, 4, 64) == _plan_bytes(2, 512, 7, 4, 64)
+    assert lib.ir_paged_prefill_plan_bytes(0, 512, 28, 4, 128) == 0
+    assert lib.ir_paged_prefill_plan_bytes(8, 512, 28, 3, 128) == 0
+    assert lib.ir_paged_prefill_plan_bytes(8, 512, 28, 4, 96) == 0
+    rc = lib.ir_paged_prefill_plan(None, None, 8, 4096, 512, 600, 16, 28, 4, 128, None, 7, None)
+    assert rc == -1 and b"plan of" in lib.ir_last_error()
+    rc = lib.ir_paged_prefill_plan(None, None, 8, 4096, 512, 600, 16, 28, 4, 128, 256, 1 << 30, None)
     assert rc == -1 and b"null" in lib.ir_last_error()
 
 

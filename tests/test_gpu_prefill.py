@@ -176,47 +176,92 @@ def _host_weights(case, tq, n_qblocks):
     return w
 
 
+def _plan_geometry(b, max_q, hq, hkv):
+    """Items, entries and piece capacity of a plan: 4-wavefront workgroups of
+    128 // n_rep query tokens, two per CU when the call has workgroups for
+    that, the capacity one piece per KV head of every workgroup slot."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    tq = 128 // (hq // hkv)
+    n_qblocks = -(-max_q // tq)
+    slots = 2 * cus if n_qblocks * hkv * b >= 2 * cus else cus
+    cap = -(-slots // hkv)
+    return tq, n_qblocks, slots, cap, b * n_qblocks + cap
+
+
+def _plan_entries(plan, entries):
+    return plan.buf[: entries * 8].view(torch.int32).view(entries, 2).cpu().tolist()
+
+
 @pytest.mark.parametrize("prefixes,q_lens", [
-    (None, None),  # the full 8 x 512-token workload (8-wavefront workgroups)
+    (None, None),  # the full 8 x 512-token workload
     ([0, 37, 512, 1000, 3, 3, 0, 5], [1, 31, 100, 512, 0, 9, 64, 33]),  # ragged, one empty chunk
-    ([0, 300], [256, 77]),  # 4-wavefront workgroups
+    ([0, 300], [256, 77]),  # few workgroups: one per CU, nothing cut
+    ([9000, 0, 0, 0], [512, 40, 40, 40]),  # one very long item among short ones
 ])
-def test_prefill_order_is_a_heaviest_first_permutation(prefixes, q_lens):
-    """The device-built order lists every item with work exactly once, heaviest
-    first (non-increasing key-tile counts: the weights here are below the
-    order's 2048 buckets, so the order is exact), then -1 for the items
-    without query rows."""
-    cfg = PrefillConfig("pf-order", 8 if prefixes is None else len(prefixes), 512, 28, 4, 128, 16,
-                        torch.bfloat16, 512, seed=4)
+def test_prefill_plan_covers_every_item_heaviest_first(prefixes, q_lens):
+    """The device-built plan lists every item with work exactly once -- whole,
+    or as nparts pieces numbered 0..nparts-1 sharing one block of partial rows
+    (blocks disjoint, inside the capacity) -- pieces in non-increasing weight
+    (ceil(tiles / nparts); the weights here are below the plan's 2048 buckets,
+    so the order is exact), then (-1, 0). Items heavier than the mean load of a
+    workgroup slot x 1.5 (raised until the pieces fit the plan's capacity) are
+    cut, and no piece is heavier than that threshold."""
+    cfg = PrefillConfig("pf-plan", 8 if prefixes is None else len(prefixes), 512, 28, 4, 128, 16,
+                        torch.bfloat16, 8192, seed=4)
     case = make_prefill_case(cfg, DEV, prefixes=prefixes, q_lens=q_lens)
     b, max_q = len(case.q_lens), max(case.q_lens)
-    n = kernels.prefill_order_len(b, max_q, 28, 4)
-    # query tokens per workgroup: 256 columns of 7 heads, or 128 when 256-column
-    # workgroups would number fewer than the CUs
-    four = -(-max_q // (256 // 7)) * 4 * b < 256
-    tq = (128 if four else 256) // 7
-    n_qblocks = -(-max_q // tq)
-    assert n == b * n_qblocks
-    order = kernels.prefill_order(case.cu_seqlens_q, case.q_start, case.q.shape[0], max_q,
-                                  case.block_tables[0].shape[1], 16, 28, 4).cpu().tolist()
+    tq, n_qblocks, slots, cap, entries = _plan_geometry(b, max_q, 28, 4)
+    plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.q.shape[0], max_q,
+                                case.block_tables[0].shape[1], 16, 28, 4, 128)
+    rows = _plan_entries(plan, entries)
     w = _host_weights(case, tq, n_qblocks)
-    busy = [i for i in range(n) if w[i] >= 0]
-    assert sorted(i for i in order if i >= 0) == busy
-    assert order[len(busy):] == [-1] * (n - len(busy))
-    ws = [w[i] for i in order[: len(busy)]]
-    assert ws == sorted(ws, reverse=True)
+    total = sum(x for x in w if x > 0)
+
+    def pieces(x, t):
+        return min(16, -(-x // t)) if x > t else (1 if x >= 0 else 0)
+
+    # the cut threshold: 1.5x the mean load of a workgroup slot (at least 8
+    # tiles), raised to the smallest value whose cut pieces fit the capacity
+    thresh = max(8, -(-total * 4 * 3 // (2 * slots)))
+    while sum(pieces(x, thresh) for x in w if x > thresh) > cap:
+        thresh += 1
+    seen, blocks, piece_w = {}, set(), []
+    for item, piece in rows:
+        if item < 0:
+            continue
+        np_, part, pb = piece & 0xFF, (piece >> 8) & 0xFF, piece >> 16
+        seen.setdefault(item, []).append((np_, part, pb))
+        piece_w.append(-(-w[item] // np_))
+    used = len(piece_w)
+    assert all(item >= 0 for item, _ in rows[:used]) and rows[used:] == [[-1, 0]] * (entries - used)
+    assert sorted(seen) == [i for i in range(len(w)) if w[i] >= 0]
+    for item, parts in seen.items():
+        np_ = parts[0][0]
+        assert sorted(p for _, p, _ in parts) == list(range(np_)) and len({(n, b_) for n, _, b_ in parts}) == 1
+        if np_ > 1:
+            pb = parts[0][2]
+            assert pb + np_ <= cap and not blocks & set(range(pb, pb + np_))
+            blocks |= set(range(pb, pb + np_))
+        assert (np_ > 1) == (w[item] > thresh)
+    assert piece_w == sorted(piece_w, reverse=True)
+    assert max(piece_w) <= thresh
+    if prefixes is not None and prefixes[0] == 9000:
+        assert blocks, "the heaviest items of this workload must be cut"
 
 
-def test_prefill_order_changes_no_result_bit():
-    """The same calls with and without the heaviest-first order: identical
-    outputs and error flags (full workload, ragged chunks, a packed mixed step,
-    bad block ids)."""
+def test_prefill_plan_results_match_the_unplanned_call():
+    """The same calls with and without a plan: equal outputs (bit for bit where
+    no item is cut; within fp32 rounding of the log-sum-exp merge where one is)
+    and the same error flags -- the full workload, ragged chunks, a packed
+    mixed step, bad block ids -- and each within the bar of the oracle."""
     cases = [
         make_prefill_case("qwen7b-prefill", DEV),
         make_prefill_case("qwen7b-prefill", DEV, prefixes=[0, 37, 512, 1000, 3, 3, 0, 5],
                           q_lens=[1, 31, 100, 512, 0, 9, 64, 33]),
         make_prefill_case(PrefillConfig("pf-mixed-o", 8, 0, 28, 4, 128, 16, torch.bfloat16, 0, seed=21), DEV,
                           prefixes=[700, 1500, 99, 2047, 16, 3000, 0, 256], q_lens=[1, 1, 1, 1, 1, 1, 256, 200]),
+        make_prefill_case(PrefillConfig("pf-long", 4, 0, 28, 4, 128, 16, torch.bfloat16, 0, seed=23), DEV,
+                          prefixes=[9000, 0, 17, 0], q_lens=[512, 40, 40, 300]),
     ]
     for i, case in enumerate(cases):
         cfg = case.config
@@ -224,80 +269,92 @@ def test_prefill_order_changes_no_result_bit():
         if i == 1:
             bt[3, 5] = case.pool_blocks + 3  # a bad block id inside sequence 3's keys
         b, max_q = len(case.q_lens), max(case.q_lens)
-        order = kernels.prefill_order(case.cu_seqlens_q, case.q_start, case.q.shape[0], max_q, bt.shape[1],
-                                      cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads)
+        plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.q.shape[0], max_q, bt.shape[1],
+                                    cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim)
         outs, errs = [], []
-        for o in (None, order):
+        for pl in (None, plan):
             err = torch.zeros(1, dtype=torch.int32, device=DEV)
             outs.append(kernels.paged_prefill(case.q, case.k_cache, case.v_cache, bt, case.cu_seqlens_q,
                                               case.q_start, max_q, cfg.block_size, cfg.scale, err_flags=err,
-                                              order=o))
+                                              plan=pl))
             errs.append(err)
         torch.cuda.synchronize()
-        assert torch.equal(outs[0], outs[1]), cfg.name
         assert errs[0].item() == errs[1].item() == (ERR_BLOCK_RANGE if i == 1 else 0)
+        cut = any((piece & 0xFF) > 1 for item, piece in _plan_entries(
+            plan, _plan_geometry(b, max_q, cfg.num_q_heads, cfg.num_kv_heads)[4]) if item >= 0)
+        assert cut or i != 3, f"{cfg.name}: its heaviest items must be cut"
+        if cut:
+            assert (outs[0].float() - outs[1].float()).abs().max().item() <= TOL, cfg.name
+        else:
+            assert torch.equal(outs[0], outs[1]), cfg.name
+        if i != 1:
+            ref = O.prefill_reference(case.q.cpu(), case.k_cache.cpu(), case.v_cache.cpu(), bt.cpu(),
+                                      case.cu_seqlens_q.cpu(), case.q_start.cpu(), cfg.block_size, cfg.scale)
+            assert (outs[1].float().cpu() - ref).abs().max().item() <= TOL, cfg.name
 
 
-def test_prefill_order_length_is_checked():
+def test_prefill_plan_size_is_checked():
     case = make_prefill_case("qwen7b-prefill", DEV)
     cfg = case.config
-    wrong = torch.full((7,), -1, dtype=torch.int32, device=DEV)
-    with pytest.raises(RuntimeError, match="order holds"):
+    small = kernels.PrefillPlan(torch.empty(1024, dtype=torch.uint8, device=DEV), cfg.num_seqs, cfg.chunk,
+                                cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim)
+    with pytest.raises(RuntimeError, match="plan of"):
         kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[0], case.cu_seqlens_q,
-                              case.q_start, cfg.chunk, cfg.block_size, cfg.scale, order=wrong)
+                              case.q_start, cfg.chunk, cfg.block_size, cfg.scale, plan=small)
 
 
-_PP_CASES = {
-    "c4": ("qwen7b-prefill", None, None),
-    "ragged": ("qwen7b-prefill", [0, 37, 512, 1000, 3, 3, 0, 5], [1, 31, 100, 512, 0, 9, 64, 33]),
-    # fp16, head_dim 64, a 12-token block (general addressing path), 8-wavefront workgroups
-    "f16-bs12": (PrefillConfig("pf-pp-f16", 8, 0, 32, 8, 64, 12, torch.float16, 0, seed=31),
-                 [0, 100, 7, 300, 12, 0, 50, 1], [300, 256, 290, 200, 310, 280, 260, 299]),
-}
-
-_PP_CHILD = r"""
+_SCHED_CHILD = r"""
 import sys, torch
 sys.path.insert(0, {root!r})
 sys.path.insert(0, {tests!r})
-from test_gpu_prefill import _PP_CASES, _run
+from test_gpu_prefill import _SCHED_CASES, _run
 from infrared_amd.workloads import make_prefill_case
-name, prefixes, q_lens = _PP_CASES[{key!r}]
+name, prefixes, q_lens = _SCHED_CASES[{key!r}]
 out = _run(make_prefill_case(name, "cuda", prefixes=prefixes, q_lens=q_lens))
 torch.cuda.synchronize()
 torch.save(out.cpu(), {path!r})
-print("PINGPONG OK")
+print("SCHED OK")
 """
 
+_SCHED_CASES = {
+    "c4": ("qwen7b-prefill", None, None),
+    "ragged": ("qwen7b-prefill", [0, 37, 512, 1000, 3, 3, 0, 5], [1, 31, 100, 512, 0, 9, 64, 33]),
+    # fp16, head_dim 64, a 12-token block (general addressing path)
+    "f16-bs12": (PrefillConfig("pf-s-f16", 8, 0, 32, 8, 64, 12, torch.float16, 0, seed=31),
+                 [0, 100, 7, 300, 12, 0, 50, 1], [300, 256, 290, 200, 310, 280, 260, 299]),
+}
 
-@pytest.mark.parametrize("key", list(_PP_CASES))
-def test_prefill_ping_pong_schedule_matches_lockstep_bit_for_bit(key, tmp_path):
-    """The 8-wavefront kernel's ping-pong schedule (waves 4..7 half an
-    iteration behind 0..3) does the same arithmetic in the same order as the
-    lockstep schedule: identical outputs, and both within the bar of the
-    oracle. The schedule knob is read once per process, so the ping-pong run
-    is a child process (IR_PREFILL_PINGPONG=1) on the same seeded case."""
+
+@pytest.mark.parametrize("key", list(_SCHED_CASES))
+def test_prefill_schedules_agree_bit_for_bit(key, tmp_path):
+    """Every workgroup shape and schedule does each column's arithmetic in the
+    same order: 4-wavefront workgroups on the 2-deep ring, on the 3-deep ring
+    (next tile's scores beside this tile's exponentials) and 8-wavefront
+    workgroups give identical outputs, within the bar of the oracle. The knobs
+    are read once per process, so each shape runs in a child process."""
     import os
     import subprocess
     import sys
 
-    name, prefixes, q_lens = _PP_CASES[key]
+    name, prefixes, q_lens = _SCHED_CASES[key]
     tests = os.path.dirname(os.path.abspath(__file__))
-    path = str(tmp_path / "pp.pt")
-    res = subprocess.run(
-        [sys.executable, "-c", _PP_CHILD.format(root=os.path.dirname(tests), tests=tests, key=key, path=path)],
-        env={**os.environ, "IR_PREFILL_PINGPONG": "1"}, capture_output=True, text=True, timeout=110,
-    )
-    assert res.returncode == 0 and "PINGPONG OK" in res.stdout, res.stdout + res.stderr[-2000:]
+    outs = []
+    for i, env in enumerate(({"IR_PREFILL_RING2": "1"}, {"IR_PREFILL_RING2": "0"}, {"IR_PREFILL_WAVES": "8"})):
+        path = str(tmp_path / f"s{i}.pt")
+        res = subprocess.run(
+            [sys.executable, "-c", _SCHED_CHILD.format(root=os.path.dirname(tests), tests=tests, key=key, path=path)],
+            env={**os.environ, **env}, capture_output=True, text=True, timeout=110,
+        )
+        assert res.returncode == 0 and "SCHED OK" in res.stdout, str(env) + res.stdout + res.stderr[-2000:]
+        outs.append(torch.load(path, weights_only=True))
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     case = make_prefill_case(name, DEV, prefixes=prefixes, q_lens=q_lens)
-    lockstep = _run(case).cpu()
-    pingpong = torch.load(path, weights_only=True)
-    assert torch.equal(pingpong, lockstep)
     cfg = case.config
     ref = O.prefill_reference(
         case.q.cpu(), case.k_cache.cpu(), case.v_cache.cpu(), case.block_tables[0].cpu(),
         case.cu_seqlens_q.cpu(), case.q_start.cpu(), cfg.block_size, cfg.scale,
     )
-    assert (lockstep.float() - ref).abs().max().item() <= TOL
+    assert (outs[0].float() - ref).abs().max().item() <= TOL
 
 
 def test_prefill_flags_understated_max_q_len():
@@ -315,25 +372,30 @@ def test_prefill_flags_understated_max_q_len():
         assert bool(err.item() & ERR_CONTEXT_RANGE) == flagged, (max_q, err.item())
 
 
-def test_prefill_order_and_kernel_replay_in_a_hip_graph():
-    """A step's order build and prefill captured in one hipGraph: each of three
-    replays -- with eager work clearing the output and scribbling over the order
-    buffer in between -- equals the eager, unordered call bit for bit."""
-    case = make_prefill_case("qwen7b-prefill", DEV)
+def test_prefill_plan_and_kernel_replay_in_a_hip_graph():
+    """A step's plan build and prefill captured in one hipGraph (one 9,000-token
+    prefix among short ones, whose heaviest items are cut and merged through
+    the plan's counters): each of three replays -- with eager work clearing the
+    output and scribbling over the plan buffer in between -- equals the eager
+    planned call bit for bit."""
+    case = make_prefill_case(PrefillConfig("pf-long-g", 4, 0, 28, 4, 128, 16, torch.bfloat16, 0, seed=23), DEV,
+                             prefixes=[9000, 0, 17, 0], q_lens=[512, 40, 40, 300])
     cfg = case.config
     b, max_q = len(case.q_lens), max(case.q_lens)
-    eager = _run(case)
+    buf = torch.empty(kernels.prefill_plan_bytes(b, max_q, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim),
+                      dtype=torch.uint8, device=DEV)
     out = torch.empty_like(case.q)
-    buf = torch.empty(kernels.prefill_order_len(b, max_q, cfg.num_q_heads, cfg.num_kv_heads), dtype=torch.int32,
-                      device=DEV)
 
     def call():
-        order = kernels.prefill_order(case.cu_seqlens_q, case.q_start, case.q.shape[0], max_q,
-                                      case.block_tables[0].shape[1], cfg.block_size, cfg.num_q_heads,
-                                      cfg.num_kv_heads, buf=buf)
+        plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.q.shape[0], max_q,
+                                    case.block_tables[0].shape[1], cfg.block_size, cfg.num_q_heads,
+                                    cfg.num_kv_heads, cfg.head_dim, buf=buf)
         kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[0], case.cu_seqlens_q,
-                              case.q_start, max_q, cfg.block_size, cfg.scale, out=out, order=order)
+                              case.q_start, max_q, cfg.block_size, cfg.scale, out=out, plan=plan)
 
+    call()
+    torch.cuda.synchronize()
+    eager = out.clone()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -344,7 +406,7 @@ def test_prefill_order_and_kernel_replay_in_a_hip_graph():
         call()
     for _ in range(3):
         out.zero_()
-        buf.fill_(-7)
+        buf.fill_(7)
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()

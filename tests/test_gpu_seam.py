@@ -99,16 +99,16 @@ def test_packed_prefill_and_decode_step_through_seam(use_triton):
     assert (out[0].float().cpu() - ref).abs().max().item() <= 2e-2
 
 
-def test_prefill_step_builds_its_work_order_once():
+def test_prefill_step_builds_its_work_plan_once():
     """A prefill step whose workgroups outnumber the CUs: the first layer builds
-    the heaviest-first order and caches it on the context, the second reuses
-    it, and both layers' outputs equal the unordered kernel bit for bit and
-    match the oracle."""
+    the work plan and caches it on the context, the second reuses it, and both
+    layers' outputs equal the unplanned kernel (within the fp32 rounding of a
+    cut item's merge) and match the oracle."""
     g = torch.Generator().manual_seed(9)
     bs, h_kv, n_rep, d = 16, 4, 7, 128
     num_cached = [0, 2000, 160, 3000, 40, 40, 900, 1200]
     q_lens = [300, 300, 280, 300, 64, 300, 1, 250]
-    assert kernels.prefill_order_pays(len(q_lens), max(q_lens), h_kv * n_rep, h_kv, DEV)
+    assert kernels.prefill_plan_pays(len(q_lens), max(q_lens), h_kv * n_rep, h_kv, DEV)
     nblk = sum(metadata.blocks_for(c + n, bs) for c, n in zip(num_cached, q_lens))
     perm = torch.randperm(nblk + 10, generator=g).tolist()
     tables, off = [], 0
@@ -120,7 +120,7 @@ def test_prefill_step_builds_its_work_order_once():
     pool.k.normal_()
     pool.v.normal_()
     paged, _ = metadata.prefill_context(pool, tables, num_cached, q_lens)
-    assert paged.prefill_order is None
+    assert paged.prefill_plan is None
     total = sum(q_lens)
     for layer in range(2):
         q = torch.randn(1, total, h_kv * n_rep, d, device=DEV).to(torch.bfloat16)
@@ -128,12 +128,12 @@ def test_prefill_step_builds_its_work_order_once():
         v = torch.randn(1, total, h_kv, d, device=DEV).to(torch.bfloat16)
         out = paged_attention(q, k, v, paged, None, layer, d**-0.5, n_rep)
         if layer == 0:
-            order = paged.prefill_order
-            assert order is not None
-        assert paged.prefill_order is order
+            plan = paged.prefill_plan
+            assert plan is not None
+        assert paged.prefill_plan is plan
         plain = kernels.paged_prefill(q[0], pool.k[layer], pool.v[layer], paged.block_tables, paged.cu_seqlens_q,
                                       paged.q_start, paged.max_q_len, bs, d**-0.5)
-        assert torch.equal(out[0], plain)
+        assert (out[0].float() - plain.float()).abs().max().item() <= 2e-2
         bt = metadata.block_tables_tensor(tables, "cpu")
         ref = O.prefill_reference(q[0].cpu(), pool.k[layer].cpu(), pool.v[layer].cpu(), bt,
                                   paged.cu_seqlens_q.cpu(), num_cached, bs, d**-0.5)
