@@ -34,7 +34,9 @@ of 224 decode rows (context U{256..4096}) + 4 x 256-token prefill chunks
 per step; ``rope`` -- the fused rotary embedding + KV scatter of one such step's
 layer (1,248 new tokens, 28 q / 4 kv heads), value in GB/s of algorithmic bytes;
 ``engine`` -- the engine ladder rows (+HIP paged-attn, +hipGraph): a decode-heavy
-burst through the seam with an attention-only model, value in output tok/s.
+burst through the seam with an attention-only model, value in output tok/s;
+``reference-form`` -- the headline decode with the metadata unchanged reference
+callers pass (gather_slots + mask), value in us per call.
 
 Prints one JSON line: value = achieved KV GB/s (algorithmic bytes sum(ctx) *
 2 * H_kv * D * 2 per call / time per call), plus us_per_call, a roofline
@@ -64,7 +66,8 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--workload", choices=("decode", "prefill", "mixed", "rope", "engine"), default="decode")
+    p.add_argument("--workload", choices=("decode", "prefill", "mixed", "rope", "engine", "reference-form"),
+                   default="decode")
     p.add_argument("--engine-batch", type=int, default=8, help="engine: sequences in the burst (max_batch)")
     p.add_argument("--config", default=None, help="decode: qwen7b-bf16 (default) | qwen0.5b-fp32 | qwen7b-skewed")
     p.add_argument("--rotations", type=int, default=3)
@@ -708,6 +711,101 @@ def _bench_engine(args) -> dict:
     }
 
 
+def _bench_reference_form(args) -> dict:
+    """Unchanged reference callers at the Qwen2.5-7B decode shape: each step's
+    metadata in the reference engine's own form (``gather_slots [B, T]`` +
+    additive mask, ``infrared/engine/paged_engine.py:290-332``, no block
+    tables) through ``paged_attention`` for ``--layers`` layers (KV write +
+    attention per layer, eager launches). Rows: the seam recognising the decode
+    form (one check per step) and running the block-table kernels; the same
+    step with block-table fields filled by the caller; and the mask kernel
+    reading gather_slots + mask as given (``use_triton=False``)."""
+    from dataclasses import dataclass
+
+    from infrared_amd import PagedContext, PagedKVPool, kernels, metadata, paged_attention
+    from infrared_amd.workloads import make_decode_case
+
+    @dataclass(slots=True)
+    class RefContext:  # the reference's PagedContext fields only
+        pool: object
+        write_slots: torch.Tensor
+        gather_slots: torch.Tensor
+        use_triton: bool = True
+
+    case = make_decode_case("qwen7b-bf16", "cuda")
+    cfg = case.config
+    b, hq, hkv, d, bs = cfg.num_seqs, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
+    pool = PagedKVPool(1, case.pool_blocks, bs, hkv, d, cfg.dtype, device="cuda")
+    pool.k[0].copy_(case.k_cache)
+    pool.v[0].copy_(case.v_cache)
+    ctx = case.context_lens.cpu().tolist()
+    tables = [row[: -(-c // bs)].tolist() for row, c in zip(case.block_tables[0].cpu(), ctx)]
+    ours, mask = metadata.decode_context(pool, tables, [c - 1 for c in ctx])
+    g = torch.Generator(device="cuda").manual_seed(2)
+    q = torch.randn(b, 1, hq, d, generator=g, device="cuda").to(cfg.dtype)
+    k = torch.randn(b, 1, hkv, d, generator=g, device="cuda").to(cfg.dtype)
+    v = torch.randn(b, 1, hkv, d, generator=g, device="cuda").to(cfg.dtype)
+    layers, steps = args.layers, 5
+
+    def step_ref():
+        # a step's metadata arrives as new tensors, as the reference engine builds them
+        gs, m = ours.gather_slots.clone(), mask.clone()
+        paged = RefContext(pool, ours.write_slots, gs)
+        for _ in range(layers):
+            paged_attention(q, k, v, paged, m, 0, cfg.scale, cfg.n_rep)
+
+    def step_ours():
+        paged = PagedContext(pool, ours.write_slots, ours.gather_slots, True, ours.block_tables, ours.context_lens)
+        for _ in range(layers):
+            paged_attention(q, k, v, paged, mask, 0, cfg.scale, cfg.n_rep)
+
+    def step_masked():
+        paged = RefContext(pool, ours.write_slots, ours.gather_slots, use_triton=False)
+        for _ in range(layers):
+            paged_attention(q, k, v, paged, mask, 0, cfg.scale, cfg.n_rep)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        per = []
+        for _ in range(steps):
+            s.record()
+            fn()
+            e.record()
+            torch.cuda.synchronize()
+            per.append(s.elapsed_time(e) / layers)
+        return statistics.median(per)
+
+    ms_ref, ms_ours, ms_masked = timed(step_ref), timed(step_ours), timed(step_masked)
+    form = pool._ref_form[2]
+    out_ref = paged_attention(q, k, v, RefContext(pool, ours.write_slots, ours.gather_slots), mask, 0, cfg.scale,
+                              cfg.n_rep)
+    out_ours = paged_attention(q, k, v, PagedContext(pool, ours.write_slots, ours.gather_slots, True,
+                                                     ours.block_tables, ours.context_lens), mask, 0, cfg.scale,
+                               cfg.n_rep)
+    torch.cuda.synchronize()
+    kv = case.kv_bytes
+    return {
+        "metric": "paged decode attn us/call for unchanged reference callers (gather_slots + mask), Qwen2.5-7B shape",
+        "value": round(ms_ref * 1e3, 2), "unit": "us/call", "ms_per_step": round(ms_ref * layers, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{cfg.name} decode in the reference's metadata form: {b} seqs, {hq}q/{hkv}kv heads, "
+                   f"head_dim {d}, block {bs}, gather_slots {tuple(ours.gather_slots.shape)}, {layers} layers per step "
+                   "(KV write + attention per layer), eager",
+                   "decode_form_recognised": form is not None,
+                   "equal_to_block_table_path": bool(torch.equal(out_ref, out_ours)),
+                   "rows_us_per_call": {"reference form, recognised (one check per step)": round(ms_ref * 1e3, 2),
+                                        "block-table fields from the caller": round(ms_ours * 1e3, 2),
+                                        "mask kernel on gather_slots + mask": round(ms_masked * 1e3, 2)},
+                   "kv_bytes_per_call": kv},
+        "roofline": {"bound": "hbm", "achieved": round(kv / (ms_ref * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(kv / (ms_ref * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "timed": "whole call (KV write + attention, eager launches, the step's check amortised)"},
+        "cpu_baseline": None,
+    }
+
+
 def _measured_peak(bound: str) -> dict:
     """The roof the kernel is held against, measured on this device beside the
     published figure. HBM-bound kernels: a read-only stream of 4 GiB with the
@@ -793,7 +891,7 @@ def main() -> int:
         return 2
     if args.workload != "decode":
         line = {"prefill": _bench_prefill, "mixed": _bench_mixed, "rope": _bench_rope,
-                "engine": _bench_engine}[args.workload](args)
+                "engine": _bench_engine, "reference-form": _bench_reference_form}[args.workload](args)
         line.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "timing": dict(_REPLAY_STATS)})
         print(json.dumps(line), flush=True)
         return 0

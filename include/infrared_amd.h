@@ -270,6 +270,28 @@ int ir_paged_attention_masked(const void* q, int64_t q_b_stride, int64_t q_s_str
                               int dtype, int32_t* err_flags, ir_stream_t stream);
 
 /*
+ * Block tables from the reference engine's own decode metadata, so unchanged
+ * callers of the seam reach the block-table decode kernels. The reference's
+ * eager decode passes gather_slots[i, p] = bt_i[p / bs] * bs + p % bs (0 past
+ * ctx_i) and the mask 0 for p < ctx_i, finfo.min after
+ * (infrared/engine/paged_engine.py:306-314, :630-638, via PagedContext,
+ * infrared/cache/paged_kv_cache.py:75-91). Writes context_lens[i] (the mask's
+ * zeros) and block_tables[i, j] = gather_slots[i, j * bs] / bs (0 past the
+ * context), and ORs 1 into *bad unless the metadata has exactly that form: the
+ * zeros a prefix, later mask values <= -6e4, every slot below ctx_i the closed
+ * form, every block id in [0, num_blocks). With *bad clear the decode kernels
+ * over these tables compute what ir_paged_attention_masked computes.
+ *   gather_slots: [batch, seq_k] int64 (strides b, t); mask: element (b, t) at
+ *   mask + b*mask_b_stride + t*mask_t_stride, dtype mask_dtype.
+ *   block_tables: [batch, bt_stride] int32, max_blocks_per_seq >= ceil(seq_k / bs).
+ */
+int ir_decode_form(const int64_t* gather_slots, int64_t gs_b_stride, int64_t gs_t_stride,
+                   const void* mask, int64_t mask_b_stride, int64_t mask_t_stride, int mask_dtype,
+                   int batch, int seq_k, int block_size, int64_t num_blocks, int32_t* block_tables,
+                   int64_t bt_stride, int max_blocks_per_seq, int32_t* context_lens, int32_t* bad,
+                   ir_stream_t stream);
+
+/*
  * Chunked prefill / prefix-hit prefill / packed mixed step over block tables
  * (16-bit dtypes, MFMA). Replaces the Sq > 1 uses of
  * _paged_attention_triton / _paged_attention_naive

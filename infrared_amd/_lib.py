@@ -93,6 +93,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_f32,
          _c_i32, _c_p, _c_i64, _c_p, _c_p],
     ),
+    "ir_decode_form": (
+        _c_i32,
+        [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_p, _c_i64,
+         _c_i32, _c_p, _c_p, _c_p],
+    ),
     "ir_hbm_read_granule": (_c_i64, []),
     "ir_hbm_read": (_c_i32, [_c_p, _c_i64, _c_p, _c_i32, _c_p]),
     "ir_paged_prefill_plan_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),

@@ -1,0 +1,94 @@
+// Block tables from the reference engine's decode metadata.
+//
+// The reference's eager decode hands the attention seam per-key slots and an
+// additive mask (infrared/engine/paged_engine.py:306-314, :630-638):
+//   gather_slots[i, p] = bt_i[p / bs] * bs + p % bs   for p < ctx_i (0 after),
+//   mask[i, 0, 0, p]   = 0 for p < ctx_i, finfo(dtype).min after.
+// One workgroup per sequence recovers ctx_i (the mask's zeros) and bt_i[j] =
+// gather_slots[i, j * bs] / bs, and verifies the form exactly: the zeros are a
+// prefix, every later mask value is at most -6e4 (masked in any dtype, fp16's
+// finfo.min included), every slot below ctx_i follows the closed form and
+// every block id lies in the pool. Any violation sets *bad; the host then
+// keeps the mask kernel, which reads the metadata as given.
+#include "common.hpp"
+#include "status.hpp"
+
+namespace ir {
+namespace {
+
+constexpr int kFormThreads = 256;
+
+__device__ __forceinline__ float mask_at(const void* m, int dtype, int64_t off) {
+  if (dtype == IR_DTYPE_F32) return ((const float*)m)[off];
+  const uint32_t h = ((const uint16_t*)m)[off];
+  return dtype == IR_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+
+__global__ __launch_bounds__(kFormThreads) void decode_form_kernel(const int64_t* gs, int64_t gs_b, int64_t gs_t,
+                                                                   const void* mask, int64_t m_b, int64_t m_t,
+                                                                   int mask_dtype, int T, int bs, int64_t num_blocks,
+                                                                   int32_t* bt, int64_t bt_stride, int width,
+                                                                   int32_t* ctx_out, int32_t* bad) {
+  __shared__ int s_zeros, s_first, s_bad;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  if (tid == 0) {
+    s_zeros = 0;
+    s_first = T;
+    s_bad = 0;
+  }
+  __syncthreads();
+  const int64_t* g = gs + (int64_t)b * gs_b;
+  const int64_t mrow = (int64_t)b * m_b;
+  int zeros = 0, first = T, wrong = 0;
+  for (int t = tid; t < T; t += kFormThreads) {
+    const float x = mask_at(mask, mask_dtype, mrow + (int64_t)t * m_t);
+    if (x == 0.f) {
+      ++zeros;
+    } else {
+      first = min(first, t);
+      wrong |= !(x <= -6e4f);
+    }
+  }
+  atomicAdd(&s_zeros, zeros);
+  atomicMin(&s_first, first);
+  if (wrong) s_bad = 1;
+  __syncthreads();
+  const int ctx = s_zeros;
+  if (s_first < ctx) s_bad = 1;  // a masked key before the last visible one
+  for (int t = tid; t < ctx; t += kFormThreads) {
+    const int64_t head = g[(int64_t)(t / bs) * bs * gs_t];
+    const int64_t id = head / bs;
+    if (head < 0 || head % bs != 0 || id >= num_blocks || g[(int64_t)t * gs_t] != id * bs + t % bs) s_bad = 1;
+  }
+  for (int j = tid; j < width; j += kFormThreads) {
+    const int p = j * bs;
+    bt[(int64_t)b * bt_stride + j] = p < ctx ? (int32_t)(g[(int64_t)p * gs_t] / bs) : 0;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    ctx_out[b] = ctx;
+    if (s_bad) atomicOr(bad, 1);
+  }
+}
+
+}  // namespace
+}  // namespace ir
+
+using namespace ir;
+
+extern "C" int ir_decode_form(const int64_t* gather_slots, int64_t gs_b_stride, int64_t gs_t_stride,
+                              const void* mask, int64_t mask_b_stride, int64_t mask_t_stride, int mask_dtype,
+                              int batch, int seq_k, int block_size, int64_t num_blocks, int32_t* block_tables,
+                              int64_t bt_stride, int max_blocks_per_seq, int32_t* context_lens, int32_t* bad,
+                              ir_stream_t stream) {
+  IR_REQUIRE(dtype_bytes(mask_dtype) > 0, "ir_decode_form: unknown mask dtype %d", mask_dtype);
+  IR_REQUIRE(batch >= 0 && seq_k >= 0 && block_size > 0 && num_blocks >= 0, "ir_decode_form: bad sizes");
+  IR_REQUIRE(max_blocks_per_seq >= (seq_k + block_size - 1) / block_size && bt_stride >= max_blocks_per_seq,
+             "ir_decode_form: block tables of %d ids cannot hold %d keys", max_blocks_per_seq, seq_k);
+  if (batch == 0) return ok();
+  IR_REQUIRE(gather_slots && mask && block_tables && context_lens && bad, "ir_decode_form: null pointer");
+  hipLaunchKernelGGL(decode_form_kernel, dim3(batch), dim3(kFormThreads), 0, (hipStream_t)stream, gather_slots,
+                     gs_b_stride, gs_t_stride, mask, mask_b_stride, mask_t_stride, mask_dtype, seq_k, block_size,
+                     num_blocks, block_tables, bt_stride, max_blocks_per_seq, context_lens, bad);
+  return check_launch("ir_decode_form");
+}

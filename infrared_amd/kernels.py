@@ -574,6 +574,31 @@ def paged_prefill(
     return out
 
 
+def decode_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int, num_blocks: int
+                ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Block tables ``[B, ceil(T / bs)]`` int32 and context lengths ``[B]`` int32
+    from the reference's decode metadata (``gather_slots`` ``[B, T]`` int64, mask
+    ``[B, 1, 1, T]``), plus an int32 flag, nonzero unless the metadata has the
+    reference engine's decode form exactly (``ir_decode_form``)."""
+    dev = require_device(gather_slots, mask)
+    if gather_slots.dtype != torch.int64 or gather_slots.dim() != 2:
+        raise RuntimeError("decode_form: gather_slots must be int64 [B, T]")
+    b, t = gather_slots.shape
+    if mask.dim() != 4 or mask.shape[0] != b or mask.shape[1] != 1 or mask.shape[2] != 1 or mask.shape[3] != t:
+        raise RuntimeError(f"decode_form: mask must be [B, 1, 1, T], got {tuple(mask.shape)}")
+    width = max(-(-t // block_size), 1)
+    bt = torch.empty(b, width, dtype=torch.int32, device=dev)
+    ctx = torch.empty(b, dtype=torch.int32, device=dev)
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    rc = lib().ir_decode_form(
+        ptr(gather_slots), gather_slots.stride(0), gather_slots.stride(1), ptr(mask), mask.stride(0),
+        mask.stride(3), dtype_code(mask.dtype), b, t, block_size, num_blocks, ptr(bt), bt.stride(0), width,
+        ptr(ctx), ptr(bad), stream_ptr(dev),
+    )
+    check(rc, "ir_decode_form")
+    return bt, ctx, bad
+
+
 def hbm_read(src: torch.Tensor, sink: torch.Tensor, workgroups: int = 0) -> None:
     """Reads all of ``src`` (contiguous, a multiple of :func:`hbm_read_granule`
     bytes) with the decode kernels' load form and discards it: timing it gives

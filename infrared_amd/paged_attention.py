@@ -19,6 +19,12 @@ calls once per layer (``infrared/model/layers.py:178-180``):
      log-sum-exp reduce) over the block tables; the mask is then implied by
      ``context_lens`` (key ``t`` valid iff ``t < context_lens[b]``, the decode
      mask of ``infrared/engine/paged_engine.py:630-638``);
+   - otherwise, for a one-token decode whose ``gather_slots`` + ``mask`` have
+     the reference engine's decode form (``gather_slots[i, p] = bt[p // bs] *
+     bs + p % bs`` and mask 0 then ``finfo.min``,
+     ``infrared/engine/paged_engine.py:306-314, 630-638``): the same decode
+     kernels over block tables derived from them on the device (checked once
+     per step, ``PagedKVPool.reference_decode_form``);
    - otherwise: the kernel that reads ``gather_slots`` + the additive ``mask``
      exactly as the reference's naive path does
      (``infrared/model/triton_attention.py:110-129``).
@@ -134,47 +140,65 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
             pool.block_size, scale, err_flags=err, plan=plan,
         ).view(b, sq, hq, d)
     elif paged.use_triton and block_tables is not None and context_lens is not None and sq == 1:
-        max_blocks = block_tables.shape[1]
-        if hasattr(pool, "plan_buffer") and kernels.decode_plan_pays(b, hq, h_kv, max_blocks, pool.block_size,
-                                                                      q.device):
-            # balanced schedule: built by the step's first layer, reused by the
-            # rest -- unless another context's plan has since taken the pool's
-            # plan buffer (two decode contexts run interleaved), then rebuilt
-            plan = paged.decode_plan
-            if plan is None or getattr(pool, "plan_owner", plan) is not plan:
-                plan_bytes = kernels.decode_plan_bytes(b, hq, h_kv, max_blocks, pool.block_size)
-                plan = kernels.decode_plan(
-                    block_tables, context_lens, hq, k_layer, pool.block_size,
-                    buf=pool.plan_buffer(plan_bytes), err_flags=err,
-                )
-                paged.decode_plan = plan
-                pool.plan_owner = plan
-            ws = pool.workspace(kernels.planned_workspace_bytes(b, hq, h_kv, d))
-            ctr = pool.decode_counters(kernels.decode_num_counters(b, hq, h_kv))
-            out = kernels.paged_decode_planned(
-                q.reshape(b, hq, d), k_layer, v_layer, plan, scale, workspace=ws, err_flags=err, counters=ctr
-            )
-        else:
-            ws = ctr = None
-            if hasattr(pool, "workspace"):
-                need = kernels.decode_workspace_bytes(b, hq, h_kv, d, max_blocks, pool.block_size)
-                if need > 0:
-                    ws = pool.workspace(need)
-                    ctr = pool.decode_counters(kernels.decode_num_counters(b, hq, h_kv))
-            out = kernels.paged_decode(
-                q.reshape(b, hq, d), k_layer, v_layer, block_tables, context_lens,
-                pool.block_size, scale, workspace=ws, err_flags=err, counters=ctr,
-            )
-        out = out.view(b, 1, hq, d)
+        out = _decode(q, pool, layer_idx, block_tables, context_lens, paged, scale, err)
     else:
         if paged.gather_slots is None or mask is None:
             raise RuntimeError(
                 "paged_attention: gather_slots and mask are required unless block_tables/"
                 "context_lens drive a single-token decode"
             )
-        out = kernels.paged_attention_masked(
-            q, k_layer, v_layer, paged.gather_slots, mask, scale, err_flags=err
-        )
+        form = None
+        if paged.use_triton and sq == 1 and hasattr(pool, "reference_decode_form"):
+            # the reference's own decode metadata (gather_slots + mask, no block
+            # tables): when it has the decode form, run the block-table kernels
+            form = pool.reference_decode_form(paged.gather_slots, mask)
+        if form is not None:
+            out = _decode(q, pool, layer_idx, form.block_tables, form.context_lens, form, scale, err)
+        else:
+            out = kernels.paged_attention_masked(
+                q, k_layer, v_layer, paged.gather_slots, mask, scale, err_flags=err
+            )
     if getattr(pool, "strict", False):
         pool.check_errors()
     return out
+
+
+def _decode(q, pool, layer_idx: int, block_tables, context_lens, holder, scale: float, err) -> torch.Tensor:
+    """One-token decode over block tables: the balanced plan when the batch fills
+    the device (cached on ``holder.decode_plan`` for the step's other layers),
+    else the fixed split-KV partitions. Returns ``[B, 1, H_q, D]``."""
+    b, _, hq, d = q.shape
+    h_kv = pool.k.shape[-2]
+    k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
+    max_blocks = block_tables.shape[1]
+    if hasattr(pool, "plan_buffer") and kernels.decode_plan_pays(b, hq, h_kv, max_blocks, pool.block_size, q.device):
+        # balanced schedule: built by the step's first layer, reused by the
+        # rest -- unless another context's plan has since taken the pool's
+        # plan buffer (two decode contexts run interleaved), then rebuilt
+        plan = holder.decode_plan
+        if plan is None or getattr(pool, "plan_owner", plan) is not plan:
+            plan_bytes = kernels.decode_plan_bytes(b, hq, h_kv, max_blocks, pool.block_size)
+            plan = kernels.decode_plan(
+                block_tables, context_lens, hq, k_layer, pool.block_size,
+                buf=pool.plan_buffer(plan_bytes), err_flags=err,
+            )
+            holder.decode_plan = plan
+            pool.plan_owner = plan
+        ws = pool.workspace(kernels.planned_workspace_bytes(b, hq, h_kv, d))
+        ctr = pool.decode_counters(kernels.decode_num_counters(b, hq, h_kv))
+        out = kernels.paged_decode_planned(
+            q.reshape(b, hq, d), k_layer, v_layer, plan, scale, workspace=ws, err_flags=err, counters=ctr
+        )
+    else:
+        ws = ctr = None
+        if hasattr(pool, "workspace"):
+            need = kernels.decode_workspace_bytes(b, hq, h_kv, d, max_blocks, pool.block_size)
+            if need > 0:
+                ws = pool.workspace(need)
+                ctr = pool.decode_counters(kernels.decode_num_counters(b, hq, h_kv))
+        out = kernels.paged_decode(
+            q.reshape(b, hq, d), k_layer, v_layer, block_tables, context_lens,
+            pool.block_size, scale, workspace=ws, err_flags=err, counters=ctr,
+        )
+    return out.view(b, 1, hq, d)
+

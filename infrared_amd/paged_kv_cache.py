@@ -105,6 +105,8 @@ class PagedKVPool:
         # the decode plan whose schedule plan_buffer() holds now: a context
         # whose cached plan is not this one was overwritten and rebuilds it
         self.plan_owner: object | None = None
+        # (gather_slots, mask, derived form) of the last reference-form check
+        self._ref_form: tuple | None = None
 
     # --- reference surface ------------------------------------------------
 
@@ -176,6 +178,39 @@ class PagedKVPool:
             self._plan_buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
         return self._plan_buf
 
+    def reference_decode_form(self, gather_slots: torch.Tensor, mask: torch.Tensor) -> _DecodeForm | None:
+        """Block tables for the reference engine's decode metadata, if it has the
+        decode form; else ``None`` (the caller runs the mask kernel).
+
+        The reference's eager decode builds ``gather_slots[i, p] = bt_i[p // bs]
+        * bs + p % bs`` for ``p < ctx_i`` (0 after) and an additive mask of 0 for
+        ``p < ctx_i`` and ``finfo(dtype).min`` after
+        (``infrared/engine/paged_engine.py:306-314, 630-638``). Derived on the
+        device by ``ir_decode_form`` -- ``bt_i[j] = gather_slots[i, j * bs] //
+        bs``, ``ctx_i`` = the mask's zeros -- and verified exactly: every slot
+        below ``ctx_i`` follows the closed form, the zeros are a prefix, and
+        every later mask value is at most -6e4 (masked in any dtype, fp16's
+        ``finfo.min`` included), so the decode kernels compute what the mask
+        kernel would. The check costs one launch and one synchronising read of
+        its flag; the result is cached for the step's other layers (same
+        ``gather_slots`` and ``mask`` tensors). Under hipGraph capture no read is
+        possible, so ``None`` is returned and the mask kernel runs.
+        """
+        c = self._ref_form
+        if c is not None and c[0] is gather_slots and c[1] is mask:
+            return c[2]
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        form = None
+        if (gather_slots.dim() == 2 and gather_slots.dtype == torch.int64 and gather_slots.is_cuda and mask.is_cuda
+                and mask.dim() == 4 and tuple(mask.shape[:3]) == (gather_slots.shape[0], 1, 1)
+                and mask.shape[3] == gather_slots.shape[1]):
+            bt, ctx, bad = kernels.decode_form(gather_slots, mask, self.block_size, self.num_blocks)
+            if int(bad.item()) == 0:
+                form = _DecodeForm(bt, ctx)
+        self._ref_form = (gather_slots, mask, form)
+        return form
+
     def check_errors(self) -> None:
         """Synchronises, raises ``IndexError`` for any flagged range error, then clears the flags."""
         flags = int(self.err_flags.item())
@@ -183,6 +218,16 @@ class PagedKVPool:
             self.err_flags.zero_()
             names = [n for bit, n in _ERR_NAMES.items() if flags & bit]
             raise IndexError("paged kernels flagged: " + ", ".join(names))
+
+
+@dataclass(slots=True)
+class _DecodeForm:
+    """Block tables and context lengths derived from reference decode metadata,
+    with the step's decode plan once built."""
+
+    block_tables: torch.Tensor
+    context_lens: torch.Tensor
+    decode_plan: object | None = None
 
 
 @dataclass(slots=True)

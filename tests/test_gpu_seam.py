@@ -4,6 +4,8 @@ pool's write/gather surface, and hipGraph capture/replay of a decode step."""
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import pytest
 import torch
 
@@ -270,3 +272,79 @@ def test_hip_graph_smaller_bucket_after_buffer_growth():
         torch.cuda.synchronize()
         assert torch.equal(got, ref), f"bucket-4 replay {it} after growth differs from eager"
     assert all(int(f.min()) == 1 and int(f.max()) == 1 for f in filler), "a replay wrote into freed memory"
+
+
+@dataclass(slots=True)
+class _ReferenceContext:
+    """The reference's own PagedContext shape (infrared/cache/paged_kv_cache.py:75-91):
+    no block-table fields, no room for any."""
+
+    pool: PagedKVPool
+    write_slots: torch.Tensor
+    gather_slots: torch.Tensor
+    use_triton: bool = True
+
+
+@pytest.mark.parametrize("num_seqs", [4, 64])  # fixed partitions / planned schedule
+def test_reference_decode_metadata_runs_the_block_table_kernels(num_seqs):
+    """Unchanged reference callers pass only gather_slots + the decode mask. Their
+    decode form is recognised (once per step: later layers reuse the derived
+    tables), and every layer equals the block-table context's output bit for
+    bit -- the same kernels on the same tables -- and the oracle."""
+    bs, h_kv, n_rep, d, layers = 16, 4, 7, 128, 3
+    g = torch.Generator().manual_seed(12)
+    num_cached = [int(x) for x in torch.randint(0, 1500, (num_seqs,), generator=g)]
+    tables = [list(range(i * 96, i * 96 + 96)) for i in range(num_seqs)]
+    pool = PagedKVPool(layers, num_seqs * 96, bs, h_kv, d, torch.bfloat16, device=DEV)
+    pool.k.normal_()
+    pool.v.normal_()
+    ours, mask = metadata.decode_context(pool, tables, num_cached)
+    ref = _ReferenceContext(pool, ours.write_slots, ours.gather_slots)
+    dgen = torch.Generator(device=DEV).manual_seed(1)
+    forms = []
+    for layer in range(layers):
+        q = torch.randn(num_seqs, 1, h_kv * n_rep, d, generator=dgen, device=DEV).bfloat16()
+        k = torch.randn(num_seqs, 1, h_kv, d, generator=dgen, device=DEV).bfloat16()
+        v = torch.randn(num_seqs, 1, h_kv, d, generator=dgen, device=DEV).bfloat16()
+        got = paged_attention(q, k, v, ref, mask, layer, d**-0.5, n_rep)
+        forms.append(pool._ref_form[2])
+        want = paged_attention(q, k, v, ours, mask, layer, d**-0.5, n_rep)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"layer {layer}"
+        assert (forms[-1].decode_plan is not None) == (num_seqs == 64)
+        expect = O.decode_reference(q[:, 0].cpu(), pool.k[layer].cpu(), pool.v[layer].cpu(),
+                                    ours.block_tables.cpu(), ours.context_lens.cpu(), bs, d**-0.5)
+        assert (got[:, 0].float().cpu() - expect).abs().max().item() <= 2e-2
+    assert forms[0] is not None and all(f is forms[0] for f in forms)
+    assert torch.equal(forms[0].context_lens, ours.context_lens)
+    for i, c in enumerate(ours.context_lens.tolist()):  # (entries past a context are never read)
+        n = -(-c // bs)
+        assert torch.equal(forms[0].block_tables[i, :n], ours.block_tables[i, :n])
+
+
+def test_reference_metadata_outside_the_decode_form_takes_the_mask_kernel():
+    """A mask that hides a key inside the context, or slots that do not follow
+    the block-table closed form, is not the decode form: the call reads
+    gather_slots + mask as given (mask kernel) and matches the oracle's naive
+    path on exactly that metadata."""
+    bs, h_kv, n_rep, d = 16, 2, 4, 64
+    num_cached = [40, 75, 3]
+    tables = [list(range(i * 8, i * 8 + 8)) for i in range(3)]
+    pool = PagedKVPool(1, 24, bs, h_kv, d, torch.float32, device=DEV)
+    pool.k.normal_()
+    pool.v.normal_()
+    ours, mask = metadata.decode_context(pool, tables, num_cached)
+    holed = mask.clone()
+    holed[1, 0, 0, 10] = torch.finfo(torch.float32).min
+    swapped = ours.gather_slots.clone()
+    swapped[0, [3, 4]] = swapped[0, [4, 3]]
+    for gs, m in ((ours.gather_slots, holed), (swapped, mask)):
+        ref = _ReferenceContext(pool, ours.write_slots, gs)
+        q = torch.randn(3, 1, h_kv * n_rep, d, device=DEV)
+        k = torch.randn(3, 1, h_kv, d, device=DEV)
+        v = torch.randn(3, 1, h_kv, d, device=DEV)
+        got = paged_attention(q, k, v, ref, m, 0, d**-0.5, n_rep)
+        torch.cuda.synchronize()
+        assert pool._ref_form[2] is None
+        expect = O.paged_attention_naive(q.cpu(), pool.k[0].cpu(), pool.v[0].cpu(), gs.cpu(), m.cpu(), d**-0.5, n_rep)
+        assert (got.cpu() - expect).abs().max().item() <= 1e-4
