@@ -21,6 +21,7 @@ from __future__ import annotations
 
 from collections.abc import Sequence
 
+import numpy as np
 import torch
 
 from infrared_amd.paged_kv_cache import PagedContext, PagedKVPool
@@ -40,12 +41,34 @@ def block_tables_tensor(
     block_tables: Sequence[Sequence[int]], device: torch.device | str, width: int | None = None
 ) -> torch.Tensor:
     """``[B, width]`` int32, rows right-padded with block 0 (entries past a row's
-    context are never read)."""
-    w = max((len(r) for r in block_tables), default=0) if width is None else width
-    if any(len(r) > w for r in block_tables):
+    context are never read). Rows are copied whole into one host array (one
+    copy per row, not per block id) and moved to the device at once."""
+    lens = [len(r) for r in block_tables]
+    w = max(lens, default=0) if width is None else width
+    if any(n > w for n in lens):
         raise ValueError(f"a block table is longer than width {w}")
-    rows = [list(r) + [0] * (w - len(r)) for r in block_tables]
-    return torch.tensor(rows, dtype=torch.int32).reshape(len(rows), w).to(device)
+    arr = np.zeros((len(lens), w), dtype=np.int32)
+    for i, (r, n) in enumerate(zip(block_tables, lens)):
+        if n:
+            arr[i, :n] = r
+    return torch.from_numpy(arr).to(device)
+
+
+def packed_write_slots(
+    block_tables: torch.Tensor, num_cached: torch.Tensor, q_lens: torch.Tensor, block_size: int
+) -> torch.Tensor:
+    """``[sum(q_lens)]`` int64 slots of a packed step's new tokens, in packing
+    order: sequence ``b``'s ``q_lens[b]`` tokens at positions ``num_cached[b] ..``
+    map to ``slot(bt_b, p) = bt_b[p // bs] * bs + p % bs``
+    (``infrared/engine/paged_engine.py:621-625``), computed on the tables' device."""
+    dev = block_tables.device
+    q_lens = q_lens.to(device=dev, dtype=torch.long)
+    nc = num_cached.to(device=dev, dtype=torch.long)
+    seq = torch.repeat_interleave(torch.arange(q_lens.numel(), device=dev), q_lens)
+    first = torch.cumsum(q_lens, 0) - q_lens  # packed row of each sequence's first token
+    pos = nc[seq] + (torch.arange(seq.numel(), device=dev) - first[seq])
+    blk = block_tables.long()[seq, pos // block_size]
+    return blk * block_size + pos % block_size
 
 
 def gather_slots_from_tables(
@@ -135,21 +158,21 @@ def prefill_context(
         raise ValueError("block_tables, num_cached and q_lens must have one entry per sequence")
     lengths = [c + n for c, n in zip(num_cached, q_lens)]
     width = max(blocks_for(n, bs) for n in lengths) if lengths else 0
-    rows = [list(r)[: max(width, 1)] for r in block_tables]
+    rows = [r[: max(width, 1)] for r in block_tables]
     bt = block_tables_tensor(rows, dev, width)
-    cu = [0]
-    for n in q_lens:
-        cu.append(cu[-1] + n)
-    write = [slot(r, p, bs) for r, c, n in zip(rows, num_cached, q_lens) for p in range(c, c + n)]
+    meta = torch.tensor([list(num_cached), list(q_lens)], dtype=torch.int32).to(dev)  # one host->device copy
+    nc_t, ql_t = meta[0], meta[1]
+    cu = torch.zeros(len(q_lens) + 1, dtype=torch.int32, device=dev)
+    cu[1:] = torch.cumsum(ql_t, 0)
     ctx = PagedContext(
         pool,
-        torch.tensor(write, dtype=torch.int64, device=dev),
+        packed_write_slots(bt, nc_t, ql_t, bs),
         None,
         use_triton,
         bt,
         None,
-        torch.tensor(cu, dtype=torch.int32, device=dev),
-        torch.tensor(list(num_cached), dtype=torch.int32, device=dev),
+        cu,
+        nc_t.contiguous(),
         max(q_lens, default=0),
     )
     if not with_mask:

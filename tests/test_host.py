@@ -123,3 +123,29 @@ def test_decode_mask_matches_oracle(dtype):
     ctx = [1, 5, 17, 3]
     got = metadata.decode_mask(torch.tensor(ctx, dtype=torch.int32), 20, dtype)
     assert torch.equal(got, O.decode_mask(ctx, 20, dtype))
+
+
+@pytest.mark.parametrize("bs", [1, 5, 16])
+def test_packed_write_slots_match_the_slot_loop(bs):
+    """The vectorised write slots of a packed step (prefill chunks after cached
+    prefixes, decode rows as one-token chunks, an empty chunk) equal the
+    reference engine's per-token loop slot(bt, p) over each chunk's positions
+    (infrared/engine/paged_engine.py:481-494, :621-625)."""
+    g = torch.Generator().manual_seed(bs)
+    num_cached = [0, 37, 5, 120, 9]
+    q_lens = [23, 1, 0, 40, 1]
+    tables = []
+    for c, n in zip(num_cached, q_lens):
+        nb = metadata.blocks_for(c + n, bs) + 2
+        tables.append(torch.randint(0, 10_000, (nb,), generator=g).tolist())
+    bt = metadata.block_tables_tensor(tables, "cpu")
+    got = metadata.packed_write_slots(bt, torch.tensor(num_cached), torch.tensor(q_lens), bs)
+    want = [O.slot(t, p, bs) for t, c, n in zip(tables, num_cached, q_lens) for p in range(c, c + n)]
+    assert got.dtype == torch.int64 and got.tolist() == want
+
+
+def test_block_tables_tensor_pads_with_block_zero():
+    bt = metadata.block_tables_tensor([[5, 6, 7], [], [9]], "cpu", 4)
+    assert bt.dtype == torch.int32 and bt.tolist() == [[5, 6, 7, 0], [0, 0, 0, 0], [9, 0, 0, 0]]
+    with pytest.raises(ValueError, match="longer than width"):
+        metadata.block_tables_tensor([[1, 2, 3]], "cpu", 2)
