@@ -76,6 +76,9 @@ def _parse() -> argparse.Namespace:
                    help="decode: the seam's choice (default: kernels.decode_plan_pays), "
                    "balanced plan + run, or fixed split-KV partitions; prefill: the seam's choice "
                    "(kernels.prefill_plan_pays), the work plan, or none")
+    p.add_argument("--placement", choices=("global", "share-groups"), default="global",
+                   help="prefill: the work plan's placement -- one global heaviest-first order, or each "
+                   "(shared-prefix group, KV head) on one XCD (fewer bytes fetched)")
     p.add_argument("--layers", type=int, default=28,
                    help="calls per decode / prefill plan (layers of one step sharing its metadata)")
     p.add_argument("--cpu-iters", type=int, default=5, help="timed CPU-baseline iterations (0 = skip)")
@@ -304,7 +307,7 @@ def _bench_prefill(args) -> dict:
     case = make_prefill_case("qwen7b-prefill", "cuda", rotations=args.rotations)
     cfg = case.config
     out = torch.empty_like(case.q)
-    total_q, max_blocks = case.q.shape[0], case.block_tables[0].shape[1]
+    total_q = case.q.shape[0]
     # the work plan (the seam's choice unless --schedule forces it), rebuilt
     # every --layers calls as an engine step would
     planned = args.schedule == "planned" or (args.schedule == "auto" and kernels.prefill_plan_pays(
@@ -316,9 +319,10 @@ def _bench_prefill(args) -> dict:
 
     def call(i: int) -> None:
         if planned and i % args.layers == 0:
-            plan[0] = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, total_q, cfg.chunk, max_blocks,
-                                           cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim,
-                                           buf=plan_buf)
+            bt = case.block_tables[i % len(case.block_tables)]
+            plan[0] = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, bt, total_q, cfg.chunk, cfg.block_size,
+                                           cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, buf=plan_buf,
+                                           share_groups=args.placement == "share-groups")
         kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[i % len(case.block_tables)],
                               case.cu_seqlens_q, case.q_start, cfg.chunk, cfg.block_size, cfg.scale, out=out,
                               plan=plan[0])
@@ -358,10 +362,12 @@ def _bench_prefill(args) -> dict:
                    f"{cfg.num_q_heads}q/{cfg.num_kv_heads}kv heads, head_dim {cfg.head_dim}, block {cfg.block_size}",
                    "flops_per_call": case.flops, "kv_bytes_per_call": case.kv_bytes, "rotations": args.rotations,
                    "schedule": "work plan (heaviest first, heavy items cut)" if planned else "unplanned",
+                   "placement": args.placement if planned else None,
                    "layers_per_plan": args.layers if planned else None},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "measured_peak": _measured_peak("mfma"),
-                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": _traffic("prefill_qwen7b-prefill")[0],
+                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": _traffic("prefill_qwen7b-prefill" if args.placement == "global"
+                                                             else "prefill_qwen7b-prefill-share-groups")[0],
                      "timed": f"prefill call, {args.mode} launches, events on the launch stream"},
         "cpu_baseline": cpu,
     }

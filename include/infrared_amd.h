@@ -54,6 +54,11 @@ enum {
   IR_ERR_GATHER_RANGE = 8    /* gather slot outside [0, num_slots) (key masked) */
 };
 
+/* flags of ir_paged_prefill_plan */
+enum {
+  IR_PLAN_SHARE_GROUPS = 1  /* keep each shared-prefix group's KV head on one XCD */
+};
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* ir_last_error(void);
 
@@ -342,16 +347,31 @@ int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
  * ir_paged_prefill_plan_bytes: bytes of plan for these shapes (0 when there is
  *   nothing to plan).
  * ir_paged_prefill_plan: writes the plan (one workgroup: weighs every (sequence,
- *   query block) item by the key tiles it walks, cuts the heaviest, sorts the
- *   pieces heaviest first, clears the arrival counters). Arguments as for
- *   ir_paged_prefill.
+ *   query block) item by the key tiles it walks, cuts the heaviest, places the
+ *   pieces, clears the arrival counters). Arguments as for ir_paged_prefill,
+ *   plus flags. Default placement: one global heaviest-first order, a piece's
+ *   KV heads on consecutive workgroups. IR_PLAN_SHARE_GROUPS: consecutive
+ *   sequences whose block tables begin with the same block id form a share
+ *   group -- the prefix cache of infrared/cache/block_manager.py:209-234
+ *   (match_prefix) hands every sequence with a common cached prefix the same
+ *   blocks for it, registered by :258-283 (register_full_blocks) -- and each
+ *   (share group, KV head) runs on one XCD (when the KV heads divide the XCD
+ *   count and the groups balance), so a shared prefix's K/V is fetched into
+ *   one L2 for the whole group: fewer bytes from memory, for callers whose
+ *   prefill shares HBM with other work. Only block_tables' first column is
+ *   read (bt_stride elements between rows); the placement changes the
+ *   schedule, never a result bit.
+ * ir_paged_prefill_plan_xcds: XCDs the plan lays its grid out for on the
+ *   current device (the plan's size depends on it).
  */
 int64_t ir_paged_prefill_plan_bytes(int num_seqs, int max_q_len, int num_q_heads, int num_kv_heads,
                                     int head_dim);
-int ir_paged_prefill_plan(const int32_t* cu_seqlens_q, const int32_t* q_start, int num_seqs,
+int ir_paged_prefill_plan(const int32_t* cu_seqlens_q, const int32_t* q_start,
+                          const int32_t* block_tables, int64_t bt_stride, int num_seqs,
                           int total_q, int max_q_len, int max_blocks_per_seq, int block_size,
-                          int num_q_heads, int num_kv_heads, int head_dim, void* plan,
+                          int num_q_heads, int num_kv_heads, int head_dim, int flags, void* plan,
                           int64_t plan_bytes, ir_stream_t stream);
+int ir_paged_prefill_plan_xcds(void);
 
 /*
  * Fused rotary embedding + KV-slot scatter. Replaces, per layer,

@@ -103,8 +103,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ir_paged_prefill_plan_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "ir_paged_prefill_plan": (
         _c_i32,
-        [_c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p],
+        [_c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p,
+         _c_i64, _c_p],
     ),
+    "ir_paged_prefill_plan_xcds": (_c_i32, []),
 }
 
 _lock = threading.Lock()

@@ -31,15 +31,18 @@
 // workgroups (256 columns) are kept for comparison (IR_PREFILL_WAVES=8).
 //
 // Plan (ir_paged_prefill_plan, built on the device once per step, shared by
-// every layer): the items in heaviest-first order -- the dispatcher places
-// workgroups in index order, so that is the longest-processing-time rule --
-// with the key range of any item heavier than the mean load of a workgroup
-// slot cut into pieces, each its own workgroup. A piece attends its share of
-// the item's key tiles and writes fp32 partial rows (max, sum, unnormalised
-// output) into the plan; the last piece of the item to arrive (an arrival
-// counter in the plan) merges them with log-sum-exp weights in part order and
-// writes the output. Without a plan, a sequence's last query blocks go first
-// and nothing is cut.
+// every layer): one entry per workgroup, (item, KV head, piece). The pieces
+// run heaviest first -- the dispatcher places workgroups in index order, so
+// that is the longest-processing-time rule -- with the key range of any item
+// heavier than the mean load of a workgroup slot cut into pieces, each its own
+// workgroup. A piece attends its share of the item's key tiles and writes fp32
+// partial rows (max, sum, unnormalised output) into the plan; the last piece of
+// the item to arrive (an arrival counter in the plan) merges them with
+// log-sum-exp weights in part order and writes the output. The plan also
+// places the work of each (shared-prefix group, KV head) on one XCD where the
+// balance allows, so its K/V tiles -- a shared prefix included -- are fetched
+// into one L2 (see the plan section). Without a plan, a sequence's last query
+// blocks go first and nothing is cut.
 //   K and V tiles: row-major [64 keys][D] (+32 bytes a row against bank
 //   conflicts), loaded and stored alike (a thread's K and V pieces share the
 //   key's slot); the PV product reads V^T with gfx950's transpose read.
@@ -95,13 +98,14 @@ struct PrefillArgs {
   int nw;                                    // wavefronts per workgroup (4 or 8)
   float scale_log2;
   int32_t* err;
-  // plan (or nulls): items[k] = (item, piece), item = seq * n_qblocks + block
-  // (-1: none), piece = nparts | part << 8 | first piece index << 16
+  // plan (or nulls): items[workgroup] = (item * H_kv + KV head, piece), item =
+  // seq * n_qblocks + block (-1: no work), piece = nparts | part << 8 | first
+  // piece index << 16
   const int2* items;
   int32_t* counters;  // one per (cut item, KV head), zero at rest
   float* ws_o;        // partial rows [piece][kv head][column][D]
   float* ws_ml;       // (max, sum) of each partial row
-  int64_t n_items_grid;  // workgroups of a planned call: plan entries x H_kv
+  int64_t n_items_grid;  // workgroups of a planned call (plan entries)
 };
 
 template <int D, int NW_ = 8, int CT_ = 2>
@@ -144,16 +148,16 @@ void paged_prefill_kernel(PrefillArgs a) {
   const int TQ = a.tq;
 
   // ---- which (query block, KV head, sequence) and which piece of its keys:
-  // plan entry i / H_kv when a plan is given, else the last query blocks (most
-  // keys within a sequence) first, uncut
+  // plan entry i when a plan is given, else the last query blocks (most keys
+  // within a sequence) first, uncut
   int tb, seq, kvh, nparts = 1, part = 0, pbase = 0;
   if (a.items) {
-    const int k = (int)(blockIdx.x / a.num_kv_heads);
-    kvh = (int)(blockIdx.x - (unsigned)k * a.num_kv_heads);
-    const int2 e = a.items[k];
-    if (e.x < 0 || e.x >= a.num_seqs * a.n_qblocks) return;
-    seq = e.x / a.n_qblocks;
-    tb = e.x - seq * a.n_qblocks;
+    const int2 e = a.items[blockIdx.x];
+    const int item = e.x < 0 ? -1 : e.x / a.num_kv_heads;
+    if (item < 0 || item >= a.num_seqs * a.n_qblocks) return;
+    kvh = e.x - item * a.num_kv_heads;
+    seq = item / a.n_qblocks;
+    tb = item - seq * a.n_qblocks;
     nparts = max(e.y & 0xff, 1);
     part = min((e.y >> 8) & 0xff, nparts - 1);
     pbase = (int)((uint32_t)e.y >> 16);
@@ -639,31 +643,65 @@ void paged_prefill_kernel(PrefillArgs a) {
 // every item heavier than 1.5x the mean load of a workgroup slot (and than
 // kMinPieceTiles) into pieces of at most that threshold, at most kMaxParts per
 // item and at most the plan's piece capacity in all (the smallest threshold
-// that fits it, found by bisection), then counting-sorts the pieces by weight
-// over kPlanBuckets ranges, heaviest first; items without query rows go last
-// as -1. Measured on 8 chunks of 512 tokens after prefixes of U{0..8192} keys
-// (per-workgroup timestamps): a workgroup costs ~7 us plus ~2.2 us per 64-key
-// tile while sharing its CU, and cutting at the mean (the longest item, 99
-// tiles, against a mean of 75) made the call 10% slower -- the pieces' fixed
-// costs and merges outweighed a tail the heaviest-first order had mostly
-// filled -- so only items well above the mean are cut. One workgroup builds it once per step (every layer shares the
-// metadata) and clears the arrival counters. Each thread owns a contiguous
-// run of items, so the pieces' partial-row indices come from a deterministic
-// scan; only the position of equal-weight pieces in the order varies, which
-// changes the schedule, never a result bit.
+// that fits it, found by bisection). Measured on 8 chunks of 512 tokens after
+// prefixes of U{0..8192} keys (per-workgroup timestamps): a workgroup costs ~7
+// us plus ~2.2 us per 64-key tile while sharing its CU, and cutting at the
+// mean (the longest item, 99 tiles, against a mean of 75) made the call 10%
+// slower -- the pieces' fixed costs and merges outweighed a tail the
+// heaviest-first order had mostly filled -- so only items well above the mean
+// are cut.
+//
+// Placement. The dispatcher hands workgroup i to XCD i mod X, and each XCD
+// has its own L2. It also dispatches in index order: an XCD without room for
+// its next workgroup holds up the workgroups behind it for every XCD, so each
+// run of X consecutive workgroups must carry similar work (placing each
+// (sequence, KV head) on one XCD by cutting a cost line into X segments cut
+// the fetched bytes of 8 x 512-token chunks by 27% but made the call 17%
+// slower). Within that constraint the plan keeps a shared prefix in one L2:
+// every query block of a sequence walks the same K/V tiles of its KV head,
+// and sequences whose block tables begin with the same block share a cached
+// prefix (the prefix cache hands each of them the same blocks for it). Share
+// groups are runs of consecutive sequences whose first block ids are equal
+// (each with at least one cached block). When the KV heads H divide X, a
+// piece's H workgroups fill one of S = X / H slots of H consecutive XCDs in a
+// row of X workgroups; every group keeps one slot (groups ranked by cost --
+// tiles + kPieceFixed per workgroup -- and dealt to slots in snake order), each
+// slot's pieces run heaviest first (counting sort over kXcdBuckets weight
+// ranges), and row r holds the r-th piece of every slot, so head h of a group
+// always runs on the same XCD. When the slots' costs differ by more than 10%,
+// a slot would overflow the grid, there is one group, or the call is too
+// large for the placement's LDS tables, the pieces keep one global
+// heaviest-first order (kPlanBuckets weight ranges), a piece's heads on
+// consecutive workgroups -- which already keeps head h on XCD h mod X when X
+// divides H.
+//
+// One workgroup builds it once per step (every layer shares the metadata) and
+// clears the arrival counters. Each thread owns a contiguous run of items, so
+// the pieces' partial-row indices come from a deterministic scan; only the
+// position of equal-weight pieces in the order varies, which changes the
+// schedule, never a result bit.
 
 constexpr int kPlanThreads = 1024;
-constexpr int kPlanBuckets = 2048;
+constexpr int kPlanBuckets = 2048;  // weight ranges of the global order
+constexpr int kXcdBuckets = 256;    // weight ranges of each XCD's order
+constexpr int kMaxXcds = 16;
+constexpr int kStartSize = kMaxXcds * kXcdBuckets + 1;
+static_assert(kStartSize >= kPlanBuckets + 1, "bucket table too small for the global order");
 constexpr int kMaxParts = 16;      // pieces per item (8-bit field)
 constexpr int kMinPieceTiles = 8;  // items of at most this many key tiles are never cut
 constexpr int kPlanWeightCache = 8192;  // items whose weights the plan keeps in LDS
+constexpr int kPlaceSeqs = kPlanThreads;  // sequences the placement handles (one per thread)
+constexpr int kPieceFixed = 3;  // a workgroup's fixed cost in key tiles (~7 us against ~2.2 us a tile)
 
 struct PlanArgs {
   const int32_t* cu_q;
   const int32_t* q_start;
-  int num_seqs, total_q, n_qblocks, tq, cap;  // cap: keys the block tables hold
-  int num_kv_heads, slots, cap_pieces;        // slots: workgroups resident on the device at once
-  int entries;
+  const int32_t* bt;  // block tables: the first id of each row groups shared prefixes
+  int64_t bt_stride;
+  int num_seqs, total_q, n_qblocks, tq, cap, bs;  // cap: keys the block tables hold
+  int num_kv_heads, slots, cap_pieces, xcds;      // slots: workgroups resident on the device at once
+  int share_groups;   // place share groups on slots of XCDs (else one global order)
+  int entries;        // workgroups of a planned call
   int2* items;        // [entries]
   int32_t* counters;  // [cap_pieces * num_kv_heads]
 };
@@ -707,12 +745,73 @@ __device__ int64_t plan_max(int64_t x, int64_t* red) {
   return t;
 }
 
-__global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PlanArgs a) {
-  __shared__ int start[kPlanBuckets + 1];
-  __shared__ int64_t red[kPlanThreads / 64];
-  __shared__ int run_base[kPlanThreads];
-  __shared__ int w_cache[kPlanWeightCache];
+// Exclusive prefix sum of x over the block's threads in thread order (buf:
+// kPlanThreads + 1 entries); *total receives the sum. One wavefront scans runs
+// of kPlanThreads / 64 values per lane.
+__device__ int64_t plan_scan(int64_t x, int64_t* buf, int64_t* total) {
   const int tid = threadIdx.x, lane = tid & 63;
+  buf[tid] = x;
+  __syncthreads();
+  if (tid < 64) {
+    constexpr int kRun = kPlanThreads / 64;
+    int64_t sum = 0;
+    for (int k = 0; k < kRun; ++k) sum += buf[lane * kRun + k];
+    int64_t incl = sum;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t y = __shfl_up(incl, o);
+      if (lane >= o) incl += y;
+    }
+    int64_t r = incl - sum;
+    for (int k = 0; k < kRun; ++k) {
+      const int64_t v = buf[lane * kRun + k];
+      buf[lane * kRun + k] = r;
+      r += v;
+    }
+    if (lane == 63) buf[kPlanThreads] = incl;
+  }
+  __syncthreads();
+  const int64_t r = buf[tid];
+  *total = buf[kPlanThreads];
+  __syncthreads();
+  return r;
+}
+
+// In-place exclusive scan of counts[0 .. len) by one wavefront (len <= 64 *
+// runs); the caller synchronises around it.
+__device__ void plan_scan_counts(int* counts, int len) {
+  const int lane = threadIdx.x & 63;
+  const int run = (len + 63) / 64;
+  const int b_lo = min(len, lane * run), b_hi = min(len, b_lo + run);
+  int sum = 0;
+  for (int i = b_lo; i < b_hi; ++i) sum += counts[i];
+  int incl = sum;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o);
+    if (lane >= o) incl += y;
+  }
+  int r = incl - sum;
+  for (int i = b_lo; i < b_hi; ++i) {
+    const int cnt = counts[i];
+    counts[i] = r;
+    r += cnt;
+  }
+}
+
+__global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PlanArgs a) {
+  __shared__ int start[kStartSize];
+  __shared__ int64_t red[kPlanThreads / 64];
+  __shared__ int64_t scan[kPlanThreads + 1];
+  __shared__ int w_cache[kPlanWeightCache];
+  __shared__ int64_t seq_cost[kPlaceSeqs + 1];  // cost before each sequence's first item
+  __shared__ int seq_gid[kPlaceSeqs];           // share group of each sequence
+  __shared__ int glead[kPlaceSeqs + 1];         // first sequence of each group, then num_seqs
+  __shared__ int64_t gcost[kPlaceSeqs];         // cost of each group
+  __shared__ int gslot[kPlaceSeqs];             // slot of each group
+  __shared__ unsigned long long slot_cost[kMaxXcds];
+  __shared__ int slot_base[kMaxXcds + 1];
+  __shared__ int s_place;
+  const int tid = threadIdx.x;
+  const int H = a.num_kv_heads;
   const int n = a.num_seqs * a.n_qblocks;
   const int per = (n + kPlanThreads - 1) / kPlanThreads;
   const int i_lo = min(n, tid * per), i_hi = min(n, i_lo + per);
@@ -731,7 +830,7 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PlanArgs a) 
   const int wmax = (int)plan_max(wm, red);
   // the cut threshold: the mean load of a workgroup slot, raised until the
   // pieces of the cut items fit the plan's capacity
-  int lo = (int)max((int64_t)kMinPieceTiles, (total * a.num_kv_heads * 3 + 2 * a.slots - 1) / (2 * a.slots));
+  int lo = (int)max((int64_t)kMinPieceTiles, (total * H * 3 + 2 * a.slots - 1) / (2 * a.slots));
   int hi = max(lo, wmax);
   while (lo < hi) {
     const int mid = lo + (hi - lo) / 2;
@@ -744,80 +843,141 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PlanArgs a) 
     else lo = mid + 1;
   }
   const int T = lo;
+  auto piece_info = [](int np, int p, int pb) { return np > 1 ? np | (p << 8) | (pb << 16) : 1; };
 
   // first partial-row piece of each cut item: exclusive scan over the runs
-  int mine = 0;
+  int64_t mine = 0, all = 0;
   for (int i = i_lo; i < i_hi; ++i) {
     const int np = pieces_of(weight(i), T);
     if (np > 1) mine += np;
   }
-  run_base[tid] = mine;
-  for (int i = tid; i <= kPlanBuckets; i += kPlanThreads) start[i] = 0;
-  __syncthreads();
-  if (tid < 64) {  // scan of the 1024 run totals by one wavefront
-    constexpr int kRun = kPlanThreads / 64;
-    int sum = 0;
-    for (int k = 0; k < kRun; ++k) sum += run_base[lane * kRun + k];
-    int incl = sum;
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(incl, o);
-      if (lane >= o) incl += y;
-    }
-    int r = incl - sum;
-    for (int k = 0; k < kRun; ++k) {
-      const int v = run_base[lane * kRun + k];
-      run_base[lane * kRun + k] = r;
-      r += v;
-    }
-  }
-  __syncthreads();
+  const int pb_run = (int)plan_scan(mine, scan, &all);
 
-  // bucket 0 holds the heaviest pieces
-  auto bucket = [&](int pw) { return (int)((int64_t)(wmax - pw) * kPlanBuckets / ((int64_t)wmax + 1)); };
-  for (int i = i_lo; i < i_hi; ++i) {
-    const int w = weight(i);
-    const int np = pieces_of(w, T);
-    if (np > 0) atomicAdd(&start[bucket((w + np - 1) / np)], np);
-  }
-  __syncthreads();
-  if (tid < 64) {  // exclusive scan of the bucket counts; start[kPlanBuckets] = pieces in all
-    constexpr int kRun = (kPlanBuckets + 1 + 63) / 64;
-    const int b_lo = lane * kRun, b_hi = min(b_lo + kRun, kPlanBuckets + 1);
-    int sum = 0;
-    for (int i = b_lo; i < b_hi; ++i) sum += start[i];
-    int incl = sum;
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(incl, o);
-      if (lane >= o) incl += y;
+  // ---- slots: share groups and their costs
+  const int X = a.xcds;
+  const int S = H < X && X % H == 0 ? X / H : 1;
+  // uniform over the block: every input of this test is
+  const bool may_place =
+      a.share_groups && S > 1 && S <= kMaxXcds && cached && a.num_seqs <= kPlaceSeqs && a.bt != nullptr;
+  if (may_place) {
+    int64_t cost_run = 0;
+    for (int i = i_lo; i < i_hi; ++i) {
+      const int w = weight(i), np = pieces_of(w, T);
+      if (np > 0) cost_run += w + kPieceFixed * np;
     }
-    int r = incl - sum;
-    for (int i = b_lo; i < b_hi; ++i) {
-      const int cnt = start[i];
-      start[i] = r;
-      r += cnt;
+    int64_t line_total = 0;
+    int64_t c = plan_scan(cost_run, scan, &line_total);
+    for (int i = i_lo; i < i_hi; ++i) {
+      if (i % a.n_qblocks == 0) seq_cost[i / a.n_qblocks] = c;
+      const int w = weight(i), np = pieces_of(w, T);
+      if (np > 0) c += w + kPieceFixed * np;
     }
+    if (tid == 0) seq_cost[a.num_seqs] = line_total;
+    // sequence tid starts a group unless its first block is the previous one's
+    int flag = 0;
+    if (tid < a.num_seqs) {
+      auto first_block = [&](int q) {
+        return a.q_start[q] >= a.bs && a.cap >= a.bs ? a.bt[(int64_t)q * a.bt_stride] : -1;
+      };
+      const int f = first_block(tid);
+      flag = tid == 0 || f < 0 || f != first_block(tid - 1);
+    }
+    int64_t ngroups = 0;
+    const int gid = (int)plan_scan(flag, scan, &ngroups) + flag - 1;
+    if (tid < a.num_seqs) {
+      seq_gid[tid] = gid;
+      if (flag) glead[gid] = tid;
+    }
+    if (tid == 0) glead[ngroups] = a.num_seqs;
+    if (tid < kMaxXcds) slot_cost[tid] = 0;
+    __syncthreads();
+    if (tid < ngroups) gcost[tid] = seq_cost[glead[tid + 1]] - seq_cost[glead[tid]];
+    __syncthreads();
+    // rank of group tid (heavier first, ties by index), dealt to the slots in
+    // snake order: 0, 1, .., S-1, S-1, .., 0, 0, ..
+    if (tid < ngroups) {
+      const int64_t mine_c = gcost[tid];
+      int rank = 0;
+      for (int o = 0; o < ngroups; ++o) rank += gcost[o] > mine_c || (gcost[o] == mine_c && o < tid);
+      const int k = rank % S;
+      const int sl = (rank / S) & 1 ? S - 1 - k : k;
+      gslot[tid] = sl;
+      atomicAdd(&slot_cost[sl], (unsigned long long)mine_c);
+    }
+    for (int k = tid; k < kStartSize; k += kPlanThreads) start[k] = 0;
+    if (tid == 0) s_place = ngroups > 1;
+    __syncthreads();
+    // the slots' costs within 10% of their mean
+    if (tid < S && (int64_t)slot_cost[tid] * 10 * S > line_total * 11) s_place = 0;
+    __syncthreads();
   }
-  __syncthreads();
-  const int used = start[kPlanBuckets];
-  __syncthreads();
-  int pb = run_base[tid];
-  for (int i = i_lo; i < i_hi; ++i) {
-    const int w = weight(i);
-    const int np = pieces_of(w, T);
-    if (np == 0) continue;
-    const int pos = atomicAdd(&start[bucket((w + np - 1) / np)], np);
-    for (int p = 0; p < np; ++p)
-      a.items[pos + p] = np > 1 ? make_int2(i, np | (p << 8) | (pb << 16)) : make_int2(i, 1);
-    if (np > 1) pb += np;
+  auto xbucket = [&](int pw) { return (int)((int64_t)(wmax - pw) * kXcdBuckets / ((int64_t)wmax + 1)); };
+  if (may_place && s_place) {
+    for (int i = i_lo; i < i_hi; ++i) {
+      const int w = weight(i), np = pieces_of(w, T);
+      if (np > 0) atomicAdd(&start[gslot[seq_gid[i / a.n_qblocks]] * kXcdBuckets + xbucket((w + np - 1) / np)], np);
+    }
+    __syncthreads();
+    if (tid < 64) plan_scan_counts(start, S * kXcdBuckets + 1);
+    __syncthreads();
+    if (tid <= S) slot_base[tid] = start[tid * kXcdBuckets];
+    __syncthreads();
+    // every slot's pieces must fit the grid's rows
+    if (tid < S && slot_base[tid + 1] - slot_base[tid] > a.entries / X) s_place = 0;
+    __syncthreads();
   }
-  for (int k = used + tid; k < a.entries; k += kPlanThreads) a.items[k] = make_int2(-1, 0);
-  for (int k = tid; k < a.cap_pieces * a.num_kv_heads; k += kPlanThreads) a.counters[k] = 0;
+  const bool place = may_place && s_place;
+
+  if (place) {
+    // row r, slot sl: the r-th heaviest piece of the slot, KV head h on XCD
+    // sl * H + h; entries past a slot's pieces are empty
+    for (int k = tid; k < a.entries; k += kPlanThreads) {
+      const int sl = (k % X) / H;
+      if (k / X >= slot_base[sl + 1] - slot_base[sl]) a.items[k] = make_int2(-1, 0);
+    }
+    int pb = pb_run;
+    for (int i = i_lo; i < i_hi; ++i) {
+      const int w = weight(i), np = pieces_of(w, T);
+      if (np == 0) continue;
+      const int sl = gslot[seq_gid[i / a.n_qblocks]];
+      const int r0 = atomicAdd(&start[sl * kXcdBuckets + xbucket((w + np - 1) / np)], np) - slot_base[sl];
+      for (int p = 0; p < np; ++p)
+        for (int h = 0; h < H; ++h) a.items[(r0 + p) * X + sl * H + h] = make_int2(i * H + h, piece_info(np, p, pb));
+      if (np > 1) pb += np;
+    }
+  } else {
+    // one global heaviest-first order of the pieces; bucket 0 holds the heaviest
+    for (int k = tid; k <= kPlanBuckets; k += kPlanThreads) start[k] = 0;
+    __syncthreads();
+    auto bucket = [&](int pw) { return (int)((int64_t)(wmax - pw) * kPlanBuckets / ((int64_t)wmax + 1)); };
+    for (int i = i_lo; i < i_hi; ++i) {
+      const int w = weight(i);
+      const int np = pieces_of(w, T);
+      if (np > 0) atomicAdd(&start[bucket((w + np - 1) / np)], np);
+    }
+    __syncthreads();
+    if (tid < 64) plan_scan_counts(start, kPlanBuckets + 1);  // start[kPlanBuckets] = pieces in all
+    __syncthreads();
+    const int used = start[kPlanBuckets];
+    __syncthreads();
+    int pb = pb_run;
+    for (int i = i_lo; i < i_hi; ++i) {
+      const int w = weight(i);
+      const int np = pieces_of(w, T);
+      if (np == 0) continue;
+      const int pos = atomicAdd(&start[bucket((w + np - 1) / np)], np);
+      for (int p = 0; p < np; ++p)
+        for (int h = 0; h < H; ++h) a.items[(pos + p) * H + h] = make_int2(i * H + h, piece_info(np, p, pb));
+      if (np > 1) pb += np;
+    }
+    for (int k = used * H + tid; k < a.entries; k += kPlanThreads) a.items[k] = make_int2(-1, 0);
+  }
+  for (int k = tid; k < a.cap_pieces * H; k += kPlanThreads) a.counters[k] = 0;
 }
 
 // Tuning knobs, read once per process: IR_PREFILL_WAVES (4 or 8) forces the
-// workgroup size, IR_PREFILL_RING2 (1 or 0) forces or forbids the 2-deep ring
-// for 4-wavefront workgroups, IR_PREFILL_CUTS=0 keeps the plan from cutting
-// items (order only).
+// workgroup size, IR_PREFILL_RING2 (1 or 0) forces or forbids the 2-deep ring,
+// IR_PREFILL_CUTS=0 keeps the plan from cutting items (order only).
 struct PrefillKnobs {
   int waves = 0;   // 0: 4, or 8 when 4 cannot hold a token's query heads
   int ring2 = -1;  // -1: by grid size
@@ -832,6 +992,13 @@ struct PrefillKnobs {
 const PrefillKnobs& prefill_knobs() {
   static const PrefillKnobs k;
   return k;
+}
+
+// XCDs the plan lays its grid out for (1: the device has one, or more than
+// the placement's tables hold).
+int plan_xcds() {
+  const int x = device_xcds();
+  return x > 1 && x <= kMaxXcds ? x : 1;
 }
 
 // Workgroup shape and schedule of a prefill call, from its shapes alone (the
@@ -851,16 +1018,19 @@ PrefillGeometry prefill_geometry(int max_q_len, int n_rep, int num_kv_heads, int
   g.n_qblocks = (max_q_len + g.tq - 1) / g.tq;
   const int cus = device_cus();
   const int64_t wgs = (int64_t)g.n_qblocks * num_kv_heads * num_seqs;
-  const bool ring2 = g.nw == 4 && (k.ring2 >= 0 ? k.ring2 == 1 : wgs >= 2 * (int64_t)cus);
+  const bool ring2 = k.ring2 >= 0 ? k.ring2 == 1 : g.nw == 4 && wgs >= 2 * (int64_t)cus;
   g.sched = ring2 ? kRing2 : kLockstep;
-  g.slots = ring2 ? 2 * cus : cus;
+  g.slots = ring2 && g.nw == 4 ? 2 * cus : cus;
   return g;
 }
 
 int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
-// Plan layout: items [entries] int2, counters [cap_pieces * H_kv] int32,
-// (max, sum) [cap_pieces * H_kv * cols] fp32 x 2, partial outputs [.. * D] fp32.
+// Plan layout: items [entries] int2 (one per workgroup of a planned call),
+// counters [cap_pieces * H_kv] int32, (max, sum) [cap_pieces * H_kv * cols]
+// fp32 x 2, partial outputs [.. * D] fp32. At most items + cap_pieces pieces
+// exist, each on H_kv workgroups; with X > 1 XCDs the grid holds 1.5x that,
+// rounded to X, so an XCD may take more pieces than the mean.
 struct PlanLayout {
   int64_t entries, cap_pieces, cols;
   int64_t off_ctr, off_ml, off_o, total;
@@ -870,7 +1040,9 @@ PlanLayout plan_layout(const PrefillGeometry& g, int num_seqs, int num_kv_heads,
   PlanLayout l;
   l.cols = 32 * g.nw;
   l.cap_pieces = (g.slots + num_kv_heads - 1) / num_kv_heads;
-  l.entries = (int64_t)num_seqs * g.n_qblocks + l.cap_pieces;
+  const int64_t wgs = ((int64_t)num_seqs * g.n_qblocks + l.cap_pieces) * num_kv_heads;
+  const int x = plan_xcds();
+  l.entries = x > 1 ? x * ((wgs * 3 / 2 + x - 1) / x) : wgs;
   l.off_ctr = align256(l.entries * 8);
   const int64_t rows = l.cap_pieces * num_kv_heads * l.cols;
   l.off_ml = l.off_ctr + align256(l.cap_pieces * num_kv_heads * 4);
@@ -901,8 +1073,13 @@ int launch_prefill(const PrefillArgs& a, int sched, hipStream_t s) {
     }
   } else {
     const dim3 block(PShape<D, 8>::NT);
-    if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 2, kLockstep>), g, block, 0, s, a);
-    else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 2, kLockstep>), g, block, 0, s, a);
+    if (sched == kRing2) {
+      if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 2, kRing2>), g, block, 0, s, a);
+      else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 2, kRing2>), g, block, 0, s, a);
+    } else {
+      if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 2, kLockstep>), g, block, 0, s, a);
+      else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 2, kLockstep>), g, block, 0, s, a);
+    }
   }
   return check_launch("ir_paged_prefill");
 }
@@ -920,6 +1097,8 @@ extern "C" int64_t ir_paged_prefill_plan_bytes(int num_seqs, int max_q_len, int 
   const PrefillGeometry geo = prefill_geometry(max_q_len, num_q_heads / num_kv_heads, num_kv_heads, num_seqs);
   return plan_layout(geo, num_seqs, num_kv_heads, head_dim).total;
 }
+
+extern "C" int ir_paged_prefill_plan_xcds(void) { return plan_xcds(); }
 
 extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_head_stride, const void* k_cache,
                                 const void* v_cache, int64_t cache_slot_stride, int64_t cache_head_stride,
@@ -977,7 +1156,8 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
   a.tq = geo.tq;
   a.n_qblocks = geo.n_qblocks;
   const int64_t n_items = (int64_t)num_seqs * a.n_qblocks;
-  IR_REQUIRE(n_items <= 0x7fffffff, "ir_paged_prefill: %lld work items", (long long)n_items);
+  IR_REQUIRE(n_items * num_kv_heads <= 0x7fffffff, "ir_paged_prefill: %lld work items x %d KV heads",
+             (long long)n_items, num_kv_heads);
   if (plan) {
     const PlanLayout ly = plan_layout(geo, num_seqs, num_kv_heads, head_dim);
     IR_REQUIRE(plan_bytes >= ly.total && ((uintptr_t)plan & 255u) == 0,
@@ -989,7 +1169,7 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
     a.counters = (int32_t*)(pl + ly.off_ctr);
     a.ws_ml = (float*)(pl + ly.off_ml);
     a.ws_o = (float*)(pl + ly.off_o);
-    a.n_items_grid = ly.entries * num_kv_heads;
+    a.n_items_grid = ly.entries;
   }
   a.out = out;
   a.o_tok = out_tok_stride;
@@ -1006,15 +1186,16 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
                          : launch_prefill<IR_DTYPE_F16, 64>(a, geo.sched, s);
 }
 
-extern "C" int ir_paged_prefill_plan(const int32_t* cu_seqlens_q, const int32_t* q_start, int num_seqs, int total_q,
-                                     int max_q_len, int max_blocks_per_seq, int block_size, int num_q_heads,
-                                     int num_kv_heads, int head_dim, void* plan, int64_t plan_bytes,
-                                     ir_stream_t stream) {
+extern "C" int ir_paged_prefill_plan(const int32_t* cu_seqlens_q, const int32_t* q_start, const int32_t* block_tables,
+                                     int64_t bt_stride, int num_seqs, int total_q, int max_q_len,
+                                     int max_blocks_per_seq, int block_size, int num_q_heads, int num_kv_heads,
+                                     int head_dim, int flags, void* plan, int64_t plan_bytes, ir_stream_t stream) {
   IR_REQUIRE(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && num_q_heads > 0 && num_kv_heads > 0 &&
                  block_size > 0 && max_blocks_per_seq >= 0,
              "ir_paged_prefill_plan: bad sizes");
   IR_REQUIRE(num_q_heads % num_kv_heads == 0, "ir_paged_prefill_plan: num_q_heads %d not a multiple of num_kv_heads %d",
              num_q_heads, num_kv_heads);
+  IR_REQUIRE((flags & ~IR_PLAN_SHARE_GROUPS) == 0, "ir_paged_prefill_plan: unknown flags 0x%x", flags);
   IR_REQUIRE((int64_t)max_blocks_per_seq * block_size <= (int64_t)1 << 30,
              "ir_paged_prefill_plan: block tables of %d x %d tokens exceed 2^30 keys", max_blocks_per_seq,
              block_size);
@@ -1023,23 +1204,32 @@ extern "C" int ir_paged_prefill_plan(const int32_t* cu_seqlens_q, const int32_t*
   IR_REQUIRE(plan && plan_bytes >= need && ((uintptr_t)plan & 255u) == 0,
              "ir_paged_prefill_plan: plan of %lld bytes (256-byte aligned) required, got %lld", (long long)need,
              (long long)plan_bytes);
-  IR_REQUIRE(cu_seqlens_q && q_start, "ir_paged_prefill_plan: null pointer");
+  IR_REQUIRE(cu_seqlens_q && q_start && (block_tables || max_blocks_per_seq == 0),
+             "ir_paged_prefill_plan: null pointer");
+  IR_REQUIRE(bt_stride >= max_blocks_per_seq, "ir_paged_prefill_plan: bt_stride %lld below max_blocks_per_seq %d",
+             (long long)bt_stride, max_blocks_per_seq);
   const PrefillGeometry geo = prefill_geometry(max_q_len, num_q_heads / num_kv_heads, num_kv_heads, num_seqs);
   const PlanLayout ly = plan_layout(geo, num_seqs, num_kv_heads, head_dim);
   IR_REQUIRE(ly.entries <= 0x7fffffff && ly.cap_pieces < 65536 &&
+                 (int64_t)num_seqs * geo.n_qblocks * num_kv_heads <= 0x7fffffff &&
                  ly.cap_pieces * num_kv_heads * ly.cols * head_dim * 4 < ((int64_t)1 << 31),
              "ir_paged_prefill_plan: plan too large for this shape");
   PlanArgs p;
   p.cu_q = cu_seqlens_q;
   p.q_start = q_start;
+  p.bt = max_blocks_per_seq > 0 ? block_tables : nullptr;
+  p.bt_stride = bt_stride;
   p.num_seqs = num_seqs;
   p.total_q = total_q;
   p.n_qblocks = geo.n_qblocks;
   p.tq = geo.tq;
   p.cap = max_blocks_per_seq * block_size;
+  p.bs = block_size;
   p.num_kv_heads = num_kv_heads;
   p.slots = geo.slots;
   p.cap_pieces = prefill_knobs().cuts ? (int)ly.cap_pieces : 0;
+  p.xcds = plan_xcds();
+  p.share_groups = (flags & IR_PLAN_SHARE_GROUPS) != 0;
   p.entries = (int)ly.entries;
   uint8_t* pl = (uint8_t*)plan;
   p.items = (int2*)pl;

@@ -21,6 +21,11 @@ int check_launch(const char* what);
 // CUs of the current device, cached per device (256 if the runtime cannot say).
 int device_cus();
 
+// Accelerator complex dies (XCDs) of the current device, cached per device (1
+// if the runtime cannot say). The dispatcher hands workgroup i of a launch to
+// XCD i mod this count; each XCD has its own L2.
+int device_xcds();
+
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 inline int dtype_bytes(int dtype) {

@@ -441,6 +441,9 @@ def rope_kv_scatter(
     return q_out
 
 
+PLAN_SHARE_GROUPS = 1  # IR_PLAN_SHARE_GROUPS
+
+
 @dataclass(frozen=True)
 class PrefillPlan:
     """A prefill work plan (``ir_paged_prefill_plan``) and the shape it was built
@@ -460,6 +463,12 @@ class PrefillPlan:
 def prefill_plan_bytes(num_seqs: int, max_q_len: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
     """Bytes of a prefill plan for these shapes (0: nothing to plan)."""
     return int(lib().ir_paged_prefill_plan_bytes(num_seqs, max_q_len, num_q_heads, num_kv_heads, head_dim))
+
+
+def prefill_plan_xcds() -> int:
+    """XCDs the prefill plan places work on for the current device (1: one
+    global heaviest-first order)."""
+    return int(lib().ir_paged_prefill_plan_xcds())
 
 
 def prefill_plan_pays(num_seqs: int, max_q_len: int, num_q_heads: int, num_kv_heads: int,
@@ -482,24 +491,34 @@ def prefill_plan_pays(num_seqs: int, max_q_len: int, num_q_heads: int, num_kv_he
 def prefill_plan(
     cu_seqlens_q: torch.Tensor,
     q_start: torch.Tensor,
+    block_tables: torch.Tensor,
     total_q: int,
     max_q_len: int,
-    max_blocks: int,
     block_size: int,
     num_q_heads: int,
     num_kv_heads: int,
     head_dim: int,
     buf: torch.Tensor | None = None,
+    share_groups: bool = False,
 ) -> PrefillPlan:
     """Work plan of a prefill call's (sequence, query block) items, built on
     the device (``ir_paged_prefill_plan``); pass it to every layer's
-    :func:`paged_prefill` over the same metadata. ``buf`` (uint8, 256-byte
-    aligned) is reused when large enough."""
-    dev = require_device(cu_seqlens_q, q_start)
+    :func:`paged_prefill` over the same metadata. ``share_groups``: keep each
+    (shared-prefix group, KV head) on one XCD -- groups are consecutive
+    sequences whose ``block_tables`` (int32 ``[B, max_blocks]``) rows begin
+    with the same block id -- so a shared prefix is fetched into one L2
+    (fewer bytes from memory; slower on a prefill that has HBM to itself);
+    by default one global heaviest-first order. Tables with other ids but the
+    same shape run correctly on the plan. ``buf`` (uint8, 256-byte aligned) is
+    reused when large enough."""
+    dev = require_device(cu_seqlens_q, q_start, block_tables)
     b = q_start.shape[0]
     for name, t, n in (("cu_seqlens_q", cu_seqlens_q, b + 1), ("q_start", q_start, b)):
         if t.dtype != torch.int32 or t.shape != (n,) or not t.is_contiguous():
             raise RuntimeError(f"prefill_plan: {name} must be contiguous int32 [{n}]")
+    if (block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.shape[0] != b
+            or block_tables.stride(1) != 1):
+        raise RuntimeError(f"prefill_plan: block_tables must be int32 [{b}, max_blocks] with unit column stride")
     n = prefill_plan_bytes(b, max_q_len, num_q_heads, num_kv_heads, head_dim)
     if n <= 0:
         raise RuntimeError("prefill_plan: nothing to plan for these shapes")
@@ -507,9 +526,11 @@ def prefill_plan(
         buf = torch.empty(n, dtype=torch.uint8, device=dev)
     if buf.dtype != torch.uint8 or buf.data_ptr() % 256:
         raise RuntimeError("prefill_plan: buf must be a 256-byte aligned uint8 tensor")
+    max_blocks = block_tables.shape[1]
     rc = lib().ir_paged_prefill_plan(
-        ptr(cu_seqlens_q), ptr(q_start), b, int(total_q), int(max_q_len), int(max_blocks), int(block_size),
-        num_q_heads, num_kv_heads, head_dim, ptr(buf), buf.numel(), stream_ptr(dev),
+        ptr(cu_seqlens_q), ptr(q_start), ptr(block_tables), max(block_tables.stride(0), max_blocks), b,
+        int(total_q), int(max_q_len), int(max_blocks), int(block_size), num_q_heads, num_kv_heads, head_dim,
+        PLAN_SHARE_GROUPS if share_groups else 0, ptr(buf), buf.numel(), stream_ptr(dev),
     )
     check(rc, "ir_paged_prefill_plan")
     return PrefillPlan(buf, b, int(max_q_len), num_q_heads, num_kv_heads, head_dim)

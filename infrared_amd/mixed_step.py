@@ -227,7 +227,7 @@ class MixedStep:
         if self.ordered:  # one prefill work plan per step, shared by every layer
             b = self.batch
             self.plan_pre = kernels.prefill_plan(
-                b.cu_seqlens_q, b.q_start, self.inputs.q_pre.shape[1], b.max_q_len, b.pre_tables.shape[1],
+                b.cu_seqlens_q, b.q_start, b.pre_tables, self.inputs.q_pre.shape[1], b.max_q_len,
                 self.pool.block_size, self.inputs.q_pre.shape[2], self.pool.num_kv_heads,
                 self.inputs.q_pre.shape[3], buf=self.plan_pre_buf,
             )

@@ -129,7 +129,7 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
         plan = getattr(paged, "prefill_plan", None)
         if plan is None and kernels.prefill_plan_pays(nseq, max_q, hq, h_kv, q.device):
             plan = kernels.prefill_plan(
-                cu_seqlens_q, q_start, b * sq, max_q, block_tables.shape[1], pool.block_size, hq, h_kv, d
+                cu_seqlens_q, q_start, block_tables, b * sq, max_q, pool.block_size, hq, h_kv, d
             )
             try:
                 paged.prefill_plan = plan

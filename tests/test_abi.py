@@ -105,19 +105,22 @@ def test_decode_plan_helpers():
     assert lib.ir_paged_decode_planned_workspace_bytes(64, 28, 4, 128) >= 256 * 16 * 128 * 4
 
 
-def _plan_bytes(num_seqs, max_q, n_rep, h_kv, d, cus=256):
+def _plan_bytes(num_seqs, max_q, n_rep, h_kv, d, cus=256, xcds=1):
     """The plan layout the header documents, restated: 4-wavefront workgroups of
     128 // n_rep query tokens (two per CU when the call has workgroups for
-    that), one entry per item plus the piece capacity (one piece per KV head of
-    every workgroup slot), the counters, and (max, sum) + D fp32 per partial
-    row of 128 columns; each region 256-byte aligned."""
+    that), one entry per workgroup -- (items + the piece capacity, one piece
+    per KV head of every workgroup slot) x KV heads, 1.5x that rounded to the
+    XCD count when the plan places work on XCDs -- the counters, and (max, sum)
+    + D fp32 per partial row of 128 columns; each region 256-byte aligned."""
     a = lambda x: (x + 255) // 256 * 256  # noqa: E731
     tq = 128 // n_rep
     nqb = -(-max_q // tq)
     slots = 2 * cus if nqb * h_kv * num_seqs >= 2 * cus else cus
     cap = -(-slots // h_kv)
     rows = cap * h_kv * 128
-    return a((num_seqs * nqb + cap) * 8) + a(cap * h_kv * 4) + a(rows * 8) + a(rows * d * 4)
+    wgs = (num_seqs * nqb + cap) * h_kv
+    entries = xcds * -(-(wgs * 3 // 2) // xcds) if xcds > 1 else wgs
+    return a(entries * 8) + a(cap * h_kv * 4) + a(rows * 8) + a(rows * d * 4)
 
 
 def test_prefill_plan_helpers():
@@ -126,14 +129,16 @@ def test_prefill_plan_helpers():
     2 chunks: one per CU), nothing is planned for empty or invalid shapes, and a
     short plan buffer or a null pointer is refused before any device work."""
     lib = _lib.lib()
-    assert lib.ir_paged_prefill_plan_bytes(8, 512, 28, 4, 128) == _plan_bytes(8, 512, 7, 4, 128)
-    assert lib.ir_paged_prefill_plan_bytes(2, 512, 28, 4, 64) == _plan_bytes(2, 512, 7, 4, 64)
+    x = lib.ir_paged_prefill_plan_xcds()
+    assert x >= 1
+    assert lib.ir_paged_prefill_plan_bytes(8, 512, 28, 4, 128) == _plan_bytes(8, 512, 7, 4, 128, xcds=x)
+    assert lib.ir_paged_prefill_plan_bytes(2, 512, 28, 4, 64) == _plan_bytes(2, 512, 7, 4, 64, xcds=x)
     assert lib.ir_paged_prefill_plan_bytes(0, 512, 28, 4, 128) == 0
     assert lib.ir_paged_prefill_plan_bytes(8, 512, 28, 3, 128) == 0
     assert lib.ir_paged_prefill_plan_bytes(8, 512, 28, 4, 96) == 0
-    rc = lib.ir_paged_prefill_plan(None, None, 8, 4096, 512, 600, 16, 28, 4, 128, None, 7, None)
+    rc = lib.ir_paged_prefill_plan(None, None, None, 600, 8, 4096, 512, 600, 16, 28, 4, 128, 0, None, 7, None)
     assert rc == -1 and b"plan of" in lib.ir_last_error()
-    rc = lib.ir_paged_prefill_plan(None, None, 8, 4096, 512, 600, 16, 28, 4, 128, 256, 1 << 30, None)
+    rc = lib.ir_paged_prefill_plan(None, None, None, 600, 8, 4096, 512, 600, 16, 28, 4, 128, 0, 256, 1 << 30, None)
     assert rc == -1 and b"null" in lib.ir_last_error()
 
 

@@ -179,81 +179,140 @@ def _host_weights(case, tq, n_qblocks):
 def _plan_geometry(b, max_q, hq, hkv):
     """Items, entries and piece capacity of a plan: 4-wavefront workgroups of
     128 // n_rep query tokens, two per CU when the call has workgroups for
-    that, the capacity one piece per KV head of every workgroup slot."""
+    that, the capacity one piece per KV head of every workgroup slot; one
+    entry per workgroup, (items + capacity) x KV heads, 1.5x that rounded to
+    the XCD count when the plan places work on XCDs."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     tq = 128 // (hq // hkv)
     n_qblocks = -(-max_q // tq)
     slots = 2 * cus if n_qblocks * hkv * b >= 2 * cus else cus
     cap = -(-slots // hkv)
-    return tq, n_qblocks, slots, cap, b * n_qblocks + cap
+    wgs = (b * n_qblocks + cap) * hkv
+    x = kernels.prefill_plan_xcds()
+    entries = x * -(-(wgs * 3 // 2) // x) if x > 1 else wgs
+    return tq, n_qblocks, slots, cap, entries, x
 
 
 def _plan_entries(plan, entries):
     return plan.buf[: entries * 8].view(torch.int32).view(entries, 2).cpu().tolist()
 
 
+def _plan_order(rows, h_kv, x, w):
+    """How the plan placed its workgroups: "slots" -- rows of x entries, each
+    row holding one piece per slot of h_kv consecutive entries (its KV heads
+    in order), every slot's pieces in non-increasing weight and then empty --
+    or "global" -- the pieces in non-increasing weight, a piece's KV heads on
+    consecutive entries, then empty entries. None if neither."""
+    def weight(e, piece):
+        return -(-w[e // h_kv] // (piece & 0xFF))
+
+    def one_piece(grp):
+        return len({(e // h_kv, p) for e, p in grp}) == 1 and [e % h_kv for e, _ in grp] == list(range(h_kv))
+
+    used = sum(1 for e, _ in rows if e >= 0)
+    if all(e >= 0 for e, _ in rows[:used]) and all(e < 0 for e, _ in rows[used:]) and used % h_kv == 0:
+        pieces = [rows[k * h_kv:(k + 1) * h_kv] for k in range(used // h_kv)]
+        if all(one_piece(grp) for grp in pieces):
+            ws = [weight(*grp[0]) for grp in pieces]
+            if ws == sorted(ws, reverse=True):
+                return "global"
+    if h_kv < x and x % h_kv == 0 and len(rows) % x == 0:
+        for sl in range(x // h_kv):
+            ws = []
+            for r in range(len(rows) // x):
+                grp = rows[r * x + sl * h_kv: r * x + (sl + 1) * h_kv]
+                if all(e < 0 for e, _ in grp):
+                    ws.append(None)
+                    continue
+                if not one_piece(grp):
+                    return None
+                ws.append(weight(*grp[0]))
+            n = sum(1 for v in ws if v is not None)
+            if any(v is None for v in ws[:n]) or ws[:n] != sorted(ws[:n], reverse=True):
+                return None
+        return "slots"
+    return None
+
+
 @pytest.mark.parametrize("prefixes,q_lens", [
-    (None, None),  # the full 8 x 512-token workload
+    (None, None),  # the full 8 x 512-token workload, sequence pairs sharing their prefix blocks
     ([0, 37, 512, 1000, 3, 3, 0, 5], [1, 31, 100, 512, 0, 9, 64, 33]),  # ragged, one empty chunk
     ([0, 300], [256, 77]),  # few workgroups: one per CU, nothing cut
     ([9000, 0, 0, 0], [512, 40, 40, 40]),  # one very long item among short ones
 ])
-def test_prefill_plan_covers_every_item_heaviest_first(prefixes, q_lens):
-    """The device-built plan lists every item with work exactly once -- whole,
-    or as nparts pieces numbered 0..nparts-1 sharing one block of partial rows
-    (blocks disjoint, inside the capacity) -- pieces in non-increasing weight
-    (ceil(tiles / nparts); the weights here are below the plan's 2048 buckets,
-    so the order is exact), then (-1, 0). Items heavier than the mean load of a
-    workgroup slot x 1.5 (raised until the pieces fit the plan's capacity) are
-    cut, and no piece is heavier than that threshold."""
+@pytest.mark.parametrize("share_groups", [False, True])
+def test_prefill_plan_covers_every_item_heaviest_first(prefixes, q_lens, share_groups):
+    """The device-built plan lists every (item with work, KV head) exactly once
+    per piece -- whole, or as nparts pieces numbered 0..nparts-1 sharing one
+    block of partial rows (blocks disjoint, inside the capacity) -- and empty
+    entries elsewhere. Items heavier than the mean load of a workgroup slot x
+    1.5 (raised until the pieces fit the plan's capacity) are cut, and no piece
+    is heavier than that threshold. Order: one global heaviest-first order,
+    or, with share groups placed, rows of X entries holding one piece per slot
+    of 4 consecutive XCDs, every slot heaviest first (the weights here are
+    below the 256 weight ranges, so the order is exact). With share groups on
+    the full workload the plan keeps each (sequence pair, KV head) -- the pairs
+    share their prefix blocks -- on one XCD."""
     cfg = PrefillConfig("pf-plan", 8 if prefixes is None else len(prefixes), 512, 28, 4, 128, 16,
                         torch.bfloat16, 8192, seed=4)
     case = make_prefill_case(cfg, DEV, prefixes=prefixes, q_lens=q_lens)
     b, max_q = len(case.q_lens), max(case.q_lens)
-    tq, n_qblocks, slots, cap, entries = _plan_geometry(b, max_q, 28, 4)
-    plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.q.shape[0], max_q,
-                                case.block_tables[0].shape[1], 16, 28, 4, 128)
+    tq, n_qblocks, slots, cap, entries, x = _plan_geometry(b, max_q, 28, 4)
+    plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.block_tables[0], case.q.shape[0], max_q,
+                                16, 28, 4, 128, share_groups=share_groups)
+    assert plan.buf.numel() >= entries * 8
     rows = _plan_entries(plan, entries)
     w = _host_weights(case, tq, n_qblocks)
-    total = sum(x for x in w if x > 0)
+    total = sum(x_ for x_ in w if x_ > 0)
 
-    def pieces(x, t):
-        return min(16, -(-x // t)) if x > t else (1 if x >= 0 else 0)
+    def pieces(x_, t):
+        return min(16, -(-x_ // t)) if x_ > t else (1 if x_ >= 0 else 0)
 
     # the cut threshold: 1.5x the mean load of a workgroup slot (at least 8
     # tiles), raised to the smallest value whose cut pieces fit the capacity
     thresh = max(8, -(-total * 4 * 3 // (2 * slots)))
-    while sum(pieces(x, thresh) for x in w if x > thresh) > cap:
+    while sum(pieces(x_, thresh) for x_ in w if x_ > thresh) > cap:
         thresh += 1
     seen, blocks, piece_w = {}, set(), []
-    for item, piece in rows:
-        if item < 0:
+    for e, piece in rows:
+        if e < 0:
+            assert piece == 0
             continue
+        item, head = divmod(e, 4)
         np_, part, pb = piece & 0xFF, (piece >> 8) & 0xFF, piece >> 16
-        seen.setdefault(item, []).append((np_, part, pb))
+        seen.setdefault((item, head), []).append((np_, part, pb))
         piece_w.append(-(-w[item] // np_))
-    used = len(piece_w)
-    assert all(item >= 0 for item, _ in rows[:used]) and rows[used:] == [[-1, 0]] * (entries - used)
-    assert sorted(seen) == [i for i in range(len(w)) if w[i] >= 0]
-    for item, parts in seen.items():
+    assert sorted(seen) == [(i, h) for i in range(len(w)) if w[i] >= 0 for h in range(4)]
+    for (item, head), parts in seen.items():
         np_ = parts[0][0]
         assert sorted(p for _, p, _ in parts) == list(range(np_)) and len({(n, b_) for n, _, b_ in parts}) == 1
-        if np_ > 1:
+        assert parts[0][::2] == seen[(item, 0)][0][::2], "every KV head of an item is cut alike"
+        if np_ > 1 and head == 0:
             pb = parts[0][2]
             assert pb + np_ <= cap and not blocks & set(range(pb, pb + np_))
             blocks |= set(range(pb, pb + np_))
         assert (np_ > 1) == (w[item] > thresh)
-    assert piece_w == sorted(piece_w, reverse=True)
     assert max(piece_w) <= thresh
+    order = _plan_order(rows, 4, x, w)
+    assert order == "global" if not share_groups else order is not None
     if prefixes is not None and prefixes[0] == 9000:
         assert blocks, "the heaviest items of this workload must be cut"
+    if share_groups and prefixes is None and x > 4 and x % 4 == 0:
+        assert order == "slots"
+        xcds = {}
+        for k, (e, _) in enumerate(rows):
+            if e >= 0:
+                item, head = divmod(e, 4)
+                xcds.setdefault((item // n_qblocks // 2, head), set()).add(k % x)
+        assert all(len(v) == 1 for v in xcds.values()), xcds
 
 
 def test_prefill_plan_results_match_the_unplanned_call():
     """The same calls with and without a plan: equal outputs (bit for bit where
     no item is cut; within fp32 rounding of the log-sum-exp merge where one is)
     and the same error flags -- the full workload, ragged chunks, a packed
-    mixed step, bad block ids -- and each within the bar of the oracle."""
+    mixed step, bad block ids -- and each within the bar of the oracle; a plan
+    placing share groups gives the default plan's outputs bit for bit."""
     cases = [
         make_prefill_case("qwen7b-prefill", DEV),
         make_prefill_case("qwen7b-prefill", DEV, prefixes=[0, 37, 512, 1000, 3, 3, 0, 5],
@@ -269,17 +328,22 @@ def test_prefill_plan_results_match_the_unplanned_call():
         if i == 1:
             bt[3, 5] = case.pool_blocks + 3  # a bad block id inside sequence 3's keys
         b, max_q = len(case.q_lens), max(case.q_lens)
-        plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.q.shape[0], max_q, bt.shape[1],
+        plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, bt, case.q.shape[0], max_q,
                                     cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim)
+        plan_g = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, bt, case.q.shape[0], max_q,
+                                      cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim,
+                                      buf=torch.empty_like(plan.buf), share_groups=True)
         outs, errs = [], []
-        for pl in (None, plan):
+        for pl in (None, plan, plan_g):
             err = torch.zeros(1, dtype=torch.int32, device=DEV)
             outs.append(kernels.paged_prefill(case.q, case.k_cache, case.v_cache, bt, case.cu_seqlens_q,
                                               case.q_start, max_q, cfg.block_size, cfg.scale, err_flags=err,
                                               plan=pl))
             errs.append(err)
         torch.cuda.synchronize()
-        assert errs[0].item() == errs[1].item() == (ERR_BLOCK_RANGE if i == 1 else 0)
+        assert errs[0].item() == errs[1].item() == errs[2].item() == (ERR_BLOCK_RANGE if i == 1 else 0)
+        # the placement changes the schedule only: both plans give identical outputs
+        assert torch.equal(outs[1], outs[2]), cfg.name
         cut = any((piece & 0xFF) > 1 for item, piece in _plan_entries(
             plan, _plan_geometry(b, max_q, cfg.num_q_heads, cfg.num_kv_heads)[4]) if item >= 0)
         assert cut or i != 3, f"{cfg.name}: its heaviest items must be cut"
@@ -387,9 +451,8 @@ def test_prefill_plan_and_kernel_replay_in_a_hip_graph():
     out = torch.empty_like(case.q)
 
     def call():
-        plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.q.shape[0], max_q,
-                                    case.block_tables[0].shape[1], cfg.block_size, cfg.num_q_heads,
-                                    cfg.num_kv_heads, cfg.head_dim, buf=buf)
+        plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.block_tables[0], case.q.shape[0], max_q,
+                                    cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, buf=buf)
         kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[0], case.cu_seqlens_q,
                               case.q_start, max_q, cfg.block_size, cfg.scale, out=out, plan=plan)
 
