@@ -27,8 +27,11 @@
 // default for batches that fill the CUs twice over. Smaller batches take
 // 4-wavefront workgroups on a 3-deep ring whose next tile's scores run beside
 // the current tile's exponentials (one per CU, up to 512 registers: the
-// shortest critical path when the CUs are not full). 8-wavefront lockstep
-// workgroups (256 columns) are kept for comparison (IR_PREFILL_WAVES=8).
+// shortest critical path when the CUs are not full). 8-wavefront workgroups
+// (256 columns, 2-deep ring) serve GQA groups wider than 128 query heads and
+// IR_PREFILL_WAVES=8; on 8 x 512-token chunks they measured 197 us against
+// 181 us for two 4-wavefront workgroups per CU, although each staged tile
+// feeds twice the columns.
 //
 // Plan (ir_paged_prefill_plan, built on the device once per step, shared by
 // every layer): one entry per workgroup, (item, KV head, piece). The pieces
@@ -1018,7 +1021,9 @@ PrefillGeometry prefill_geometry(int max_q_len, int n_rep, int num_kv_heads, int
   g.n_qblocks = (max_q_len + g.tq - 1) / g.tq;
   const int cus = device_cus();
   const int64_t wgs = (int64_t)g.n_qblocks * num_kv_heads * num_seqs;
-  const bool ring2 = k.ring2 >= 0 ? k.ring2 == 1 : g.nw == 4 && wgs >= 2 * (int64_t)cus;
+  // 8 wavefronts always take the 2-deep ring (224 registers; their 3-deep
+  // lockstep form needs more than 256 and spilled)
+  const bool ring2 = g.nw == 8 || (k.ring2 >= 0 ? k.ring2 == 1 : wgs >= 2 * (int64_t)cus);
   g.sched = ring2 ? kRing2 : kLockstep;
   g.slots = ring2 && g.nw == 4 ? 2 * cus : cus;
   return g;
@@ -1073,13 +1078,8 @@ int launch_prefill(const PrefillArgs& a, int sched, hipStream_t s) {
     }
   } else {
     const dim3 block(PShape<D, 8>::NT);
-    if (sched == kRing2) {
-      if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 2, kRing2>), g, block, 0, s, a);
-      else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 2, kRing2>), g, block, 0, s, a);
-    } else {
-      if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 2, kLockstep>), g, block, 0, s, a);
-      else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 2, kLockstep>), g, block, 0, s, a);
-    }
+    if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 2, kRing2>), g, block, 0, s, a);
+    else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 2, kRing2>), g, block, 0, s, a);
   }
   return check_launch("ir_paged_prefill");
 }
