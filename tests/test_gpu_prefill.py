@@ -436,14 +436,19 @@ def test_prefill_flags_understated_max_q_len():
         assert bool(err.item() & ERR_CONTEXT_RANGE) == flagged, (max_q, err.item())
 
 
-def test_prefill_plan_and_kernel_replay_in_a_hip_graph():
-    """A step's plan build and prefill captured in one hipGraph (one 9,000-token
-    prefix among short ones, whose heaviest items are cut and merged through
-    the plan's counters): each of three replays -- with eager work clearing the
-    output and scribbling over the plan buffer in between -- equals the eager
-    planned call bit for bit."""
-    case = make_prefill_case(PrefillConfig("pf-long-g", 4, 0, 28, 4, 128, 16, torch.bfloat16, 0, seed=23), DEV,
-                             prefixes=[9000, 0, 17, 0], q_lens=[512, 40, 40, 300])
+@pytest.mark.parametrize("share_groups", [False, True])
+def test_prefill_plan_and_kernel_replay_in_a_hip_graph(share_groups):
+    """A step's plan build and prefill captured in one hipGraph: each of three
+    replays -- with eager work clearing the output and scribbling over the plan
+    buffer in between -- equals the eager planned call bit for bit. Default
+    placement: one 9,000-token prefix among short ones, whose heaviest items are
+    cut and merged through the plan's counters; share groups: the 8 x 512-token
+    workload, whose sequence pairs share prefix blocks."""
+    if share_groups:
+        case = make_prefill_case("qwen7b-prefill", DEV)
+    else:
+        case = make_prefill_case(PrefillConfig("pf-long-g", 4, 0, 28, 4, 128, 16, torch.bfloat16, 0, seed=23), DEV,
+                                 prefixes=[9000, 0, 17, 0], q_lens=[512, 40, 40, 300])
     cfg = case.config
     b, max_q = len(case.q_lens), max(case.q_lens)
     buf = torch.empty(kernels.prefill_plan_bytes(b, max_q, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim),
@@ -452,7 +457,8 @@ def test_prefill_plan_and_kernel_replay_in_a_hip_graph():
 
     def call():
         plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.block_tables[0], case.q.shape[0], max_q,
-                                    cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, buf=buf)
+                                    cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, buf=buf,
+                                    share_groups=share_groups)
         kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[0], case.cu_seqlens_q,
                               case.q_start, max_q, cfg.block_size, cfg.scale, out=out, plan=plan)
 
