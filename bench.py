@@ -76,6 +76,9 @@ def _parse() -> argparse.Namespace:
                    help="decode: the seam's choice (default: kernels.decode_plan_pays), "
                    "balanced plan + run, or fixed split-KV partitions; prefill: the seam's choice "
                    "(kernels.prefill_plan_pays), the work plan, or none")
+    p.add_argument("--pairs", action="store_true",
+                   help="decode: plan with share groups -- sequences 2i, 2i+1 whose block tables share prefix "
+                   "blocks run as one unit per KV head, the shared blocks read once (--config qwen7b-pairs)")
     p.add_argument("--placement", choices=("global", "share-groups"), default="global",
                    help="prefill: the work plan's placement -- one global heaviest-first order, or each "
                    "(shared-prefix group, KV head) on one XCD (fewer bytes fetched)")
@@ -170,7 +173,8 @@ def _gpu_decode(case, args):
         planned = args.schedule == "planned" and kernels.decode_plan_bytes(b, hq, hkv, max_blocks, bs) > 0
     info = {"schedule": "planned" if planned else "fixed"}
     if planned:
-        plans = [kernels.decode_plan(bt, case.context_lens, hq, case.k_cache, bs) for bt in case.block_tables]
+        plans = [kernels.decode_plan(bt, case.context_lens, hq, case.k_cache, bs, share_groups=args.pairs)
+                 for bt in case.block_tables]
         ws_bytes = kernels.planned_workspace_bytes(b, hq, hkv, cfg.head_dim)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         ctr = torch.zeros(kernels.decode_num_counters(b, hq, hkv), dtype=torch.int32, device=dev)
@@ -182,7 +186,8 @@ def _gpu_decode(case, args):
 
         def plan(i: int) -> None:
             p = i % rot
-            kernels.decode_plan(case.block_tables[p], case.context_lens, hq, case.k_cache, bs, buf=plans[p].buf)
+            kernels.decode_plan(case.block_tables[p], case.context_lens, hq, case.k_cache, bs, buf=plans[p].buf,
+                                share_groups=args.pairs)
 
         def call(i: int) -> None:
             if i % args.layers == 0:
@@ -190,7 +195,8 @@ def _gpu_decode(case, args):
             run(i)
 
         info.update({"layers_per_plan": args.layers, "plan_bytes": int(plans[0].buf.numel()),
-                     "workspace_bytes": ws_bytes})
+                     "workspace_bytes": ws_bytes, "pairs": bool(args.pairs),
+                     "pairs_formed": int(plans[0].buf[:16].view(torch.int32)[3].item())})
     else:
         part = args.partition or kernels.default_partition(b, hkv, max_blocks, bs)
         ws_bytes = kernels.decode_workspace_bytes(b, hq, hkv, cfg.head_dim, max_blocks, bs, part)
@@ -907,10 +913,12 @@ def main() -> int:
     case = make_decode_case(args.config, "cuda", rotations=args.rotations)
     cfg = case.config
     kv = case.kv_bytes
+    # bytes the kernel reads: with pairs, a shared prefix block once per pair
+    read = case.unique_kv_bytes if args.pairs else kv
     info, eager_ms, graph_ms, kernel_ms, outs = _gpu_decode(case, args)
     us = graph_ms * 1e3
     gbps = kv / (graph_ms * 1e-3) / 1e9
-    kgbps = kv / (kernel_ms * 1e-3) / 1e9
+    kgbps = read / (kernel_ms * 1e-3) / 1e9
     check = None
     if args.check:
         from oracle import naive as O
@@ -923,7 +931,8 @@ def main() -> int:
     if args.copy_calib_mib > 0:
         _copy_calibration(args.copy_calib_mib)
     cpu = _cpu_baseline(case, args) if args.cpu_iters > 0 else None
-    traffic, traffic_src = _traffic(f"decode_{'planned_' if info['schedule'] == 'planned' else ''}{args.config}")
+    traffic, traffic_src = _traffic(f"decode_{'planned_' if info['schedule'] == 'planned' else ''}{args.config}"
+                                    f"{'-pairs' if args.pairs else ''}")
     esize = torch.tensor([], dtype=cfg.dtype).element_size()
     line = {
         "metric": METRIC,
@@ -947,6 +956,7 @@ def main() -> int:
             "num_seqs": cfg.num_seqs,
             "sum_ctx": int(case.context_lens.long().sum()),
             "kv_bytes_per_call": kv,
+            "unique_kv_bytes_per_call": case.unique_kv_bytes,
             "rotations": args.rotations,
             **info,
             "bytes_per_token": 2 * cfg.num_kv_heads * cfg.head_dim * esize,

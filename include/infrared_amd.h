@@ -51,12 +51,15 @@ enum {
   IR_ERR_SLOT_RANGE = 1,     /* scatter slot >= num_slots (write skipped) */
   IR_ERR_BLOCK_RANGE = 2,    /* block id outside [0, num_blocks) (block masked) */
   IR_ERR_CONTEXT_RANGE = 4,  /* context_len > max_blocks*block_size (clamped) or < 0 */
-  IR_ERR_GATHER_RANGE = 8    /* gather slot outside [0, num_slots) (key masked) */
+  IR_ERR_GATHER_RANGE = 8,   /* gather slot outside [0, num_slots) (key masked) */
+  IR_ERR_PLAN = 16           /* a decode plan with sequence pairs run without IR_PLAN_SHARE_GROUPS
+                                (nothing written) */
 };
 
-/* flags of ir_paged_prefill_plan */
+/* flags of ir_paged_prefill_plan, ir_paged_decode_plan and ir_paged_decode_planned */
 enum {
-  IR_PLAN_SHARE_GROUPS = 1  /* keep each shared-prefix group's KV head on one XCD */
+  IR_PLAN_SHARE_GROUPS = 1  /* prefill: keep each shared-prefix group's KV head on one XCD;
+                               decode: run sequence pairs that share prefix blocks as one unit */
 };
 
 /* Message of the last failed call on this thread ("" if none). */
@@ -227,6 +230,16 @@ int ir_paged_decode_noalloc(const void* q, int64_t q_seq_stride, int64_t q_head_
  *   strides must be those the plan was built for; q/out as in ir_paged_decode.
  *   Calls sharing a workspace must be stream-ordered; a plan may be rebuilt
  *   only after the runs that read it.
+ * flags: IR_PLAN_SHARE_GROUPS (plan and run alike; taken when a KV head has at
+ *   most 8 query heads) pairs sequences b, b + 1 whose block tables begin with
+ *   the same block ids -- the blocks the prefix cache hands sequences with a
+ *   common prompt prefix (infrared/cache/block_manager.py:209-234,
+ *   match_prefix) -- into one unit per KV head: both sequences' query heads in
+ *   the MFMA columns one sequence leaves empty, so the shared blocks (those
+ *   wholly inside both contexts) are read once for the pair. Runs of
+ *   consecutive sharing sequences pair from their start. Outputs are the same
+ *   attention (each column sees exactly its sequence's keys). A plan that
+ *   holds pairs run without the flag writes nothing and sets IR_ERR_PLAN.
  */
 int64_t ir_paged_decode_plan_bytes(int num_seqs, int num_q_heads, int num_kv_heads,
                                    int max_blocks_per_seq, int block_size);
@@ -236,13 +249,14 @@ int ir_paged_decode_plan(const int32_t* block_tables, int64_t bt_stride, int max
                          const int32_t* context_lens, int num_seqs, int num_q_heads,
                          int num_kv_heads, int block_size, int64_t num_blocks,
                          int64_t cache_slot_stride, int64_t cache_head_stride, int dtype,
-                         void* plan, int64_t plan_bytes, int32_t* err_flags, ir_stream_t stream);
+                         int flags, void* plan, int64_t plan_bytes, int32_t* err_flags,
+                         ir_stream_t stream);
 int ir_paged_decode_planned(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
                             const void* k_cache, const void* v_cache, int64_t cache_slot_stride,
                             void* out, int64_t out_seq_stride, int64_t out_head_stride,
                             int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                             int max_blocks_per_seq, int block_size, float scale, int dtype,
-                            const void* plan, int32_t* counters, int64_t num_counters,
+                            int flags, const void* plan, int32_t* counters, int64_t num_counters,
                             void* workspace, int64_t workspace_bytes, int32_t* err_flags,
                             ir_stream_t stream);
 

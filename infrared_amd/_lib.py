@@ -24,6 +24,7 @@ ERR_SLOT_RANGE = 1
 ERR_BLOCK_RANGE = 2
 ERR_CONTEXT_RANGE = 4
 ERR_GATHER_RANGE = 8
+ERR_PLAN = 16
 
 _c_i32, _c_i64, _c_f32, _c_p = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -68,12 +69,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ir_paged_decode_plan": (
         _c_i32,
         [_c_p, _c_i64, _c_i32, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_i64, _c_i64,
-         _c_i32, _c_p, _c_i64, _c_p, _c_p],
+         _c_i32, _c_i32, _c_p, _c_i64, _c_p, _c_p],
     ),
     "ir_paged_decode_planned": (
         _c_i32,
         [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32,
-         _c_i32, _c_i32, _c_i32, _c_f32, _c_i32, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p],
+         _c_i32, _c_i32, _c_i32, _c_f32, _c_i32, _c_i32, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p],
     ),
     "ir_paged_attention_masked": (
         _c_i32,

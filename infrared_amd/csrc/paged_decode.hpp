@@ -141,10 +141,15 @@ __device__ __forceinline__ uint32_t load_tile(const DecodeArgs& a, const int32_t
 }
 
 // kmask: which of this lane's keys 4r+g are usable; a tile whose keys are
-// all usable in every lane takes the unmasked path.
+// all usable in every lane takes the unmasked path. col_on: whether this
+// lane's query column attends the tile at all (a unit shared by two sequences
+// runs each one's private tiles with the other's columns off). An off column
+// gets -inf scores, so zero probabilities; the V rows stay, since a lane's V
+// operand serves every column of the PV product.
 template <int DT, int D>
 __device__ __forceinline__ void compute_tile(const Tile<DT, D>& tl, const uint32_t (&qr)[TileShape<DT, D>::KDW],
-                                             uint32_t kmask, float scale_log2, uint8_t* kst, int lane, State<D>& st) {
+                                             uint32_t kmask, float scale_log2, uint8_t* kst, int lane, State<D>& st,
+                                             bool col_on = true) {
   uint32_t kop[TileShape<DT, D>::KDW];
   kstage_transpose<DT, D>(kst, lane, tl.k, kop);
   const f32x4 s = qk_tile<DT, D>(kop, qr);
@@ -154,14 +159,14 @@ __device__ __forceinline__ void compute_tile(const Tile<DT, D>& tl, const uint32
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       vok[r] = true;
-      sv[r] = s[r] * scale_log2;
+      sv[r] = col_on ? s[r] * scale_log2 : kNegInf;
     }
     softmax_pv<DT, D, true>(sv, tl.v, vok, st);
   } else {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       vok[r] = (kmask >> r) & 1u;
-      sv[r] = vok[r] ? s[r] * scale_log2 : kNegInf;
+      sv[r] = vok[r] && col_on ? s[r] * scale_log2 : kNegInf;
     }
     softmax_pv<DT, D, false>(sv, tl.v, vok, st);
   }

@@ -49,15 +49,17 @@ constexpr int kPlanRun = 64;        // tile facts per wavefront and run (one per
 constexpr int kPlanMinTiles = 16;   // smallest slice
 
 // Plan regions (byte offsets, 256-byte aligned):
-//   hdr[8]             T, R, number of sequences with no usable key
+//   hdr[8]             T, R, number of sequences with no usable key, number of pairs
 //   seq_pre[B + 1]     list tiles before sequence b, per unit
 //   empty[B]           sequences with no usable key
+//   pair[B]            shared tiles of a pair's first sequence, -1 for its second, 0 alone
 //   whdr[G][NW][8]     per wavefront: wlo, count, first unit, last unit, slice lo, hi,
 //                      the slice's first and last unit
 //   first[G][NW][64]   the first 64 tile facts of each wavefront
-//   facts[T_cap]       every tile's facts in list order
+//   facts[T_cap]       every tile's facts in list order: (pool offset / 16 B,
+//                      unit << 7 | column mask << 5 | valid keys)
 struct PlanLayout {
-  int64_t hdr, seq_pre, empty, whdr, first, facts, total;
+  int64_t hdr, seq_pre, empty, pair, whdr, first, facts, total;
 };
 
 PlanLayout plan_layout(int64_t num_seqs, int64_t grid, int64_t t_cap) {
@@ -66,7 +68,8 @@ PlanLayout plan_layout(int64_t num_seqs, int64_t grid, int64_t t_cap) {
   p.hdr = 0;
   p.seq_pre = al(p.hdr + 8 * 4);
   p.empty = al(p.seq_pre + (num_seqs + 1) * 4);
-  p.whdr = al(p.empty + num_seqs * 4);
+  p.pair = al(p.empty + num_seqs * 4);
+  p.whdr = al(p.pair + num_seqs * 4);
   p.first = al(p.whdr + grid * kPlanWaves * 8 * 4);
   p.facts = al(p.first + grid * kPlanWaves * kPlanRun * 8);
   p.total = al(p.facts + t_cap * 8);
@@ -81,6 +84,7 @@ struct PlanArgs {
   int num_seqs, n_ups, n_hg, bs;
   int64_t num_blocks, c_slot16, c_head16;
   int min_tiles;
+  int pairs;  // pair sequences that share prefix blocks into one unit
   uint8_t* plan;
   PlanLayout ly;
   int32_t* err;
@@ -178,29 +182,71 @@ struct WaveSlots {
   float l[NW][16];
 };
 
+// Shared-prefix pairs. The prefix cache hands sequences with a common prompt
+// prefix the same blocks for it (infrared/cache/block_manager.py:209-234,
+// match_prefix), and a unit's query heads fill only n_rep of the 16 MFMA
+// columns. So with pairs on (and 2 n_rep <= 16, one head group per KV head),
+// sequence b and b + 1 whose tables begin with the same block ids become one
+// unit per KV head: columns 0..n_rep-1 are b's query heads, n_rep..2 n_rep-1
+// b + 1's, and the unit's tiles are the S shared tiles (both halves on), then
+// b's private tiles (b's half on), then b + 1's (b + 1's half on). The shared
+// prefix is read once instead of twice, each column still sees exactly its
+// own sequence's keys in ascending order, and no extra merge is needed. Runs
+// of consecutive sharing sequences pair from the run's start: (r, r+1),
+// (r+2, r+3), ...; the second sequence of a pair has no tiles of its own.
+// S counts the leading blocks equal in both tables that lie wholly inside
+// both contexts (found by comparing every such block, all candidates at once).
+
+// Inclusive max / sum over the block's threads in thread order, through
+// per-wavefront totals in `wsum` (NW entries); every thread gets its prefix.
+template <int NW, bool MAX>
+__device__ __forceinline__ int block_scan_incl(int x, int* wsum) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int v = __shfl_up(x, off);
+    if (lane >= off) x = MAX ? max(x, v) : x + v;
+  }
+  __syncthreads();
+  if (lane == 63) wsum[w] = x;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NW; ++i)
+    if (i < w) x = MAX ? max(x, wsum[i]) : x + wsum[i];
+  __syncthreads();
+  return x;
+}
+
 // Builds the plan: every workgroup scans the context lengths (block-wide
 // prefix sum, one int32 per sequence), finds its slice, and writes its
 // wavefronts' headers and tile facts; workgroup 0 also writes the header, the
-// prefix sums and the list of sequences with no usable key.
+// prefix sums, the list of sequences with no usable key and the pairs.
 template <int NW>
 __global__ __launch_bounds__(NW * 64) void paged_decode_plan_kernel(PlanArgs p) {
   constexpr int NT = NW * 64;
   __shared__ int s_pre[kPlanMaxSeqs + 1];
   __shared__ int s_ctx[kPlanMaxSeqs];
+  __shared__ int s_share[kPlanMaxSeqs];  // shared tiles of pair (b, b + 1) / of a pair's first sequence
+  __shared__ int s_lead[kPlanMaxSeqs];   // 1: first of a pair, -1: second, 0: alone
+  __shared__ int s_cand[kPlanMaxSeqs];   // candidate pairs (b, b + 1): b
+  __shared__ int s_mis[kPlanMaxSeqs];    // their first differing block (blocks wholly in both contexts)
+  __shared__ int s_wpre[kPlanMaxSeqs + 1];
   __shared__ int s_wsum[NW];
   __shared__ int s_seq[2];
-  __shared__ int s_nempty;
+  __shared__ int s_nempty, s_npairs, s_ncand;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int grp = blockIdx.x;
   const int B = p.num_seqs, n_ups = p.n_ups;
   int32_t* hdr = (int32_t*)(p.plan + p.ly.hdr);
-  if (tid == 0) s_nempty = 0;
+  if (tid == 0) {
+    s_nempty = 0;
+    s_npairs = 0;
+  }
 
   const int per = (B + NT - 1) / NT;
   const int b_lo = min(B, tid * per);
   const int b_hi = min(B, b_lo + per);
   const int cap = p.max_blocks * p.bs;
-  int mine = 0;
   for (int b = b_lo; b < b_hi; ++b) {
     int ctx = p.ctx[b];
     if (ctx < 0 || ctx > cap) {
@@ -208,8 +254,108 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_plan_kernel(PlanArgs p) 
       ctx = ctx < 0 ? 0 : cap;
     }
     s_ctx[b] = ctx;
-    mine += p.num_blocks > 0 ? (ctx + 15) >> 4 : 0;
+    s_share[b] = 0;
+    s_lead[b] = 0;
   }
+  __syncthreads();
+  auto tiles0 = [&](int b) { return p.num_blocks > 0 ? (s_ctx[b] + 15) >> 4 : 0; };
+  const int32_t* bt = p.bt;
+  if (p.pairs) {
+    // candidates: b and b + 1 begin with the same valid block id and a whole
+    // block lies inside both contexts; nbm = the blocks that do
+    auto cand_nbm = [&](int b) -> int {
+      if (b + 1 >= B) return 0;
+      const int nbm = min(s_ctx[b], s_ctx[b + 1]) / p.bs;
+      if (nbm < 1) return 0;
+      const int32_t f = bt[(int64_t)b * p.bt_stride];
+      return f >= 0 && (int64_t)f < p.num_blocks && f == bt[(int64_t)(b + 1) * p.bt_stride] ? nbm : 0;
+    };
+    int nc = 0;
+    for (int b = b_lo; b < b_hi; ++b) nc += cand_nbm(b) > 0;
+    const int c_incl = block_scan_incl<NW, false>(nc, s_wsum);
+    int k = c_incl - nc;
+    for (int b = b_lo; b < b_hi; ++b) {
+      const int nbm = cand_nbm(b);
+      if (nbm > 0) {
+        s_cand[k] = b;
+        s_mis[k] = nbm;
+        ++k;
+      }
+    }
+    if (tid == NT - 1) s_ncand = c_incl;
+    __syncthreads();
+    const int ncand = s_ncand;
+    // blocks 1 .. nbm-1 of every candidate are compared all at once: an
+    // exclusive scan of their counts by one wavefront, then a strided loop
+    if (tid < 64) {
+      const int run = (ncand + 63) / 64;
+      const int c_lo = min(ncand, lane * run), c_hi = min(ncand, c_lo + run);
+      int sum = 0;
+      for (int c2 = c_lo; c2 < c_hi; ++c2) sum += s_mis[c2] - 1;
+      int cin = sum;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_up(cin, off);
+        if (lane >= off) cin += v;
+      }
+      int r = cin - sum;
+      for (int c2 = c_lo; c2 < c_hi; ++c2) {
+        s_wpre[c2] = r;
+        r += s_mis[c2] - 1;
+      }
+      if (lane == 63) s_wpre[ncand] = cin;
+    }
+    __syncthreads();
+    const int W = s_wpre[ncand];
+    int kc = -1;
+    for (int idx = tid; idx < W; idx += NT) {
+      if (kc < 0 || idx >= s_wpre[kc + 1]) {  // the candidate whose range holds idx
+        int k0 = max(kc, 0), k1 = ncand;
+        while (k1 - k0 > 1) {
+          const int mid = (k0 + k1) >> 1;
+          if (s_wpre[mid] <= idx) k0 = mid;
+          else k1 = mid;
+        }
+        kc = k0;
+      }
+      const int b = s_cand[kc];
+      const int j = 1 + idx - s_wpre[kc];
+      if (bt[(int64_t)b * p.bt_stride + j] != bt[(int64_t)(b + 1) * p.bt_stride + j]) atomicMin(&s_mis[kc], j);
+    }
+    __syncthreads();
+    for (int c2 = tid; c2 < ncand; c2 += NT) s_share[s_cand[c2]] = s_mis[c2] * p.bs / 16;
+    __syncthreads();
+    // pairs from the start of each run of consecutive sharing sequences: the
+    // run start before this thread's sequences is an exclusive prefix max
+    int rmax = -1;
+    for (int b = b_lo; b < b_hi; ++b)
+      if (b == 0 || s_share[b - 1] == 0) rmax = b;
+    const int r_incl = block_scan_incl<NW, true>(rmax, s_wsum);
+    int rs = __shfl_up(r_incl, 1);
+    if (lane == 0) {
+      rs = -1;
+      for (int i = 0; i < w; ++i) rs = max(rs, s_wsum[i]);
+    }
+    for (int b = b_lo; b < b_hi; ++b) {
+      if (b == 0 || s_share[b - 1] == 0) rs = b;
+      if (s_share[b] > 0 && ((b - rs) & 1) == 0) s_lead[b] = 1;
+    }
+    __syncthreads();
+    for (int b = b_lo; b < b_hi; ++b)
+      if (b > 0 && s_lead[b - 1] == 1) s_lead[b] = -1;
+    __syncthreads();
+    for (int b = b_lo; b < b_hi; ++b)
+      if (s_lead[b] != 1) s_share[b] = 0;
+    __syncthreads();
+  }
+  // tiles of each sequence's units: a pair's first sequence carries both
+  // sequences' tiles less the shared ones, its second none
+  auto tiles = [&](int b) {
+    const int l = s_lead[b];
+    return l < 0 ? 0 : l > 0 ? tiles0(b) + tiles0(b + 1) - s_share[b] : tiles0(b);
+  };
+  int mine = 0;
+  for (int b = b_lo; b < b_hi; ++b) mine += tiles(b);
   int incl = mine;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
@@ -233,14 +379,16 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_plan_kernel(PlanArgs p) 
     int pre = incl - mine;
     for (int b = b_lo; b < b_hi; ++b) {
       s_pre[b] = pre;
-      const int nxt = pre + (p.num_blocks > 0 ? (s_ctx[b] + 15) >> 4 : 0);
+      const int nxt = pre + tiles(b);
       if (lo < hi) {
         if (pre * n_ups <= lo && lo < nxt * n_ups) s_seq[0] = b;
         if (pre * n_ups <= hi - 1 && hi - 1 < nxt * n_ups) s_seq[1] = b;
       }
       if (grp == 0) {
         ((int32_t*)(p.plan + p.ly.seq_pre))[b] = pre;
-        if (nxt == pre) ((int32_t*)(p.plan + p.ly.empty))[atomicAdd(&s_nempty, 1)] = b;
+        ((int32_t*)(p.plan + p.ly.pair))[b] = s_lead[b] > 0 ? s_share[b] : s_lead[b];
+        if (nxt == pre && s_lead[b] == 0) ((int32_t*)(p.plan + p.ly.empty))[atomicAdd(&s_nempty, 1)] = b;
+        if (s_lead[b] > 0) atomicAdd(&s_npairs, 1);
       }
       pre = nxt;
     }
@@ -252,6 +400,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_plan_kernel(PlanArgs p) 
     hdr[0] = T;
     hdr[1] = R;
     hdr[2] = s_nempty;
+    hdr[3] = s_npairs;
   }
   int32_t* wh = (int32_t*)(p.plan + p.ly.whdr) + ((int64_t)grp * NW + w) * 8;
   if (lo >= hi) {
@@ -297,15 +446,27 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_plan_kernel(PlanArgs p) 
       const int ts = s_pre[b + 1] - s_pre[b];
       const int rel = t - s_pre[b] * n_ups;
       const int j = fdiv(rel, ts);
-      const int tok0 = (rel - j * ts) * 16;
+      const int ti = rel - j * ts;  // tile of the unit
       const int kvh = p.n_hg == 1 ? j : fdiv(j, p.n_hg);
-      const int32_t bid = p.bt[(int64_t)b * p.bt_stride + tok0 / p.bs];
+      // which sequence's keys the tile holds, and which column halves see it
+      int sq = b, tok0 = ti * 16;
+      uint32_t cm = 1u;
+      if (s_lead[b] > 0) {
+        const int S = s_share[b], ta = tiles0(b);
+        if (ti < S) cm = 3u;
+        else if (ti >= ta) {
+          sq = b + 1;
+          tok0 = (ti - ta + S) * 16;
+          cm = 2u;
+        }
+      }
+      const int32_t bid = bt[(int64_t)sq * p.bt_stride + tok0 / p.bs];
       const bool ok = bid >= 0 && (int64_t)bid < p.num_blocks;
       bad |= !ok;
       const int64_t slot = ok ? (int64_t)bid * p.bs + (tok0 % p.bs) : 0;
       const uint32_t off16 = (uint32_t)(slot * p.c_slot16 + kvh * p.c_head16);
-      const int valid = ok ? min(16, s_ctx[b] - tok0) : 0;
-      const u32x2 f = {off16, ((uint32_t)(b * n_ups + j) << 5) | (uint32_t)valid};
+      const int valid = ok ? min(16, s_ctx[sq] - tok0) : 0;
+      const u32x2 f = {off16, ((uint32_t)(b * n_ups + j) << 7) | (cm << 5) | (uint32_t)valid};
       facts[t] = f;
       if (r0 == 0) first[lane] = f;
     }
@@ -347,7 +508,7 @@ __device__ __forceinline__ void slot_read(const float* row, int g, f32x4 (&acc)[
 // The decode over a plan: no scan, no block-table reads. A wavefront's header
 // and its first 64 tile facts sit at fixed addresses, so its first tile loads
 // go out one round trip after launch.
-template <int DT, int D, int NW, int DEPTH>
+template <int DT, int D, int NW, int DEPTH, bool PAIRS>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(DT == IR_DTYPE_F32 ? 1 : 2)))
 void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout ly) {
   typedef TileShape<DT, D> Sh;
@@ -358,6 +519,7 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
   __shared__ WaveSlots<2, D> stg;  // this slice's cross-workgroup partials: [0] first unit, [1] last unit
   __shared__ __attribute__((aligned(16))) uint8_t kstage[NW][KStage<DT, D>::BYTES];
   __shared__ int s_pre[kPlanMaxSeqs + 1];
+  __shared__ int s_pair[PAIRS ? kPlanMaxSeqs : 1];
   __shared__ int s_fl[NW];
   __shared__ int s_stg[2];
   __shared__ int s_last[2];
@@ -374,11 +536,19 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
   const int32_t* wh = (const int32_t*)(plan + ly.whdr) + ((int64_t)grp * NW + w) * 8;
   const u32x2* facts = (const u32x2*)(plan + ly.facts);
   const int R = hdr[1];
+  if (!PAIRS && hdr[3] != 0) {  // a plan with pairs needs the pair kernel
+    if (grp == 0 && tid == 0) flag_error(a.err, IR_ERR_PLAN);
+    return;
+  }
   const int wlo = wh[0], cnt_w = wh[1], fl = wh[2], ll = wh[3], lo = wh[4], hi = wh[5], u_first = wh[6];
   u32x2 f0 = ((const u32x2*)(plan + ly.first))[((int64_t)grp * NW + w) * kPlanRun + lane];
   {
     const int32_t* sp = (const int32_t*)(plan + ly.seq_pre);
     for (int b = tid; b <= B; b += NT) s_pre[b] = sp[b];
+    if constexpr (PAIRS) {
+      const int32_t* pp = (const int32_t*)(plan + ly.pair);
+      for (int b = tid; b < B; b += NT) s_pair[b] = pp[b];
+    }
   }
   if (tid < NW) s_fl[tid] = -1;
   if (tid < 2) s_stg[tid] = -1;
@@ -416,11 +586,17 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     x.ue = x.us + ts;
     return x;
   };
+  auto paired = [&](int b) { return PAIRS && s_pair[b] > 0; };
   auto q_of = [&](int u, uint32_t (&dst)[Sh::KDW]) {
     const int b = fdiv(u, n_ups);
     const int j = u - b * n_ups;
     const int hg = a.n_hg == 1 ? 0 : j - fdiv(j, a.n_hg) * a.n_hg;
     const int kvh = a.n_hg == 1 ? j : fdiv(j, a.n_hg);
+    if (paired(b)) {  // columns 0..n_rep-1: sequence b, n_rep..2 n_rep-1: b + 1
+      const int second = c >= a.n_rep;
+      load_query<DT, D>(a, b + second, kvh * a.n_rep + c - second * a.n_rep, c < 2 * a.n_rep, g, dst);
+      return;
+    }
     const int hl = hg * 16 + c;
     load_query<DT, D>(a, b, kvh * a.n_rep + hl, hl < a.n_rep, g, dst);
   };
@@ -446,18 +622,24 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
   // that no barrier of the end phase waits for its stores
   int cur = -1, keep = -1, pend = -1;
 
-  auto out_row = [&](const Lbl& x, int& h, int& nh) {
+  // Columns of unit x that are outputs, and column col's (sequence, head).
+  auto n_cols = [&](const Lbl& x) {
+    const int hg = a.n_hg == 1 ? 0 : x.j - fdiv(x.j, a.n_hg) * a.n_hg;
+    return paired(x.b) ? 2 * a.n_rep : min(16, a.n_rep - hg * 16);
+  };
+  auto out_of = [&](const Lbl& x, int col, int& sq, int& h) {
     const int hg = a.n_hg == 1 ? 0 : x.j - fdiv(x.j, a.n_hg) * a.n_hg;
     const int kvh = a.n_hg == 1 ? x.j : fdiv(x.j, a.n_hg);
-    nh = min(16, a.n_rep - hg * 16);
-    h = kvh * a.n_rep + hg * 16 + c;
+    const int second = paired(x.b) && col >= a.n_rep;
+    sq = x.b + second;
+    h = kvh * a.n_rep + hg * 16 + col - second * a.n_rep;
   };
   auto write_out = [&](const Lbl& x) {
-    int h, nh;
-    out_row(x, h, nh);
-    if (c < nh) {
+    if (c < n_cols(x)) {
+      int sq, h;
+      out_of(x, c, sq, h);
       const float inv = st.l > 0.f ? 1.f / st.l : 0.f;
-      uint8_t* row = (uint8_t*)a.out + ((int64_t)x.b * a.o_seq + (int64_t)h * a.o_head) * EB;
+      uint8_t* row = (uint8_t*)a.out + ((int64_t)sq * a.o_seq + (int64_t)h * a.o_head) * EB;
 #pragma unroll
       for (int r = 0; r < 4; ++r) store_acc_run<DT, D>(row + TILES * (4 * g + r) * EB, st, r, inv);
     }
@@ -501,12 +683,14 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     // computed) it issues nothing: the end phase reuses the ring's registers,
     // and a load still in flight into them would hold it up (padding loads
     // cost 0.7 us per call this way).
-    auto issue = [&](int i, Tile<DT, D>& tl, int& lb, bool real) -> uint32_t {
+    auto issue = [&](int i, Tile<DT, D>& tl, int& lb, bool& con, bool real) -> uint32_t {
       const int ii = real || i <= last ? i : last;
       const uint32_t off = (uint32_t)__builtin_amdgcn_readlane((int)info_off, ii);
       const uint32_t meta = (uint32_t)__builtin_amdgcn_readlane((int)info_meta, ii);
       if (real || i <= last) issue_tile<DT, D>(kc, vc, off, lo_off, tl);
-      lb = (int)(meta >> 5);
+      lb = (int)(meta >> 7);
+      // this lane's column half sees the tile (column mask bits 5, 6)
+      con = !PAIRS || ((meta >> (c >= a.n_rep ? 6 : 5)) & 1u);
       const int valid = (int)(meta & 31u);
       uint32_t m = 0;
 #pragma unroll
@@ -516,6 +700,7 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     Tile<DT, D> ring[DEPTH];
     uint32_t mk[DEPTH];
     int lb[DEPTH];
+    bool con[DEPTH];
     // Computes ring slot r, switching units (and queries) at a label change.
     auto step = [&](int r) {
       if (lb[r] != cur) {
@@ -535,10 +720,10 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
           qn_lbl = cur + 1;
         }
       }
-      compute_tile<DT, D>(ring[r], qr, mk[r], a.scale_log2, kstage[w], lane, st);
+      compute_tile<DT, D>(ring[r], qr, mk[r], a.scale_log2, kstage[w], lane, st, con[r]);
     };
 #pragma unroll
-    for (int r = 0; r < DEPTH; ++r) mk[r] = issue(r, ring[r], lb[r], false);
+    for (int r = 0; r < DEPTH; ++r) mk[r] = issue(r, ring[r], lb[r], con[r], false);
     int i = 0;
     // Steady state: every issue is a real tile and the body has no branch
     // around it (the branch cost 0.9 us per call on 64 sequences, even with
@@ -547,14 +732,14 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
 #pragma unroll
       for (int r = 0; r < DEPTH; ++r) {
         step(r);
-        mk[r] = issue(i + r + DEPTH, ring[r], lb[r], true);
+        mk[r] = issue(i + r + DEPTH, ring[r], lb[r], con[r], true);
       }
     }
     for (; i < cnt; i += DEPTH) {
 #pragma unroll
       for (int r = 0; r < DEPTH; ++r) {
         if (i + r < cnt) step(r);
-        mk[r] = issue(i + r + DEPTH, ring[r], lb[r], false);
+        mk[r] = issue(i + r + DEPTH, ring[r], lb[r], con[r], false);
       }
     }
   }
@@ -589,8 +774,7 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     const int u = k == 0 ? U0 : U1;
     if (u < 0) continue;
     const Lbl x = label(u);
-    int h0, nh;
-    out_row(x, h0, nh);
+    const int nh = n_cols(x);
     for (int it = tid; it < nh * (D / 4); it += NT) {
       const int hc = it / (D / 4);
       const int d0 = (it - hc * (D / 4)) * 4;
@@ -617,26 +801,19 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
   // after the other, the slices that end last -- which merge both -- took 2.15
   // instead of 1.17 us): items of 8 columns of one head, U0's first.
   constexpr int C8 = D / 8;
-  int n0 = 0, n1 = 0, b0 = 0, b1 = 0, h00 = 0, h01 = 0, f0r = 0, f1r = 0, np0 = 0, np1 = 0;
+  int n0 = 0, n1 = 0, f0r = 0, f1r = 0, np0 = 0, np1 = 0;
+  Lbl x0 = {}, x1 = {};
   if (U0 >= 0 && s_last[0]) {
-    const Lbl x = label(U0);
-    int nh;
-    out_row(x, h00, nh);
-    h00 -= c;
-    n0 = nh * C8;
-    b0 = x.b;
-    f0r = (x.us / R + U0) * 16;
-    np0 = (x.ue - 1) / R - x.us / R + 1;
+    x0 = label(U0);
+    n0 = n_cols(x0) * C8;
+    f0r = (x0.us / R + U0) * 16;
+    np0 = (x0.ue - 1) / R - x0.us / R + 1;
   }
   if (U1 >= 0 && s_last[1]) {
-    const Lbl x = label(U1);
-    int nh;
-    out_row(x, h01, nh);
-    h01 -= c;
-    n1 = nh * C8;
-    b1 = x.b;
-    f1r = (x.us / R + U1) * 16;
-    np1 = (x.ue - 1) / R - x.us / R + 1;
+    x1 = label(U1);
+    n1 = n_cols(x1) * C8;
+    f1r = (x1.us / R + U1) * 16;
+    np1 = (x1.ue - 1) / R - x1.us / R + 1;
   }
   for (int it = tid; it < n0 + n1; it += NT) {
     const bool k1 = it >= n0;
@@ -646,8 +823,9 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     float o[8], Ls;
     lse_merge_dev<D, 8, 8>(r_o, r_ml, (k1 ? f1r : f0r) + hc, 16, k1 ? np1 : np0, d0, o, Ls);
     const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
-    uint8_t* dst = (uint8_t*)a.out +
-                   ((int64_t)(k1 ? b1 : b0) * a.o_seq + (int64_t)((k1 ? h01 : h00) + hc) * a.o_head + d0) * EB;
+    int sq, h;
+    out_of(k1 ? x1 : x0, hc, sq, h);
+    uint8_t* dst = (uint8_t*)a.out + ((int64_t)sq * a.o_seq + (int64_t)h * a.o_head + d0) * EB;
     const float lo4[4] = {o[0], o[1], o[2], o[3]}, hi4[4] = {o[4], o[5], o[6], o[7]};
     store4<DT>(dst, lo4, inv);
     store4<DT>(dst + 4 * EB, hi4, inv);
@@ -658,14 +836,23 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
 }
 
 template <int DT, int D>
-void launch_planned_dt_d(const DecodeArgs& a, const uint8_t* plan, const PlanLayout& ly, int grid, hipStream_t s) {
+void launch_planned_dt_d(const DecodeArgs& a, const uint8_t* plan, const PlanLayout& ly, int grid, bool pairs,
+                         hipStream_t s) {
   // One tile in flight per wavefront: at ~6.6 TB/s four wavefronts per CU keep
   // HBM saturated with one tile each, and the shorter queues halve the latency
   // of the end phase's round trips (two tiles in flight: 0.4 us slower per call
   // on 64 sequences x 28/4 heads, contexts 512..4096).
-  hipLaunchKernelGGL((paged_decode_planned_kernel<DT, D, kPlanWaves, 1>), dim3(grid), dim3(kPlanWaves * 64), 0, s, a,
-                     plan, ly);
+  if (pairs)
+    hipLaunchKernelGGL((paged_decode_planned_kernel<DT, D, kPlanWaves, 1, true>), dim3(grid), dim3(kPlanWaves * 64), 0,
+                       s, a, plan, ly);
+  else
+    hipLaunchKernelGGL((paged_decode_planned_kernel<DT, D, kPlanWaves, 1, false>), dim3(grid), dim3(kPlanWaves * 64),
+                       0, s, a, plan, ly);
 }
+
+// Pairs fit one unit's 16 MFMA columns when a KV head has at most 8 query
+// heads (one head group).
+bool pairs_fit(int num_q_heads, int num_kv_heads) { return 2 * (num_q_heads / num_kv_heads) <= 16; }
 
 int n_hg_of(int num_q_heads, int num_kv_heads) { return (num_q_heads / num_kv_heads + 15) / 16; }
 
@@ -675,7 +862,7 @@ int64_t t_cap_of(int num_seqs, int n_ups, int max_blocks, int bs) {
 }
 
 // Shapes the plan takes: 16-token tiles inside one block, the prefix sums in
-// LDS, tile-list indices (and (unit << 5)) in int32, and fewer than 2^17 units,
+// LDS, tile-list indices (and (unit << 7)) in int32, and fewer than 2^17 units,
 // so the partial rows ((#CUs + units) x 16 x head_dim fp32) sit below the 2 GiB
 // the device-scope buffer accesses address.
 bool plannable(int num_seqs, int num_q_heads, int num_kv_heads, int max_blocks, int bs) {
@@ -709,10 +896,11 @@ extern "C" int64_t ir_paged_decode_planned_workspace_bytes(int num_seqs, int num
 extern "C" int ir_paged_decode_plan(const int32_t* block_tables, int64_t bt_stride, int max_blocks_per_seq,
                                     const int32_t* context_lens, int num_seqs, int num_q_heads, int num_kv_heads,
                                     int block_size, int64_t num_blocks, int64_t cache_slot_stride,
-                                    int64_t cache_head_stride, int dtype, void* plan, int64_t plan_bytes,
+                                    int64_t cache_head_stride, int dtype, int flags, void* plan, int64_t plan_bytes,
                                     int32_t* err_flags, ir_stream_t stream) {
   const int eb = dtype_bytes(dtype);
   IR_REQUIRE(eb > 0, "ir_paged_decode_plan: unknown dtype %d", dtype);
+  IR_REQUIRE((flags & ~IR_PLAN_SHARE_GROUPS) == 0, "ir_paged_decode_plan: unknown flags 0x%x", flags);
   IR_REQUIRE(plannable(num_seqs, num_q_heads, num_kv_heads, max_blocks_per_seq, block_size),
              "ir_paged_decode_plan: shape not plannable (1 <= batch <= %d, block size a multiple of 16)",
              kPlanMaxSeqs);
@@ -741,6 +929,7 @@ extern "C" int ir_paged_decode_plan(const int32_t* block_tables, int64_t bt_stri
   p.c_slot16 = slot16;
   p.c_head16 = head16;
   p.min_tiles = kPlanMinTiles;
+  p.pairs = (flags & IR_PLAN_SHARE_GROUPS) && pairs_fit(num_q_heads, num_kv_heads);
   p.plan = (uint8_t*)plan;
   const int grid = device_cus();
   p.ly = plan_layout(num_seqs, grid, t_cap_of(num_seqs, p.n_ups, max_blocks_per_seq, block_size));
@@ -754,11 +943,12 @@ extern "C" int ir_paged_decode_planned(const void* q, int64_t q_seq_stride, int6
                                        const void* v_cache, int64_t cache_slot_stride, void* out,
                                        int64_t out_seq_stride, int64_t out_head_stride, int num_seqs,
                                        int num_q_heads, int num_kv_heads, int head_dim, int max_blocks_per_seq,
-                                       int block_size, float scale, int dtype, const void* plan,
+                                       int block_size, float scale, int dtype, int flags, const void* plan,
                                        int32_t* counters, int64_t num_counters, void* workspace,
                                        int64_t workspace_bytes, int32_t* err_flags, ir_stream_t stream) {
   const int eb = dtype_bytes(dtype);
   IR_REQUIRE(eb > 0, "ir_paged_decode_planned: unknown dtype %d", dtype);
+  IR_REQUIRE((flags & ~IR_PLAN_SHARE_GROUPS) == 0, "ir_paged_decode_planned: unknown flags 0x%x", flags);
   if (head_dim != 64 && head_dim != 128)
     return fail(IR_EUNSUPPORTED, "ir_paged_decode_planned: head_dim %d not supported (64, 128)", head_dim);
   IR_REQUIRE(plannable(num_seqs, num_q_heads, num_kv_heads, max_blocks_per_seq, block_size),
@@ -806,18 +996,19 @@ extern "C" int ir_paged_decode_planned(const void* q, int64_t q_seq_stride, int6
       plan_layout(num_seqs, grid, t_cap_of(num_seqs, a.n_ups, max_blocks_per_seq, block_size));
   const uint8_t* pl = (const uint8_t*)plan;
   hipStream_t s = (hipStream_t)stream;
+  const bool pairs = (flags & IR_PLAN_SHARE_GROUPS) && pairs_fit(num_q_heads, num_kv_heads);
   switch (dtype) {
     case IR_DTYPE_BF16:
-      head_dim == 128 ? launch_planned_dt_d<IR_DTYPE_BF16, 128>(a, pl, ly, grid, s)
-                      : launch_planned_dt_d<IR_DTYPE_BF16, 64>(a, pl, ly, grid, s);
+      head_dim == 128 ? launch_planned_dt_d<IR_DTYPE_BF16, 128>(a, pl, ly, grid, pairs, s)
+                      : launch_planned_dt_d<IR_DTYPE_BF16, 64>(a, pl, ly, grid, pairs, s);
       break;
     case IR_DTYPE_F16:
-      head_dim == 128 ? launch_planned_dt_d<IR_DTYPE_F16, 128>(a, pl, ly, grid, s)
-                      : launch_planned_dt_d<IR_DTYPE_F16, 64>(a, pl, ly, grid, s);
+      head_dim == 128 ? launch_planned_dt_d<IR_DTYPE_F16, 128>(a, pl, ly, grid, pairs, s)
+                      : launch_planned_dt_d<IR_DTYPE_F16, 64>(a, pl, ly, grid, pairs, s);
       break;
     default:
-      head_dim == 128 ? launch_planned_dt_d<IR_DTYPE_F32, 128>(a, pl, ly, grid, s)
-                      : launch_planned_dt_d<IR_DTYPE_F32, 64>(a, pl, ly, grid, s);
+      head_dim == 128 ? launch_planned_dt_d<IR_DTYPE_F32, 128>(a, pl, ly, grid, pairs, s)
+                      : launch_planned_dt_d<IR_DTYPE_F32, 64>(a, pl, ly, grid, pairs, s);
   }
   return check_launch("ir_paged_decode_planned");
 }

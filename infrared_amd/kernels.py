@@ -229,6 +229,7 @@ class DecodePlan:
     slot_stride: int
     head_stride: int
     dtype: torch.dtype
+    share_groups: bool = False
 
 
 def decode_plan_bytes(num_seqs: int, num_q_heads: int, num_kv_heads: int, max_blocks: int, block_size: int) -> int:
@@ -275,10 +276,15 @@ def decode_plan(
     block_size: int,
     buf: torch.Tensor | None = None,
     err_flags: torch.Tensor | None = None,
+    share_groups: bool = False,
 ) -> DecodePlan:
     """Builds the balanced decode schedule of ``(block_tables, context_lens)``
     for query heads ``num_q_heads`` over pool layers shaped like ``k_cache``
-    ``[num_slots, H_kv, D]`` (any layer: all share the strides)."""
+    ``[num_slots, H_kv, D]`` (any layer: all share the strides).
+    ``share_groups``: consecutive sequences whose tables begin with the same
+    block ids (a shared cached prefix) run as pairs, one unit per KV head with
+    both sequences' query heads, so the shared blocks are read once (taken when
+    a KV head has at most 8 query heads)."""
     dev = require_device(block_tables, context_lens, k_cache)
     _cache_layer("decode_plan", k_cache)
     _check_tables("decode_plan", block_tables, context_lens)
@@ -294,11 +300,12 @@ def decode_plan(
     rc = lib().ir_paged_decode_plan(
         ptr(block_tables), block_tables.stride(0), max_blocks, ptr(context_lens), b, num_q_heads, h_kv,
         block_size, k_cache.shape[0] // block_size, k_cache.stride(0), k_cache.stride(1),
-        dtype_code(k_cache.dtype), ptr(buf), buf.numel(), ptr(err_flags), stream_ptr(dev),
+        dtype_code(k_cache.dtype), PLAN_SHARE_GROUPS if share_groups else 0, ptr(buf), buf.numel(), ptr(err_flags),
+        stream_ptr(dev),
     )
     check(rc, "ir_paged_decode_plan")
     return DecodePlan(buf, b, num_q_heads, h_kv, max_blocks, block_size, k_cache.shape[0] // block_size,
-                      k_cache.stride(0), k_cache.stride(1), k_cache.dtype)
+                      k_cache.stride(0), k_cache.stride(1), k_cache.dtype, bool(share_groups))
 
 
 def paged_decode_planned(
@@ -340,7 +347,8 @@ def paged_decode_planned(
     rc = lib().ir_paged_decode_planned(
         ptr(q), q.stride(0), q.stride(1), ptr(k_cache), ptr(v_cache), k_cache.stride(0), ptr(out),
         out.stride(0), out.stride(1), b, hq, plan.num_kv_heads, d, plan.max_blocks, plan.block_size,
-        float(scale), dtype_code(q.dtype), ptr(plan.buf), ptr(counters), n_ctr, ptr(workspace),
+        float(scale), dtype_code(q.dtype), PLAN_SHARE_GROUPS if plan.share_groups else 0, ptr(plan.buf),
+        ptr(counters), n_ctr, ptr(workspace),
         workspace.numel(), ptr(err_flags), stream_ptr(dev),
     )
     check(rc, "ir_paged_decode_planned")

@@ -174,13 +174,15 @@ def _decode(q, pool, layer_idx: int, block_tables, context_lens, holder, scale: 
     if hasattr(pool, "plan_buffer") and kernels.decode_plan_pays(b, hq, h_kv, max_blocks, pool.block_size, q.device):
         # balanced schedule: built by the step's first layer, reused by the
         # rest -- unless another context's plan has since taken the pool's
-        # plan buffer (two decode contexts run interleaved), then rebuilt
+        # plan buffer (two decode contexts run interleaved), then rebuilt.
+        # Consecutive sequences whose tables share prefix blocks (the prefix
+        # cache's reuse) run as pairs, reading those blocks once.
         plan = holder.decode_plan
         if plan is None or getattr(pool, "plan_owner", plan) is not plan:
             plan_bytes = kernels.decode_plan_bytes(b, hq, h_kv, max_blocks, pool.block_size)
             plan = kernels.decode_plan(
                 block_tables, context_lens, hq, k_layer, pool.block_size,
-                buf=pool.plan_buffer(plan_bytes), err_flags=err,
+                buf=pool.plan_buffer(plan_bytes), err_flags=err, share_groups=True,
             )
             holder.decode_plan = plan
             pool.plan_owner = plan

@@ -41,6 +41,7 @@ from infrared_amd._lib import (
     ERR_BLOCK_RANGE,
     ERR_CONTEXT_RANGE,
     ERR_GATHER_RANGE,
+    ERR_PLAN,
     ERR_SLOT_RANGE,
 )
 
@@ -49,6 +50,7 @@ _ERR_NAMES = {
     ERR_BLOCK_RANGE: "block id outside the pool",
     ERR_CONTEXT_RANGE: "context length outside the block table",
     ERR_GATHER_RANGE: "gather slot outside the pool",
+    ERR_PLAN: "decode plan with sequence pairs run without share groups",
 }
 
 

@@ -8,6 +8,10 @@ Decode workloads (one query token per sequence):
   context U{512..4096}, pool 1.25x the blocks needed.
 - ``qwen7b-skewed``: 16 seqs, 28/4 heads, head_dim 128, bf16, context
   round(lognormal(8, 1.2)) clipped to [16, 32768], pool 1.25x.
+- ``qwen7b-pairs``: ``qwen7b-bf16`` where sequences 2i and 2i+1 share the
+  block ids of the first half of the shorter context (whole blocks) -- a
+  cached prompt prefix the prefix cache hands both (parallel samples, a
+  common system prompt); the rest of each context is private.
 
 Prefill workload (``make_prefill_case``):
 
@@ -53,6 +57,7 @@ class DecodeConfig:
     lognormal_mu: float = 0.0
     lognormal_sigma: float = 1.0
     seed: int = 0
+    pair_share: float = 0.0  # sequences 2i, 2i+1 share this fraction of the shorter context (whole blocks)
 
     @property
     def n_rep(self) -> int:
@@ -73,6 +78,9 @@ DECODE_CONFIGS: dict[str, DecodeConfig] = {
     "qwen7b-skewed": DecodeConfig(
         "qwen7b-skewed", 16, 28, 4, 128, 16, torch.bfloat16, "lognormal", 16, 32768,
         lognormal_mu=8.0, lognormal_sigma=1.2, seed=3,
+    ),
+    "qwen7b-pairs": DecodeConfig(
+        "qwen7b-pairs", 64, 28, 4, 128, 16, torch.bfloat16, "uniform", 512, 4096, seed=2, pair_share=0.5
     ),
 }
 
@@ -97,6 +105,29 @@ class DecodeCase:
         c = self.config
         esize = torch.tensor([], dtype=c.dtype).element_size()
         return int(self.context_lens.long().sum()) * 2 * c.num_kv_heads * c.head_dim * esize
+
+    @property
+    def shared_tokens(self) -> int:
+        """Tokens the second sequence of each sharing pair reads from the
+        first one's blocks (whole shared blocks inside both contexts)."""
+        if self.config.pair_share <= 0:
+            return 0
+        bs, bt, ctx = self.config.block_size, self.block_tables[0].cpu(), self.context_lens.cpu().tolist()
+        n = 0
+        for i in range(0, len(ctx) - 1, 2):
+            full = min(ctx[i], ctx[i + 1]) // bs
+            j = 0
+            while j < full and int(bt[i, j]) == int(bt[i + 1, j]):
+                j += 1
+            n += j * bs
+        return n
+
+    @property
+    def unique_kv_bytes(self) -> int:
+        """K+V bytes of the distinct keys: shared prefix blocks counted once."""
+        c = self.config
+        esize = torch.tensor([], dtype=c.dtype).element_size()
+        return (int(self.context_lens.long().sum()) - self.shared_tokens) * 2 * c.num_kv_heads * c.head_dim * esize
 
 
 def context_lengths(cfg: DecodeConfig, gen: torch.Generator) -> torch.Tensor:
@@ -138,6 +169,10 @@ def make_decode_case(
         for i, n in enumerate(nblk.tolist()):
             bt[i, :n] = perm[off : off + n].to(torch.int32)
             off += n
+        if cfg.pair_share > 0:  # 2i+1 reads the first whole blocks of 2i's table
+            for i in range(0, cfg.num_seqs - 1, 2):
+                sh = int(cfg.pair_share * min(int(ctx[i]), int(ctx[i + 1]))) // bs
+                bt[i + 1, :sh] = bt[i, :sh]
         tables.append(bt.to(device))
     dgen = torch.Generator(device=device).manual_seed(seed)
     num_slots = rotations * pool_blocks * bs

@@ -66,7 +66,7 @@ def test_validation_errors_report_codes_and_messages():
     )
     assert rc == -1 and b"multiple" in lib.ir_last_error()
     # a plan for a shape the plan does not take
-    rc = lib.ir_paged_decode_plan(None, 0, 16, None, 2000, 28, 4, 16, 100, 512, 128, 2, None, 0, None, None)
+    rc = lib.ir_paged_decode_plan(None, 0, 16, None, 2000, 28, 4, 16, 100, 512, 128, 2, 0, None, 0, None, None)
     assert rc == -1 and b"plannable" in lib.ir_last_error()
     # null pointers with work to do
     rc = lib.ir_paged_attention_masked(
