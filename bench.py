@@ -931,8 +931,8 @@ def main() -> int:
     if args.copy_calib_mib > 0:
         _copy_calibration(args.copy_calib_mib)
     cpu = _cpu_baseline(case, args) if args.cpu_iters > 0 else None
-    traffic, traffic_src = _traffic(f"decode_{'planned_' if info['schedule'] == 'planned' else ''}{args.config}"
-                                    f"{'-pairs' if args.pairs else ''}")
+    sched = ("pairs_" if args.pairs else "planned_") if info["schedule"] == "planned" else ""
+    traffic, traffic_src = _traffic(f"decode_{sched}{args.config}")
     esize = torch.tensor([], dtype=cfg.dtype).element_size()
     line = {
         "metric": METRIC,
@@ -972,7 +972,8 @@ def main() -> int:
             "traffic_source": traffic_src,
             "kernel_us": round(kernel_ms * 1e3, 2),
             "timed": (f"{'paged_decode_planned_kernel' if info['schedule'] == 'planned' else 'paged_decode_kernel'}"
-                      f" launches alone, {args.mode}, events on the launch stream"),
+                      f" launches alone, {args.mode}, events on the launch stream"
+                      + ("; achieved counts each shared prefix block once per pair" if args.pairs else "")),
         },
         "cpu_baseline": cpu,
     }

@@ -52,6 +52,7 @@ constexpr int kPlanMinTiles = 16;   // smallest slice
 //   hdr[8]             T, R, number of sequences with no usable key, number of pairs
 //   seq_pre[B + 1]     list tiles before sequence b, per unit
 //   empty[B]           sequences with no usable key
+//   share[B]           shared 16-key tiles of sequences b, b + 1 (ir_paged_decode_plan's pair scan)
 //   pair[B]            shared tiles of a pair's first sequence, -1 for its second, 0 alone
 //   whdr[G][NW][8]     per wavefront: wlo, count, first unit, last unit, slice lo, hi,
 //                      the slice's first and last unit
@@ -59,7 +60,7 @@ constexpr int kPlanMinTiles = 16;   // smallest slice
 //   facts[T_cap]       every tile's facts in list order: (pool offset / 16 B,
 //                      unit << 7 | column mask << 5 | valid keys)
 struct PlanLayout {
-  int64_t hdr, seq_pre, empty, pair, whdr, first, facts, total;
+  int64_t hdr, seq_pre, empty, share, pair, whdr, first, facts, total;
 };
 
 PlanLayout plan_layout(int64_t num_seqs, int64_t grid, int64_t t_cap) {
@@ -68,7 +69,8 @@ PlanLayout plan_layout(int64_t num_seqs, int64_t grid, int64_t t_cap) {
   p.hdr = 0;
   p.seq_pre = al(p.hdr + 8 * 4);
   p.empty = al(p.seq_pre + (num_seqs + 1) * 4);
-  p.pair = al(p.empty + num_seqs * 4);
+  p.share = al(p.empty + num_seqs * 4);
+  p.pair = al(p.share + num_seqs * 4);
   p.whdr = al(p.pair + num_seqs * 4);
   p.first = al(p.whdr + grid * kPlanWaves * 8 * 4);
   p.facts = al(p.first + grid * kPlanWaves * kPlanRun * 8);
@@ -217,6 +219,35 @@ __device__ __forceinline__ int block_scan_incl(int x, int* wsum) {
   return x;
 }
 
+// The pair scan (before the plan, when pairs are on): workgroup b compares
+// the tables of sequences b and b + 1 over the blocks wholly inside both
+// contexts and writes share[b], the 16-key tiles of their common leading
+// blocks (0 unless both begin with the same valid block id).
+constexpr int kPairThreads = 256;
+
+__global__ __launch_bounds__(kPairThreads) void paged_decode_pair_kernel(PlanArgs p) {
+  __shared__ int s_mis;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  int32_t* share = (int32_t*)(p.plan + p.ly.share);
+  const int cap = p.max_blocks * p.bs;
+  auto ctx_of = [&](int q) { return max(0, min(p.ctx[q], cap)); };
+  int nbm = 0;
+  if (b + 1 < p.num_seqs) nbm = min(ctx_of(b), ctx_of(b + 1)) / p.bs;
+  const int32_t* r0 = p.bt + (int64_t)b * p.bt_stride;
+  const int32_t* r1 = r0 + p.bt_stride;
+  const bool cand = nbm >= 1 && r0[0] >= 0 && (int64_t)r0[0] < p.num_blocks && r0[0] == r1[0];
+  if (!cand) {  // uniform over the workgroup
+    if (tid == 0) share[b] = 0;
+    return;
+  }
+  if (tid == 0) s_mis = nbm;
+  __syncthreads();
+  for (int j = 1 + tid; j < nbm; j += kPairThreads)
+    if (r0[j] != r1[j]) atomicMin(&s_mis, j);
+  __syncthreads();
+  if (tid == 0) share[b] = s_mis * p.bs / 16;
+}
+
 // Builds the plan: every workgroup scans the context lengths (block-wide
 // prefix sum, one int32 per sequence), finds its slice, and writes its
 // wavefronts' headers and tile facts; workgroup 0 also writes the header, the
@@ -228,12 +259,9 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_plan_kernel(PlanArgs p) 
   __shared__ int s_ctx[kPlanMaxSeqs];
   __shared__ int s_share[kPlanMaxSeqs];  // shared tiles of pair (b, b + 1) / of a pair's first sequence
   __shared__ int s_lead[kPlanMaxSeqs];   // 1: first of a pair, -1: second, 0: alone
-  __shared__ int s_cand[kPlanMaxSeqs];   // candidate pairs (b, b + 1): b
-  __shared__ int s_mis[kPlanMaxSeqs];    // their first differing block (blocks wholly in both contexts)
-  __shared__ int s_wpre[kPlanMaxSeqs + 1];
   __shared__ int s_wsum[NW];
   __shared__ int s_seq[2];
-  __shared__ int s_nempty, s_npairs, s_ncand;
+  __shared__ int s_nempty, s_npairs;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int grp = blockIdx.x;
   const int B = p.num_seqs, n_ups = p.n_ups;
@@ -259,74 +287,14 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_plan_kernel(PlanArgs p) 
   }
   __syncthreads();
   auto tiles0 = [&](int b) { return p.num_blocks > 0 ? (s_ctx[b] + 15) >> 4 : 0; };
-  const int32_t* bt = p.bt;
   if (p.pairs) {
-    // candidates: b and b + 1 begin with the same valid block id and a whole
-    // block lies inside both contexts; nbm = the blocks that do
-    auto cand_nbm = [&](int b) -> int {
-      if (b + 1 >= B) return 0;
-      const int nbm = min(s_ctx[b], s_ctx[b + 1]) / p.bs;
-      if (nbm < 1) return 0;
-      const int32_t f = bt[(int64_t)b * p.bt_stride];
-      return f >= 0 && (int64_t)f < p.num_blocks && f == bt[(int64_t)(b + 1) * p.bt_stride] ? nbm : 0;
-    };
-    int nc = 0;
-    for (int b = b_lo; b < b_hi; ++b) nc += cand_nbm(b) > 0;
-    const int c_incl = block_scan_incl<NW, false>(nc, s_wsum);
-    int k = c_incl - nc;
-    for (int b = b_lo; b < b_hi; ++b) {
-      const int nbm = cand_nbm(b);
-      if (nbm > 0) {
-        s_cand[k] = b;
-        s_mis[k] = nbm;
-        ++k;
-      }
-    }
-    if (tid == NT - 1) s_ncand = c_incl;
+    // s_share[b]: shared tiles of (b, b + 1), from the pair scan that ran
+    // before this launch; pairs from the start of each run of consecutive
+    // sharing sequences (the run start before this thread's sequences is an
+    // exclusive prefix max)
+    const int32_t* sh = (const int32_t*)(p.plan + p.ly.share);
+    for (int b = b_lo; b < b_hi; ++b) s_share[b] = sh[b];
     __syncthreads();
-    const int ncand = s_ncand;
-    // blocks 1 .. nbm-1 of every candidate are compared all at once: an
-    // exclusive scan of their counts by one wavefront, then a strided loop
-    if (tid < 64) {
-      const int run = (ncand + 63) / 64;
-      const int c_lo = min(ncand, lane * run), c_hi = min(ncand, c_lo + run);
-      int sum = 0;
-      for (int c2 = c_lo; c2 < c_hi; ++c2) sum += s_mis[c2] - 1;
-      int cin = sum;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int v = __shfl_up(cin, off);
-        if (lane >= off) cin += v;
-      }
-      int r = cin - sum;
-      for (int c2 = c_lo; c2 < c_hi; ++c2) {
-        s_wpre[c2] = r;
-        r += s_mis[c2] - 1;
-      }
-      if (lane == 63) s_wpre[ncand] = cin;
-    }
-    __syncthreads();
-    const int W = s_wpre[ncand];
-    int kc = -1;
-    for (int idx = tid; idx < W; idx += NT) {
-      if (kc < 0 || idx >= s_wpre[kc + 1]) {  // the candidate whose range holds idx
-        int k0 = max(kc, 0), k1 = ncand;
-        while (k1 - k0 > 1) {
-          const int mid = (k0 + k1) >> 1;
-          if (s_wpre[mid] <= idx) k0 = mid;
-          else k1 = mid;
-        }
-        kc = k0;
-      }
-      const int b = s_cand[kc];
-      const int j = 1 + idx - s_wpre[kc];
-      if (bt[(int64_t)b * p.bt_stride + j] != bt[(int64_t)(b + 1) * p.bt_stride + j]) atomicMin(&s_mis[kc], j);
-    }
-    __syncthreads();
-    for (int c2 = tid; c2 < ncand; c2 += NT) s_share[s_cand[c2]] = s_mis[c2] * p.bs / 16;
-    __syncthreads();
-    // pairs from the start of each run of consecutive sharing sequences: the
-    // run start before this thread's sequences is an exclusive prefix max
     int rmax = -1;
     for (int b = b_lo; b < b_hi; ++b)
       if (b == 0 || s_share[b - 1] == 0) rmax = b;
@@ -460,7 +428,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_plan_kernel(PlanArgs p) 
           cm = 2u;
         }
       }
-      const int32_t bid = bt[(int64_t)sq * p.bt_stride + tok0 / p.bs];
+      const int32_t bid = p.bt[(int64_t)sq * p.bt_stride + tok0 / p.bs];
       const bool ok = bid >= 0 && (int64_t)bid < p.num_blocks;
       bad |= !ok;
       const int64_t slot = ok ? (int64_t)bid * p.bs + (tok0 % p.bs) : 0;
@@ -934,6 +902,8 @@ extern "C" int ir_paged_decode_plan(const int32_t* block_tables, int64_t bt_stri
   const int grid = device_cus();
   p.ly = plan_layout(num_seqs, grid, t_cap_of(num_seqs, p.n_ups, max_blocks_per_seq, block_size));
   p.err = err_flags;
+  if (p.pairs)
+    hipLaunchKernelGGL(paged_decode_pair_kernel, dim3(num_seqs), dim3(kPairThreads), 0, (hipStream_t)stream, p);
   hipLaunchKernelGGL((paged_decode_plan_kernel<kPlanWaves>), dim3(grid), dim3(kPlanWaves * 64), 0,
                      (hipStream_t)stream, p);
   return check_launch("ir_paged_decode_plan");
