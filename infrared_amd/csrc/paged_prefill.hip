@@ -245,7 +245,9 @@ void paged_prefill_kernel(PrefillArgs a) {
   // load is issued (from slot 0 when unusable) and zeroed afterwards.
   auto slot_of = [&](int k, bool& use) -> int64_t {
     const bool in = k < kmax;
-    const int kk = in ? k : 0;
+    // an unusable key looks up the cache's first id, inside the staged
+    // window (key 0 would index below it once the window has moved)
+    const int kk = in ? k : bt_base * a.bs;
     if constexpr (FAST) {
       const int blk = kk >> a.bs_shift;
       const int32_t bid = bt_lds[blk - bt_base];
