@@ -419,15 +419,18 @@ __device__ __forceinline__ void lse_merge_dev(__amdgpu_buffer_rsrc_t r_o, __amdg
   }
 }
 
+// Output stores are non-temporal: the next kernel reads them, so nothing is
+// gained by leaving them dirty in this XCD's L2, whose write-back the end of
+// the kernel would then wait for (0.3 us per planned 64-sequence decode).
 template <int DT>
 __device__ __forceinline__ void store4(uint8_t* dst, const float (&o)[4], float scale) {
   if constexpr (DT == IR_DTYPE_F32) {
     const f32x4 x = {o[0] * scale, o[1] * scale, o[2] * scale, o[3] * scale};
-    *(f32x4*)dst = x;
+    __builtin_nontemporal_store(x, (f32x4*)dst);
   } else {
     using E = Elem<DT>;
     const u32x2 x = {E::pack2(o[0] * scale, o[1] * scale), E::pack2(o[2] * scale, o[3] * scale)};
-    *(u32x2*)dst = x;
+    __builtin_nontemporal_store(x, (u32x2*)dst);
   }
 }
 

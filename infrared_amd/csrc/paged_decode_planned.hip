@@ -143,7 +143,7 @@ __device__ __forceinline__ void issue_tile(const uint8_t* kc, const uint8_t* vc,
 }
 
 // Writes the TILES consecutive outputs acc[0..TILES)[r] (one O^T register row
-// of this lane) times `inv` to dst.
+// of this lane) times `inv` to dst (non-temporal, as store4).
 template <int DT, int D>
 __device__ __forceinline__ void store_acc_run(uint8_t* dst, const State<D>& st, int r, float inv) {
   constexpr int TILES = D / 16;
@@ -158,9 +158,9 @@ __device__ __forceinline__ void store_acc_run(uint8_t* dst, const State<D>& st, 
 #pragma unroll
     for (int n = 0; n < TILES; n += 2) wv[n / 2] = E::pack2(st.acc[n][r] * inv, st.acc[n + 1][r] * inv);
     if constexpr (TILES == 8)
-      *(u32x4*)dst = u32x4{wv[0], wv[1], wv[2], wv[3]};
+      __builtin_nontemporal_store(u32x4{wv[0], wv[1], wv[2], wv[3]}, (u32x4*)dst);
     else
-      *(u32x2*)dst = u32x2{wv[0], wv[1]};
+      __builtin_nontemporal_store(u32x2{wv[0], wv[1]}, (u32x2*)dst);
   }
 }
 
