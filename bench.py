@@ -224,6 +224,35 @@ def _gpu_decode(case, args):
     return info, eager_ms, call_ms, kernel_ms, outs
 
 
+def _gpu_scatter(case, args) -> dict:
+    """The decode step's KV-slot scatter (``PagedKVPool.write``, reported beside
+    the attention call): one new K and V row per sequence, at its last context
+    position, through ``ir_kv_scatter``. The rows written are copies of what the
+    pool already holds there, so the pool is left as it was."""
+    from infrared_amd import kernels
+
+    cfg = case.config
+    bs = cfg.block_size
+    pos = (case.context_lens.long() - 1).clamp(min=0)
+    bt = case.block_tables[0].long()
+    slots = bt.gather(1, (pos // bs)[:, None])[:, 0] * bs + pos % bs
+    k_new, v_new = case.k_cache[slots].clone(), case.v_cache[slots].clone()
+
+    def call(i: int) -> None:
+        kernels.kv_scatter(case.k_cache, case.v_cache, k_new, v_new, slots)
+
+    for i in range(args.warmup):
+        call(i)
+    torch.cuda.synchronize()
+    ms = _graph_ms(call, args.steps, "scatter")
+    esize = torch.tensor([], dtype=cfg.dtype).element_size()
+    nbytes = 2 * cfg.num_seqs * cfg.num_kv_heads * cfg.head_dim * esize * 2
+    return {"us_per_call": round(ms * 1e3, 3), "tokens": cfg.num_seqs, "bytes": nbytes,
+            "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 2),
+            "timed": "ir_kv_scatter of the step's new K/V rows (one per sequence; read + write bytes), "
+                     f"{args.mode} launches, events on the launch stream"}
+
+
 def _cpu_host() -> dict:
     """Host facts for the CPU baseline: the threads torch uses (the box's CPU
     share: OMP_NUM_THREADS), the CPUs the OS reports and the CPU model."""
@@ -928,6 +957,7 @@ def main() -> int:
             case.context_lens.cpu(), cfg.block_size, cfg.scale,
         )
         check = round((outs[0].float().cpu() - ref).abs().max().item(), 6)
+    scatter = _gpu_scatter(case, args) if args.mode == "graph" else None
     if args.copy_calib_mib > 0:
         _copy_calibration(args.copy_calib_mib)
     cpu = _cpu_baseline(case, args) if args.cpu_iters > 0 else None
@@ -976,6 +1006,7 @@ def main() -> int:
                       + ("; achieved counts each shared prefix block once per pair" if args.pairs else "")),
         },
         "cpu_baseline": cpu,
+        "scatter": scatter,
     }
     line["timing"] = dict(_REPLAY_STATS)
     if check is not None:
