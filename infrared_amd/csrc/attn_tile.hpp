@@ -420,8 +420,9 @@ __device__ __forceinline__ void lse_merge_dev(__amdgpu_buffer_rsrc_t r_o, __amdg
 }
 
 // Output stores are non-temporal: the next kernel reads them, so nothing is
-// gained by leaving them dirty in this XCD's L2, whose write-back the end of
-// the kernel would then wait for (0.3 us per planned 64-sequence decode).
+// gained by leaving them dirty in this XCD's L2 for the end of the kernel to
+// write back (measured neutral to 0.3 us faster per planned 64-sequence
+// decode, neutral for the prefill).
 template <int DT>
 __device__ __forceinline__ void store4(uint8_t* dst, const float (&o)[4], float scale) {
   if constexpr (DT == IR_DTYPE_F32) {
