@@ -985,7 +985,7 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PlanArgs a) 
 // IR_PREFILL_CUTS=0 keeps the plan from cutting items (order only).
 struct PrefillKnobs {
   int waves = 0;   // 0: 4, or 8 when 4 cannot hold a token's query heads
-  int ring2 = -1;  // -1: by grid size
+  int ring2 = -1;  // -1: the default (2-deep)
   bool cuts = true;
   PrefillKnobs() {
     if (const char* e = getenv("IR_PREFILL_WAVES")) waves = atoi(e) == 8 ? 8 : 4;
@@ -1008,24 +1008,24 @@ int plan_xcds() {
 
 // Workgroup shape and schedule of a prefill call, from its shapes alone (the
 // plan and every layer's call agree on it): 4 wavefronts (128 query columns)
-// on the 2-deep ring when the call has workgroups for two per CU, else on the
-// 3-deep ring; 8 wavefronts (256 columns) when a token's query heads need more
-// than 128 columns or on request. `slots`: workgroups resident at once.
+// on the 2-deep ring (the 3-deep ring only on request: it measured slower for
+// every call shape, 9-21% on grids of fewer than two workgroups per CU); 8
+// wavefronts (256 columns) when a token's query heads need more than 128
+// columns or on request. `slots`: workgroups resident at once.
 struct PrefillGeometry {
   int nw, tq, n_qblocks, sched, slots;
 };
 
-PrefillGeometry prefill_geometry(int max_q_len, int n_rep, int num_kv_heads, int num_seqs) {
+PrefillGeometry prefill_geometry(int max_q_len, int n_rep) {
   const PrefillKnobs& k = prefill_knobs();
   PrefillGeometry g;
   g.nw = (n_rep > PShape<128, 4>::COLS || k.waves == 8) ? 8 : 4;
   g.tq = (g.nw == 4 ? PShape<128, 4>::COLS : PShape<128, 8>::COLS) / n_rep;
   g.n_qblocks = (max_q_len + g.tq - 1) / g.tq;
   const int cus = device_cus();
-  const int64_t wgs = (int64_t)g.n_qblocks * num_kv_heads * num_seqs;
   // 8 wavefronts always take the 2-deep ring (224 registers; their 3-deep
   // lockstep form needs more than 256 and spilled)
-  const bool ring2 = g.nw == 8 || (k.ring2 >= 0 ? k.ring2 == 1 : wgs >= 2 * (int64_t)cus);
+  const bool ring2 = g.nw == 8 || k.ring2 != 0;
   g.sched = ring2 ? kRing2 : kLockstep;
   g.slots = ring2 && g.nw == 4 ? 2 * cus : cus;
   return g;
@@ -1096,7 +1096,7 @@ extern "C" int64_t ir_paged_prefill_plan_bytes(int num_seqs, int max_q_len, int 
   if (num_seqs <= 0 || max_q_len <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads ||
       num_q_heads / num_kv_heads > 256 || (head_dim != 64 && head_dim != 128))
     return 0;
-  const PrefillGeometry geo = prefill_geometry(max_q_len, num_q_heads / num_kv_heads, num_kv_heads, num_seqs);
+  const PrefillGeometry geo = prefill_geometry(max_q_len, num_q_heads / num_kv_heads);
   return plan_layout(geo, num_seqs, num_kv_heads, head_dim).total;
 }
 
@@ -1153,7 +1153,7 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
   a.num_seqs = num_seqs;
   a.total_q = total_q;
   a.n_rep = num_q_heads / num_kv_heads;
-  const PrefillGeometry geo = prefill_geometry(max_q_len, a.n_rep, num_kv_heads, num_seqs);
+  const PrefillGeometry geo = prefill_geometry(max_q_len, a.n_rep);
   a.nw = geo.nw;
   a.tq = geo.tq;
   a.n_qblocks = geo.n_qblocks;
@@ -1210,7 +1210,7 @@ extern "C" int ir_paged_prefill_plan(const int32_t* cu_seqlens_q, const int32_t*
              "ir_paged_prefill_plan: null pointer");
   IR_REQUIRE(bt_stride >= max_blocks_per_seq, "ir_paged_prefill_plan: bt_stride %lld below max_blocks_per_seq %d",
              (long long)bt_stride, max_blocks_per_seq);
-  const PrefillGeometry geo = prefill_geometry(max_q_len, num_q_heads / num_kv_heads, num_kv_heads, num_seqs);
+  const PrefillGeometry geo = prefill_geometry(max_q_len, num_q_heads / num_kv_heads);
   const PlanLayout ly = plan_layout(geo, num_seqs, num_kv_heads, head_dim);
   IR_REQUIRE(ly.entries <= 0x7fffffff && ly.cap_pieces < 65536 &&
                  (int64_t)num_seqs * geo.n_qblocks * num_kv_heads <= 0x7fffffff &&

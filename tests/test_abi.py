@@ -107,15 +107,15 @@ def test_decode_plan_helpers():
 
 def _plan_bytes(num_seqs, max_q, n_rep, h_kv, d, cus=256, xcds=1):
     """The plan layout the header documents, restated: 4-wavefront workgroups of
-    128 // n_rep query tokens (two per CU when the call has workgroups for
-    that), one entry per workgroup -- (items + the piece capacity, one piece
-    per KV head of every workgroup slot) x KV heads, 1.5x that rounded to the
-    XCD count when the plan places work on XCDs -- the counters, and (max, sum)
-    + D fp32 per partial row of 128 columns; each region 256-byte aligned."""
+    128 // n_rep query tokens (two resident per CU), one entry per workgroup --
+    (items + the piece capacity, one piece per KV head of every workgroup
+    slot) x KV heads, 1.5x that rounded to the XCD count when the plan places
+    work on XCDs -- the counters, and (max, sum) + D fp32 per partial row of
+    128 columns; each region 256-byte aligned."""
     a = lambda x: (x + 255) // 256 * 256  # noqa: E731
     tq = 128 // n_rep
     nqb = -(-max_q // tq)
-    slots = 2 * cus if nqb * h_kv * num_seqs >= 2 * cus else cus
+    slots = 2 * cus
     cap = -(-slots // h_kv)
     rows = cap * h_kv * 128
     wgs = (num_seqs * nqb + cap) * h_kv
@@ -124,9 +124,9 @@ def _plan_bytes(num_seqs, max_q, n_rep, h_kv, d, cus=256, xcds=1):
 
 
 def test_prefill_plan_helpers():
-    """A prefill plan's size follows its documented layout (8 chunks of 512
-    tokens at 28 / 4 heads: 29 blocks of 18 tokens each, two workgroups per CU;
-    2 chunks: one per CU), nothing is planned for empty or invalid shapes, and a
+    """A prefill plan's size follows its documented layout (8 or 2 chunks of
+    512 tokens at 28 / 4 heads: 29 blocks of 18 tokens each, two workgroups per
+    CU), nothing is planned for empty or invalid shapes, and a
     short plan buffer or a null pointer is refused before any device work."""
     lib = _lib.lib()
     x = lib.ir_paged_prefill_plan_xcds()

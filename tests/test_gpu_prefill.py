@@ -178,14 +178,14 @@ def _host_weights(case, tq, n_qblocks):
 
 def _plan_geometry(b, max_q, hq, hkv):
     """Items, entries and piece capacity of a plan: 4-wavefront workgroups of
-    128 // n_rep query tokens, two per CU when the call has workgroups for
-    that, the capacity one piece per KV head of every workgroup slot; one
-    entry per workgroup, (items + capacity) x KV heads, 1.5x that rounded to
-    the XCD count when the plan places work on XCDs."""
+    128 // n_rep query tokens, two resident per CU, the capacity one piece per
+    KV head of every workgroup slot; one entry per workgroup, (items +
+    capacity) x KV heads, 1.5x that rounded to the XCD count when the plan
+    places work on XCDs."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     tq = 128 // (hq // hkv)
     n_qblocks = -(-max_q // tq)
-    slots = 2 * cus if n_qblocks * hkv * b >= 2 * cus else cus
+    slots = 2 * cus
     cap = -(-slots // hkv)
     wgs = (b * n_qblocks + cap) * hkv
     x = kernels.prefill_plan_xcds()
@@ -237,7 +237,7 @@ def _plan_order(rows, h_kv, x, w):
 @pytest.mark.parametrize("prefixes,q_lens", [
     (None, None),  # the full 8 x 512-token workload, sequence pairs sharing their prefix blocks
     ([0, 37, 512, 1000, 3, 3, 0, 5], [1, 31, 100, 512, 0, 9, 64, 33]),  # ragged, one empty chunk
-    ([0, 300], [256, 77]),  # few workgroups: one per CU, nothing cut
+    ([0, 300], [256, 77]),  # few workgroups, nothing cut
     ([9000, 0, 0, 0], [512, 40, 40, 40]),  # one very long item among short ones
 ])
 @pytest.mark.parametrize("share_groups", [False, True])
