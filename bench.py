@@ -36,7 +36,9 @@ layer (1,248 new tokens, 28 q / 4 kv heads), value in GB/s of algorithmic bytes;
 ``engine`` -- the engine ladder rows (+HIP paged-attn, +hipGraph): a decode-heavy
 burst through the seam with an attention-only model, value in output tok/s;
 ``reference-form`` -- the headline decode with the metadata unchanged reference
-callers pass (gather_slots + mask), value in us per call.
+callers pass (gather_slots + mask), value in us per call; with ``--config
+qwen7b-prefill`` the 8 x 512-token prefill in the reference's packed form
+(gather_slots over every history + the varlen mask).
 
 Prints one JSON line: value = achieved KV GB/s (algorithmic bytes sum(ctx) *
 2 * H_kv * D * 2 per call / time per call), plus us_per_call, a roofline
@@ -69,7 +71,7 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--workload", choices=("decode", "prefill", "mixed", "rope", "engine", "reference-form"),
                    default="decode")
     p.add_argument("--engine-batch", type=int, default=8, help="engine: sequences in the burst (max_batch)")
-    p.add_argument("--config", default=None, help="decode: qwen7b-bf16 (default) | qwen0.5b-fp32 | qwen7b-skewed")
+    p.add_argument("--config", default=None, help="decode: qwen7b-bf16 (default) | qwen0.5b-fp32 | qwen7b-skewed; reference-form: also qwen7b-prefill")
     p.add_argument("--rotations", type=int, default=3)
     p.add_argument("--partition", type=int, default=0, help="split-KV partition tokens (0 = library default)")
     p.add_argument("--schedule", choices=("auto", "planned", "fixed"), default="auto",
@@ -752,6 +754,117 @@ def _bench_engine(args) -> dict:
     }
 
 
+def _bench_reference_form_prefill(args) -> dict:
+    """Unchanged reference callers at the 8 x 512-token chunked-prefill shape:
+    the step's metadata as the reference engine packs it for prefill and mixed
+    steps (one frame: ``gather_slots [1, K]`` over every sequence's history +
+    the varlen mask ``[1, 1, Q, K]``, ``infrared/engine/paged_engine.py:461-516``,
+    no block tables) through ``paged_attention`` for ``--layers`` layers (KV
+    write + attention per layer, eager launches). Rows: the seam recognising
+    the packed form (one check per step) and running the chunked-prefill
+    kernel; the same step with block-table fields filled by the caller; the
+    mask kernel reading gather_slots + mask as given (``use_triton=False``,
+    one step); and the form check alone."""
+    from dataclasses import dataclass
+
+    from infrared_amd import PagedContext, PagedKVPool, metadata, paged_attention
+    from infrared_amd.workloads import make_prefill_case
+
+    @dataclass(slots=True)
+    class RefContext:  # the reference's PagedContext fields only
+        pool: object
+        write_slots: torch.Tensor
+        gather_slots: torch.Tensor
+        use_triton: bool = True
+
+    case = make_prefill_case(args.config, "cuda")
+    cfg = case.config
+    hq, hkv, d, bs = cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
+    pool = PagedKVPool(1, case.pool_blocks, bs, hkv, d, cfg.dtype, device="cuda")
+    pool.k[0].copy_(case.k_cache)
+    pool.v[0].copy_(case.v_cache)
+    nblk = [-(-(p + n) // bs) for p, n in zip(case.prefixes, case.q_lens)]
+    tables = [row[:n].tolist() for row, n in zip(case.block_tables[0].cpu(), nblk)]
+    ours, mask = metadata.prefill_context(pool, tables, case.prefixes, case.q_lens, with_mask=True)
+    total = sum(case.q_lens)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    q = case.q.view(1, total, hq, d)
+    k = torch.randn(1, total, hkv, d, generator=g, device="cuda").to(cfg.dtype)
+    v = torch.randn(1, total, hkv, d, generator=g, device="cuda").to(cfg.dtype)
+    layers = args.layers
+    fresh = []
+
+    def step_ref():
+        # a step's metadata arrives as new tensors, as the reference engine builds them
+        gs, m = fresh.pop()
+        paged = RefContext(pool, ours.write_slots, gs)
+        for _ in range(layers):
+            paged_attention(q, k, v, paged, m, 0, cfg.scale, cfg.n_rep)
+
+    def step_ours():
+        paged = PagedContext(pool, ours.write_slots, None, True, ours.block_tables, None, ours.cu_seqlens_q,
+                             ours.q_start, ours.max_q_len)
+        for _ in range(layers):
+            paged_attention(q, k, v, paged, None, 0, cfg.scale, cfg.n_rep)
+
+    def step_masked():
+        paged = RefContext(pool, ours.write_slots, ours.gather_slots, use_triton=False)
+        for _ in range(layers):
+            paged_attention(q, k, v, paged, mask, 0, cfg.scale, cfg.n_rep)
+
+    def check_only():
+        gs, m = fresh.pop()
+        pool.reference_varlen_form(gs, m)
+
+    def timed(fn, steps, per_call=True):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        per = []
+        for _ in range(steps):
+            fresh.append((ours.gather_slots.clone(), mask.clone()))
+            torch.cuda.synchronize()
+            s.record()
+            fn()
+            e.record()
+            torch.cuda.synchronize()
+            per.append(s.elapsed_time(e) / (layers if per_call else 1))
+        return statistics.median(per)
+
+    timed(step_ref, 1)
+    timed(step_ours, 1)
+    ms_ref, ms_ours = timed(step_ref, 5), timed(step_ours, 5)
+    ms_check = timed(check_only, 5, per_call=False)
+    form = pool._ref_varlen[2]
+    ms_masked = timed(step_masked, 1)
+    out_ref = paged_attention(q, k, v, RefContext(pool, ours.write_slots, ours.gather_slots), mask, 0, cfg.scale,
+                              cfg.n_rep)
+    out_ours = paged_attention(q, k, v, PagedContext(pool, ours.write_slots, None, True, ours.block_tables, None,
+                                                     ours.cu_seqlens_q, ours.q_start, ours.max_q_len),
+                               None, 0, cfg.scale, cfg.n_rep)
+    torch.cuda.synchronize()
+    tflops = case.flops / (ms_ref * 1e-3) / 1e12
+    return {
+        "metric": "chunked prefill attn us/call for unchanged reference callers (gather_slots + varlen mask), "
+                  "8 x 512-token chunks",
+        "value": round(ms_ref * 1e3, 2), "unit": "us/call", "ms_per_step": round(ms_ref * layers, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{cfg.name} in the reference's packed form: {len(case.q_lens)} chunks of "
+                   f"{cfg.chunk} tokens after prefixes {case.prefixes}, {hq}q/{hkv}kv heads, head_dim {d}, block "
+                   f"{bs}, gather_slots {tuple(ours.gather_slots.shape)}, mask {tuple(mask.shape)} "
+                   f"({mask.numel() * mask.element_size() / 1e6:.0f} MB), {layers} layers per step (KV write + "
+                   "attention per layer), eager",
+                   "varlen_form_recognised": form is not None,
+                   "equal_to_block_table_path": bool(torch.equal(out_ref, out_ours)),
+                   "rows_us_per_call": {"reference form, recognised (one check per step)": round(ms_ref * 1e3, 2),
+                                        "block-table fields from the caller": round(ms_ours * 1e3, 2),
+                                        "mask kernel on gather_slots + mask": round(ms_masked * 1e3, 2)},
+                   "form_check_us_per_step": round(ms_check * 1e3, 2)},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "timed": "whole call (KV write + attention, eager launches, the step's check amortised)"},
+        "cpu_baseline": None,
+    }
+
+
 def _bench_reference_form(args) -> dict:
     """Unchanged reference callers at the Qwen2.5-7B decode shape: each step's
     metadata in the reference engine's own form (``gather_slots [B, T]`` +
@@ -764,7 +877,10 @@ def _bench_reference_form(args) -> dict:
     from dataclasses import dataclass
 
     from infrared_amd import PagedContext, PagedKVPool, kernels, metadata, paged_attention
-    from infrared_amd.workloads import make_decode_case
+    from infrared_amd.workloads import PREFILL_CONFIGS, make_decode_case
+
+    if args.config in PREFILL_CONFIGS:
+        return _bench_reference_form_prefill(args)
 
     @dataclass(slots=True)
     class RefContext:  # the reference's PagedContext fields only

@@ -99,6 +99,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_p, _c_i64,
          _c_i32, _c_p, _c_p, _c_p],
     ),
+    "ir_varlen_form_scan": (
+        _c_i32,
+        [_c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p],
+    ),
+    "ir_varlen_form_tables": (
+        _c_i32,
+        [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i64, _c_p, _c_i64, _c_i32, _c_p, _c_p],
+    ),
     "ir_hbm_read_granule": (_c_i64, []),
     "ir_hbm_read": (_c_i32, [_c_p, _c_i64, _c_p, _c_i32, _c_p]),
     "ir_paged_prefill_plan_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),

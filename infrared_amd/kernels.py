@@ -628,6 +628,62 @@ def decode_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int,
     return bt, ctx, bad
 
 
+@dataclass(slots=True)
+class VarlenForm:
+    """Prefill metadata derived from a reference packed frame: ``block_tables``
+    ``[B, W]``, ``cu_seqlens_q`` ``[B + 1]`` and ``q_start`` ``[B]`` (int32,
+    device) and the longest chunk ``max_q_len`` (host), with the step's prefill
+    plan once built."""
+
+    block_tables: torch.Tensor
+    cu_seqlens_q: torch.Tensor
+    q_start: torch.Tensor
+    max_q_len: int
+    prefill_plan: object | None = None
+
+
+def varlen_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int, num_blocks: int
+                ) -> VarlenForm | None:
+    """Prefill metadata from the reference's packed prefill / mixed-step frame
+    (``gather_slots`` ``[1, K]`` int64, mask ``[1, 1, Q, K]``), or ``None``
+    unless it has that form exactly (``ir_varlen_form_scan`` /
+    ``ir_varlen_form_tables``). Synchronises twice: the sequence count sizes the
+    block tables, and the second pass's verdict decides."""
+    dev = require_device(gather_slots, mask)
+    if gather_slots.dtype != torch.int64 or gather_slots.dim() != 2 or gather_slots.shape[0] != 1:
+        raise RuntimeError("varlen_form: gather_slots must be int64 [1, K]")
+    k = gather_slots.shape[1]
+    if mask.dim() != 4 or tuple(mask.shape[:2]) != (1, 1) or mask.shape[3] != k:
+        raise RuntimeError(f"varlen_form: mask must be [1, 1, Q, K], got {tuple(mask.shape)}")
+    q = mask.shape[2]
+    if q == 0 or k == 0 or q >= 2**31 or k >= 2**31:
+        return None
+    i32 = dict(dtype=torch.int32, device=dev)
+    ranges = torch.empty(2 * q, **i32)
+    cu = torch.empty(q + 1, **i32)
+    q_start = torch.empty(q, **i32)
+    k_off = torch.empty(q, **i32)
+    info = torch.zeros(4, **i32)
+    rc = lib().ir_varlen_form_scan(
+        ptr(mask), mask.stride(2), mask.stride(3), dtype_code(mask.dtype), q, k, block_size, ptr(ranges), ptr(cu),
+        ptr(q_start), ptr(k_off), ptr(info), stream_ptr(dev),
+    )
+    check(rc, "ir_varlen_form_scan")
+    bad, nseq, max_q, width = info.tolist()
+    if bad or nseq <= 0:
+        return None
+    width = max(width, 1)
+    bt = torch.empty(nseq, width, **i32)
+    rc = lib().ir_varlen_form_tables(
+        ptr(gather_slots), gather_slots.stride(1), ptr(k_off), ptr(cu), ptr(q_start), nseq, block_size, num_blocks,
+        ptr(bt), bt.stride(0), width, ptr(info), stream_ptr(dev),
+    )
+    check(rc, "ir_varlen_form_tables")
+    if int(info[0].item()):
+        return None
+    return VarlenForm(bt, cu[: nseq + 1], q_start[:nseq], max_q)
+
+
 def hbm_read(src: torch.Tensor, sink: torch.Tensor, workgroups: int = 0) -> None:
     """Reads all of ``src`` (contiguous, a multiple of :func:`hbm_read_granule`
     bytes) with the decode kernels' load form and discards it: timing it gives

@@ -25,6 +25,14 @@ calls once per layer (``infrared/model/layers.py:178-180``):
      ``infrared/engine/paged_engine.py:306-314, 630-638``): the same decode
      kernels over block tables derived from them on the device (checked once
      per step, ``PagedKVPool.reference_decode_form``);
+   - otherwise, for the reference engine's packed prefill / mixed-step frame
+     (batch 1: every scheduled sequence's query tokens, a key axis
+     concatenating their histories in order, ``gather_slots`` with the closed
+     form per sequence and the mask of ``build_attention_mask`` /
+     ``build_varlen_mask``, ``infrared/engine/paged_engine.py:194-206,
+     461-516``): the chunked-prefill kernel over ``cu_seqlens_q``, ``q_start``
+     and block tables derived from them on the device (checked once per step,
+     ``PagedKVPool.reference_varlen_form``);
    - otherwise: the kernel that reads ``gather_slots`` + the additive ``mask``
      exactly as the reference's naive path does
      (``infrared/model/triton_attention.py:110-129``).
@@ -107,8 +115,7 @@ def rope_paged_attention(
 def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, scale: float) -> torch.Tensor:
     """Attention over the pool (this step's K/V already written)."""
     pool = paged.pool
-    b, sq, hq, d = q.shape
-    h_kv = pool.k.shape[-2]
+    b, sq = q.shape[:2]
     k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
     err = getattr(pool, "err_flags", None)
 
@@ -124,21 +131,7 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
         and q.dtype in (torch.bfloat16, torch.float16)
     ):
         max_q = getattr(paged, "max_q_len", 0) or b * sq
-        nseq = q_start.shape[0]
-        # work plan: built by the step's first layer, reused by the rest
-        plan = getattr(paged, "prefill_plan", None)
-        if plan is None and kernels.prefill_plan_pays(nseq, max_q, hq, h_kv, q.device):
-            plan = kernels.prefill_plan(
-                cu_seqlens_q, q_start, block_tables, b * sq, max_q, pool.block_size, hq, h_kv, d
-            )
-            try:
-                paged.prefill_plan = plan
-            except AttributeError:  # a context object without the field keeps none
-                pass
-        out = kernels.paged_prefill(
-            q.reshape(b * sq, hq, d), k_layer, v_layer, block_tables, cu_seqlens_q, q_start, max_q,
-            pool.block_size, scale, err_flags=err, plan=plan,
-        ).view(b, sq, hq, d)
+        out = _prefill(q, pool, layer_idx, block_tables, cu_seqlens_q, q_start, max_q, paged, scale, err)
     elif paged.use_triton and block_tables is not None and context_lens is not None and sq == 1:
         out = _decode(q, pool, layer_idx, block_tables, context_lens, paged, scale, err)
     else:
@@ -152,8 +145,17 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
             # the reference's own decode metadata (gather_slots + mask, no block
             # tables): when it has the decode form, run the block-table kernels
             form = pool.reference_decode_form(paged.gather_slots, mask)
+        vform = None
+        if (form is None and paged.use_triton and b == 1 and q.dtype in (torch.bfloat16, torch.float16)
+                and hasattr(pool, "reference_varlen_form")):
+            # the reference's packed prefill / mixed-step frame: when it has
+            # that form, run the chunked-prefill kernel over derived metadata
+            vform = pool.reference_varlen_form(paged.gather_slots, mask)
         if form is not None:
             out = _decode(q, pool, layer_idx, form.block_tables, form.context_lens, form, scale, err)
+        elif vform is not None:
+            out = _prefill(q, pool, layer_idx, vform.block_tables, vform.cu_seqlens_q, vform.q_start,
+                           vform.max_q_len, vform, scale, err)
         else:
             out = kernels.paged_attention_masked(
                 q, k_layer, v_layer, paged.gather_slots, mask, scale, err_flags=err
@@ -161,6 +163,29 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
     if getattr(pool, "strict", False):
         pool.check_errors()
     return out
+
+
+def _prefill(q, pool, layer_idx: int, block_tables, cu_seqlens_q, q_start, max_q: int, holder, scale: float,
+             err) -> torch.Tensor:
+    """Packed query chunks over block tables: the chunked-prefill kernel with
+    the step's work plan (built by the first layer, cached on ``holder``).
+    Returns ``q``'s shape."""
+    b, sq, hq, d = q.shape
+    h_kv = pool.k.shape[-2]
+    nseq = q_start.shape[0]
+    plan = getattr(holder, "prefill_plan", None)
+    if plan is None and kernels.prefill_plan_pays(nseq, max_q, hq, h_kv, q.device):
+        plan = kernels.prefill_plan(
+            cu_seqlens_q, q_start, block_tables, b * sq, max_q, pool.block_size, hq, h_kv, d
+        )
+        try:
+            holder.prefill_plan = plan
+        except AttributeError:  # a context object without the field keeps none
+            pass
+    return kernels.paged_prefill(
+        q.reshape(b * sq, hq, d), pool.k[layer_idx], pool.v[layer_idx], block_tables, cu_seqlens_q, q_start, max_q,
+        pool.block_size, scale, err_flags=err, plan=plan,
+    ).view(b, sq, hq, d)
 
 
 def _decode(q, pool, layer_idx: int, block_tables, context_lens, holder, scale: float, err) -> torch.Tensor:

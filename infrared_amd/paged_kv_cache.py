@@ -109,6 +109,7 @@ class PagedKVPool:
         self.plan_owner: object | None = None
         # (gather_slots, mask, derived form) of the last reference-form check
         self._ref_form: tuple | None = None
+        self._ref_varlen: tuple | None = None
 
     # --- reference surface ------------------------------------------------
 
@@ -211,6 +212,38 @@ class PagedKVPool:
             if int(bad.item()) == 0:
                 form = _DecodeForm(bt, ctx)
         self._ref_form = (gather_slots, mask, form)
+        return form
+
+    def reference_varlen_form(self, gather_slots: torch.Tensor, mask: torch.Tensor) -> kernels.VarlenForm | None:
+        """Chunked-prefill metadata for the reference engine's packed prefill
+        frame, if it has that form; else ``None`` (the caller runs the mask
+        kernel).
+
+        The reference's prefix-hit prefill and mixed steps pass one frame (batch
+        1) of Q query tokens, a key axis concatenating each scheduled sequence's
+        history ``[0, start + q)`` in order, ``gather_slots[1, K]`` with the
+        closed form per sequence and the additive mask of
+        ``build_attention_mask`` / ``build_varlen_mask``
+        (``infrared/engine/paged_engine.py:194-206, 461-516``,
+        ``infrared/model/inputs.py:33-85``). ``ir_varlen_form_scan`` /
+        ``ir_varlen_form_tables`` recover ``cu_seqlens_q``, ``q_start`` and the
+        block tables on the device and verify the form exactly, so the
+        chunked-prefill kernel computes what the mask kernel would. The check
+        reads the mask once and synchronises twice; the result is cached for
+        the step's other layers (same ``gather_slots`` and ``mask`` tensors).
+        Under hipGraph capture ``None`` is returned and the mask kernel runs.
+        """
+        c = self._ref_varlen
+        if c is not None and c[0] is gather_slots and c[1] is mask:
+            return c[2]
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        form = None
+        if (gather_slots.dim() == 2 and gather_slots.shape[0] == 1 and gather_slots.dtype == torch.int64
+                and gather_slots.is_cuda and mask.is_cuda and mask.dim() == 4 and tuple(mask.shape[:2]) == (1, 1)
+                and mask.shape[3] == gather_slots.shape[1]):
+            form = kernels.varlen_form(gather_slots, mask, self.block_size, self.num_blocks)
+        self._ref_varlen = (gather_slots, mask, form)
         return form
 
     def check_errors(self) -> None:

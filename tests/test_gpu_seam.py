@@ -348,3 +348,129 @@ def test_reference_metadata_outside_the_decode_form_takes_the_mask_kernel():
         assert pool._ref_form[2] is None
         expect = O.paged_attention_naive(q.cpu(), pool.k[0].cpu(), pool.v[0].cpu(), gs.cpu(), m.cpu(), d**-0.5, n_rep)
         assert (got.cpu() - expect).abs().max().item() <= 1e-4
+
+
+def _reference_prefill_frame(pool, tables, num_cached, q_lens, one_sequence_mask=False):
+    """The reference engine's packed prefill frame, built by its own loops
+    (infrared/engine/paged_engine.py:476-506, :194-206): per sequence the new
+    tokens' write slots and its whole history's gather slots, and the mask of
+    build_varlen_mask -- or, for one sequence, build_attention_mask
+    (infrared/model/inputs.py:33-85; restated in the oracle)."""
+    bs = pool.block_size
+    write, gather, q_seq, q_pos, k_seq, k_pos = [], [], [], [], [], []
+    for i, (bt, start, q) in enumerate(zip(tables, num_cached, q_lens)):
+        for p in range(start, start + q):
+            write.append(O.slot(bt, p, bs))
+            q_seq.append(i)
+            q_pos.append(p)
+        for p in range(start + q):
+            gather.append(O.slot(bt, p, bs))
+            k_seq.append(i)
+            k_pos.append(p)
+    if one_sequence_mask:
+        assert len(tables) == 1
+        mask = O.attention_mask([0], num_cached[0], q_lens[0], num_cached[0] + q_lens[0], pool.dtype)
+    else:
+        mask = O.varlen_mask(torch.tensor(q_seq), torch.tensor(q_pos), torch.tensor(k_seq), torch.tensor(k_pos),
+                             pool.dtype)
+    return (torch.tensor(write, dtype=torch.int64, device=DEV), torch.tensor([gather], dtype=torch.int64, device=DEV),
+            mask.to(DEV))
+
+
+def _prefill_case(kind):
+    g = torch.Generator().manual_seed(21)
+    if kind == "prefix-hit":  # one sequence after a cached prefix
+        num_cached, q_lens = [300], [77]
+    elif kind == "mixed":  # two chunks (one after a prefix) and three decode rows
+        num_cached, q_lens = [0, 300, 41, 1000, 7], [77, 130, 1, 1, 1]
+    else:  # eight chunks after prefixes, enough work for the prefill plan
+        num_cached = [int(x) for x in torch.randint(0, 2000, (8,), generator=g)]
+        q_lens = [int(x) for x in torch.randint(64, 260, (8,), generator=g)]
+    bs = 16
+    need = [metadata.blocks_for(c + n, bs) for c, n in zip(num_cached, q_lens)]
+    perm = torch.randperm(sum(need) + 40, generator=g).tolist()
+    tables, off = [], 0
+    for nb in need:
+        tables.append(perm[off : off + nb])
+        off += nb
+    return tables, num_cached, q_lens, sum(need) + 40
+
+
+@pytest.mark.parametrize("kind", ["prefix-hit", "mixed", "chunks"])
+def test_reference_prefill_metadata_runs_the_prefill_kernel(kind):
+    """Unchanged reference callers pass a packed frame (batch 1) of gather_slots
+    + the varlen / causal mask for prefix-hit prefills and mixed steps. Its
+    form is recognised once per step (later layers reuse the derived metadata:
+    cu_seqlens_q, q_start, block tables), and every layer equals the
+    block-table context's output bit for bit -- the same chunked-prefill
+    kernel on the same metadata -- and the oracle."""
+    tables, num_cached, q_lens, num_blocks = _prefill_case(kind)
+    bs, h_kv, n_rep, d, layers = 16, 4, 7, 128, 3
+    pool = PagedKVPool(layers, num_blocks, bs, h_kv, d, torch.bfloat16, device=DEV)
+    pool.k.normal_()
+    pool.v.normal_()
+    ours, _ = metadata.prefill_context(pool, tables, num_cached, q_lens)
+    write, gather, mask = _reference_prefill_frame(pool, tables, num_cached, q_lens, kind == "prefix-hit")
+    assert torch.equal(write, ours.write_slots)
+    ref = _ReferenceContext(pool, write, gather)
+    total = sum(q_lens)
+    dgen = torch.Generator(device=DEV).manual_seed(2)
+    forms = []
+    for layer in range(layers):
+        q = torch.randn(1, total, h_kv * n_rep, d, generator=dgen, device=DEV).bfloat16()
+        k = torch.randn(1, total, h_kv, d, generator=dgen, device=DEV).bfloat16()
+        v = torch.randn(1, total, h_kv, d, generator=dgen, device=DEV).bfloat16()
+        got = paged_attention(q, k, v, ref, mask, layer, d**-0.5, n_rep)
+        forms.append(pool._ref_varlen[2])
+        want = paged_attention(q, k, v, ours, None, layer, d**-0.5, n_rep)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"layer {layer}"
+        expect = O.prefill_reference(q[0].cpu(), pool.k[layer].cpu(), pool.v[layer].cpu(),
+                                     ours.block_tables.cpu(), ours.cu_seqlens_q.cpu(), num_cached, bs, d**-0.5)
+        assert (got[0].float().cpu() - expect).abs().max().item() <= 2e-2
+    f = forms[0]
+    assert f is not None and all(x is f for x in forms)
+    assert f.max_q_len == max(q_lens)
+    assert torch.equal(f.cu_seqlens_q, ours.cu_seqlens_q) and torch.equal(f.q_start, ours.q_start)
+    for i, (c, n) in enumerate(zip(num_cached, q_lens)):  # (entries past a history are never read)
+        nb = metadata.blocks_for(c + n, bs)
+        assert f.block_tables[i, :nb].tolist() == tables[i][:nb]
+
+
+def test_reference_prefill_metadata_outside_the_form_takes_the_mask_kernel():
+    """A frame that is not the reference's packed form -- a visible key hidden,
+    a key of another sequence let through, two slots swapped, a mask value that
+    is neither 0 nor a large negative, a key column no sequence owns -- is read
+    as given (mask kernel) and matches the oracle's naive path on exactly that
+    metadata."""
+    tables, num_cached, q_lens, num_blocks = _prefill_case("mixed")
+    bs, h_kv, n_rep, d = 16, 4, 7, 128
+    pool = PagedKVPool(1, num_blocks, bs, h_kv, d, torch.bfloat16, device=DEV)
+    pool.k.normal_()
+    pool.v.normal_()
+    write, gather, mask = _reference_prefill_frame(pool, tables, num_cached, q_lens)
+    lo1 = num_cached[0] + q_lens[0]  # sequence 1's first key
+    neg = torch.finfo(torch.bfloat16).min
+    holed = mask.clone()
+    holed[0, 0, 100, lo1 + 5] = neg  # row 100 is sequence 1's 24th query
+    leaked = mask.clone()
+    leaked[0, 0, 100, 3] = 0.0  # a key of sequence 0
+    soft = mask.clone()
+    soft[0, 0, 0, 70] = -1.0
+    swapped = gather.clone()
+    swapped[0, [lo1 + 3, lo1 + 4]] = swapped[0, [lo1 + 4, lo1 + 3]]
+    extra_g = torch.cat([gather, gather[:, :1]], 1)
+    extra_m = torch.cat([mask, torch.full_like(mask[..., :1], neg)], 3)
+    total = sum(q_lens)
+    for gs, m in ((gather, holed), (gather, leaked), (gather, soft), (swapped, mask), (extra_g, extra_m)):
+        ref = _ReferenceContext(pool, write, gs)
+        q = torch.randn(1, total, h_kv * n_rep, d, device=DEV).bfloat16()
+        k = torch.randn(1, total, h_kv, d, device=DEV).bfloat16()
+        v = torch.randn(1, total, h_kv, d, device=DEV).bfloat16()
+        got = paged_attention(q, k, v, ref, m, 0, d**-0.5, n_rep)
+        torch.cuda.synchronize()
+        assert pool._ref_varlen[2] is None
+        # the bar for a bf16 kernel: within 2e-2 of the same path in fp32
+        expect = O.paged_attention_naive(q.float().cpu(), pool.k[0].float().cpu(), pool.v[0].float().cpu(),
+                                         gs.cpu(), m.float().cpu(), d**-0.5, n_rep)
+        assert (got.float().cpu() - expect).abs().max().item() <= 2e-2
