@@ -141,13 +141,14 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
                 "context_lens drive a single-token decode"
             )
         form = None
-        if paged.use_triton and sq == 1 and hasattr(pool, "reference_decode_form"):
+        if (paged.use_triton and sq == 1 and hasattr(pool, "reference_decode_form")
+                and paged.gather_slots.dim() == 2 and paged.gather_slots.shape[0] == b):
             # the reference's own decode metadata (gather_slots + mask, no block
             # tables): when it has the decode form, run the block-table kernels
             form = pool.reference_decode_form(paged.gather_slots, mask)
         vform = None
         if (form is None and paged.use_triton and b == 1 and q.dtype in (torch.bfloat16, torch.float16)
-                and hasattr(pool, "reference_varlen_form")):
+                and hasattr(pool, "reference_varlen_form") and mask.dim() == 4 and mask.shape[2] == sq):
             # the reference's packed prefill / mixed-step frame: when it has
             # that form, run the chunked-prefill kernel over derived metadata
             vform = pool.reference_varlen_form(paged.gather_slots, mask)
