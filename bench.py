@@ -833,7 +833,7 @@ def _bench_reference_form_prefill(args) -> dict:
     timed(step_ours, 1)
     ms_ref, ms_ours = timed(step_ref, 5), timed(step_ours, 5)
     ms_check = timed(check_only, 5, per_call=False)
-    form = pool._ref_varlen[2]
+    form = pool._ref_varlen[1]
     ms_masked = timed(step_masked, 1)
     out_ref = paged_attention(q, k, v, RefContext(pool, ours.write_slots, ours.gather_slots), mask, 0, cfg.scale,
                               cfg.n_rep)
@@ -935,7 +935,7 @@ def _bench_reference_form(args) -> dict:
         return statistics.median(per)
 
     ms_ref, ms_ours, ms_masked = timed(step_ref), timed(step_ours), timed(step_masked)
-    form = pool._ref_form[2]
+    form = pool._ref_form[1]
     out_ref = paged_attention(q, k, v, RefContext(pool, ours.write_slots, ours.gather_slots), mask, 0, cfg.scale,
                               cfg.n_rep)
     out_ours = paged_attention(q, k, v, PagedContext(pool, ours.write_slots, ours.gather_slots, True,

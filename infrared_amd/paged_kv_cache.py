@@ -196,12 +196,14 @@ class PagedKVPool:
         ``finfo.min`` included), so the decode kernels compute what the mask
         kernel would. The check costs one launch and one synchronising read of
         its flag; the result is cached for the step's other layers (same
-        ``gather_slots`` and ``mask`` tensors). Under hipGraph capture no read is
-        possible, so ``None`` is returned and the mask kernel runs.
+        ``gather_slots`` and ``mask`` tensors, not modified in place since).
+        Under hipGraph capture no read is possible, so ``None`` is returned and
+        the mask kernel runs.
         """
+        key = _metadata_key(gather_slots, mask)
         c = self._ref_form
-        if c is not None and c[0] is gather_slots and c[1] is mask:
-            return c[2]
+        if c is not None and _same_metadata(c[0], key):
+            return c[1]
         if torch.cuda.is_current_stream_capturing():
             return None
         form = None
@@ -211,7 +213,7 @@ class PagedKVPool:
             bt, ctx, bad = kernels.decode_form(gather_slots, mask, self.block_size, self.num_blocks)
             if int(bad.item()) == 0:
                 form = _DecodeForm(bt, ctx)
-        self._ref_form = (gather_slots, mask, form)
+        self._ref_form = (key, form)
         return form
 
     def reference_varlen_form(self, gather_slots: torch.Tensor, mask: torch.Tensor) -> kernels.VarlenForm | None:
@@ -230,12 +232,14 @@ class PagedKVPool:
         block tables on the device and verify the form exactly, so the
         chunked-prefill kernel computes what the mask kernel would. The check
         reads the mask once and synchronises twice; the result is cached for
-        the step's other layers (same ``gather_slots`` and ``mask`` tensors).
+        the step's other layers (same ``gather_slots`` and ``mask`` tensors, not
+        modified in place since).
         Under hipGraph capture ``None`` is returned and the mask kernel runs.
         """
+        key = _metadata_key(gather_slots, mask)
         c = self._ref_varlen
-        if c is not None and c[0] is gather_slots and c[1] is mask:
-            return c[2]
+        if c is not None and _same_metadata(c[0], key):
+            return c[1]
         if torch.cuda.is_current_stream_capturing():
             return None
         form = None
@@ -243,7 +247,7 @@ class PagedKVPool:
                 and gather_slots.is_cuda and mask.is_cuda and mask.dim() == 4 and tuple(mask.shape[:2]) == (1, 1)
                 and mask.shape[3] == gather_slots.shape[1]):
             form = kernels.varlen_form(gather_slots, mask, self.block_size, self.num_blocks)
-        self._ref_varlen = (gather_slots, mask, form)
+        self._ref_varlen = (key, form)
         return form
 
     def check_errors(self) -> None:
@@ -253,6 +257,17 @@ class PagedKVPool:
             self.err_flags.zero_()
             names = [n for bit, n in _ERR_NAMES.items() if flags & bit]
             raise IndexError("paged kernels flagged: " + ", ".join(names))
+
+
+def _metadata_key(gather_slots: torch.Tensor, mask: torch.Tensor) -> tuple:
+    """Identity of a step's metadata for the form caches: the two tensors
+    (held, so their ids are not reused) and their in-place version counters, so
+    a caller that refills the same tensors for the next step is checked again."""
+    return (gather_slots, gather_slots._version, mask, mask._version)
+
+
+def _same_metadata(a: tuple, b: tuple) -> bool:
+    return a[0] is b[0] and a[1] == b[1] and a[2] is b[2] and a[3] == b[3]
 
 
 @dataclass(slots=True)

@@ -307,7 +307,7 @@ def test_reference_decode_metadata_runs_the_block_table_kernels(num_seqs):
         k = torch.randn(num_seqs, 1, h_kv, d, generator=dgen, device=DEV).bfloat16()
         v = torch.randn(num_seqs, 1, h_kv, d, generator=dgen, device=DEV).bfloat16()
         got = paged_attention(q, k, v, ref, mask, layer, d**-0.5, n_rep)
-        forms.append(pool._ref_form[2])
+        forms.append(pool._ref_form[1])
         want = paged_attention(q, k, v, ours, mask, layer, d**-0.5, n_rep)
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"layer {layer}"
@@ -345,7 +345,7 @@ def test_reference_metadata_outside_the_decode_form_takes_the_mask_kernel():
         v = torch.randn(3, 1, h_kv, d, device=DEV)
         got = paged_attention(q, k, v, ref, m, 0, d**-0.5, n_rep)
         torch.cuda.synchronize()
-        assert pool._ref_form[2] is None
+        assert pool._ref_form[1] is None
         expect = O.paged_attention_naive(q.cpu(), pool.k[0].cpu(), pool.v[0].cpu(), gs.cpu(), m.cpu(), d**-0.5, n_rep)
         assert (got.cpu() - expect).abs().max().item() <= 1e-4
 
@@ -421,7 +421,7 @@ def test_reference_prefill_metadata_runs_the_prefill_kernel(kind):
         k = torch.randn(1, total, h_kv, d, generator=dgen, device=DEV).bfloat16()
         v = torch.randn(1, total, h_kv, d, generator=dgen, device=DEV).bfloat16()
         got = paged_attention(q, k, v, ref, mask, layer, d**-0.5, n_rep)
-        forms.append(pool._ref_varlen[2])
+        forms.append(pool._ref_varlen[1])
         want = paged_attention(q, k, v, ours, None, layer, d**-0.5, n_rep)
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"layer {layer}"
@@ -469,8 +469,37 @@ def test_reference_prefill_metadata_outside_the_form_takes_the_mask_kernel():
         v = torch.randn(1, total, h_kv, d, device=DEV).bfloat16()
         got = paged_attention(q, k, v, ref, m, 0, d**-0.5, n_rep)
         torch.cuda.synchronize()
-        assert pool._ref_varlen[2] is None
+        assert pool._ref_varlen[1] is None
         # the bar for a bf16 kernel: within 2e-2 of the same path in fp32
         expect = O.paged_attention_naive(q.float().cpu(), pool.k[0].float().cpu(), pool.v[0].float().cpu(),
                                          gs.cpu(), m.float().cpu(), d**-0.5, n_rep)
         assert (got.float().cpu() - expect).abs().max().item() <= 2e-2
+
+
+def test_reference_metadata_refilled_in_place_is_checked_again():
+    """A caller that reuses its gather_slots and mask tensors, refilling them in
+    place for the next step, gets that step's form derived again (the cache of
+    the step's check follows the tensors' in-place versions), not the last
+    step's block tables and context lengths."""
+    bs, h_kv, n_rep, d = 16, 4, 7, 128
+    tables = [list(range(i * 32, i * 32 + 32)) for i in range(4)]
+    pool = PagedKVPool(1, 128, bs, h_kv, d, torch.bfloat16, device=DEV)
+    pool.k.normal_()
+    pool.v.normal_()
+    steps = [metadata.decode_context(pool, tables, nc) for nc in ([100, 300, 5, 400], [400, 12, 250, 99])]
+    assert steps[0][0].gather_slots.shape == steps[1][0].gather_slots.shape
+    gs, m = steps[0][0].gather_slots.clone(), steps[0][1].clone()
+    for ours, mask in steps:
+        gs.copy_(ours.gather_slots)
+        m.copy_(mask)
+        ref = _ReferenceContext(pool, ours.write_slots, gs)
+        q = torch.randn(4, 1, h_kv * n_rep, d, device=DEV).bfloat16()
+        k = torch.randn(4, 1, h_kv, d, device=DEV).bfloat16()
+        v = torch.randn(4, 1, h_kv, d, device=DEV).bfloat16()
+        got = paged_attention(q, k, v, ref, m, 0, d**-0.5, n_rep)
+        torch.cuda.synchronize()
+        form = pool._ref_form[1]
+        assert form is not None and torch.equal(form.context_lens, ours.context_lens)
+        expect = O.decode_reference(q[:, 0].cpu(), pool.k[0].cpu(), pool.v[0].cpu(), ours.block_tables.cpu(),
+                                    ours.context_lens.cpu(), bs, d**-0.5)
+        assert (got[:, 0].float().cpu() - expect).abs().max().item() <= 2e-2
