@@ -130,8 +130,12 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
         and q_start is not None
         and q.dtype in (torch.bfloat16, torch.float16)
     ):
-        max_q = getattr(paged, "max_q_len", 0) or b * sq
-        out = _prefill(q, pool, layer_idx, block_tables, cu_seqlens_q, q_start, max_q, paged, scale, err)
+        split = getattr(paged, "row_split", None)
+        if split is not None:
+            out = _split_step(q, pool, layer_idx, split, scale, err)
+        else:
+            max_q = getattr(paged, "max_q_len", 0) or b * sq
+            out = _prefill(q, pool, layer_idx, block_tables, cu_seqlens_q, q_start, max_q, paged, scale, err)
     elif paged.use_triton and block_tables is not None and context_lens is not None and sq == 1:
         out = _decode(q, pool, layer_idx, block_tables, context_lens, paged, scale, err)
     else:
@@ -166,8 +170,27 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
     return out
 
 
+def _split_step(q, pool, layer_idx: int, split, scale: float, err) -> torch.Tensor:
+    """A packed step whose one-token rows (decodes) form one block of rows:
+    those rows through the decode kernels (the balanced schedule when the batch
+    fills the device), the other block through the prefill kernel, each kernel
+    reading its rows of ``q`` and writing its rows of the output in place. A
+    one-token row is a decode: it attends its whole history, as the prefill
+    kernel would. Returns ``q``'s shape."""
+    b, sq, hq, d = q.shape
+    qf = q.reshape(b * sq, hq, d)
+    out = torch.empty_like(qf)
+    (d0, d1), (p0, p1) = split.dec_range, split.pre_range
+    _decode(qf[d0:d1].unsqueeze(1), pool, layer_idx, split.dec_tables, split.dec_ctx, split, scale, err,
+            out=out[d0:d1])
+    if p1 > p0:
+        _prefill(qf[p0:p1].unsqueeze(0), pool, layer_idx, split.pre_tables, split.pre_cu, split.pre_q_start,
+                 split.pre_max_q, split, scale, err, out=out[p0:p1])
+    return out.view(b, sq, hq, d)
+
+
 def _prefill(q, pool, layer_idx: int, block_tables, cu_seqlens_q, q_start, max_q: int, holder, scale: float,
-             err) -> torch.Tensor:
+             err, out: torch.Tensor | None = None) -> torch.Tensor:
     """Packed query chunks over block tables: the chunked-prefill kernel with
     the step's work plan (built by the first layer, cached on ``holder``).
     Returns ``q``'s shape."""
@@ -185,11 +208,12 @@ def _prefill(q, pool, layer_idx: int, block_tables, cu_seqlens_q, q_start, max_q
             pass
     return kernels.paged_prefill(
         q.reshape(b * sq, hq, d), pool.k[layer_idx], pool.v[layer_idx], block_tables, cu_seqlens_q, q_start, max_q,
-        pool.block_size, scale, err_flags=err, plan=plan,
+        pool.block_size, scale, out=out, err_flags=err, plan=plan,
     ).view(b, sq, hq, d)
 
 
-def _decode(q, pool, layer_idx: int, block_tables, context_lens, holder, scale: float, err) -> torch.Tensor:
+def _decode(q, pool, layer_idx: int, block_tables, context_lens, holder, scale: float, err,
+            out: torch.Tensor | None = None) -> torch.Tensor:
     """One-token decode over block tables: the balanced plan when the batch fills
     the device (cached on ``holder.decode_plan`` for the step's other layers),
     else the fixed split-KV partitions. Returns ``[B, 1, H_q, D]``."""
@@ -215,7 +239,7 @@ def _decode(q, pool, layer_idx: int, block_tables, context_lens, holder, scale: 
         ws = pool.workspace(kernels.planned_workspace_bytes(b, hq, h_kv, d))
         ctr = pool.decode_counters(kernels.decode_num_counters(b, hq, h_kv))
         out = kernels.paged_decode_planned(
-            q.reshape(b, hq, d), k_layer, v_layer, plan, scale, workspace=ws, err_flags=err, counters=ctr
+            q.reshape(b, hq, d), k_layer, v_layer, plan, scale, out=out, workspace=ws, err_flags=err, counters=ctr
         )
     else:
         ws = ctr = None
@@ -226,7 +250,7 @@ def _decode(q, pool, layer_idx: int, block_tables, context_lens, holder, scale: 
                 ctr = pool.decode_counters(kernels.decode_num_counters(b, hq, h_kv))
         out = kernels.paged_decode(
             q.reshape(b, hq, d), k_layer, v_layer, block_tables, context_lens,
-            pool.block_size, scale, workspace=ws, err_flags=err, counters=ctr,
+            pool.block_size, scale, out=out, workspace=ws, err_flags=err, counters=ctr,
         )
     return out.view(b, 1, hq, d)
 

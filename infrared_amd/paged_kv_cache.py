@@ -281,6 +281,27 @@ class _DecodeForm:
 
 
 @dataclass(slots=True)
+class RowSplit:
+    """A packed step divided by kernel: its one-token rows (decodes), one block
+    of packed rows ``dec_range`` = (first, end), run as a decode batch
+    (``dec_tables``, ``dec_ctx`` = contexts including the new token, int32);
+    the other sequences' rows, the block ``pre_range``, as chunked prefill
+    (``pre_tables``, ``pre_cu``, ``pre_q_start``, ``pre_max_q``). The parts'
+    plans are cached here for the step's other layers."""
+
+    dec_range: tuple[int, int]
+    dec_tables: torch.Tensor
+    dec_ctx: torch.Tensor
+    pre_range: tuple[int, int]
+    pre_tables: torch.Tensor
+    pre_cu: torch.Tensor
+    pre_q_start: torch.Tensor
+    pre_max_q: int
+    decode_plan: object | None = None
+    prefill_plan: object | None = None
+
+
+@dataclass(slots=True)
 class PagedContext:
     """Per-forward paged metadata handed to the attention layer.
 
@@ -301,7 +322,10 @@ class PagedContext:
     ``decode_plan`` caches the balanced decode schedule of ``block_tables`` /
     ``context_lens``, ``prefill_plan`` the heaviest-first work plan of a
     prefill step: the step's first layer builds them, the others reuse them (a
-    context is one step's metadata, shared by every layer).
+    context is one step's metadata, shared by every layer). ``row_split``
+    (from ``metadata.prefill_context``, for a packed step whose one-token rows
+    form one block) sends those rows to the decode kernels and the chunks to
+    the prefill kernel.
     """
 
     pool: PagedKVPool
@@ -315,3 +339,4 @@ class PagedContext:
     max_q_len: int = 0
     decode_plan: object | None = None
     prefill_plan: object | None = None
+    row_split: RowSplit | None = None

@@ -109,7 +109,7 @@ def test_prefill_step_builds_its_work_plan_once():
     g = torch.Generator().manual_seed(9)
     bs, h_kv, n_rep, d = 16, 4, 7, 128
     num_cached = [0, 2000, 160, 3000, 40, 40, 900, 1200]
-    q_lens = [300, 300, 280, 300, 64, 300, 1, 250]
+    q_lens = [300, 300, 280, 300, 64, 300, 2, 250]
     assert kernels.prefill_plan_pays(len(q_lens), max(q_lens), h_kv * n_rep, h_kv, DEV)
     nblk = sum(metadata.blocks_for(c + n, bs) for c, n in zip(num_cached, q_lens))
     perm = torch.randperm(nblk + 10, generator=g).tolist()
@@ -410,6 +410,7 @@ def test_reference_prefill_metadata_runs_the_prefill_kernel(kind):
     pool.k.normal_()
     pool.v.normal_()
     ours, _ = metadata.prefill_context(pool, tables, num_cached, q_lens)
+    ours.row_split = None  # every row through the prefill kernel, as the packed form runs
     write, gather, mask = _reference_prefill_frame(pool, tables, num_cached, q_lens, kind == "prefix-hit")
     assert torch.equal(write, ours.write_slots)
     ref = _ReferenceContext(pool, write, gather)
@@ -503,3 +504,44 @@ def test_reference_metadata_refilled_in_place_is_checked_again():
         expect = O.decode_reference(q[:, 0].cpu(), pool.k[0].cpu(), pool.v[0].cpu(), ours.block_tables.cpu(),
                                     ours.context_lens.cpu(), bs, d**-0.5)
         assert (got[:, 0].float().cpu() - expect).abs().max().item() <= 2e-2
+
+
+@pytest.mark.parametrize("order", ["decodes-first", "decodes-last", "interleaved"])
+def test_packed_step_runs_its_decode_rows_on_the_decode_kernels(order):
+    """A packed step whose one-token rows form one block (packed first or last)
+    is split: those rows run as a decode batch, the chunks as prefill, each
+    writing its rows of the output in place; with the decodes interleaved
+    among the chunks the step stays one prefill launch. Every layout matches
+    the oracle."""
+    g = torch.Generator().manual_seed(31)
+    bs, h_kv, n_rep, d = 16, 4, 7, 128
+    dec_cached = [int(x) for x in torch.randint(20, 900, (6,), generator=g)]
+    chunks = [(0, 90), (300, 45)]
+    if order == "decodes-first":
+        seqs = [(c, 1) for c in dec_cached] + chunks
+    elif order == "decodes-last":
+        seqs = chunks + [(c, 1) for c in dec_cached]
+    else:
+        seqs = [chunks[0]] + [(c, 1) for c in dec_cached[:3]] + [chunks[1]] + [(c, 1) for c in dec_cached[3:]]
+    num_cached, q_lens = [c for c, _ in seqs], [n for _, n in seqs]
+    need = [metadata.blocks_for(c + n, bs) for c, n in seqs]
+    perm = torch.randperm(sum(need) + 8, generator=g).tolist()
+    tables, off = [], 0
+    for nb in need:
+        tables.append(perm[off : off + nb])
+        off += nb
+    pool = PagedKVPool(1, sum(need) + 8, bs, h_kv, d, torch.bfloat16, device=DEV, strict=True)
+    pool.k.normal_()
+    pool.v.normal_()
+    paged, _ = metadata.prefill_context(pool, tables, num_cached, q_lens)
+    assert (paged.row_split is None) == (order == "interleaved")
+    total = sum(q_lens)
+    q = torch.randn(1, total, h_kv * n_rep, d, device=DEV).bfloat16()
+    k = torch.randn(1, total, h_kv, d, device=DEV).bfloat16()
+    v = torch.randn(1, total, h_kv, d, device=DEV).bfloat16()
+    out = paged_attention(q, k, v, paged, None, 0, d**-0.5, n_rep)
+    torch.cuda.synchronize()
+    bt = metadata.block_tables_tensor(tables, "cpu")
+    ref = O.prefill_reference(q[0].cpu(), pool.k[0].cpu(), pool.v[0].cpu(), bt, paged.cu_seqlens_q.cpu(),
+                              num_cached, bs, d**-0.5)
+    assert (out[0].float().cpu() - ref).abs().max().item() <= 2e-2
