@@ -639,7 +639,10 @@ class VarlenForm:
     cu_seqlens_q: torch.Tensor
     q_start: torch.Tensor
     max_q_len: int
+    q_lens: tuple[int, ...] = ()  # host copies of the derived chunk sizes and prefixes
+    prefixes: tuple[int, ...] = ()
     prefill_plan: object | None = None
+    row_split: object | None = None
 
 
 def varlen_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int, num_blocks: int
@@ -648,7 +651,8 @@ def varlen_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int,
     (``gather_slots`` ``[1, K]`` int64, mask ``[1, 1, Q, K]``), or ``None``
     unless it has that form exactly (``ir_varlen_form_scan`` /
     ``ir_varlen_form_tables``). Synchronises twice: the sequence count sizes the
-    block tables, and the second pass's verdict decides."""
+    block tables, and the second pass's verdict decides (read together with
+    the derived chunk sizes and prefixes, host copies for the caller)."""
     dev = require_device(gather_slots, mask)
     if gather_slots.dtype != torch.int64 or gather_slots.dim() != 2 or gather_slots.shape[0] != 1:
         raise RuntimeError("varlen_form: gather_slots must be int64 [1, K]")
@@ -679,9 +683,12 @@ def varlen_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int,
         ptr(bt), bt.stride(0), width, ptr(info), stream_ptr(dev),
     )
     check(rc, "ir_varlen_form_tables")
-    if int(info[0].item()):
+    host = torch.cat([info[:1], cu[: nseq + 1], q_start[:nseq]]).tolist()  # the verdict and the split, one read
+    if host[0]:
         return None
-    return VarlenForm(bt, cu[: nseq + 1], q_start[:nseq], max_q)
+    offs, prefixes = host[1 : nseq + 2], host[nseq + 2 :]
+    q_lens = tuple(b - a for a, b in zip(offs, offs[1:]))
+    return VarlenForm(bt, cu[: nseq + 1], q_start[:nseq], max_q, q_lens, tuple(prefixes))
 
 
 def hbm_read(src: torch.Tensor, sink: torch.Tensor, workgroups: int = 0) -> None:

@@ -24,7 +24,7 @@ from collections.abc import Sequence
 import numpy as np
 import torch
 
-from infrared_amd.paged_kv_cache import PagedContext, PagedKVPool, RowSplit
+from infrared_amd.paged_kv_cache import PagedContext, PagedKVPool, row_split
 
 
 def slot(block_table: Sequence[int], pos: int, block_size: int) -> int:
@@ -133,40 +133,6 @@ def decode_context(
     return PagedContext(pool, ws, gs, use_triton, bt, cl), mask
 
 
-def _row_split(bt: torch.Tensor, num_cached: Sequence[int], q_lens: Sequence[int]) -> RowSplit | None:
-    """The packed step's one-token rows as a decode batch and the rest as
-    chunked prefill, when those rows form one block (the decodes packed first
-    or last, as a scheduler lists them); else ``None`` (one prefill launch, no
-    row copies)."""
-    dec = [i for i, n in enumerate(q_lens) if n == 1]
-    if not dec or dec != list(range(dec[0], dec[0] + len(dec))):
-        return None
-    if dec[0] != 0 and dec[-1] != len(q_lens) - 1:
-        return None
-    pre = [i for i, n in enumerate(q_lens) if n > 1]
-    first = sum(q_lens[: dec[0]])  # packed row of the first decode
-    nd = len(dec)
-    dec_range = (first, first + nd)
-    total = sum(q_lens)
-    pre_range = (nd, total) if first == 0 else (0, first)
-    pre_cu = np.concatenate([[0], np.cumsum([q_lens[i] for i in pre], dtype=np.int64)])
-    host = torch.from_numpy(np.concatenate([
-        np.asarray(dec, np.int64), np.asarray(pre, np.int64), np.asarray([num_cached[i] + 1 for i in dec], np.int64),
-        pre_cu, np.asarray([num_cached[i] for i in pre], np.int64)]).astype(np.int64))
-    t = host.to(bt.device)  # one host->device copy
-    dec_idx, pre_idx, dec_ctx, pre_cu_t, pre_qs = torch.split(t, [nd, len(pre), nd, len(pre) + 1, len(pre)])
-    return RowSplit(
-        dec_range=dec_range,
-        dec_tables=bt.index_select(0, dec_idx).contiguous(),
-        dec_ctx=dec_ctx.to(torch.int32),
-        pre_range=pre_range,
-        pre_tables=bt.index_select(0, pre_idx).contiguous(),
-        pre_cu=pre_cu_t.to(torch.int32),
-        pre_q_start=pre_qs.to(torch.int32),
-        pre_max_q=max((q_lens[i] for i in pre), default=0),
-    )
-
-
 def prefill_context(
     pool: PagedKVPool,
     block_tables: Sequence[Sequence[int]],
@@ -209,7 +175,7 @@ def prefill_context(
         nc_t.contiguous(),
         max(q_lens, default=0),
     )
-    ctx.row_split = _row_split(bt, num_cached, q_lens)
+    ctx.row_split = row_split(bt, num_cached, q_lens)
     if not with_mask:
         return ctx, None
     k_seq, k_pos, gslots = [], [], []

@@ -158,6 +158,8 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
             vform = pool.reference_varlen_form(paged.gather_slots, mask)
         if form is not None:
             out = _decode(q, pool, layer_idx, form.block_tables, form.context_lens, form, scale, err)
+        elif vform is not None and vform.row_split is not None:
+            out = _split_step(q, pool, layer_idx, vform.row_split, scale, err)
         elif vform is not None:
             out = _prefill(q, pool, layer_idx, vform.block_tables, vform.cu_seqlens_q, vform.q_start,
                            vform.max_q_len, vform, scale, err)

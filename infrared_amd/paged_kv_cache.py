@@ -32,8 +32,10 @@ rather than handled by a fallback.
 
 from __future__ import annotations
 
+from collections.abc import Sequence
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from infrared_amd import kernels
@@ -247,6 +249,9 @@ class PagedKVPool:
                 and gather_slots.is_cuda and mask.is_cuda and mask.dim() == 4 and tuple(mask.shape[:2]) == (1, 1)
                 and mask.shape[3] == gather_slots.shape[1]):
             form = kernels.varlen_form(gather_slots, mask, self.block_size, self.num_blocks)
+            if form is not None:
+                # the reference packs decodes first (infrared/engine/scheduler.py:104-115)
+                form.row_split = row_split(form.block_tables, form.prefixes, form.q_lens)
         self._ref_varlen = (key, form)
         return form
 
@@ -299,6 +304,40 @@ class RowSplit:
     pre_max_q: int
     decode_plan: object | None = None
     prefill_plan: object | None = None
+
+
+def row_split(bt: torch.Tensor, num_cached: Sequence[int], q_lens: Sequence[int]) -> RowSplit | None:
+    """The packed step's one-token rows as a decode batch and the rest as
+    chunked prefill, when those rows form one block (the decodes packed first
+    or last, as a scheduler lists them); else ``None`` (one prefill launch, no
+    row copies)."""
+    dec = [i for i, n in enumerate(q_lens) if n == 1]
+    if not dec or dec != list(range(dec[0], dec[0] + len(dec))):
+        return None
+    if dec[0] != 0 and dec[-1] != len(q_lens) - 1:
+        return None
+    pre = [i for i, n in enumerate(q_lens) if n > 1]
+    first = sum(q_lens[: dec[0]])  # packed row of the first decode
+    nd = len(dec)
+    dec_range = (first, first + nd)
+    total = sum(q_lens)
+    pre_range = (nd, total) if first == 0 else (0, first)
+    pre_cu = np.concatenate([[0], np.cumsum([q_lens[i] for i in pre], dtype=np.int64)])
+    host = torch.from_numpy(np.concatenate([
+        np.asarray(dec, np.int64), np.asarray(pre, np.int64), np.asarray([num_cached[i] + 1 for i in dec], np.int64),
+        pre_cu, np.asarray([num_cached[i] for i in pre], np.int64)]).astype(np.int64))
+    t = host.to(bt.device)  # one host->device copy
+    dec_idx, pre_idx, dec_ctx, pre_cu_t, pre_qs = torch.split(t, [nd, len(pre), nd, len(pre) + 1, len(pre)])
+    return RowSplit(
+        dec_range=dec_range,
+        dec_tables=bt.index_select(0, dec_idx).contiguous(),
+        dec_ctx=dec_ctx.to(torch.int32),
+        pre_range=pre_range,
+        pre_tables=bt.index_select(0, pre_idx).contiguous(),
+        pre_cu=pre_cu_t.to(torch.int32),
+        pre_q_start=pre_qs.to(torch.int32),
+        pre_max_q=max((q_lens[i] for i in pre), default=0),
+    )
 
 
 @dataclass(slots=True)

@@ -401,16 +401,15 @@ def test_reference_prefill_metadata_runs_the_prefill_kernel(kind):
     """Unchanged reference callers pass a packed frame (batch 1) of gather_slots
     + the varlen / causal mask for prefix-hit prefills and mixed steps. Its
     form is recognised once per step (later layers reuse the derived metadata:
-    cu_seqlens_q, q_start, block tables), and every layer equals the
-    block-table context's output bit for bit -- the same chunked-prefill
-    kernel on the same metadata -- and the oracle."""
+    cu_seqlens_q, q_start, block tables, and for a mixed step the split of its
+    decode rows), and every layer equals the block-table context's output bit
+    for bit -- the same kernels on the same metadata -- and the oracle."""
     tables, num_cached, q_lens, num_blocks = _prefill_case(kind)
     bs, h_kv, n_rep, d, layers = 16, 4, 7, 128, 3
     pool = PagedKVPool(layers, num_blocks, bs, h_kv, d, torch.bfloat16, device=DEV)
     pool.k.normal_()
     pool.v.normal_()
     ours, _ = metadata.prefill_context(pool, tables, num_cached, q_lens)
-    ours.row_split = None  # every row through the prefill kernel, as the packed form runs
     write, gather, mask = _reference_prefill_frame(pool, tables, num_cached, q_lens, kind == "prefix-hit")
     assert torch.equal(write, ours.write_slots)
     ref = _ReferenceContext(pool, write, gather)
@@ -432,6 +431,8 @@ def test_reference_prefill_metadata_runs_the_prefill_kernel(kind):
     f = forms[0]
     assert f is not None and all(x is f for x in forms)
     assert f.max_q_len == max(q_lens)
+    assert (f.row_split is not None) == (kind == "mixed")  # its decodes form one block of rows
+    assert f.q_lens == tuple(q_lens) and f.prefixes == tuple(num_cached)
     assert torch.equal(f.cu_seqlens_q, ours.cu_seqlens_q) and torch.equal(f.q_start, ours.q_start)
     for i, (c, n) in enumerate(zip(num_cached, q_lens)):  # (entries past a history are never read)
         nb = metadata.blocks_for(c + n, bs)
