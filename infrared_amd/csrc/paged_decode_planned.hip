@@ -500,29 +500,39 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
   const int n_ups = a.n_ups;
 
   // ---- 1. everything the wavefront needs, requested at once
+  // (a plan with pairs needs the pair kernel: its flag empties this
+  // workgroup's slice rather than branching, so no read waits on it)
   const int32_t* hdr = (const int32_t*)(plan + ly.hdr);
   const int32_t* wh = (const int32_t*)(plan + ly.whdr) + ((int64_t)grp * NW + w) * 8;
   const u32x2* facts = (const u32x2*)(plan + ly.facts);
-  const int R = hdr[1];
-  if (!PAIRS && hdr[3] != 0) {  // a plan with pairs needs the pair kernel
-    if (grp == 0 && tid == 0) flag_error(a.err, IR_ERR_PLAN);
-    return;
-  }
-  const int wlo = wh[0], cnt_w = wh[1], fl = wh[2], ll = wh[3], lo = wh[4], hi = wh[5], u_first = wh[6];
+  const int32_t* sp = (const int32_t*)(plan + ly.seq_pre);
+  const int32_t* pp = (const int32_t*)(plan + ly.pair);
+  const int pre0 = tid <= B ? sp[tid] : 0;  // every sequence's when B < NT
+  const int pair0 = PAIRS && tid < B ? pp[tid] : 0;
+  const int R = hdr[1], hdr_pairs = hdr[3];
+  // the wavefront's header in two 16-byte reads (the plan is 256-byte
+  // aligned), so the select below cannot become a skipped load
+  const u32x4 wh0 = *(const u32x4*)wh, wh1 = *(const u32x4*)(wh + 4);
   u32x2 f0 = ((const u32x2*)(plan + ly.first))[((int64_t)grp * NW + w) * kPlanRun + lane];
-  {
-    const int32_t* sp = (const int32_t*)(plan + ly.seq_pre);
-    for (int b = tid; b <= B; b += NT) s_pre[b] = sp[b];
-    if constexpr (PAIRS) {
-      const int32_t* pp = (const int32_t*)(plan + ly.pair);
-      for (int b = tid; b < B; b += NT) s_pair[b] = pp[b];
-    }
+  // every read above is used here, so they all go out before the first wait
+  // (one round trip) instead of each behind the last one's use
+  asm volatile("" ::"s"(R), "s"(hdr_pairs), "s"(wh0[0]), "s"(wh0[1]), "s"(wh0[2]), "s"(wh0[3]), "s"(wh1[0]),
+               "s"(wh1[1]), "s"(wh1[2]), "v"(f0[0]), "v"(f0[1]), "v"(pre0), "v"(pair0));
+  const bool wrong_plan = !PAIRS && hdr_pairs != 0;
+  const int wlo = (int)wh0[0], cnt_w = (int)wh0[1], fl = (int)wh0[2], ll = (int)wh0[3];
+  const int lo = (int)wh1[0], u_first = (int)wh1[2];
+  const int hi = wrong_plan ? lo : (int)wh1[1];
+  if (tid <= B) s_pre[tid] = pre0;
+  for (int b = tid + NT; b <= B; b += NT) s_pre[b] = sp[b];
+  if constexpr (PAIRS) {
+    if (tid < B) s_pair[tid] = pair0;
+    for (int b = tid + NT; b < B; b += NT) s_pair[b] = pp[b];
   }
   if (tid < NW) s_fl[tid] = -1;
   if (tid < 2) s_stg[tid] = -1;
 
   // sequences with no usable key get a zero output row (workgroup 0)
-  if (grp == 0) {
+  if (grp == 0 && !wrong_plan) {
     const int n_empty = hdr[2];
     const int32_t* empty = (const int32_t*)(plan + ly.empty);
     constexpr int C8 = D / 8;
@@ -539,7 +549,8 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
     }
   }
   __syncthreads();
-  if (lo >= hi) return;  // uniform: past the end of the list
+  if (wrong_plan && grp == 0 && tid == 0) flag_error(a.err, IR_ERR_PLAN);
+  if (lo >= hi) return;  // uniform: past the end of the list (or a plan with pairs)
 
   struct Lbl {
     int u, b, j, us, ue;
