@@ -42,7 +42,15 @@ COMMON_FLAGS = [
 
 # Per-source extras. The prefill kernel's max reductions never see a NaN from
 # its own arithmetic (masked scores are -inf), so fmaxf needs no NaN quieting.
-FILE_FLAGS = {"paged_prefill.hip": ["-fno-honor-nans"]}
+# The planned decode's six leading scalar arguments (the plan and the offsets
+# of its first reads) are preloaded into SGPRs; kernels whose first argument is
+# an aggregate preload nothing. A code object built so starts with a 256-byte
+# block that loads those arguments the ordinary way, for firmware that does
+# not preload.
+FILE_FLAGS = {
+    "paged_prefill.hip": ["-fno-honor-nans"],
+    "paged_decode_planned.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=6"],
+}
 
 
 def hipcc() -> str:

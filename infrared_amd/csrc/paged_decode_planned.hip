@@ -475,10 +475,16 @@ __device__ __forceinline__ void slot_read(const float* row, int g, f32x4 (&acc)[
 
 // The decode over a plan: no scan, no block-table reads. A wavefront's header
 // and its first 64 tile facts sit at fixed addresses, so its first tile loads
-// go out one round trip after launch.
+// go out one round trip after launch. The addresses those first reads need
+// lead the argument list as plain scalars (the plan header sits at the plan's
+// start; the other offsets precede the facts, so they fit 32 bits): this file
+// is built with kernel-argument preloading, which hands the leading scalar
+// arguments over in SGPRs at wave start, so the plan reads do not wait for a
+// kernel-argument load.
 template <int DT, int D, int NW, int DEPTH, bool PAIRS>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(DT == IR_DTYPE_F32 ? 1 : 2)))
-void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout ly) {
+void paged_decode_planned_kernel(const uint8_t* plan, uint32_t o_seq_pre, uint32_t o_pair, uint32_t o_whdr,
+                                 uint32_t o_first, int B, DecodeArgs a, PlanLayout ly) {
   typedef TileShape<DT, D> Sh;
   constexpr int EB = Sh::EB;
   constexpr int NT = NW * 64;
@@ -496,24 +502,24 @@ void paged_decode_planned_kernel(DecodeArgs a, const uint8_t* plan, PlanLayout l
   const int lane = tid & 63, g = lane >> 4, c = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = blockIdx.x;
-  const int B = a.num_seqs;
   const int n_ups = a.n_ups;
 
   // ---- 1. everything the wavefront needs, requested at once
   // (a plan with pairs needs the pair kernel: its flag empties this
   // workgroup's slice rather than branching, so no read waits on it)
-  const int32_t* hdr = (const int32_t*)(plan + ly.hdr);
-  const int32_t* wh = (const int32_t*)(plan + ly.whdr) + ((int64_t)grp * NW + w) * 8;
+  const int32_t* hdr = (const int32_t*)plan;
+  const int32_t* wh = (const int32_t*)(plan + o_whdr) + ((int64_t)grp * NW + w) * 8;
   const u32x2* facts = (const u32x2*)(plan + ly.facts);
-  const int32_t* sp = (const int32_t*)(plan + ly.seq_pre);
-  const int32_t* pp = (const int32_t*)(plan + ly.pair);
+  const int32_t* sp = (const int32_t*)(plan + o_seq_pre);
+  const int32_t* pp = (const int32_t*)(plan + o_pair);
   const int pre0 = tid <= B ? sp[tid] : 0;  // every sequence's when B < NT
   const int pair0 = PAIRS && tid < B ? pp[tid] : 0;
-  const int R = hdr[1], hdr_pairs = hdr[3];
+  const u32x4 h4 = *(const u32x4*)hdr;
+  const int R = (int)h4[1], hdr_pairs = (int)h4[3];
   // the wavefront's header in two 16-byte reads (the plan is 256-byte
   // aligned), so the select below cannot become a skipped load
   const u32x4 wh0 = *(const u32x4*)wh, wh1 = *(const u32x4*)(wh + 4);
-  u32x2 f0 = ((const u32x2*)(plan + ly.first))[((int64_t)grp * NW + w) * kPlanRun + lane];
+  u32x2 f0 = ((const u32x2*)(plan + o_first))[((int64_t)grp * NW + w) * kPlanRun + lane];
   // every read above is used here, so they all go out before the first wait
   // (one round trip) instead of each behind the last one's use
   asm volatile("" ::"s"(R), "s"(hdr_pairs), "s"(wh0[0]), "s"(wh0[1]), "s"(wh0[2]), "s"(wh0[3]), "s"(wh1[0]),
@@ -821,12 +827,16 @@ void launch_planned_dt_d(const DecodeArgs& a, const uint8_t* plan, const PlanLay
   // HBM saturated with one tile each, and the shorter queues halve the latency
   // of the end phase's round trips (two tiles in flight: 0.4 us slower per call
   // on 64 sequences x 28/4 heads, contexts 512..4096).
+  // plan_layout: the header is at 0, and sequence, pair, wavefront-header and
+  // first-fact regions are sized by the sequence count and grid only
+  const uint32_t o_sp = (uint32_t)ly.seq_pre, o_pr = (uint32_t)ly.pair, o_wh = (uint32_t)ly.whdr,
+                 o_fi = (uint32_t)ly.first;
   if (pairs)
     hipLaunchKernelGGL((paged_decode_planned_kernel<DT, D, kPlanWaves, 1, true>), dim3(grid), dim3(kPlanWaves * 64), 0,
-                       s, a, plan, ly);
+                       s, plan, o_sp, o_pr, o_wh, o_fi, a.num_seqs, a, ly);
   else
     hipLaunchKernelGGL((paged_decode_planned_kernel<DT, D, kPlanWaves, 1, false>), dim3(grid), dim3(kPlanWaves * 64),
-                       0, s, a, plan, ly);
+                       0, s, plan, o_sp, o_pr, o_wh, o_fi, a.num_seqs, a, ly);
 }
 
 // Pairs fit one unit's 16 MFMA columns when a KV head has at most 8 query
