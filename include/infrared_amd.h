@@ -324,11 +324,11 @@ int ir_decode_form(const int64_t* gather_slots, int64_t gs_b_stride, int64_t gs_
  *   ir_varlen_form_scan: reads every mask row (element (r, k) at
  *     mask + r*mask_q_stride + k*mask_k_stride); writes row_ranges [2*num_q]
  *     (scratch), cu_seqlens_q [num_q + 1], q_start [num_q] and seq_k_offsets
- *     [num_q] for the sequences found, and info[1..3] = sequence count, longest
- *     chunk, widest block table (blocks). ORs 1 into info[0] unless each row's
- *     visible keys are one contiguous range, every other value <= -6e4, the
- *     rows of a sequence each see one key more than the last, and the
- *     sequences' key ranges tile [0, num_k) in order.
+ *     [num_q] for the sequences found, and info[0..3] (no clearing needed):
+ *     info[1..3] = sequence count, longest chunk, widest block table (blocks);
+ *     info[0] = 0 if each row's visible keys are one contiguous range, every
+ *     other value <= -6e4, the rows of a sequence each see one key more than
+ *     the last, and the sequences' key ranges tile [0, num_k) in order, else 1.
  *   ir_varlen_form_tables: block_tables[i, j] = gather_slots[k_off_i + j*bs] / bs
  *     ([num_seqs, bt_stride] int32, max_blocks_per_seq >= info[3]); ORs 1 into
  *     info[0] unless every slot of every sequence has the closed form with a

@@ -36,21 +36,47 @@ __device__ __forceinline__ float mask_value(const void* m, int dtype, int64_t of
   return dtype == IR_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
 }
 
-// Element e (0 <= e < 16 / bytes) of a 16-byte piece of the mask.
-__device__ __forceinline__ float piece_value(u32x4 x, int dtype, int e) {
-  if (dtype == IR_DTYPE_F32) return __uint_as_float(x[e]);
-  const uint32_t h = (x[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-  return dtype == IR_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+// Two wavefronts per row and four 16-byte pieces per lane and pass: of
+// 64-1024 threads x 3-12 pieces, the fastest on a 4096 x 22819 bf16 mask.
+constexpr int kRowThreads = 128;
+constexpr int kRowPieces = 4;  // 16-byte pieces a lane has in flight per pass
+
+// finfo(dtype).min in every element of a 32-bit word (two for 16-bit masks).
+template <int DT>
+constexpr uint32_t kMinWord = DT == IR_DTYPE_F32 ? 0xff7fffffu : DT == IR_DTYPE_BF16 ? 0xff7fff7fu : 0xfbfffbffu;
+
+// Bit e of `zero`: element e of a 16-byte piece is 0 (visible); bit e of
+// `bad`: it is neither 0 nor masked (at most -6e4; NaN fails both).
+template <int DT>
+__device__ __forceinline__ void piece_bits(u32x4 x, uint32_t& zero, uint32_t& bad) {
+  constexpr int PER = DT == IR_DTYPE_F32 ? 4 : 8;
+  zero = 0;
+  bad = 0;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    float v;
+    if constexpr (DT == IR_DTYPE_F32) {
+      v = __uint_as_float(x[e]);
+    } else {
+      const uint32_t h = (x[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+      v = DT == IR_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+    }
+    zero |= (uint32_t)(v == 0.f) << e;
+    bad |= (uint32_t)(v != 0.f && !(v <= -6e4f)) << e;
+  }
 }
 
 // One workgroup per mask row: the first and last visible key, their count and
 // whether any other value fails to mask. A contiguous mask is read as 16-byte
-// pieces of the flat [Q * K] array (rows need not start on a piece: a piece's
-// elements outside the row are skipped); the last piece of the array, when
-// partial, and strided masks are read element by element.
-__global__ __launch_bounds__(kScanThreads) void varlen_rows_kernel(const void* mask, int64_t m_q, int64_t m_k,
-                                                                  int mask_dtype, int Q, int K, bool flat,
-                                                                  int32_t* range, int32_t* info) {
+// pieces of the flat [Q * K] array, a lane's pieces of a pass all in flight
+// before any is inspected; rows need not start on a piece, so the first
+// and last piece of a row keep only the row's elements, and the array's last
+// piece, when partial, is read element by element. Strided masks are read
+// element by element.
+template <int DT>
+__global__ __launch_bounds__(kRowThreads) void varlen_rows_kernel(const void* mask, int64_t m_q, int64_t m_k, int Q,
+                                                                  int K, bool flat, int32_t* range) {
+  constexpr int PER = DT == IR_DTYPE_F32 ? 4 : 8;  // elements per 16-byte piece
   __shared__ int s_first, s_last, s_count, s_wrong;
   const int r = blockIdx.x, tid = threadIdx.x;
   if (tid == 0) {
@@ -71,40 +97,81 @@ __global__ __launch_bounds__(kScanThreads) void varlen_rows_kernel(const void* m
     }
   };
   if (flat) {
-    const int per = mask_dtype == IR_DTYPE_F32 ? 4 : 8;  // elements per 16-byte piece
-    const int64_t n = (int64_t)Q * K, e0 = (int64_t)r * K, e1 = e0 + K;
-    const int64_t c0 = e0 / per, c1 = (e1 + per - 1) / per;
-#pragma unroll 4
-    for (int64_t c = c0 + tid; c < c1; c += kScanThreads) {
-      const int64_t g0 = c * per;
-      if (g0 + per <= n) {
-        const u32x4 x = ((const u32x4*)mask)[c];
-        for (int e = 0; e < per; ++e)
-          if (g0 + e >= e0 && g0 + e < e1) visit((int)(g0 + e - e0), piece_value(x, mask_dtype, e));
-      } else {
-        for (int64_t g = max(g0, e0); g < min(g0 + per, e1); ++g)
-          visit((int)(g - e0), mask_value(mask, mask_dtype, g));
+    const int64_t e0 = (int64_t)r * K, e1 = e0 + K;
+    const int64_t c0 = e0 / PER, c1 = (e1 + PER - 1) / PER;
+    const int64_t whole = (int64_t)Q * K / PER;  // pieces wholly inside the array
+    // every lane loads every pass, past the row's last whole piece from that
+    // piece again (a row with no whole piece of its own loads nothing and
+    // inspects its elements one by one)
+    const int64_t c_end = min(c1, whole) - 1;
+    const u32x4* pieces = (const u32x4*)mask;
+    auto inspect = [&](const u32x4& v, int64_t c) {
+      const int k0 = (int)(c * PER - e0);  // key of the piece's element 0 (negative in a row's first piece)
+      if (c >= whole) {
+        for (int e = max(0, -k0); e < PER && k0 + e < K; ++e) visit(k0 + e, mask_value(mask, DT, e0 + k0 + e));
+        return;
+      }
+      const int lo = max(0, -k0), hi = min(PER, K - k0);  // the row's elements of this piece
+      const uint32_t keep = ((1u << hi) - 1u) & ~((1u << lo) - 1u);
+      // a piece wholly in the row that is all +0 or all finfo(dtype).min --
+      // nearly every piece of the reference's mask -- is settled from its
+      // four words; anything else is inspected element by element
+      const uint32_t any = v[0] | v[1] | v[2] | v[3];
+      const uint32_t all = v[0] & v[1] & v[2] & v[3];
+      const bool whole_piece = keep == (1u << PER) - 1u;
+      if (whole_piece && any == 0u) {
+        first = min(first, k0);
+        last = max(last, k0 + PER - 1);
+        count += PER;
+        return;
+      }
+      if (whole_piece && any == kMinWord<DT> && all == kMinWord<DT>) return;
+      uint32_t zero, bad;
+      piece_bits<DT>(v, zero, bad);
+      zero &= keep;
+      wrong |= (bad & keep) != 0u;
+      if (zero) {
+        first = min(first, k0 + __builtin_ctz(zero));
+        last = max(last, k0 + 31 - __builtin_clz(zero));
+        count += __builtin_popcount(zero);
+      }
+    };
+    for (int64_t base = c0; base < c1; base += (int64_t)kRowThreads * kRowPieces) {
+      u32x4 x[kRowPieces];
+      if (c_end >= c0) {  // uniform: the row holds a whole piece
+#pragma unroll
+        for (int i = 0; i < kRowPieces; ++i) x[i] = load_nt(pieces + min(base + i * kRowThreads + tid, c_end));
+      }
+#pragma unroll
+      for (int i = 0; i < kRowPieces; ++i) {
+        const int64_t c = base + i * kRowThreads + tid;
+        if (c >= c1) break;
+        inspect(x[i], c);
       }
     }
   } else {
     const int64_t row = (int64_t)r * m_q;
-    for (int k = tid; k < K; k += kScanThreads) visit(k, mask_value(mask, mask_dtype, row + (int64_t)k * m_k));
+    for (int k = tid; k < K; k += kRowThreads) visit(k, mask_value(mask, DT, row + (int64_t)k * m_k));
   }
-  atomicMin(&s_first, first);
-  atomicMax(&s_last, last);
-  atomicAdd(&s_count, count);
+  if (count) {
+    atomicMin(&s_first, first);
+    atomicMax(&s_last, last);
+    atomicAdd(&s_count, count);
+  }
   if (wrong) s_wrong = 1;
   __syncthreads();
   if (tid == 0) {
-    range[2 * r] = s_first;
-    range[2 * r + 1] = s_last;
-    // no visible key, or a masked key between two visible ones
-    if (s_wrong || s_count == 0 || s_last - s_first + 1 != s_count) atomicOr(&info[0], 1);
+    // no visible key, or a masked key between two visible ones: the row's
+    // range is (-1, -1), which the segment pass reports
+    const bool bad = s_wrong || s_count == 0 || s_last - s_first + 1 != s_count;
+    range[2 * r] = bad ? -1 : s_first;
+    range[2 * r + 1] = bad ? -1 : s_last;
   }
 }
 
 // One workgroup: rows -> sequences (block-wide scan of the rows where lo
-// moves), then the longest chunk and the widest table.
+// moves), then the longest chunk and the widest table; info[0..3] written
+// whole (no clearing before the pass).
 __global__ __launch_bounds__(kSegThreads) void varlen_segments_kernel(const int32_t* range, int Q, int K, int bs,
                                                                      int32_t* cu, int32_t* q_start, int32_t* seq_lo,
                                                                      int32_t* info) {
@@ -125,9 +192,9 @@ __global__ __launch_bounds__(kSegThreads) void varlen_segments_kernel(const int3
       const int lo = range[2 * r], hi = range[2 * r + 1];
       const int plo = r > 0 ? range[2 * r - 2] : -1, phi = r > 0 ? range[2 * r - 1] : -1;
       start = r == 0 || lo != plo;
-      // a new sequence's keys follow the last one's; a row of the same
-      // sequence sees one key more than the row before it
-      if (start ? lo != phi + 1 : hi != phi + 1) s_bad = 1;
+      // a row whose own scan failed; a new sequence's keys follow the last
+      // one's; a row of the same sequence sees one key more than the row before
+      if (lo < 0 || (start ? lo != phi + 1 : hi != phi + 1)) s_bad = 1;
       if (r == Q - 1 && hi != K - 1) s_bad = 1;  // the key axis ends with the last sequence
     }
     s_scan[tid] = start;
@@ -161,7 +228,7 @@ __global__ __launch_bounds__(kSegThreads) void varlen_segments_kernel(const int3
   }
   __syncthreads();
   if (tid == 0) {
-    if (s_bad) atomicOr(&info[0], 1);
+    info[0] = s_bad;
     info[1] = nseq;
     info[2] = s_maxq;
     info[3] = s_maxb;
@@ -215,8 +282,15 @@ extern "C" int ir_varlen_form_scan(const void* mask, int64_t mask_q_stride, int6
   hipStream_t s = (hipStream_t)stream;
   // contiguous rows from a 16-byte-aligned start: read as 16-byte pieces
   const bool flat = mask_k_stride == 1 && mask_q_stride == num_k && ((uintptr_t)mask & 15) == 0;
-  hipLaunchKernelGGL(varlen_rows_kernel, dim3(num_q), dim3(kScanThreads), 0, s, mask, mask_q_stride, mask_k_stride,
-                     mask_dtype, num_q, num_k, flat, row_ranges, info);
+  if (mask_dtype == IR_DTYPE_F32)
+    hipLaunchKernelGGL(varlen_rows_kernel<IR_DTYPE_F32>, dim3(num_q), dim3(kRowThreads), 0, s, mask, mask_q_stride,
+                       mask_k_stride, num_q, num_k, flat, row_ranges);
+  else if (mask_dtype == IR_DTYPE_BF16)
+    hipLaunchKernelGGL(varlen_rows_kernel<IR_DTYPE_BF16>, dim3(num_q), dim3(kRowThreads), 0, s, mask, mask_q_stride,
+                       mask_k_stride, num_q, num_k, flat, row_ranges);
+  else
+    hipLaunchKernelGGL(varlen_rows_kernel<IR_DTYPE_F16>, dim3(num_q), dim3(kRowThreads), 0, s, mask, mask_q_stride,
+                       mask_k_stride, num_q, num_k, flat, row_ranges);
   hipLaunchKernelGGL(varlen_segments_kernel, dim3(1), dim3(kSegThreads), 0, s, row_ranges, num_q, num_k, block_size,
                      cu_seqlens_q, q_start, seq_k_offsets, info);
   return check_launch("ir_varlen_form_scan");

@@ -663,11 +663,14 @@ def varlen_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int,
     if q == 0 or k == 0 or q >= 2**31 or k >= 2**31:
         return None
     i32 = dict(dtype=torch.int32, device=dev)
-    ranges = torch.empty(2 * q, **i32)
-    cu = torch.empty(q + 1, **i32)
-    q_start = torch.empty(q, **i32)
-    k_off = torch.empty(q, **i32)
-    info = torch.zeros(4, **i32)
+    # one allocation for the scan's outputs (info is written whole by the scan)
+    a = lambda n: (n + 63) // 64 * 64  # noqa: E731 -- 256-byte regions
+    buf = torch.empty(a(q + 1) + 2 * a(q) + 64 + 2 * q, **i32)
+    cu = buf[: q + 1]
+    q_start = buf[a(q + 1) : a(q + 1) + q]
+    k_off = buf[a(q + 1) + a(q) : a(q + 1) + a(q) + q]
+    info = buf[a(q + 1) + 2 * a(q) : a(q + 1) + 2 * a(q) + 4]
+    ranges = buf[a(q + 1) + 2 * a(q) + 64 :]
     rc = lib().ir_varlen_form_scan(
         ptr(mask), mask.stride(2), mask.stride(3), dtype_code(mask.dtype), q, k, block_size, ptr(ranges), ptr(cu),
         ptr(q_start), ptr(k_off), ptr(info), stream_ptr(dev),

@@ -478,6 +478,94 @@ def test_reference_prefill_metadata_outside_the_form_takes_the_mask_kernel():
         assert (got.float().cpu() - expect).abs().max().item() <= 2e-2
 
 
+@pytest.mark.parametrize("layout", ["flat", "misaligned", "strided"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_packed_form_check_reads_every_mask_layout(dtype, layout):
+    """The packed-form check on masks of each dtype, stored contiguously from an
+    aligned start (read as 16-byte pieces), from an unaligned start, or with a
+    padded row stride (both read element by element). K and Q are odd, so rows
+    start inside pieces and the array ends in a partial piece, and the longest
+    history spans more than one pass of a row's loads. The derived metadata
+    matches the frame; a NaN, a masked value above -6e4, a hidden key at the
+    array's last element or inside the long history, and a leaked key at a
+    row's first element each reject the frame, while -inf still masks."""
+    bs, num_cached, q_lens = 16, [0, 13, 26001], [5, 3, 5]
+    need = [metadata.blocks_for(c + n, bs) for c, n in zip(num_cached, q_lens)]
+    perm = torch.randperm(sum(need) + 7, generator=torch.Generator().manual_seed(5)).tolist()
+    tables = [perm[sum(need[:i]) : sum(need[: i + 1])] for i in range(3)]
+    q_seq, q_pos, k_seq, k_pos, gather = [], [], [], [], []
+    for i, (bt, c, n) in enumerate(zip(tables, num_cached, q_lens)):
+        q_seq += [i] * n
+        q_pos += list(range(c, c + n))
+        k_seq += [i] * (c + n)
+        k_pos += list(range(c + n))
+        gather += [O.slot(bt, p, bs) for p in range(c + n)]
+    base = O.varlen_mask(torch.tensor(q_seq), torch.tensor(q_pos), torch.tensor(k_seq), torch.tensor(k_pos), dtype)
+    Q, K = base.shape[2:]
+    assert Q % 2 == 1 and K % 2 == 1
+    gs = torch.tensor([gather], dtype=torch.int64, device=DEV)
+    neg = torch.finfo(dtype).min
+    long_key = 5 + 16 + 25000  # inside sequence 2's history, past a row's first pass of loads in every dtype
+
+    def on_device(m):
+        if layout == "flat":
+            return m.to(DEV).contiguous()
+        if layout == "misaligned":
+            flat = torch.empty(Q * K + 1, dtype=dtype, device=DEV)
+            flat[1:] = m.reshape(-1).to(DEV)
+            return flat[1:].view(1, 1, Q, K)
+        padded = torch.full((1, 1, Q, K + 3), neg, dtype=dtype, device=DEV)
+        padded[..., :K] = m.to(DEV)
+        return padded[..., :K]
+
+    def planted(r, k, value):
+        m = base.clone()
+        m[0, 0, r, k] = value
+        return m
+
+    for m, accepted in (
+        (base, True),
+        (planted(0, 100, float("-inf")), True),
+        (planted(0, K - 1, float("nan")), False),
+        (planted(Q - 1, 0, -1.0), False),
+        (planted(Q - 1, K - 1, neg), False),
+        (planted(8, long_key, neg), False),
+        (planted(5, 0, 0.0), False),
+    ):
+        f = kernels.varlen_form(gs, on_device(m), bs, sum(need) + 7)
+        if not accepted:
+            assert f is None
+            continue
+        assert f is not None
+        assert f.q_lens == tuple(q_lens) and f.prefixes == tuple(num_cached) and f.max_q_len == max(q_lens)
+        assert f.cu_seqlens_q.tolist() == [0, 5, 8, 13] and f.q_start.tolist() == num_cached
+        for i, nb in enumerate(need):
+            assert f.block_tables[i, :nb].tolist() == tables[i]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("case", [([0], [1]), ([0], [3]), ([2], [1]), ([0, 0], [1, 2]), ([1, 0, 3], [2, 1, 1])])
+def test_packed_form_check_on_tiny_frames(dtype, case):
+    """Frames of a few mask elements: shorter than one 16-byte piece (read
+    element by element) or a whole piece followed by a partial one, where rows
+    end in the partial piece."""
+    num_cached, q_lens = case
+    bs = 16
+    tables = [[i] for i in range(len(q_lens))]
+    q_seq, q_pos, k_seq, k_pos, gather = [], [], [], [], []
+    for i, (c, n) in enumerate(zip(num_cached, q_lens)):
+        q_seq += [i] * n
+        q_pos += list(range(c, c + n))
+        k_seq += [i] * (c + n)
+        k_pos += list(range(c + n))
+        gather += [O.slot(tables[i], p, bs) for p in range(c + n)]
+    m = O.varlen_mask(torch.tensor(q_seq), torch.tensor(q_pos), torch.tensor(k_seq), torch.tensor(k_pos), dtype)
+    f = kernels.varlen_form(torch.tensor([gather], dtype=torch.int64, device=DEV), m.to(DEV), bs, len(q_lens))
+    assert f is not None
+    assert f.q_lens == tuple(q_lens) and f.prefixes == tuple(num_cached)
+    assert f.block_tables[:, 0].tolist() == [t[0] for t in tables]
+
+
 def test_reference_metadata_refilled_in_place_is_checked_again():
     """A caller that reuses its gather_slots and mask tensors, refilling them in
     place for the next step, gets that step's form derived again (the cache of
