@@ -17,18 +17,25 @@ namespace ir {
 namespace {
 
 constexpr int kFormThreads = 256;
+constexpr int kFormBatch = 16;  // loads a lane has in flight per pass
 
-__device__ __forceinline__ float mask_at(const void* m, int dtype, int64_t off) {
-  if (dtype == IR_DTYPE_F32) return ((const float*)m)[off];
+template <int DT>
+__device__ __forceinline__ float mask_at(const void* m, int64_t off) {
+  if constexpr (DT == IR_DTYPE_F32) return ((const float*)m)[off];
   const uint32_t h = ((const uint16_t*)m)[off];
-  return dtype == IR_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+  return DT == IR_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
 }
 
+// Each phase issues a lane's kFormBatch loads before it inspects any of them,
+// so a sequence of T keys costs about T / (kFormThreads * kFormBatch) round
+// trips per phase. Slots are divided in 32 bits when every slot of the pool
+// fits (the uniform `narrow`).
+template <int DT>
 __global__ __launch_bounds__(kFormThreads) void decode_form_kernel(const int64_t* gs, int64_t gs_b, int64_t gs_t,
-                                                                   const void* mask, int64_t m_b, int64_t m_t,
-                                                                   int mask_dtype, int T, int bs, int64_t num_blocks,
-                                                                   int32_t* bt, int64_t bt_stride, int width,
-                                                                   int32_t* ctx_out, int32_t* bad) {
+                                                                   const void* mask, int64_t m_b, int64_t m_t, int T,
+                                                                   int bs, int64_t num_blocks, int32_t* bt,
+                                                                   int64_t bt_stride, int width, int32_t* ctx_out,
+                                                                   int32_t* bad) {
   __shared__ int s_zeros, s_first, s_bad;
   const int b = blockIdx.x, tid = threadIdx.x;
   if (tid == 0) {
@@ -39,14 +46,24 @@ __global__ __launch_bounds__(kFormThreads) void decode_form_kernel(const int64_t
   __syncthreads();
   const int64_t* g = gs + (int64_t)b * gs_b;
   const int64_t mrow = (int64_t)b * m_b;
+  const int64_t n_slots = num_blocks * bs;
+  const bool narrow = n_slots <= 0x7fffffff;
   int zeros = 0, first = T, wrong = 0;
-  for (int t = tid; t < T; t += kFormThreads) {
-    const float x = mask_at(mask, mask_dtype, mrow + (int64_t)t * m_t);
-    if (x == 0.f) {
-      ++zeros;
-    } else {
-      first = min(first, t);
-      wrong |= !(x <= -6e4f);
+  for (int base = 0; base < T; base += kFormThreads * kFormBatch) {
+    float x[kFormBatch];
+#pragma unroll
+    for (int i = 0; i < kFormBatch; ++i) {  // past T: key T - 1 again, not inspected
+      const int t = min(base + i * kFormThreads + tid, T - 1);
+      x[i] = mask_at<DT>(mask, mrow + (int64_t)t * m_t);
+    }
+#pragma unroll
+    for (int i = 0; i < kFormBatch; ++i) {
+      const int t = base + i * kFormThreads + tid;
+      if (t < T && x[i] == 0.f) ++zeros;
+      if (t < T && x[i] != 0.f) {
+        first = min(first, t);
+        wrong |= !(x[i] <= -6e4f);
+      }
     }
   }
   atomicAdd(&s_zeros, zeros);
@@ -55,14 +72,36 @@ __global__ __launch_bounds__(kFormThreads) void decode_form_kernel(const int64_t
   __syncthreads();
   const int ctx = s_zeros;
   if (s_first < ctx) s_bad = 1;  // a masked key before the last visible one
-  for (int t = tid; t < ctx; t += kFormThreads) {
-    const int64_t head = g[(int64_t)(t / bs) * bs * gs_t];
-    const int64_t id = head / bs;
-    if (head < 0 || head % bs != 0 || id >= num_blocks || g[(int64_t)t * gs_t] != id * bs + t % bs) s_bad = 1;
+  // block id of a block's first slot, or -1 unless it is a block start in the pool
+  auto block_of = [&](int64_t head) -> int64_t {
+    if (head < 0 || head >= n_slots) return -1;
+    if (narrow) {
+      const int h = (int)head;
+      return h % bs == 0 ? h / bs : -1;
+    }
+    return head % bs == 0 ? head / bs : -1;
+  };
+  for (int base = 0; base < ctx; base += kFormThreads * kFormBatch) {
+    int64_t slot[kFormBatch], head[kFormBatch];
+#pragma unroll
+    for (int i = 0; i < kFormBatch; ++i) {
+      const int t = base + i * kFormThreads + tid;
+      const bool in = t < ctx;
+      slot[i] = in ? g[(int64_t)t * gs_t] : 0;
+      head[i] = in ? g[(int64_t)(t / bs) * bs * gs_t] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < kFormBatch; ++i) {
+      const int t = base + i * kFormThreads + tid;
+      if (t >= ctx) break;
+      const int64_t id = block_of(head[i]);
+      if (id < 0 || slot[i] != id * bs + t % bs) s_bad = 1;
+    }
   }
   for (int j = tid; j < width; j += kFormThreads) {
     const int p = j * bs;
-    bt[(int64_t)b * bt_stride + j] = p < ctx ? (int32_t)(g[(int64_t)p * gs_t] / bs) : 0;
+    const int64_t id = p < ctx ? block_of(g[(int64_t)p * gs_t]) : 0;
+    bt[(int64_t)b * bt_stride + j] = (int32_t)max(id, (int64_t)0);
   }
   __syncthreads();
   if (tid == 0) {
@@ -87,8 +126,18 @@ extern "C" int ir_decode_form(const int64_t* gather_slots, int64_t gs_b_stride, 
              "ir_decode_form: block tables of %d ids cannot hold %d keys", max_blocks_per_seq, seq_k);
   if (batch == 0) return ok();
   IR_REQUIRE(gather_slots && mask && block_tables && context_lens && bad, "ir_decode_form: null pointer");
-  hipLaunchKernelGGL(decode_form_kernel, dim3(batch), dim3(kFormThreads), 0, (hipStream_t)stream, gather_slots,
-                     gs_b_stride, gs_t_stride, mask, mask_b_stride, mask_t_stride, mask_dtype, seq_k, block_size,
-                     num_blocks, block_tables, bt_stride, max_blocks_per_seq, context_lens, bad);
+  hipStream_t s = (hipStream_t)stream;
+  if (mask_dtype == IR_DTYPE_F32)
+    hipLaunchKernelGGL(decode_form_kernel<IR_DTYPE_F32>, dim3(batch), dim3(kFormThreads), 0, s, gather_slots,
+                       gs_b_stride, gs_t_stride, mask, mask_b_stride, mask_t_stride, seq_k, block_size, num_blocks,
+                       block_tables, bt_stride, max_blocks_per_seq, context_lens, bad);
+  else if (mask_dtype == IR_DTYPE_BF16)
+    hipLaunchKernelGGL(decode_form_kernel<IR_DTYPE_BF16>, dim3(batch), dim3(kFormThreads), 0, s, gather_slots,
+                       gs_b_stride, gs_t_stride, mask, mask_b_stride, mask_t_stride, seq_k, block_size, num_blocks,
+                       block_tables, bt_stride, max_blocks_per_seq, context_lens, bad);
+  else
+    hipLaunchKernelGGL(decode_form_kernel<IR_DTYPE_F16>, dim3(batch), dim3(kFormThreads), 0, s, gather_slots,
+                       gs_b_stride, gs_t_stride, mask, mask_b_stride, mask_t_stride, seq_k, block_size, num_blocks,
+                       block_tables, bt_stride, max_blocks_per_seq, context_lens, bad);
   return check_launch("ir_decode_form");
 }

@@ -322,6 +322,50 @@ def test_reference_decode_metadata_runs_the_block_table_kernels(num_seqs):
         assert torch.equal(forms[0].block_tables[i, :n], ours.block_tables[i, :n])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("num_blocks", [600, 2**28])  # slots divided in 32 bits / in 64 bits
+def test_decode_form_check_over_mask_dtypes(dtype, num_blocks):
+    """The decode-form check on every mask dtype: context lengths and block
+    tables come back exact (contexts longer than one pass of a lane's loads
+    included); a NaN, a masked value above -6e4, a hidden key inside a context
+    or a slot off its block each reject the metadata, while -inf still masks."""
+    bs = 16
+    g = torch.Generator().manual_seed(31)
+    num_cached = [0, 4999, 17, 4096, 1]
+    perm = torch.randperm(600, generator=g).tolist()
+    tables, off = [], 0
+    for nc in num_cached:
+        nb = metadata.blocks_for(nc + 1, bs)
+        tables.append(perm[off : off + nb])
+        off += nb
+    t = max(num_cached) + 1
+    gs = torch.zeros(len(tables), t, dtype=torch.int64)
+    mask = torch.full((len(tables), 1, 1, t), torch.finfo(dtype).min, dtype=dtype)
+    for i, (bt, nc) in enumerate(zip(tables, num_cached)):
+        gs[i, : nc + 1] = torch.tensor([O.slot(bt, p, bs) for p in range(nc + 1)])
+        mask[i, 0, 0, : nc + 1] = 0
+    ctx_want = [nc + 1 for nc in num_cached]
+
+    def run(gs_, mask_):
+        bt, ctx, bad = kernels.decode_form(gs_.to(DEV), mask_.to(DEV), bs, num_blocks)
+        torch.cuda.synchronize()
+        return bt.cpu(), ctx.cpu(), int(bad.item())
+
+    bt, ctx, bad = run(gs, mask)
+    assert bad == 0 and ctx.tolist() == ctx_want
+    for i, (tb, c) in enumerate(zip(tables, ctx_want)):
+        assert bt[i, : metadata.blocks_for(c, bs)].tolist() == tb
+    planted = []
+    for r, k, value in ((0, t - 1, float("-inf")), (3, t - 1, float("nan")), (2, 100, -1.0), (1, 4500, torch.finfo(dtype).min)):
+        m = mask.clone()
+        m[r, 0, 0, k] = value
+        planted.append(run(gs, m)[2])
+    off_block = gs.clone()
+    off_block[1, 4500] += 1
+    planted.append(run(off_block, mask)[2])
+    assert planted == [0, 1, 1, 1, 1]
+
+
 def test_reference_metadata_outside_the_decode_form_takes_the_mask_kernel():
     """A mask that hides a key inside the context, or slots that do not follow
     the block-table closed form, is not the decode form: the call reads
