@@ -934,7 +934,33 @@ def _bench_reference_form(args) -> dict:
             per.append(s.elapsed_time(e) / layers)
         return statistics.median(per)
 
+    # the reference's CudaGraphDecoder (infrared/engine/cuda_graph.py:263-285):
+    # static gather_slots / mask, three warm-ups on a side stream, then the
+    # step's layers captured; a replay re-checks the metadata on the device
+    gs_s, m_s = ours.gather_slots.clone(), mask.clone()
+
+    def forward_static():
+        paged = RefContext(pool, ours.write_slots, gs_s)
+        out = None
+        for _ in range(layers):
+            out = paged_attention(q, k, v, paged, m_s, 0, cfg.scale, cfg.n_rep)
+        return out
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            forward_static()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_graph = forward_static()
+
+    def step_graph():
+        graph.replay()
+
     ms_ref, ms_ours, ms_masked = timed(step_ref), timed(step_ours), timed(step_masked)
+    ms_graph = timed(step_graph)
     form = pool._ref_form[1]
     out_ref = paged_attention(q, k, v, RefContext(pool, ours.write_slots, ours.gather_slots), mask, 0, cfg.scale,
                               cfg.n_rep)
@@ -952,7 +978,11 @@ def _bench_reference_form(args) -> dict:
                    "(KV write + attention per layer), eager",
                    "decode_form_recognised": form is not None,
                    "equal_to_block_table_path": bool(torch.equal(out_ref, out_ours)),
+                   "graph_replay_equal_to_block_table_path": bool(torch.equal(out_graph, out_ours)),
                    "rows_us_per_call": {"reference form, recognised (one check per step)": round(ms_ref * 1e3, 2),
+                                        "reference form captured as the reference's CudaGraphDecoder does "
+                                        "(check recorded, gating the mask kernel on the device)":
+                                            round(ms_graph * 1e3, 2),
                                         "block-table fields from the caller": round(ms_ours * 1e3, 2),
                                         "mask kernel on gather_slots + mask": round(ms_masked * 1e3, 2)},
                    "kv_bytes_per_call": kv},

@@ -62,11 +62,26 @@ enum {
                                decode: run sequence pairs that share prefix blocks as one unit */
 };
 
+/* flags of ir_decode_form */
+enum {
+  IR_FORM_CLEAR_ON_FAIL = 1 /* after the check, set every context length to 0 when *bad is set */
+};
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* ir_last_error(void);
 
 /* Version string of the library build. */
 const char* ir_version(void);
+
+/*
+ * Identity of the stream capture in progress on `stream`: *capture_id = 0 when
+ * the stream is not capturing, else a value unique to that capture (the HIP
+ * capture sequence id + 1). No counterpart in the reference: the seam uses it
+ * to record its reference-form checks once per captured graph
+ * (infrared/engine/cuda_graph.py:263-285 captures the decode forward with the
+ * reference's own metadata).
+ */
+int ir_stream_capture_id(ir_stream_t stream, uint64_t* capture_id);
 
 /*
  * KV-slot scatter: k_cache[slot_mapping[i]] = k[i]; v_cache[slot_mapping[i]] = v[i].
@@ -275,6 +290,10 @@ int ir_paged_decode_planned(const void* q, int64_t q_seq_stride, int64_t q_head_
  *                 dtype mask_dtype (f32/f16/bf16); strides may be 0 (broadcast).
  * Scores are q.k*scale + mask; a row whose keys are all masked with finfo.min
  * averages V uniformly, as the reference softmax does.
+ *   run_if:       null, or a device int32 read by every workgroup first: the
+ *                 call does nothing (writes no output) while it is 0. A graph
+ *                 captured over the reference's decode metadata records this
+ *                 kernel gated on ir_decode_form's *bad.
  */
 int ir_paged_attention_masked(const void* q, int64_t q_b_stride, int64_t q_s_stride,
                               int64_t q_h_stride, const void* k_cache, const void* v_cache,
@@ -286,7 +305,8 @@ int ir_paged_attention_masked(const void* q, int64_t q_b_stride, int64_t q_s_str
                               int64_t out_b_stride, int64_t out_s_stride,
                               int64_t out_h_stride, int batch, int seq_q, int seq_k,
                               int num_q_heads, int num_kv_heads, int head_dim, float scale,
-                              int dtype, int32_t* err_flags, ir_stream_t stream);
+                              int dtype, int32_t* err_flags, const int32_t* run_if,
+                              ir_stream_t stream);
 
 /*
  * Block tables from the reference engine's own decode metadata, so unchanged
@@ -297,9 +317,14 @@ int ir_paged_attention_masked(const void* q, int64_t q_b_stride, int64_t q_s_str
  * infrared/cache/paged_kv_cache.py:75-91). Writes context_lens[i] (the mask's
  * zeros) and block_tables[i, j] = gather_slots[i, j * bs] / bs (0 past the
  * context), and ORs 1 into *bad unless the metadata has exactly that form: the
- * zeros a prefix, later mask values <= -6e4, every slot below ctx_i the closed
- * form, every block id in [0, num_blocks). With *bad clear the decode kernels
- * over these tables compute what ir_paged_attention_masked computes.
+ * zeros a prefix, later mask values <= -6e4, at least one zero, every slot
+ * below ctx_i the closed form, every block id in [0, num_blocks). With *bad
+ * clear the decode kernels over these tables compute what
+ * ir_paged_attention_masked computes. *bad must be 0 before the call.
+ *   flags: IR_FORM_CLEAR_ON_FAIL launches a second kernel that sets every
+ *   context_lens[i] to 0 when the check failed (for graph capture, where the
+ *   host cannot read *bad: the block-table decode then reads no key and the
+ *   mask kernel, gated on *bad, computes the call).
  *   gather_slots: [batch, seq_k] int64 (strides b, t); mask: element (b, t) at
  *   mask + b*mask_b_stride + t*mask_t_stride, dtype mask_dtype.
  *   block_tables: [batch, bt_stride] int32, max_blocks_per_seq >= ceil(seq_k / bs).
@@ -308,7 +333,7 @@ int ir_decode_form(const int64_t* gather_slots, int64_t gs_b_stride, int64_t gs_
                    const void* mask, int64_t mask_b_stride, int64_t mask_t_stride, int mask_dtype,
                    int batch, int seq_k, int block_size, int64_t num_blocks, int32_t* block_tables,
                    int64_t bt_stride, int max_blocks_per_seq, int32_t* context_lens, int32_t* bad,
-                   ir_stream_t stream);
+                   int flags, ir_stream_t stream);
 
 /*
  * Prefill metadata from the reference engine's packed prefill / mixed-step

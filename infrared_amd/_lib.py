@@ -80,7 +80,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_i32,
         [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64,
          _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32,
-         _c_i32, _c_i32, _c_i32, _c_i32, _c_f32, _c_i32, _c_p, _c_p],
+         _c_i32, _c_i32, _c_i32, _c_i32, _c_f32, _c_i32, _c_p, _c_p, _c_p],
     ),
     "ir_rope_kv_scatter": (
         _c_i32,
@@ -97,8 +97,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ir_decode_form": (
         _c_i32,
         [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_p, _c_i64,
-         _c_i32, _c_p, _c_p, _c_p],
+         _c_i32, _c_p, _c_p, _c_i32, _c_p],
     ),
+    "ir_stream_capture_id": (_c_i32, [_c_p, ctypes.POINTER(ctypes.c_uint64)]),
     "ir_varlen_form_scan": (
         _c_i32,
         [_c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p],

@@ -8,8 +8,16 @@
 // gather_slots[i, j * bs] / bs, and verifies the form exactly: the zeros are a
 // prefix, every later mask value is at most -6e4 (masked in any dtype, fp16's
 // finfo.min included), every slot below ctx_i follows the closed form and
-// every block id lies in the pool. Any violation sets *bad; the host then
-// keeps the mask kernel, which reads the metadata as given.
+// every block id lies in the pool, and at least one key is visible (a row
+// masked entirely is the mask kernel's uniform average over its keys, not an
+// empty context). Any violation sets *bad; the host then keeps the mask
+// kernel, which reads the metadata as given.
+//
+// Under hipGraph capture the host cannot read the verdict, so both kernels are
+// recorded and the verdict gates them on the device: with IR_FORM_CLEAR_ON_FAIL
+// a second launch sets every context length to 0 when *bad is set (the
+// block-table decode then reads nothing and writes zero rows), and the mask
+// kernel, given *bad as its run_if gate, runs after it only in that case.
 #include "common.hpp"
 #include "status.hpp"
 
@@ -72,6 +80,7 @@ __global__ __launch_bounds__(kFormThreads) void decode_form_kernel(const int64_t
   __syncthreads();
   const int ctx = s_zeros;
   if (s_first < ctx) s_bad = 1;  // a masked key before the last visible one
+  if (ctx == 0 && T > 0) s_bad = 1;  // no visible key: the mask kernel's uniform average
   // block id of a block's first slot, or -1 unless it is a block start in the pool
   auto block_of = [&](int64_t head) -> int64_t {
     if (head < 0 || head >= n_slots) return -1;
@@ -110,6 +119,12 @@ __global__ __launch_bounds__(kFormThreads) void decode_form_kernel(const int64_t
   }
 }
 
+// After the check: when it failed, every context length becomes 0.
+__global__ __launch_bounds__(256) void decode_form_clear_kernel(const int32_t* bad, int32_t* ctx_out, int batch) {
+  if (*bad == 0) return;
+  for (int b = blockIdx.x * 256 + threadIdx.x; b < batch; b += gridDim.x * 256) ctx_out[b] = 0;
+}
+
 }  // namespace
 }  // namespace ir
 
@@ -119,8 +134,9 @@ extern "C" int ir_decode_form(const int64_t* gather_slots, int64_t gs_b_stride, 
                               const void* mask, int64_t mask_b_stride, int64_t mask_t_stride, int mask_dtype,
                               int batch, int seq_k, int block_size, int64_t num_blocks, int32_t* block_tables,
                               int64_t bt_stride, int max_blocks_per_seq, int32_t* context_lens, int32_t* bad,
-                              ir_stream_t stream) {
+                              int flags, ir_stream_t stream) {
   IR_REQUIRE(dtype_bytes(mask_dtype) > 0, "ir_decode_form: unknown mask dtype %d", mask_dtype);
+  IR_REQUIRE((flags & ~IR_FORM_CLEAR_ON_FAIL) == 0, "ir_decode_form: unknown flags %#x", flags);
   IR_REQUIRE(batch >= 0 && seq_k >= 0 && block_size > 0 && num_blocks >= 0, "ir_decode_form: bad sizes");
   IR_REQUIRE(max_blocks_per_seq >= (seq_k + block_size - 1) / block_size && bt_stride >= max_blocks_per_seq,
              "ir_decode_form: block tables of %d ids cannot hold %d keys", max_blocks_per_seq, seq_k);
@@ -139,5 +155,8 @@ extern "C" int ir_decode_form(const int64_t* gather_slots, int64_t gs_b_stride, 
     hipLaunchKernelGGL(decode_form_kernel<IR_DTYPE_F16>, dim3(batch), dim3(kFormThreads), 0, s, gather_slots,
                        gs_b_stride, gs_t_stride, mask, mask_b_stride, mask_t_stride, seq_k, block_size, num_blocks,
                        block_tables, bt_stride, max_blocks_per_seq, context_lens, bad);
+  if (flags & IR_FORM_CLEAR_ON_FAIL)
+    hipLaunchKernelGGL(decode_form_clear_kernel, dim3((batch + 255) / 256), dim3(256), 0, s, bad, context_lens,
+                       batch);
   return check_launch("ir_decode_form");
 }

@@ -38,6 +38,7 @@ struct MaskedArgs {
   int batch, seq_q, seq_k, num_q_heads, num_kv_heads, n_rep, n_rt;
   float scale;
   int32_t* err;
+  const int32_t* run_if;  // null, or run only when *run_if != 0
 };
 
 __device__ __forceinline__ float mask_at(const MaskedArgs& a, int64_t off) {
@@ -63,6 +64,9 @@ __global__ __launch_bounds__(kWaves * 64) void paged_masked_kernel(MaskedArgs a)
   typedef TileShape<DT, D> Sh;
   constexpr int EB = Sh::EB;
   __shared__ MergeSmem<kWaves, D> sm;
+  // a gated call (the fallback half of a graph-captured decode-form check)
+  // does nothing unless the check failed
+  if (a.run_if && *a.run_if == 0) return;
 
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -160,7 +164,8 @@ extern "C" int ir_paged_attention_masked(const void* q, int64_t q_b_stride, int6
                                          void* out, int64_t out_b_stride, int64_t out_s_stride,
                                          int64_t out_h_stride, int batch, int seq_q, int seq_k,
                                          int num_q_heads, int num_kv_heads, int head_dim, float scale,
-                                         int dtype, int32_t* err_flags, ir_stream_t stream) {
+                                         int dtype, int32_t* err_flags, const int32_t* run_if,
+                                         ir_stream_t stream) {
   const int eb = dtype_bytes(dtype);
   IR_REQUIRE(eb > 0, "ir_paged_attention_masked: unknown dtype %d", dtype);
   IR_REQUIRE(dtype_bytes(mask_dtype) > 0, "ir_paged_attention_masked: unknown mask dtype %d", mask_dtype);
@@ -212,6 +217,7 @@ extern "C" int ir_paged_attention_masked(const void* q, int64_t q_b_stride, int6
   a.n_rt = (seq_q * a.n_rep + 15) / 16;
   a.scale = scale;
   a.err = err_flags;
+  a.run_if = run_if;
   const int64_t nwg = (int64_t)batch * num_kv_heads * a.n_rt;
   IR_REQUIRE(nwg < (1ll << 31), "ir_paged_attention_masked: grid too large");
   hipStream_t s = (hipStream_t)stream;

@@ -60,3 +60,13 @@ int device_xcds() {
 extern "C" const char* ir_last_error(void) { return g_last_error; }
 
 extern "C" const char* ir_version(void) { return "infrared_amd 0.1 gfx950"; }
+
+extern "C" int ir_stream_capture_id(ir_stream_t stream, uint64_t* capture_id) {
+  IR_REQUIRE(capture_id, "ir_stream_capture_id: null pointer");
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  unsigned long long id = 0;
+  const hipError_t e = hipStreamGetCaptureInfo((hipStream_t)stream, &st, &id);
+  if (e != hipSuccess) return ir::fail(IR_ELAUNCH, "ir_stream_capture_id: %s", hipGetErrorString(e));
+  *capture_id = st == hipStreamCaptureStatusActive ? (uint64_t)id + 1 : 0;
+  return ir::ok();
+}

@@ -364,11 +364,14 @@ def paged_attention_masked(
     scale: float,
     out: torch.Tensor | None = None,
     err_flags: torch.Tensor | None = None,
+    run_if: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Attention over per-key slots + additive mask (the reference seam's metadata).
 
     ``q`` ``[B, Sq, H_q, D]``; ``gather_slots`` int64 ``[B, T]``; ``mask``
     broadcastable to ``[B, 1, Sq, T]``. Returns ``[B, Sq, H_q, D]``.
+    ``run_if``: an int32 device flag; the kernel then writes ``out`` only
+    when the flag is nonzero (read on the device, so it works under capture).
     """
     dev = require_device(q, k_cache, v_cache, gather_slots, mask)
     _cache_layer("paged_attention_masked", k_cache)
@@ -387,12 +390,16 @@ def paged_attention_masked(
     _last_dim_contiguous("paged_attention_masked q", q)
     if out is None:
         out = torch.empty(b, sq, hq, d, dtype=q.dtype, device=dev)
+    if run_if is not None:
+        require_device(q, run_if)
+        if run_if.dtype != torch.int32 or run_if.numel() < 1:
+            raise RuntimeError("paged_attention_masked: run_if must be an int32 device tensor")
     rc = lib().ir_paged_attention_masked(
         ptr(q), q.stride(0), q.stride(1), q.stride(2), ptr(k_cache), ptr(v_cache),
         k_cache.stride(0), k_cache.stride(1), k_cache.shape[0], ptr(gather_slots),
         gather_slots.stride(0), gather_slots.stride(1), ptr(m), m.stride(0), m.stride(2),
         m.stride(3), dtype_code(m.dtype), ptr(out), out.stride(0), out.stride(1), out.stride(2),
-        b, sq, t, hq, h_kv, d, float(scale), dtype_code(q.dtype), ptr(err_flags), stream_ptr(dev),
+        b, sq, t, hq, h_kv, d, float(scale), dtype_code(q.dtype), ptr(err_flags), ptr(run_if), stream_ptr(dev),
     )
     check(rc, "ir_paged_attention_masked")
     return out
@@ -603,12 +610,17 @@ def paged_prefill(
     return out
 
 
-def decode_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int, num_blocks: int
-                ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+FORM_CLEAR_ON_FAIL = 1  # IR_FORM_CLEAR_ON_FAIL
+
+
+def decode_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int, num_blocks: int,
+                clear_on_fail: bool = False) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Block tables ``[B, ceil(T / bs)]`` int32 and context lengths ``[B]`` int32
     from the reference's decode metadata (``gather_slots`` ``[B, T]`` int64, mask
     ``[B, 1, 1, T]``), plus an int32 flag, nonzero unless the metadata has the
-    reference engine's decode form exactly (``ir_decode_form``)."""
+    reference engine's decode form exactly (``ir_decode_form``).
+    ``clear_on_fail``: when the check fails, every context length is set to 0
+    on the device (for capture, where the flag cannot be read on the host)."""
     dev = require_device(gather_slots, mask)
     if gather_slots.dtype != torch.int64 or gather_slots.dim() != 2:
         raise RuntimeError("decode_form: gather_slots must be int64 [B, T]")
@@ -622,7 +634,7 @@ def decode_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int,
     rc = lib().ir_decode_form(
         ptr(gather_slots), gather_slots.stride(0), gather_slots.stride(1), ptr(mask), mask.stride(0),
         mask.stride(3), dtype_code(mask.dtype), b, t, block_size, num_blocks, ptr(bt), bt.stride(0), width,
-        ptr(ctx), ptr(bad), stream_ptr(dev),
+        ptr(ctx), ptr(bad), FORM_CLEAR_ON_FAIL if clear_on_fail else 0, stream_ptr(dev),
     )
     check(rc, "ir_decode_form")
     return bt, ctx, bad
@@ -692,6 +704,17 @@ def varlen_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int,
     offs, prefixes = host[1 : nseq + 2], host[nseq + 2 :]
     q_lens = tuple(b - a for a, b in zip(offs, offs[1:]))
     return VarlenForm(bt, cu[: nseq + 1], q_start[:nseq], max_q, q_lens, tuple(prefixes))
+
+
+def stream_capture_id(device: torch.device | str | int | None = None) -> int:
+    """0 unless torch's current stream on ``device`` is capturing a graph; then
+    a value unique to that capture (``ir_stream_capture_id``)."""
+    import ctypes
+
+    dev = torch.device(device if device is not None else "cuda")
+    out = ctypes.c_uint64(0)
+    check(lib().ir_stream_capture_id(stream_ptr(dev), ctypes.byref(out)), "ir_stream_capture_id")
+    return int(out.value)
 
 
 def hbm_read(src: torch.Tensor, sink: torch.Tensor, workgroups: int = 0) -> None:

@@ -24,7 +24,9 @@ calls once per layer (``infrared/model/layers.py:178-180``):
      bs + p % bs`` and mask 0 then ``finfo.min``,
      ``infrared/engine/paged_engine.py:306-314, 630-638``): the same decode
      kernels over block tables derived from them on the device (checked once
-     per step, ``PagedKVPool.reference_decode_form``);
+     per step, ``PagedKVPool.reference_decode_form``; under graph capture the
+     check is recorded and gates, on the device, a mask kernel recorded after
+     the decode, so each replay takes the path its own metadata allows);
    - otherwise, for the reference engine's packed prefill / mixed-step frame
      (batch 1: every scheduled sequence's query tokens, a key axis
      concatenating their histories in order, ``gather_slots`` with the closed
@@ -158,6 +160,12 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
             vform = pool.reference_varlen_form(paged.gather_slots, mask)
         if form is not None:
             out = _decode(q, pool, layer_idx, form.block_tables, form.context_lens, form, scale, err)
+            if form.gate is not None:
+                # recorded under graph capture: the replay's own check decides,
+                # on the device, whether this mask kernel overwrites the rows
+                kernels.paged_attention_masked(
+                    q, k_layer, v_layer, paged.gather_slots, mask, scale, out=out, err_flags=err, run_if=form.gate
+                )
         elif vform is not None and vform.row_split is not None:
             out = _split_step(q, pool, layer_idx, vform.row_split, scale, err)
         elif vform is not None:
@@ -229,17 +237,28 @@ def _decode(q, pool, layer_idx: int, block_tables, context_lens, holder, scale: 
         # plan buffer (two decode contexts run interleaved), then rebuilt.
         # Consecutive sequences whose tables share prefix blocks (the prefix
         # cache's reuse) run as pairs, reading those blocks once.
+        # A form recorded under graph capture (``gate`` set) plans into its own
+        # buffer, which its graph's replays rebuild, and holds it.
+        own = getattr(holder, "gate", None) is not None
         plan = holder.decode_plan
-        if plan is None or getattr(pool, "plan_owner", plan) is not plan:
+        if plan is None or (not own and getattr(pool, "plan_owner", plan) is not plan):
             plan_bytes = kernels.decode_plan_bytes(b, hq, h_kv, max_blocks, pool.block_size)
+            if own:
+                buf = torch.empty(plan_bytes, dtype=torch.uint8, device=q.device)
+                holder.plan_buf = buf
+            else:
+                buf = pool.plan_buffer(plan_bytes)
             plan = kernels.decode_plan(
                 block_tables, context_lens, hq, k_layer, pool.block_size,
-                buf=pool.plan_buffer(plan_bytes), err_flags=err, share_groups=True,
+                buf=buf, err_flags=err, share_groups=True,
             )
             holder.decode_plan = plan
-            pool.plan_owner = plan
+            if not own:
+                pool.plan_owner = plan
         ws = pool.workspace(kernels.planned_workspace_bytes(b, hq, h_kv, d))
         ctr = pool.decode_counters(kernels.decode_num_counters(b, hq, h_kv))
+        if own:
+            _hold(holder, ws, ctr)
         out = kernels.paged_decode_planned(
             q.reshape(b, hq, d), k_layer, v_layer, plan, scale, out=out, workspace=ws, err_flags=err, counters=ctr
         )
@@ -250,9 +269,19 @@ def _decode(q, pool, layer_idx: int, block_tables, context_lens, holder, scale: 
             if need > 0:
                 ws = pool.workspace(need)
                 ctr = pool.decode_counters(kernels.decode_num_counters(b, hq, h_kv))
+        if ws is not None and getattr(holder, "gate", None) is not None:
+            _hold(holder, ws, ctr)
         out = kernels.paged_decode(
             q.reshape(b, hq, d), k_layer, v_layer, block_tables, context_lens,
             pool.block_size, scale, out=out, workspace=ws, err_flags=err, counters=ctr,
         )
     return out.view(b, 1, hq, d)
 
+
+
+def _hold(holder, *tensors: torch.Tensor) -> None:
+    """Keeps pool buffers a captured graph addresses alive with its form (the
+    pool may replace them when a later call needs more)."""
+    for t in tensors:
+        if not any(h is t for h in holder.held):
+            holder.held.append(t)

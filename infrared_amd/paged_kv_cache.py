@@ -32,8 +32,9 @@ rather than handled by a fallback.
 
 from __future__ import annotations
 
+import weakref
 from collections.abc import Sequence
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import numpy as np
 import torch
@@ -109,9 +110,13 @@ class PagedKVPool:
         # the decode plan whose schedule plan_buffer() holds now: a context
         # whose cached plan is not this one was overwritten and rebuilds it
         self.plan_owner: object | None = None
-        # (gather_slots, mask, derived form) of the last reference-form check
+        # (metadata key, derived form) of the last eager reference-form check
         self._ref_form: tuple | None = None
         self._ref_varlen: tuple | None = None
+        # decode forms recorded into a graph under capture, by (capture id,
+        # id(gather_slots), id(mask)): each holds the buffers its graph's
+        # replays address and lives as long as the captured gather_slots
+        self._captured_forms: dict[tuple, tuple] = {}
 
     # --- reference surface ------------------------------------------------
 
@@ -193,29 +198,55 @@ class PagedKVPool:
         (``infrared/engine/paged_engine.py:306-314, 630-638``). Derived on the
         device by ``ir_decode_form`` -- ``bt_i[j] = gather_slots[i, j * bs] //
         bs``, ``ctx_i`` = the mask's zeros -- and verified exactly: every slot
-        below ``ctx_i`` follows the closed form, the zeros are a prefix, and
-        every later mask value is at most -6e4 (masked in any dtype, fp16's
-        ``finfo.min`` included), so the decode kernels compute what the mask
-        kernel would. The check costs one launch and one synchronising read of
-        its flag; the result is cached for the step's other layers (same
+        below ``ctx_i`` follows the closed form, the zeros are a nonempty
+        prefix, and every later mask value is at most -6e4 (masked in any
+        dtype, fp16's ``finfo.min`` included), so the decode kernels compute
+        what the mask kernel would.
+
+        Eager: the check costs one launch and one synchronising read of its
+        flag; the result is cached for the step's other layers (same
         ``gather_slots`` and ``mask`` tensors, not modified in place since).
-        Under hipGraph capture no read is possible, so ``None`` is returned and
-        the mask kernel runs.
+
+        Under hipGraph capture (the reference's ``CudaGraphDecoder`` captures
+        its decode forward on static ``gather_slots`` / ``mask`` buffers that
+        each replay refills, ``infrared/engine/cuda_graph.py:231-285``) no read
+        is possible, so the check itself is recorded, once per capture and
+        metadata pair, with ``IR_FORM_CLEAR_ON_FAIL``; the returned form
+        carries the flag as ``gate``, and the caller records the block-table
+        decode followed by the mask kernel gated on the flag. Each replay then
+        checks its own metadata: in the decode form it runs the block-table
+        kernels, otherwise the mask kernel. The eager cache is never consulted
+        under capture. The form holds the buffers its graph addresses (its own
+        plan buffer, the decode workspace and counters) for as long as the
+        captured ``gather_slots`` tensor lives.
         """
-        key = _metadata_key(gather_slots, mask)
-        c = self._ref_form
-        if c is not None and _same_metadata(c[0], key):
-            return c[1]
-        if torch.cuda.is_current_stream_capturing():
-            return None
-        form = None
-        if (gather_slots.dim() == 2 and gather_slots.dtype == torch.int64 and gather_slots.is_cuda and mask.is_cuda
-                and mask.dim() == 4 and tuple(mask.shape[:3]) == (gather_slots.shape[0], 1, 1)
+        if not (gather_slots.dim() == 2 and gather_slots.dtype == torch.int64 and gather_slots.is_cuda
+                and mask.is_cuda and mask.dim() == 4 and tuple(mask.shape[:3]) == (gather_slots.shape[0], 1, 1)
                 and mask.shape[3] == gather_slots.shape[1]):
-            bt, ctx, bad = kernels.decode_form(gather_slots, mask, self.block_size, self.num_blocks)
-            if int(bad.item()) == 0:
-                form = _DecodeForm(bt, ctx)
-        self._ref_form = (key, form)
+            return None
+        if torch.cuda.is_current_stream_capturing():
+            return self._captured_decode_form(gather_slots, mask)
+        c = self._ref_form
+        if c is not None and _same_metadata(c[0], gather_slots, mask):
+            return c[1]
+        form = None
+        bt, ctx, bad = kernels.decode_form(gather_slots, mask, self.block_size, self.num_blocks)
+        if int(bad.item()) == 0:
+            form = _DecodeForm(bt, ctx)
+        self._ref_form = (_metadata_key(gather_slots, mask), form)
+        return form
+
+    def _captured_decode_form(self, gather_slots: torch.Tensor, mask: torch.Tensor) -> _DecodeForm:
+        cid = kernels.stream_capture_id(gather_slots.device)
+        slot = (cid, id(gather_slots), id(mask))
+        c = self._captured_forms.get(slot)
+        if c is not None and _same_metadata(c[0], gather_slots, mask):
+            return c[1]
+        bt, ctx, bad = kernels.decode_form(gather_slots, mask, self.block_size, self.num_blocks,
+                                           clear_on_fail=True)
+        form = _DecodeForm(bt, ctx, gate=bad)
+        self._captured_forms[slot] = (_metadata_key(gather_slots, mask), form)
+        weakref.finalize(gather_slots, _drop_captured, weakref.ref(self), slot)
         return form
 
     def reference_varlen_form(self, gather_slots: torch.Tensor, mask: torch.Tensor) -> kernels.VarlenForm | None:
@@ -238,12 +269,11 @@ class PagedKVPool:
         modified in place since).
         Under hipGraph capture ``None`` is returned and the mask kernel runs.
         """
-        key = _metadata_key(gather_slots, mask)
-        c = self._ref_varlen
-        if c is not None and _same_metadata(c[0], key):
-            return c[1]
         if torch.cuda.is_current_stream_capturing():
             return None
+        c = self._ref_varlen
+        if c is not None and _same_metadata(c[0], gather_slots, mask):
+            return c[1]
         form = None
         if (gather_slots.dim() == 2 and gather_slots.shape[0] == 1 and gather_slots.dtype == torch.int64
                 and gather_slots.is_cuda and mask.is_cuda and mask.dim() == 4 and tuple(mask.shape[:2]) == (1, 1)
@@ -252,7 +282,7 @@ class PagedKVPool:
             if form is not None:
                 # the reference packs decodes first (infrared/engine/scheduler.py:104-115)
                 form.row_split = row_split(form.block_tables, form.prefixes, form.q_lens)
-        self._ref_varlen = (key, form)
+        self._ref_varlen = (_metadata_key(gather_slots, mask), form)
         return form
 
     def check_errors(self) -> None:
@@ -265,24 +295,41 @@ class PagedKVPool:
 
 
 def _metadata_key(gather_slots: torch.Tensor, mask: torch.Tensor) -> tuple:
-    """Identity of a step's metadata for the form caches: the two tensors
-    (held, so their ids are not reused) and their in-place version counters, so
-    a caller that refills the same tensors for the next step is checked again."""
-    return (gather_slots, gather_slots._version, mask, mask._version)
+    """Identity of a step's metadata for the form caches: weak references to
+    the two tensors (a cache entry pins neither, and a dead reference matches
+    nothing, so a reused id is never mistaken for them) and their in-place
+    version counters, so a caller that refills the same tensors for the next
+    step is checked again."""
+    return (weakref.ref(gather_slots), gather_slots._version, weakref.ref(mask), mask._version)
 
 
-def _same_metadata(a: tuple, b: tuple) -> bool:
-    return a[0] is b[0] and a[1] == b[1] and a[2] is b[2] and a[3] == b[3]
+def _same_metadata(key: tuple, gather_slots: torch.Tensor, mask: torch.Tensor) -> bool:
+    return (key[0]() is gather_slots and key[1] == gather_slots._version and key[2]() is mask
+            and key[3] == mask._version)
+
+
+def _drop_captured(pool_ref, slot) -> None:
+    pool = pool_ref()
+    if pool is not None:
+        pool._captured_forms.pop(slot, None)
 
 
 @dataclass(slots=True)
 class _DecodeForm:
     """Block tables and context lengths derived from reference decode metadata,
-    with the step's decode plan once built."""
+    with the step's decode plan once built.
+
+    A form recorded under graph capture has ``gate`` (the check's int32 flag
+    on the device, nonzero when the metadata is not in the decode form; the
+    context lengths are then 0) and its own ``plan_buf``; ``held`` keeps the
+    pool buffers its graph's kernels address alive."""
 
     block_tables: torch.Tensor
     context_lens: torch.Tensor
     decode_plan: object | None = None
+    gate: torch.Tensor | None = None
+    plan_buf: torch.Tensor | None = None
+    held: list = field(default_factory=list)
 
 
 @dataclass(slots=True)

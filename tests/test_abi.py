@@ -71,7 +71,7 @@ def test_validation_errors_report_codes_and_messages():
     # null pointers with work to do
     rc = lib.ir_paged_attention_masked(
         None, 0, 0, 0, None, None, 0, 0, 10, None, 0, 0, None, 0, 0, 0, 2, None, 0, 0, 0, 1, 1, 4,
-        4, 2, 128, 1.0, 2, None, None,
+        4, 2, 128, 1.0, 2, None, None, None,
     )
     assert rc == -1 and b"null" in lib.ir_last_error()
     # the packed-form check: unknown mask dtype, empty frame (no-op), null pointers

@@ -327,8 +327,10 @@ def test_reference_decode_metadata_runs_the_block_table_kernels(num_seqs):
 def test_decode_form_check_over_mask_dtypes(dtype, num_blocks):
     """The decode-form check on every mask dtype: context lengths and block
     tables come back exact (contexts longer than one pass of a lane's loads
-    included); a NaN, a masked value above -6e4, a hidden key inside a context
-    or a slot off its block each reject the metadata, while -inf still masks."""
+    included); a NaN, a masked value above -6e4, a hidden key inside a context,
+    a slot off its block or a row with no visible key each reject the
+    metadata, while -inf still masks. With IR_FORM_CLEAR_ON_FAIL a rejected
+    check leaves every context length 0."""
     bs = 16
     g = torch.Generator().manual_seed(31)
     num_cached = [0, 4999, 17, 4096, 1]
@@ -363,7 +365,16 @@ def test_decode_form_check_over_mask_dtypes(dtype, num_blocks):
     off_block = gs.clone()
     off_block[1, 4500] += 1
     planted.append(run(off_block, mask)[2])
-    assert planted == [0, 1, 1, 1, 1]
+    hidden = mask.clone()  # a row with no visible key: the mask kernel's uniform average, not ctx 0
+    hidden[4, 0, 0, :] = torch.finfo(dtype).min
+    planted.append(run(gs, hidden)[2])
+    assert planted == [0, 1, 1, 1, 1, 1]
+    # the capture form of the check zeroes every context length when it fails
+    for m, ok in ((mask, True), (hidden, False)):
+        _, ctx, bad = kernels.decode_form(gs.to(DEV), m.to(DEV), bs, num_blocks, clear_on_fail=True)
+        torch.cuda.synchronize()
+        assert int(bad.item()) == (0 if ok else 1)
+        assert ctx.cpu().tolist() == (ctx_want if ok else [0] * len(ctx_want))
 
 
 def test_reference_metadata_outside_the_decode_form_takes_the_mask_kernel():

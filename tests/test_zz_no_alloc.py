@@ -8,6 +8,11 @@ any device work."""
 
 from __future__ import annotations
 
+import os
+import subprocess
+import sys
+import textwrap
+
 import pytest
 import torch
 
@@ -77,3 +82,60 @@ def test_noalloc_decode_refuses_shapes_beyond_its_scratch():
     )
     assert rc == IR_EWORKSPACE
     assert "no-alloc scratch holds" in lib().ir_last_error().decode()
+
+
+_FIRST_CALL_IN_CAPTURE = textwrap.dedent("""
+    import sys
+    sys.path.insert(0, {root!r})
+    import torch
+    from infrared_amd import kernels
+    from infrared_amd._lib import check, dtype_code, lib, ptr, stream_ptr
+    from infrared_amd.workloads import DecodeConfig, make_decode_case
+
+    cfg = DecodeConfig("na-capture", 8, 28, 4, 128, 16, torch.bfloat16, "uniform", 3000, 20000, seed=43)
+    case = make_decode_case(cfg, "cuda")
+    q, kc, vc, bt = case.q, case.k_cache, case.v_cache, case.block_tables[0]
+    part = kernels.default_partition(cfg.num_seqs, cfg.num_kv_heads, bt.shape[1], cfg.block_size)
+    assert kernels.decode_workspace_bytes(cfg.num_seqs, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim,
+                                          bt.shape[1], cfg.block_size, part) > 0, "shape must split"
+    out = torch.full_like(q, 7.0)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    # another entry point runs eagerly first (the library's code is on the device)
+    kernels.paged_decode(q, kc, vc, bt, case.context_lens, cfg.block_size, cfg.scale, partition_tokens=part)
+    torch.cuda.synchronize()
+    print("capturing the first no-alloc call", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib().ir_paged_decode_noalloc(
+            ptr(q), q.stride(0), q.stride(1), ptr(kc), ptr(vc), kc.stride(0), kc.stride(1),
+            kc.shape[0] // cfg.block_size, cfg.block_size, ptr(bt), bt.stride(0), bt.shape[1],
+            ptr(case.context_lens), ptr(out), out.stride(0), out.stride(1), cfg.num_seqs, cfg.num_q_heads,
+            cfg.num_kv_heads, cfg.head_dim, float(cfg.scale), dtype_code(q.dtype), part, ptr(err),
+            stream_ptr(q.device))
+        check(rc, "ir_paged_decode_noalloc")
+    for rep in range(3):
+        if rep:
+            q.normal_()  # a new query for the same graph
+        graph.replay()
+        ref = kernels.paged_decode(q, kc, vc, bt, case.context_lens, cfg.block_size, cfg.scale,
+                                   partition_tokens=part)
+        torch.cuda.synchronize()
+        assert err.item() == 0
+        assert torch.equal(out, ref), f"replay {{rep}}: differs from ir_paged_decode"
+        print(f"replay {{rep}}: equal", flush=True)
+""")
+
+
+def test_noalloc_first_call_inside_graph_capture():
+    """In a fresh process (nothing of the no-alloc entry point set up yet; one
+    eager ir_paged_decode call before), its first call is made under
+    torch.cuda.graph capture: the device-array lookup
+    and the counter clear happen there (the clear is a kernel, so it is
+    recorded), and every replay equals ir_paged_decode bit for bit, also after
+    the query changes in place."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = subprocess.run([sys.executable, "-u", "-c", _FIRST_CALL_IN_CAPTURE.format(root=root)], cwd=root,
+                         capture_output=True, text=True, timeout=240)
+    print(res.stdout)
+    assert res.returncode == 0, res.stderr[-4000:]
+    assert "replay 2: equal" in res.stdout
