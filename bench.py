@@ -91,6 +91,9 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--check", action="store_true", help="also check the output against the oracle")
     p.add_argument("--mode", choices=("graph", "eager"), default="graph",
                    help="time a hipGraph replay of the K calls (default) or host-launched calls")
+    p.add_argument("--layout", choices=("head_major", "slot_major"), default="head_major",
+                   help="decode: the pool's physical layout -- head-major (default: a KV head's block is one "
+                   "contiguous run) or the reference's contiguous [slots, H_kv, D] storage")
     p.add_argument("--overlap", action="store_true",
                    help="mixed: decode and prefill on two streams (default: one stream, measured faster)")
     p.add_argument("--copy-calib-mib", type=int, default=0,
@@ -1085,7 +1088,7 @@ def main() -> int:
     from infrared_amd.workloads import make_decode_case
 
     args.config = args.config or "qwen7b-bf16"
-    case = make_decode_case(args.config, "cuda", rotations=args.rotations)
+    case = make_decode_case(args.config, "cuda", rotations=args.rotations, layout=args.layout)
     cfg = case.config
     kv = case.kv_bytes
     # bytes the kernel reads: with pairs, a shared prefix block once per pair
@@ -1108,7 +1111,8 @@ def main() -> int:
         _copy_calibration(args.copy_calib_mib)
     cpu = _cpu_baseline(case, args) if args.cpu_iters > 0 else None
     sched = ("pairs_" if args.pairs else "planned_") if info["schedule"] == "planned" else ""
-    traffic, traffic_src = _traffic(f"decode_{sched}{args.config}")
+    lay = "" if args.layout == "head_major" else f"{args.layout}_"
+    traffic, traffic_src = _traffic(f"decode_{sched}{lay}{args.config}")
     esize = torch.tensor([], dtype=cfg.dtype).element_size()
     line = {
         "metric": METRIC,
@@ -1134,6 +1138,7 @@ def main() -> int:
             "kv_bytes_per_call": kv,
             "unique_kv_bytes_per_call": case.unique_kv_bytes,
             "rotations": args.rotations,
+            "pool_layout": args.layout,
             **info,
             "bytes_per_token": 2 * cfg.num_kv_heads * cfg.head_dim * esize,
         },

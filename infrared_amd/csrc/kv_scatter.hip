@@ -26,25 +26,42 @@ struct ScatterArgs {
   int32_t* err;
 };
 
-// One lane per 16-byte piece of a (token, head) row.
+// One lane per 16-byte piece of a (token, head) row. The slot and both source
+// pieces are loaded before the slot is inspected (the sources are in bounds
+// for every lane of the grid), so a lane waits for one round trip, not two.
+// NARROW: the grid's piece count fits 31 bits, so the index math is 32-bit.
+template <bool NARROW>
 __global__ __launch_bounds__(256) void kv_scatter_vec16(ScatterArgs a) {
   const int pieces = a.row_bytes >> 4;
-  const int64_t per_tok = (int64_t)pieces * a.num_kv_heads;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= a.n_tokens * per_tok) return;
-  const int64_t tok = idx / per_tok;
-  const int rem = (int)(idx - tok * per_tok);
-  const int head = rem / pieces;
-  const int piece = rem - head * pieces;
+  int64_t tok;
+  int head, piece;
+  if constexpr (NARROW) {
+    const int per_tok = pieces * a.num_kv_heads;
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int)a.n_tokens * per_tok) return;
+    const int t = idx / per_tok;
+    const int rem = idx - t * per_tok;
+    tok = t;
+    head = rem / pieces;
+    piece = rem - head * pieces;
+  } else {
+    const int64_t per_tok = (int64_t)pieces * a.num_kv_heads;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= a.n_tokens * per_tok) return;
+    tok = idx / per_tok;
+    const int rem = (int)(idx - tok * per_tok);
+    head = rem / pieces;
+    piece = rem - head * pieces;
+  }
+  const int64_t off = (int64_t)piece * 16;
   const int64_t slot = a.slots[tok];
+  const u32x4 kx = *(const u32x4*)(a.k + tok * a.k_tok + head * a.k_head + off);
+  const u32x4 vx = *(const u32x4*)(a.v + tok * a.v_tok + head * a.v_head + off);
   if (slot < 0) return;  // padding sentinel
   if (slot >= a.num_slots) {
     flag_error(a.err, IR_ERR_SLOT_RANGE);
     return;
   }
-  const int64_t off = (int64_t)piece * 16;
-  const u32x4 kx = *(const u32x4*)(a.k + tok * a.k_tok + head * a.k_head + off);
-  const u32x4 vx = *(const u32x4*)(a.v + tok * a.v_tok + head * a.v_head + off);
   *(u32x4*)(a.kc + slot * a.c_slot + head * a.c_head + off) = kx;
   *(u32x4*)(a.vc + slot * a.c_slot + head * a.c_head + off) = vx;
 }
@@ -217,7 +234,11 @@ extern "C" int ir_kv_scatter(const void* k, int64_t k_tok_stride, int64_t k_head
   hipStream_t s = (hipStream_t)stream;
   if (vec) {
     const int64_t total = n_tokens * num_kv_heads * (a.row_bytes / 16);
-    hipLaunchKernelGGL(kv_scatter_vec16, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
+    const dim3 grid((unsigned)((total + 255) / 256));
+    if (total + 255 < ((int64_t)1 << 31))
+      hipLaunchKernelGGL(kv_scatter_vec16<true>, grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(kv_scatter_vec16<false>, grid, dim3(256), 0, s, a);
   } else {
     const int64_t total = n_tokens * num_kv_heads * (int64_t)head_dim;
     const dim3 grid((unsigned)((total + 255) / 256));

@@ -17,13 +17,13 @@ metadata:
 3. ``ir_paged_prefill`` for the chunks (causal after their cached prefix).
 
 By default the three run on one stream. With ``overlap=True`` the decode
-(HBM-bound) and prefill (MFMA-bound) launches of a layer run on two streams
-that fork after the scatter and join before the next layer's scatter;
-captured, they become parallel graph branches (both streams at the default
-priority). That measured slower on MI355X (203 vs 190 us per layer at
-224 decode rows + 4 x 256-token chunks): the planned decode runs one
-workgroup per CU, and the prefill's workgroups (110 KB of LDS each) hold CUs
-that those slices then wait for.
+rows' scatter runs first, then the stream forks: the decode (HBM-bound) on
+one branch, the chunks' scatter and prefill (MFMA-bound) on the other, joined
+before the next layer; captured, they become parallel graph branches (both
+streams at the default priority). That measured slower on MI355X at 224
+decode rows + 4 x 256-token chunks: 187.5 against 177.5 us per layer, with a
+prefill workgroup (~78 KB of LDS) fitting beside each decode workgroup
+(72 KB), so the loss is the branches' cost, not CUs held by the prefill.
 
 The per-layer projections around attention are not part of this path; the
 caller supplies each layer's q and new K/V (``MixedInputs``).
@@ -205,14 +205,22 @@ class MixedStep:
 
     def _layer(self, layer: int) -> None:
         b, inp, pool = self.batch, self.inputs, self.pool
-        kernels.kv_scatter(pool.k[layer], pool.v[layer], inp.k_new[layer], inp.v_new[layer], b.write_slots, self.err)
         if self._side is None:
+            kernels.kv_scatter(pool.k[layer], pool.v[layer], inp.k_new[layer], inp.v_new[layer], b.write_slots,
+                               self.err)
             self._decode(layer)
             self._prefill(layer)
             return
+        # the decode rows' new K/V first (the decode reads them), then the
+        # chunks' rows and the prefill on the side stream beside the decode
+        nd = inp.q_dec.shape[1]
         main = torch.cuda.current_stream(pool.device)
-        self._side.wait_stream(main)  # the scatter is done before either attention reads the pool
+        kernels.kv_scatter(pool.k[layer], pool.v[layer], inp.k_new[layer, :nd], inp.v_new[layer, :nd],
+                           b.write_slots[:nd], self.err)
+        self._side.wait_stream(main)
         with torch.cuda.stream(self._side):
+            kernels.kv_scatter(pool.k[layer], pool.v[layer], inp.k_new[layer, nd:], inp.v_new[layer, nd:],
+                               b.write_slots[nd:], self.err)
             self._prefill(layer)
         self._decode(layer)
         main.wait_stream(self._side)  # both are done before the next layer's scatter
