@@ -344,30 +344,33 @@ int ir_decode_form(const int64_t* gather_slots, int64_t gs_b_stride, int64_t gs_
  * build_varlen_mask / build_attention_mask (0 where the key is the query's own
  * sequence at or before its position, finfo.min elsewhere)
  * (infrared/engine/paged_engine.py:194-206, :461-516;
- * infrared/model/inputs.py:33-85). Two passes, the host reading info between
- * them (it sizes block_tables):
- *   ir_varlen_form_scan: reads every mask row (element (r, k) at
- *     mask + r*mask_q_stride + k*mask_k_stride); writes row_ranges [2*num_q]
- *     (scratch), cu_seqlens_q [num_q + 1], q_start [num_q] and seq_k_offsets
- *     [num_q] for the sequences found, and info[0..3] (no clearing needed):
- *     info[1..3] = sequence count, longest chunk, widest block table (blocks);
- *     info[0] = 0 if each row's visible keys are one contiguous range, every
- *     other value <= -6e4, the rows of a sequence each see one key more than
- *     the last, and the sequences' key ranges tile [0, num_k) in order, else 1.
+ * infrared/model/inputs.py:33-85). Two calls, the host reading info once,
+ * between them (it sizes block_tables):
+ *   ir_varlen_form_scan: reads every mask element once (element (r, k) at
+ *     mask + r*mask_q_stride + k*mask_k_stride; a contiguous 16-byte-aligned
+ *     mask as one flat array) and every key's slot; writes cu_seqlens_q
+ *     [num_q + 1], q_start [num_q] and seq_k_offsets [num_q] for the sequences
+ *     found, and info[0..3] (no clearing needed): info[1..3] = sequence count,
+ *     longest chunk, widest block table (blocks); info[0] = 0 if each row's
+ *     visible keys are one contiguous range, every other value <= -6e4, the
+ *     rows of a sequence each see one key more than the last, the sequences'
+ *     key ranges tile [0, num_k) in order, and every slot
+ *     gather_slots[k_off_i + p] (stride gs_k_stride) has the closed form with a
+ *     block id in [0, num_blocks); else 1. row_records: [4*num_q] int32
+ *     scratch, 16-byte aligned, zero before the first call; every call leaves
+ *     it zero (calls sharing it must be stream-ordered).
  *   ir_varlen_form_tables: block_tables[i, j] = gather_slots[k_off_i + j*bs] / bs
- *     ([num_seqs, bt_stride] int32, max_blocks_per_seq >= info[3]); ORs 1 into
- *     info[0] unless every slot of every sequence has the closed form with a
- *     block id in [0, num_blocks).
- * With info[0] clear after both, ir_paged_prefill over this metadata computes
- * what ir_paged_attention_masked computes from the frame.
+ *     ([num_seqs, bt_stride] int32, max_blocks_per_seq >= info[3]).
+ * With info[0] clear after the scan, ir_paged_prefill over this metadata
+ * computes what ir_paged_attention_masked computes from the frame.
  */
 int ir_varlen_form_scan(const void* mask, int64_t mask_q_stride, int64_t mask_k_stride, int mask_dtype,
-                        int num_q, int num_k, int block_size, int32_t* row_ranges, int32_t* cu_seqlens_q,
-                        int32_t* q_start, int32_t* seq_k_offsets, int32_t* info, ir_stream_t stream);
+                        int num_q, int num_k, const int64_t* gather_slots, int64_t gs_k_stride, int block_size,
+                        int64_t num_blocks, int32_t* row_records, int32_t* cu_seqlens_q, int32_t* q_start,
+                        int32_t* seq_k_offsets, int32_t* info, ir_stream_t stream);
 int ir_varlen_form_tables(const int64_t* gather_slots, int64_t gs_k_stride, const int32_t* seq_k_offsets,
                           const int32_t* cu_seqlens_q, const int32_t* q_start, int num_seqs, int block_size,
-                          int64_t num_blocks, int32_t* block_tables, int64_t bt_stride,
-                          int max_blocks_per_seq, int32_t* info, ir_stream_t stream);
+                          int32_t* block_tables, int64_t bt_stride, int max_blocks_per_seq, ir_stream_t stream);
 
 /*
  * Chunked prefill / prefix-hit prefill / packed mixed step over block tables

@@ -102,11 +102,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ir_stream_capture_id": (_c_i32, [_c_p, ctypes.POINTER(ctypes.c_uint64)]),
     "ir_varlen_form_scan": (
         _c_i32,
-        [_c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p],
+        [_c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i32, _c_i64, _c_p, _c_p, _c_p, _c_p,
+         _c_p, _c_p],
     ),
     "ir_varlen_form_tables": (
         _c_i32,
-        [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i64, _c_p, _c_i64, _c_i32, _c_p, _c_p],
+        [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_p, _c_i64, _c_i32, _c_p],
     ),
     "ir_hbm_read_granule": (_c_i64, []),
     "ir_hbm_read": (_c_i32, [_c_p, _c_i64, _c_p, _c_i32, _c_p]),

@@ -15,12 +15,16 @@
 // one, each row sees one key more than the row before; the sequences' key
 // ranges tile [0, K) in order. That yields cu_seqlens_q, q_start (= the first
 // row's hi - lo) and each sequence's key offset, and the sizes the host needs
-// (sequence count, longest chunk, widest block table). Pass 2
-// (ir_varlen_form_tables) recovers bt_i[j] = gather_slots[k_off_i + j bs] / bs
-// and verifies every slot of every sequence against the closed form and the
-// pool. Any violation sets info[0]; the host then keeps the mask kernel, which
-// reads the metadata as given. When both passes hold, the chunked-prefill
-// kernel over these block tables attends exactly the keys the mask allows.
+// (sequence count, longest chunk, widest block table); the same call then
+// verifies every slot of every sequence against the closed form and the pool,
+// on the device, before the host reads anything. Any violation sets
+// info[0]; the host then keeps the mask kernel, which reads the metadata as
+// given. With info[0] clear the host sizes the block tables from info and
+// ir_varlen_form_tables writes bt_i[j] = gather_slots[k_off_i + j bs] / bs; the
+// chunked-prefill kernel over them attends exactly the keys the mask allows.
+// One synchronising read per step: info, cu_seqlens_q and q_start together.
+#include <algorithm>
+
 #include "common.hpp"
 #include "status.hpp"
 
@@ -35,11 +39,6 @@ __device__ __forceinline__ float mask_value(const void* m, int dtype, int64_t of
   const uint32_t h = ((const uint16_t*)m)[off];
   return dtype == IR_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
 }
-
-// Two wavefronts per row and four 16-byte pieces per lane and pass: of
-// 64-1024 threads x 3-12 pieces, the fastest on a 4096 x 22819 bf16 mask.
-constexpr int kRowThreads = 128;
-constexpr int kRowPieces = 4;  // 16-byte pieces a lane has in flight per pass
 
 // finfo(dtype).min in every element of a 32-bit word (two for 16-bit masks).
 template <int DT>
@@ -66,17 +65,204 @@ __device__ __forceinline__ void piece_bits(u32x4 x, uint32_t& zero, uint32_t& ba
   }
 }
 
-// One workgroup per mask row: the first and last visible key, their count and
-// whether any other value fails to mask. A contiguous mask is read as 16-byte
-// pieces of the flat [Q * K] array, a lane's pieces of a pass all in flight
-// before any is inspected; rows need not start on a piece, so the first
-// and last piece of a row keep only the row's elements, and the array's last
-// piece, when partial, is read element by element. Strided masks are read
-// element by element.
-template <int DT>
-__global__ __launch_bounds__(kRowThreads) void varlen_rows_kernel(const void* mask, int64_t m_q, int64_t m_k, int Q,
-                                                                  int K, bool flat, int32_t* range) {
-  constexpr int PER = DT == IR_DTYPE_F32 ? 4 : 8;  // elements per 16-byte piece
+// Per-row record of the scan, zero at rest (every scan leaves it zero):
+// INT_MAX - first visible key, last visible key + 1, their count, and whether
+// any value is neither visible nor masked -- encoded so that the empty record
+// is all zeros and every update is an atomic max, max, add or or.
+struct RowRec {
+  int first_c, last1, count, wrong;
+};
+constexpr int kFirstBias = 0x7fffffff;
+
+// A row's share of a run of visible keys [k_lo, k_hi] (count keys) and of
+// wrong values, added to its record.
+__device__ __forceinline__ void rec_add(RowRec* rec, int r, int k_lo, int k_hi, int count, int wrong) {
+  if (count) {
+    atomicMax(&rec[r].first_c, kFirstBias - k_lo);
+    atomicMax(&rec[r].last1, k_hi + 1);
+    atomicAdd(&rec[r].count, count);
+  }
+  if (wrong) atomicOr(&rec[r].wrong, 1);
+}
+
+// Contiguous masks: the flat [Q * K] array as 16-byte pieces, grid-stride.
+// A wavefront takes 64 * kFlatPieces consecutive pieces per pass (each load
+// instruction 1 KiB contiguous), all in flight before any is inspected. A
+// piece that is all finfo.min -- nearly all of them -- costs an OR and an
+// AND of its words; a wavefront whose pieces hold no visible key and no bad
+// value moves on without any reduction. Otherwise each lane describes its
+// piece as a run of visible keys in at most two rows (a piece straddles a row
+// end when K is not a multiple of its elements), and the wavefront folds the
+// lanes of the first two rows it touches into one atomic update per row
+// (rows shorter than 64 pieces fall back to an update per lane). NARROW: the
+// element index fits 31 bits.
+constexpr int kFlatThreads = 256;
+constexpr int kFlatPieces = 8;
+
+template <int DT, bool NARROW>
+__global__ __launch_bounds__(kFlatThreads) void varlen_flat_kernel(const u32x4* pieces, int64_t whole, int K, RowRec* rec) {
+  constexpr int PER = DT == IR_DTYPE_F32 ? 4 : 8;
+  constexpr uint32_t M = kMinWord<DT>;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * (kFlatThreads / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * (kFlatThreads / 64);
+  constexpr int64_t kSpan = 64 * kFlatPieces;
+  auto row_of = [&](int64_t e) -> int { return NARROW ? (int)((uint32_t)e / (uint32_t)K) : (int)(e / K); };
+  for (int64_t base = wave * kSpan; base < whole; base += nwaves * kSpan) {
+    const bool full = base + kSpan <= whole;  // uniform: every piece of the span exists
+    const char* p = (const char*)(pieces + base);  // uniform base, unsigned 32-bit lane offsets
+    u32x4 x[kFlatPieces];
+    if (full) {
+#pragma unroll
+      for (int i = 0; i < kFlatPieces; ++i) x[i] = load_nt((const u32x4*)(p + (uint32_t)(i * 64 + lane) * 16u));
+    } else {
+      const int last = (int)(whole - 1 - base);
+#pragma unroll
+      for (int i = 0; i < kFlatPieces; ++i)
+        x[i] = load_nt((const u32x4*)(p + (uint32_t)min(i * 64 + lane, last) * 16u));
+    }
+    // the common case: every piece of the span all finfo(dtype).min
+    uint32_t special = 0;
+#pragma unroll
+    for (int i = 0; i < kFlatPieces; ++i)
+      special |= ((x[i][0] | x[i][1] | x[i][2] | x[i][3]) ^ M) | ((x[i][0] & x[i][1] & x[i][2] & x[i][3]) ^ M);
+    if (full && __ballot(special != 0u) == 0ull) continue;  // uniform
+    // rows the span touches: with rows at least a span long, at most two, and
+    // each lane folds its pieces into both before one wavefront reduction
+    const int r0 = row_of(base * PER);
+    const int r1 = row_of(min(base + kSpan, whole) * PER - 1);
+    if (r1 - r0 <= 1) {  // uniform
+      const int64_t b1 = (int64_t)(r0 + 1) * K;  // first element of row r0 + 1
+      int f[2] = {K, K}, l[2] = {-1, -1}, n[2] = {0, 0}, wr[2] = {0, 0};
+#pragma unroll
+      for (int i = 0; i < kFlatPieces; ++i) {
+        const int64_t c = base + i * 64 + lane;
+        const uint32_t any = x[i][0] | x[i][1] | x[i][2] | x[i][3];
+        const uint32_t all = x[i][0] & x[i][1] & x[i][2] & x[i][3];
+        if (c >= whole || (any == M && all == M)) continue;
+        uint32_t zero = (1u << PER) - 1u, bad = 0;
+        if (any != 0u) piece_bits<DT>(x[i], zero, bad);
+        const int64_t e0 = c * PER;
+        const int split = (int)max((int64_t)0, min((int64_t)PER, b1 - e0));  // elements in row r0
+        const uint32_t in_a = (1u << split) - 1u;
+        const uint32_t za = zero & in_a, zb = zero & ~in_a;
+        if (za) {
+          const int k0 = (int)(e0 - (b1 - K));
+          f[0] = min(f[0], k0 + __builtin_ctz(za));
+          l[0] = max(l[0], k0 + 31 - __builtin_clz(za));
+          n[0] += __builtin_popcount(za);
+        }
+        if (zb) {
+          const int k0 = (int)(e0 - b1);
+          f[1] = min(f[1], k0 + __builtin_ctz(zb));
+          l[1] = max(l[1], k0 + 31 - __builtin_clz(zb));
+          n[1] += __builtin_popcount(zb);
+        }
+        wr[0] |= (bad & in_a) != 0u;
+        wr[1] |= (bad & ~in_a) != 0u;
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl) {
+          f[sl] = min(f[sl], __shfl_xor(f[sl], o));
+          l[sl] = max(l[sl], __shfl_xor(l[sl], o));
+          n[sl] += __shfl_xor(n[sl], o);
+          wr[sl] |= __shfl_xor(wr[sl], o);
+        }
+      }
+      if (lane < 2 && r0 + lane <= r1) {
+        const bool one = lane == 1;  // lane 0 updates row r0, lane 1 row r0 + 1
+        rec_add(rec, r0 + lane, one ? f[1] : f[0], one ? l[1] : l[0], one ? n[1] : n[0], one ? wr[1] : wr[0]);
+      }
+      continue;
+    }
+    // rows shorter than a span: each load instruction's 64 pieces on their own
+#pragma unroll
+    for (int i = 0; i < kFlatPieces; ++i) {
+      const int64_t c = base + i * 64 + lane;
+      const bool in = c < whole;
+      const uint32_t any = x[i][0] | x[i][1] | x[i][2] | x[i][3];
+      const uint32_t all = x[i][0] & x[i][1] & x[i][2] & x[i][3];
+      uint32_t zero = 0, bad = 0;
+      if (in && !(any == M && all == M)) {
+        if (any == 0u) zero = (1u << PER) - 1u;
+        else piece_bits<DT>(x[i], zero, bad);
+      }
+      if (__ballot((zero | bad) != 0u) == 0ull) continue;  // uniform
+      // the wavefront's first row and the row of its last element
+      const int64_t c_first = base + i * 64;
+      const int r0 = row_of(c_first * PER);
+      const int64_t c_last = min(c_first + 63, whole - 1);
+      const int r_end = row_of(c_last * PER + PER - 1);
+      // this lane's piece: elements e0 .. e0 + PER - 1, row ra up to key
+      // K - 1, then (rows of at least 64 pieces) row ra + 1; split = its
+      // elements in row ra
+      const int64_t e0 = c * PER;
+      const int ra = row_of(e0);
+      const int k0 = (int)(e0 - (int64_t)ra * K);
+      const int split = min(PER, K - k0);
+      const uint32_t in_a = (1u << split) - 1u;
+      const uint32_t za = zero & in_a, zb = zero & ~in_a;
+      const int wa = (bad & in_a) != 0u, wb = (bad & ~in_a) != 0u;
+      if (r_end - r0 > 1) {  // short rows (a piece may span several): one update per element
+        for (uint32_t bits = zero | bad; bits; bits &= bits - 1u) {
+          const int e = __builtin_ctz(bits);
+          const int r = row_of(e0 + e), k = (int)(e0 + e - (int64_t)r * K);
+          if ((zero >> e) & 1u) rec_add(rec, r, k, k, 1, 0);
+          else rec_add(rec, r, 0, 0, 0, 1);
+        }
+        continue;
+      }
+      // fold into rows r0 (slot 0) and r0 + 1 (slot 1)
+      int f[2] = {K, K}, l[2] = {-1, -1}, n[2] = {0, 0}, wr[2] = {0, 0};
+      const int sa = ra - r0;  // 0 or 1
+      if (za) {
+        f[sa] = k0 + __builtin_ctz(za);
+        l[sa] = k0 + 31 - __builtin_clz(za);
+        n[sa] = __builtin_popcount(za);
+      }
+      wr[sa] |= wa;
+      if (sa == 0) {  // the second part of a straddling piece belongs to r0 + 1
+        if (zb) {
+          f[1] = __builtin_ctz(zb) - split;
+          l[1] = 31 - __builtin_clz(zb) - split;
+          n[1] = __builtin_popcount(zb);
+        }
+        wr[1] |= wb;
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl) {
+          f[sl] = min(f[sl], __shfl_xor(f[sl], o));
+          l[sl] = max(l[sl], __shfl_xor(l[sl], o));
+          n[sl] += __shfl_xor(n[sl], o);
+          wr[sl] |= __shfl_xor(wr[sl], o);
+        }
+      }
+      if (lane < 2 && r0 + lane <= r_end) {
+        const bool one = lane == 1;  // lane 0 updates row r0, lane 1 row r0 + 1
+        rec_add(rec, r0 + lane, one ? f[1] : f[0], one ? l[1] : l[0], one ? n[1] : n[0], one ? wr[1] : wr[0]);
+      }
+    }
+  }
+}
+
+// The array's last partial piece (Q * K not a multiple of a piece), element by
+// element, and strided masks: one workgroup per row.
+__global__ __launch_bounds__(64) void varlen_tail_kernel(const void* mask, int dtype, int64_t e_from, int64_t e_to,
+                                                          int K, RowRec* rec) {
+  for (int64_t e = e_from + threadIdx.x; e < e_to; e += 64) {
+    const float x = mask_value(mask, dtype, e);
+    const int r = (int)(e / K), k = (int)(e - (int64_t)r * K);
+    if (x == 0.f) rec_add(rec, r, k, k, 1, 0);
+    else if (!(x <= -6e4f)) rec_add(rec, r, 0, 0, 0, 1);
+  }
+}
+
+__global__ __launch_bounds__(kScanThreads) void varlen_rows_strided_kernel(const void* mask, int dtype, int64_t m_q,
+                                                                          int64_t m_k, int K, RowRec* rec) {
   __shared__ int s_first, s_last, s_count, s_wrong;
   const int r = blockIdx.x, tid = threadIdx.x;
   if (tid == 0) {
@@ -87,7 +273,9 @@ __global__ __launch_bounds__(kRowThreads) void varlen_rows_kernel(const void* ma
   }
   __syncthreads();
   int first = K, last = -1, count = 0, wrong = 0;
-  auto visit = [&](int k, float x) {
+  const int64_t row = (int64_t)r * m_q;
+  for (int k = tid; k < K; k += kScanThreads) {
+    const float x = mask_value(mask, dtype, row + (int64_t)k * m_k);
     if (x == 0.f) {
       first = min(first, k);
       last = max(last, k);
@@ -95,63 +283,6 @@ __global__ __launch_bounds__(kRowThreads) void varlen_rows_kernel(const void* ma
     } else {
       wrong |= !(x <= -6e4f);
     }
-  };
-  if (flat) {
-    const int64_t e0 = (int64_t)r * K, e1 = e0 + K;
-    const int64_t c0 = e0 / PER, c1 = (e1 + PER - 1) / PER;
-    const int64_t whole = (int64_t)Q * K / PER;  // pieces wholly inside the array
-    // every lane loads every pass, past the row's last whole piece from that
-    // piece again (a row with no whole piece of its own loads nothing and
-    // inspects its elements one by one)
-    const int64_t c_end = min(c1, whole) - 1;
-    const u32x4* pieces = (const u32x4*)mask;
-    auto inspect = [&](const u32x4& v, int64_t c) {
-      const int k0 = (int)(c * PER - e0);  // key of the piece's element 0 (negative in a row's first piece)
-      if (c >= whole) {
-        for (int e = max(0, -k0); e < PER && k0 + e < K; ++e) visit(k0 + e, mask_value(mask, DT, e0 + k0 + e));
-        return;
-      }
-      const int lo = max(0, -k0), hi = min(PER, K - k0);  // the row's elements of this piece
-      const uint32_t keep = ((1u << hi) - 1u) & ~((1u << lo) - 1u);
-      // a piece wholly in the row that is all +0 or all finfo(dtype).min --
-      // nearly every piece of the reference's mask -- is settled from its
-      // four words; anything else is inspected element by element
-      const uint32_t any = v[0] | v[1] | v[2] | v[3];
-      const uint32_t all = v[0] & v[1] & v[2] & v[3];
-      const bool whole_piece = keep == (1u << PER) - 1u;
-      if (whole_piece && any == 0u) {
-        first = min(first, k0);
-        last = max(last, k0 + PER - 1);
-        count += PER;
-        return;
-      }
-      if (whole_piece && any == kMinWord<DT> && all == kMinWord<DT>) return;
-      uint32_t zero, bad;
-      piece_bits<DT>(v, zero, bad);
-      zero &= keep;
-      wrong |= (bad & keep) != 0u;
-      if (zero) {
-        first = min(first, k0 + __builtin_ctz(zero));
-        last = max(last, k0 + 31 - __builtin_clz(zero));
-        count += __builtin_popcount(zero);
-      }
-    };
-    for (int64_t base = c0; base < c1; base += (int64_t)kRowThreads * kRowPieces) {
-      u32x4 x[kRowPieces];
-      if (c_end >= c0) {  // uniform: the row holds a whole piece
-#pragma unroll
-        for (int i = 0; i < kRowPieces; ++i) x[i] = load_nt(pieces + min(base + i * kRowThreads + tid, c_end));
-      }
-#pragma unroll
-      for (int i = 0; i < kRowPieces; ++i) {
-        const int64_t c = base + i * kRowThreads + tid;
-        if (c >= c1) break;
-        inspect(x[i], c);
-      }
-    }
-  } else {
-    const int64_t row = (int64_t)r * m_q;
-    for (int k = tid; k < K; k += kRowThreads) visit(k, mask_value(mask, DT, row + (int64_t)k * m_k));
   }
   if (count) {
     atomicMin(&s_first, first);
@@ -160,24 +291,25 @@ __global__ __launch_bounds__(kRowThreads) void varlen_rows_kernel(const void* ma
   }
   if (wrong) s_wrong = 1;
   __syncthreads();
-  if (tid == 0) {
-    // no visible key, or a masked key between two visible ones: the row's
-    // range is (-1, -1), which the segment pass reports
-    const bool bad = s_wrong || s_count == 0 || s_last - s_first + 1 != s_count;
-    range[2 * r] = bad ? -1 : s_first;
-    range[2 * r + 1] = bad ? -1 : s_last;
-  }
+  if (tid == 0) rec[r] = s_count ? RowRec{kFirstBias - s_first, s_last + 1, s_count, s_wrong} : RowRec{0, 0, 0, s_wrong};
 }
 
-// One workgroup: rows -> sequences (block-wide scan of the rows where lo
-// moves), then the longest chunk and the widest table; info[0..3] written
-// whole (no clearing before the pass).
-__global__ __launch_bounds__(kSegThreads) void varlen_segments_kernel(const int32_t* range, int Q, int K, int bs,
+// One workgroup: rows -> sequences, then the longest chunk and the widest
+// table; info[0..3] written whole (no clearing before the pass). A row is
+// usable when its visible keys are one contiguous range; a sequence starts
+// where that range's first key moves. A thread takes kSegRows consecutive
+// rows per pass (their records and the one before requested together), and
+// the sequences a pass starts are numbered with a block-wide scan of the
+// threads' counts (wavefront prefix sums, then the wavefronts' totals): two
+// barriers per pass of kSegThreads * kSegRows rows.
+constexpr int kSegRows = 4;
+__global__ __launch_bounds__(kSegThreads) void varlen_segments_kernel(RowRec* rec, int Q, int K, int bs,
                                                                      int32_t* cu, int32_t* q_start, int32_t* seq_lo,
                                                                      int32_t* info) {
-  __shared__ int s_scan[kSegThreads];
+  constexpr int NWV = kSegThreads / 64;
+  __shared__ int s_wave[NWV];
   __shared__ int s_base, s_bad, s_maxq, s_maxb;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   if (tid == 0) {
     s_base = 0;
     s_bad = 0;
@@ -185,40 +317,70 @@ __global__ __launch_bounds__(kSegThreads) void varlen_segments_kernel(const int3
     s_maxb = 0;
   }
   __syncthreads();
-  for (int c0 = 0; c0 < Q; c0 += kSegThreads) {
-    const int r = c0 + tid;
-    int start = 0;
-    if (r < Q) {
-      const int lo = range[2 * r], hi = range[2 * r + 1];
-      const int plo = r > 0 ? range[2 * r - 2] : -1, phi = r > 0 ? range[2 * r - 1] : -1;
-      start = r == 0 || lo != plo;
-      // a row whose own scan failed; a new sequence's keys follow the last
-      // one's; a row of the same sequence sees one key more than the row before
-      if (lo < 0 || (start ? lo != phi + 1 : hi != phi + 1)) s_bad = 1;
-      if (r == Q - 1 && hi != K - 1) s_bad = 1;  // the key axis ends with the last sequence
+  auto range = [](const RowRec& x, int& lo, int& hi) {
+    const int first = kFirstBias - x.first_c, last = x.last1 - 1;
+    const bool bad = x.wrong || x.count == 0 || last - first + 1 != x.count;
+    lo = bad ? -1 : first;
+    hi = bad ? -1 : last;
+  };
+  for (int c0 = 0; c0 < Q; c0 += kSegThreads * kSegRows) {
+    const int r0 = c0 + tid * kSegRows;
+    RowRec x[kSegRows + 1];  // the row before this thread's first, then its rows
+#pragma unroll
+    for (int j = 0; j <= kSegRows; ++j) {
+      const int r = r0 - 1 + j;
+      x[j] = r >= 0 && r < Q ? rec[r] : RowRec{0, 0, 0, 0};
     }
-    s_scan[tid] = start;
+    int lo[kSegRows + 1], hi[kSegRows + 1], start[kSegRows];
+    range(x[0], lo[0], hi[0]);
+    if (r0 == 0) lo[0] = hi[0] = -1;
+    int mine = 0;
+#pragma unroll
+    for (int j = 0; j < kSegRows; ++j) {
+      const int r = r0 + j;
+      range(x[j + 1], lo[j + 1], hi[j + 1]);
+      start[j] = 0;
+      if (r < Q) {
+        start[j] = r == 0 || lo[j + 1] != lo[j];
+        // a row whose own scan failed; a new sequence's keys follow the last
+        // one's; a row of the same sequence sees one key more than the row before
+        if (lo[j + 1] < 0 || (start[j] ? lo[j + 1] != hi[j] + 1 : hi[j + 1] != hi[j] + 1)) s_bad = 1;
+        if (r == Q - 1 && hi[j + 1] != K - 1) s_bad = 1;  // the key axis ends with the last sequence
+        mine += start[j];
+      }
+    }
+    // exclusive prefix of `mine` over the block
+    int incl = mine;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o);
+      if (lane >= o) incl += y;
+    }
+    if (lane == 63) s_wave[wv] = incl;
     __syncthreads();
-    // inclusive Hillis-Steele scan of the start flags
-    for (int off = 1; off < kSegThreads; off <<= 1) {
-      const int add = tid >= off ? s_scan[tid - off] : 0;
-      __syncthreads();
-      s_scan[tid] += add;
-      __syncthreads();
-    }
-    if (r < Q && start) {
-      const int i = s_base + s_scan[tid] - 1;
-      const int lo = range[2 * r], hi = range[2 * r + 1];
-      cu[i] = r;
-      seq_lo[i] = lo;
-      q_start[i] = hi - lo;
+    int i = s_base + incl - mine;
+    for (int v = 0; v < wv; ++v) i += s_wave[v];
+#pragma unroll
+    for (int j = 0; j < kSegRows; ++j) {
+      if (start[j]) {
+        cu[i] = r0 + j;
+        seq_lo[i] = lo[j + 1];
+        q_start[i] = hi[j + 1] - lo[j + 1];
+        ++i;
+      }
     }
     __syncthreads();
-    if (tid == 0) s_base += s_scan[kSegThreads - 1];
+    if (tid == 0) {
+      int t = 0;
+      for (int v = 0; v < NWV; ++v) t += s_wave[v];
+      s_base += t;
+    }
     __syncthreads();
   }
   const int nseq = s_base;
   if (tid == 0) cu[nseq] = Q;
+  // every record read: leave them zero for the next scan
+  for (int r = tid; r < Q; r += kSegThreads) rec[r] = RowRec{0, 0, 0, 0};
   __syncthreads();
   for (int i = tid; i < nseq; i += kSegThreads) {
     const int q = cu[i + 1] - cu[i];
@@ -235,35 +397,60 @@ __global__ __launch_bounds__(kSegThreads) void varlen_segments_kernel(const int3
   }
 }
 
-// Workgroup (i, y): keys [y * kTableKeys, (y + 1) * kTableKeys) of sequence
-// i -- its block-table entries written, every slot checked.
+// Every key of the axis against the closed form: key k of sequence i (found
+// by binary search of the sequences' first keys, staged in LDS when they fit)
+// at position p = k - k_off_i must hold bt_i[p / bs] * bs + p % bs, where
+// bt_i[j] = gather_slots[k_off_i + j * bs] / bs is a block id in the pool.
+// ORs 1 into info[0] on any violation. The sequence count comes from info[1].
+constexpr int kCheckStage = 4096;
+__global__ __launch_bounds__(kScanThreads) void varlen_check_kernel(const int64_t* gs, int64_t gs_k,
+                                                                   const int32_t* seq_lo, int K, int bs,
+                                                                   int64_t num_blocks, int32_t* info) {
+  __shared__ int s_lo[kCheckStage];
+  __shared__ int s_bad;
+  const int tid = threadIdx.x;
+  const int nseq = info[1];
+  if (info[0] != 0 || nseq <= 0) return;  // uniform: the scan already failed
+  const bool staged = nseq <= kCheckStage;
+  if (tid == 0) s_bad = 0;
+  if (staged)
+    for (int i = tid; i < nseq; i += kScanThreads) s_lo[i] = seq_lo[i];
+  __syncthreads();
+  const int k = blockIdx.x * kScanThreads + tid;
+  if (k < K) {
+    int lo = 0, hi = nseq - 1;  // the last sequence whose first key is <= k
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if ((staged ? s_lo[mid] : seq_lo[mid]) <= k) lo = mid;
+      else hi = mid - 1;
+    }
+    const int64_t off = staged ? s_lo[lo] : seq_lo[lo];
+    const int p = (int)(k - off);
+    const int64_t head = gs[(off + (int64_t)(p / bs) * bs) * gs_k];
+    const int64_t id = head / bs;
+    if (p < 0 || head < 0 || head % bs != 0 || id >= num_blocks || gs[(int64_t)k * gs_k] != id * bs + p % bs)
+      s_bad = 1;
+  }
+  __syncthreads();
+  if (tid == 0 && s_bad) atomicOr(&info[0], 1);
+}
+
+// Workgroup (i, y): entries of sequence i's table whose first key lies in
+// keys [y * kTableKeys, (y + 1) * kTableKeys).
 constexpr int kTableKeys = 2048;
 __global__ __launch_bounds__(kScanThreads) void varlen_tables_kernel(const int64_t* gs, int64_t gs_k,
                                                                     const int32_t* seq_lo, const int32_t* cu,
-                                                                    const int32_t* q_start, int bs,
-                                                                    int64_t num_blocks, int32_t* bt,
-                                                                    int64_t bt_stride, int width, int32_t* info) {
-  __shared__ int s_bad;
+                                                                    const int32_t* q_start, int bs, int32_t* bt,
+                                                                    int64_t bt_stride, int width) {
   const int i = blockIdx.x, tid = threadIdx.x;
-  if (tid == 0) s_bad = 0;
-  __syncthreads();
   const int64_t lo = seq_lo[i];
   const int t_len = q_start[i] + (cu[i + 1] - cu[i]);
-  if ((t_len + bs - 1) / bs > width) s_bad = 1;
-  const int t0 = blockIdx.y * kTableKeys, t1 = min(t0 + kTableKeys, t_len);
-  for (int t = t0 + tid; t < t1; t += kScanThreads) {
-    const int64_t head = gs[(lo + (int64_t)(t / bs) * bs) * gs_k];
-    const int64_t id = head / bs;
-    if (head < 0 || head % bs != 0 || id >= num_blocks || gs[(lo + t) * gs_k] != id * bs + t % bs) s_bad = 1;
-  }
-  // entry j belongs to the slice holding its first key, j * bs
+  const int t0 = blockIdx.y * kTableKeys;
   const int j0 = (t0 + bs - 1) / bs, j1 = min((t0 + kTableKeys + bs - 1) / bs, width);
   for (int j = j0 + tid; j < j1; j += kScanThreads) {
     const int p = j * bs;
     bt[(int64_t)i * bt_stride + j] = p < t_len ? (int32_t)(gs[(lo + p) * gs_k] / bs) : 0;
   }
-  __syncthreads();
-  if (tid == 0 && s_bad) atomicOr(&info[0], 1);
 }
 
 }  // namespace
@@ -272,45 +459,81 @@ __global__ __launch_bounds__(kScanThreads) void varlen_tables_kernel(const int64
 using namespace ir;
 
 extern "C" int ir_varlen_form_scan(const void* mask, int64_t mask_q_stride, int64_t mask_k_stride, int mask_dtype,
-                                   int num_q, int num_k, int block_size, int32_t* row_ranges, int32_t* cu_seqlens_q,
+                                   int num_q, int num_k, const int64_t* gather_slots, int64_t gs_k_stride,
+                                   int block_size, int64_t num_blocks, int32_t* row_records, int32_t* cu_seqlens_q,
                                    int32_t* q_start, int32_t* seq_k_offsets, int32_t* info, ir_stream_t stream) {
   IR_REQUIRE(dtype_bytes(mask_dtype) > 0, "ir_varlen_form_scan: unknown mask dtype %d", mask_dtype);
-  IR_REQUIRE(num_q >= 0 && num_k >= 0 && block_size > 0, "ir_varlen_form_scan: bad sizes");
+  IR_REQUIRE(num_q >= 0 && num_k >= 0 && block_size > 0 && num_blocks >= 0, "ir_varlen_form_scan: bad sizes");
   if (num_q == 0) return ok();
-  IR_REQUIRE(mask && row_ranges && cu_seqlens_q && q_start && seq_k_offsets && info,
+  IR_REQUIRE(mask && gather_slots && row_records && cu_seqlens_q && q_start && seq_k_offsets && info,
              "ir_varlen_form_scan: null pointer");
+  IR_REQUIRE(((uintptr_t)row_records & 15) == 0, "ir_varlen_form_scan: row_records must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
-  // contiguous rows from a 16-byte-aligned start: read as 16-byte pieces
-  const bool flat = mask_k_stride == 1 && mask_q_stride == num_k && ((uintptr_t)mask & 15) == 0;
-  if (mask_dtype == IR_DTYPE_F32)
-    hipLaunchKernelGGL(varlen_rows_kernel<IR_DTYPE_F32>, dim3(num_q), dim3(kRowThreads), 0, s, mask, mask_q_stride,
-                       mask_k_stride, num_q, num_k, flat, row_ranges);
-  else if (mask_dtype == IR_DTYPE_BF16)
-    hipLaunchKernelGGL(varlen_rows_kernel<IR_DTYPE_BF16>, dim3(num_q), dim3(kRowThreads), 0, s, mask, mask_q_stride,
-                       mask_k_stride, num_q, num_k, flat, row_ranges);
-  else
-    hipLaunchKernelGGL(varlen_rows_kernel<IR_DTYPE_F16>, dim3(num_q), dim3(kRowThreads), 0, s, mask, mask_q_stride,
-                       mask_k_stride, num_q, num_k, flat, row_ranges);
-  hipLaunchKernelGGL(varlen_segments_kernel, dim3(1), dim3(kSegThreads), 0, s, row_ranges, num_q, num_k, block_size,
+  RowRec* rec = (RowRec*)row_records;
+  const int per = 16 / dtype_bytes(mask_dtype);
+  // contiguous rows from a 16-byte-aligned start: the flat array as 16-byte pieces
+  const bool flat = num_k > 0 && mask_k_stride == 1 && mask_q_stride == num_k && ((uintptr_t)mask & 15) == 0;
+  if (flat) {
+    const int64_t elems = (int64_t)num_q * num_k, whole = elems / per;
+    if (whole > 0) {
+      const int64_t spans = (whole + 64 * kFlatPieces - 1) / (64 * kFlatPieces);
+      const int64_t waves = std::min<int64_t>(spans, (int64_t)device_cus() * 32);
+      const dim3 grid((unsigned)((waves + kFlatThreads / 64 - 1) / (kFlatThreads / 64)));
+      const bool narrow = elems + 64 * kFlatPieces * per < ((int64_t)1 << 31);
+      const u32x4* pc = (const u32x4*)mask;
+      if (mask_dtype == IR_DTYPE_F32) {
+        if (narrow)
+          hipLaunchKernelGGL((varlen_flat_kernel<IR_DTYPE_F32, true>), grid, dim3(kFlatThreads), 0, s, pc, whole,
+                             num_k, rec);
+        else
+          hipLaunchKernelGGL((varlen_flat_kernel<IR_DTYPE_F32, false>), grid, dim3(kFlatThreads), 0, s, pc, whole,
+                             num_k, rec);
+      } else if (mask_dtype == IR_DTYPE_BF16) {
+        if (narrow)
+          hipLaunchKernelGGL((varlen_flat_kernel<IR_DTYPE_BF16, true>), grid, dim3(kFlatThreads), 0, s, pc, whole,
+                             num_k, rec);
+        else
+          hipLaunchKernelGGL((varlen_flat_kernel<IR_DTYPE_BF16, false>), grid, dim3(kFlatThreads), 0, s, pc, whole,
+                             num_k, rec);
+      } else {
+        if (narrow)
+          hipLaunchKernelGGL((varlen_flat_kernel<IR_DTYPE_F16, true>), grid, dim3(kFlatThreads), 0, s, pc, whole,
+                             num_k, rec);
+        else
+          hipLaunchKernelGGL((varlen_flat_kernel<IR_DTYPE_F16, false>), grid, dim3(kFlatThreads), 0, s, pc, whole,
+                             num_k, rec);
+      }
+    }
+    if (whole * per < elems)
+      hipLaunchKernelGGL(varlen_tail_kernel, dim3(1), dim3(64), 0, s, mask, mask_dtype, whole * per, elems, num_k,
+                         rec);
+  } else {
+    hipLaunchKernelGGL(varlen_rows_strided_kernel, dim3(num_q), dim3(kScanThreads), 0, s, mask, mask_dtype,
+                       mask_q_stride, mask_k_stride, num_k, rec);
+  }
+  hipLaunchKernelGGL(varlen_segments_kernel, dim3(1), dim3(kSegThreads), 0, s, rec, num_q, num_k, block_size,
                      cu_seqlens_q, q_start, seq_k_offsets, info);
+  if (num_k > 0)
+    hipLaunchKernelGGL(varlen_check_kernel, dim3((unsigned)((num_k + kScanThreads - 1) / kScanThreads)),
+                       dim3(kScanThreads), 0, s, gather_slots, gs_k_stride, seq_k_offsets, num_k, block_size,
+                       num_blocks, info);
   return check_launch("ir_varlen_form_scan");
 }
 
 extern "C" int ir_varlen_form_tables(const int64_t* gather_slots, int64_t gs_k_stride, const int32_t* seq_k_offsets,
                                      const int32_t* cu_seqlens_q, const int32_t* q_start, int num_seqs,
-                                     int block_size, int64_t num_blocks, int32_t* block_tables, int64_t bt_stride,
-                                     int max_blocks_per_seq, int32_t* info, ir_stream_t stream) {
-  IR_REQUIRE(num_seqs >= 0 && block_size > 0 && num_blocks >= 0 && max_blocks_per_seq >= 1 &&
-                 bt_stride >= max_blocks_per_seq,
+                                     int block_size, int32_t* block_tables, int64_t bt_stride,
+                                     int max_blocks_per_seq, ir_stream_t stream) {
+  IR_REQUIRE(num_seqs >= 0 && block_size > 0 && max_blocks_per_seq >= 1 && bt_stride >= max_blocks_per_seq,
              "ir_varlen_form_tables: bad sizes");
   if (num_seqs == 0) return ok();
-  IR_REQUIRE(gather_slots && seq_k_offsets && cu_seqlens_q && q_start && block_tables && info,
+  IR_REQUIRE(gather_slots && seq_k_offsets && cu_seqlens_q && q_start && block_tables,
              "ir_varlen_form_tables: null pointer");
   const int64_t slices = ((int64_t)max_blocks_per_seq * block_size + kTableKeys - 1) / kTableKeys;
   IR_REQUIRE(slices <= 65535, "ir_varlen_form_tables: %d blocks of %d keys per sequence is too many",
              max_blocks_per_seq, block_size);
   hipLaunchKernelGGL(varlen_tables_kernel, dim3(num_seqs, (unsigned)slices), dim3(kScanThreads), 0,
                      (hipStream_t)stream, gather_slots, gs_k_stride, seq_k_offsets, cu_seqlens_q, q_start,
-                     block_size, num_blocks, block_tables, bt_stride, max_blocks_per_seq, info);
+                     block_size, block_tables, bt_stride, max_blocks_per_seq);
   return check_launch("ir_varlen_form_tables");
 }

@@ -657,14 +657,21 @@ class VarlenForm:
     row_split: object | None = None
 
 
-def varlen_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int, num_blocks: int
-                ) -> VarlenForm | None:
+def varlen_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int, num_blocks: int,
+                records: torch.Tensor | None = None, staging: torch.Tensor | None = None) -> VarlenForm | None:
     """Prefill metadata from the reference's packed prefill / mixed-step frame
     (``gather_slots`` ``[1, K]`` int64, mask ``[1, 1, Q, K]``), or ``None``
     unless it has that form exactly (``ir_varlen_form_scan`` /
-    ``ir_varlen_form_tables``). Synchronises twice: the sequence count sizes the
-    block tables, and the second pass's verdict decides (read together with
-    the derived chunk sizes and prefixes, host copies for the caller)."""
+    ``ir_varlen_form_tables``). Synchronises once: the verdict (mask and every
+    slot checked on the device), the sizes and the derived chunk sizes and
+    prefixes (host copies for the caller) are read together; the block tables
+    are then written without a further read.
+
+    ``records``: int32 scratch of at least ``4 * Q`` elements, zero at rest
+    (every call leaves it zero), 16-byte aligned; allocated zeroed when not
+    given. ``staging``: a pinned host int32 tensor the read lands in (at
+    least :func:`varlen_staging_size` ``(Q)`` elements); a pageable copy
+    otherwise."""
     dev = require_device(gather_slots, mask)
     if gather_slots.dtype != torch.int64 or gather_slots.dim() != 2 or gather_slots.shape[0] != 1:
         raise RuntimeError("varlen_form: gather_slots must be int64 [1, K]")
@@ -675,35 +682,52 @@ def varlen_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int,
     if q == 0 or k == 0 or q >= 2**31 or k >= 2**31:
         return None
     i32 = dict(dtype=torch.int32, device=dev)
-    # one allocation for the scan's outputs (info is written whole by the scan)
-    a = lambda n: (n + 63) // 64 * 64  # noqa: E731 -- 256-byte regions
-    buf = torch.empty(a(q + 1) + 2 * a(q) + 64 + 2 * q, **i32)
-    cu = buf[: q + 1]
-    q_start = buf[a(q + 1) : a(q + 1) + q]
-    k_off = buf[a(q + 1) + a(q) : a(q + 1) + a(q) + q]
-    info = buf[a(q + 1) + 2 * a(q) : a(q + 1) + 2 * a(q) + 4]
-    ranges = buf[a(q + 1) + 2 * a(q) + 64 :]
+    if records is None:
+        records = torch.zeros(4 * q, **i32)
+    if records.dtype != torch.int32 or records.numel() < 4 * q or records.data_ptr() % 16:
+        raise RuntimeError(f"varlen_form: records must be int32 [>= {4 * q}], 16-byte aligned, zero at rest")
+    # one allocation: info | cu | q_start (read back together) | k_off
+    o_cu, o_qs, o_ko = _varlen_offsets(q)
+    buf = torch.empty(o_ko + q, **i32)
+    info, cu, q_start, k_off = buf[:4], buf[o_cu : o_cu + q + 1], buf[o_qs : o_qs + q], buf[o_ko : o_ko + q]
     rc = lib().ir_varlen_form_scan(
-        ptr(mask), mask.stride(2), mask.stride(3), dtype_code(mask.dtype), q, k, block_size, ptr(ranges), ptr(cu),
-        ptr(q_start), ptr(k_off), ptr(info), stream_ptr(dev),
+        ptr(mask), mask.stride(2), mask.stride(3), dtype_code(mask.dtype), q, k, ptr(gather_slots),
+        gather_slots.stride(1), block_size, num_blocks, ptr(records), ptr(cu), ptr(q_start), ptr(k_off), ptr(info),
+        stream_ptr(dev),
     )
     check(rc, "ir_varlen_form_scan")
-    bad, nseq, max_q, width = info.tolist()
+    n = o_ko  # the verdict, the sizes and the split, one read
+    if staging is not None and staging.is_pinned() and staging.dtype == torch.int32 and staging.numel() >= n:
+        host = staging[:n]
+        host.copy_(buf[:n], non_blocking=True)
+        torch.cuda.current_stream(dev).synchronize()
+    else:
+        host = buf[:n].cpu()
+    bad, nseq, max_q, width = host[:4].tolist()
     if bad or nseq <= 0:
         return None
+    offs, prefixes = host[o_cu : o_cu + nseq + 1].tolist(), host[o_qs : o_qs + nseq].tolist()
     width = max(width, 1)
     bt = torch.empty(nseq, width, **i32)
     rc = lib().ir_varlen_form_tables(
-        ptr(gather_slots), gather_slots.stride(1), ptr(k_off), ptr(cu), ptr(q_start), nseq, block_size, num_blocks,
-        ptr(bt), bt.stride(0), width, ptr(info), stream_ptr(dev),
+        ptr(gather_slots), gather_slots.stride(1), ptr(k_off), ptr(cu), ptr(q_start), nseq, block_size, ptr(bt),
+        bt.stride(0), width, stream_ptr(dev),
     )
     check(rc, "ir_varlen_form_tables")
-    host = torch.cat([info[:1], cu[: nseq + 1], q_start[:nseq]]).tolist()  # the verdict and the split, one read
-    if host[0]:
-        return None
-    offs, prefixes = host[1 : nseq + 2], host[nseq + 2 :]
-    q_lens = tuple(b - a for a, b in zip(offs, offs[1:]))
+    q_lens = tuple(b - a_ for a_, b in zip(offs, offs[1:]))
     return VarlenForm(bt, cu[: nseq + 1], q_start[:nseq], max_q, q_lens, tuple(prefixes))
+
+
+def _varlen_offsets(q: int) -> tuple[int, int, int]:
+    """Element offsets of cu_seqlens_q, q_start and the key offsets in the
+    check's buffer (info at 0; 256-byte regions)."""
+    a = (q + 1 + 63) // 64 * 64
+    return 64, 64 + a, 64 + a + (q + 63) // 64 * 64
+
+
+def varlen_staging_size(q: int) -> int:
+    """int32 elements of the pinned host buffer :func:`varlen_form` reads into."""
+    return _varlen_offsets(q)[2]
 
 
 def stream_capture_id(device: torch.device | str | int | None = None) -> int:

@@ -117,6 +117,9 @@ class PagedKVPool:
         # id(gather_slots), id(mask)): each holds the buffers its graph's
         # replays address and lives as long as the captured gather_slots
         self._captured_forms: dict[tuple, tuple] = {}
+        # the packed-form check's row records (zero at rest) and pinned read buffer
+        self._varlen_records: torch.Tensor | None = None
+        self._varlen_staging: torch.Tensor | None = None
 
     # --- reference surface ------------------------------------------------
 
@@ -278,7 +281,13 @@ class PagedKVPool:
         if (gather_slots.dim() == 2 and gather_slots.shape[0] == 1 and gather_slots.dtype == torch.int64
                 and gather_slots.is_cuda and mask.is_cuda and mask.dim() == 4 and tuple(mask.shape[:2]) == (1, 1)
                 and mask.shape[3] == gather_slots.shape[1]):
-            form = kernels.varlen_form(gather_slots, mask, self.block_size, self.num_blocks)
+            q = mask.shape[2]
+            if self._varlen_records is None or self._varlen_records.numel() < 4 * q:
+                self._varlen_records = torch.zeros(max(4 * q, 1024), dtype=torch.int32, device=self.device)
+                self._varlen_staging = torch.empty(kernels.varlen_staging_size(max(q, 256)), dtype=torch.int32,
+                                                   pin_memory=True)
+            form = kernels.varlen_form(gather_slots, mask, self.block_size, self.num_blocks,
+                                       records=self._varlen_records, staging=self._varlen_staging)
             if form is not None:
                 # the reference packs decodes first (infrared/engine/scheduler.py:104-115)
                 form.row_split = row_split(form.block_tables, form.prefixes, form.q_lens)

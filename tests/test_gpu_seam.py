@@ -543,7 +543,8 @@ def test_packed_form_check_reads_every_mask_layout(dtype, layout):
     history spans more than one pass of a row's loads. The derived metadata
     matches the frame; a NaN, a masked value above -6e4, a hidden key at the
     array's last element or inside the long history, and a leaked key at a
-    row's first element each reject the frame, while -inf still masks."""
+    row's first element each reject the frame, while -inf still masks; so do a
+    slot off its block's closed form and a block outside the pool."""
     bs, num_cached, q_lens = 16, [0, 13, 26001], [5, 3, 5]
     need = [metadata.blocks_for(c + n, bs) for c, n in zip(num_cached, q_lens)]
     perm = torch.randperm(sum(need) + 7, generator=torch.Generator().manual_seed(5)).tolist()
@@ -596,6 +597,14 @@ def test_packed_form_check_reads_every_mask_layout(dtype, layout):
         assert f.cu_seqlens_q.tolist() == [0, 5, 8, 13] and f.q_start.tolist() == num_cached
         for i, nb in enumerate(need):
             assert f.block_tables[i, :nb].tolist() == tables[i]
+    # slots the device check rejects: one off its block's closed form deep in
+    # sequence 2, and a block head outside the pool
+    off_form = gs.clone()
+    off_form[0, long_key] += 1
+    outside = gs.clone()
+    outside[0, 5 + 16 + 25008 : 5 + 16 + 25024] += (sum(need) + 7) * bs  # one whole block, ids past the pool
+    for bad_gs in (off_form, outside):
+        assert kernels.varlen_form(bad_gs, on_device(base), bs, sum(need) + 7) is None
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
