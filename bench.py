@@ -757,6 +757,33 @@ def _bench_engine(args) -> dict:
     }
 
 
+def _rows_ms(rows: dict, steps: int, per: int, warm: bool = True, prep=None) -> dict:
+    """Median ms per call (a step's time / ``per``) of each row, the rows' steps
+    interleaved (A, B, C, A, B, C, ...), after untimed rounds of at least
+    ``WARM_MS`` of GPU time when ``warm``: the device's clock takes tens of
+    milliseconds of sustained work to settle, so rows timed one after another
+    would favour the later ones. ``prep`` runs before each step, outside the
+    timed region."""
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = {name: [] for name in rows}
+    warm_ms, timed = (0.0 if warm else WARM_MS), 0
+    while timed < steps:
+        for name, fn in rows.items():
+            if prep is not None:
+                prep()
+            torch.cuda.synchronize()
+            s.record()
+            fn()
+            e.record()
+            torch.cuda.synchronize()
+            if warm_ms < WARM_MS:
+                warm_ms += s.elapsed_time(e)
+            else:
+                times[name].append(s.elapsed_time(e) / per)
+        timed = min(len(v) for v in times.values())
+    return {name: statistics.median(v) for name, v in times.items()}
+
+
 def _bench_reference_form_prefill(args) -> dict:
     """Unchanged reference callers at the 8 x 512-token chunked-prefill shape:
     the step's metadata as the reference engine packs it for prefill and mixed
@@ -819,25 +846,15 @@ def _bench_reference_form_prefill(args) -> dict:
         gs, m = fresh.pop()
         pool.reference_varlen_form(gs, m)
 
-    def timed(fn, steps, per_call=True):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        per = []
-        for _ in range(steps):
-            fresh.append((ours.gather_slots.clone(), mask.clone()))
-            torch.cuda.synchronize()
-            s.record()
-            fn()
-            e.record()
-            torch.cuda.synchronize()
-            per.append(s.elapsed_time(e) / (layers if per_call else 1))
-        return statistics.median(per)
+    def prep():
+        fresh.clear()
+        fresh.append((ours.gather_slots.clone(), mask.clone()))
 
-    timed(step_ref, 1)
-    timed(step_ours, 1)
-    ms_ref, ms_ours = timed(step_ref, 5), timed(step_ours, 5)
-    ms_check = timed(check_only, 5, per_call=False)
+    ms = _rows_ms({"ref": step_ref, "ours": step_ours}, 7, layers, prep=prep)
+    ms_ref, ms_ours = ms["ref"], ms["ours"]
+    ms_check = _rows_ms({"check": check_only}, 7, 1, prep=prep)["check"]
     form = pool._ref_varlen[1]
-    ms_masked = timed(step_masked, 1)
+    ms_masked = _rows_ms({"masked": step_masked}, 1, layers, warm=False)["masked"]
     out_ref = paged_attention(q, k, v, RefContext(pool, ours.write_slots, ours.gather_slots), mask, 0, cfg.scale,
                               cfg.n_rep)
     out_ours = paged_attention(q, k, v, PagedContext(pool, ours.write_slots, None, True, ours.block_tables, None,
@@ -905,7 +922,7 @@ def _bench_reference_form(args) -> dict:
     q = torch.randn(b, 1, hq, d, generator=g, device="cuda").to(cfg.dtype)
     k = torch.randn(b, 1, hkv, d, generator=g, device="cuda").to(cfg.dtype)
     v = torch.randn(b, 1, hkv, d, generator=g, device="cuda").to(cfg.dtype)
-    layers, steps = args.layers, 5
+    layers, steps = args.layers, 7
 
     def step_ref():
         # a step's metadata arrives as new tensors, as the reference engine builds them
@@ -923,19 +940,6 @@ def _bench_reference_form(args) -> dict:
         paged = RefContext(pool, ours.write_slots, ours.gather_slots, use_triton=False)
         for _ in range(layers):
             paged_attention(q, k, v, paged, mask, 0, cfg.scale, cfg.n_rep)
-
-    def timed(fn):
-        fn()
-        torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        per = []
-        for _ in range(steps):
-            s.record()
-            fn()
-            e.record()
-            torch.cuda.synchronize()
-            per.append(s.elapsed_time(e) / layers)
-        return statistics.median(per)
 
     # the reference's CudaGraphDecoder (infrared/engine/cuda_graph.py:263-285):
     # static gather_slots / mask, three warm-ups on a side stream, then the
@@ -962,8 +966,8 @@ def _bench_reference_form(args) -> dict:
     def step_graph():
         graph.replay()
 
-    ms_ref, ms_ours, ms_masked = timed(step_ref), timed(step_ours), timed(step_masked)
-    ms_graph = timed(step_graph)
+    ms = _rows_ms({"ref": step_ref, "ours": step_ours, "graph": step_graph, "masked": step_masked}, steps, layers)
+    ms_ref, ms_ours, ms_masked, ms_graph = ms["ref"], ms["ours"], ms["masked"], ms["graph"]
     form = pool._ref_form[1]
     out_ref = paged_attention(q, k, v, RefContext(pool, ours.write_slots, ours.gather_slots), mask, 0, cfg.scale,
                               cfg.n_rep)

@@ -344,19 +344,28 @@ int ir_decode_form(const int64_t* gather_slots, int64_t gs_b_stride, int64_t gs_
  * build_varlen_mask / build_attention_mask (0 where the key is the query's own
  * sequence at or before its position, finfo.min elsewhere)
  * (infrared/engine/paged_engine.py:194-206, :461-516;
- * infrared/model/inputs.py:33-85). Two calls, the host reading info once,
- * between them (it sizes block_tables):
+ * infrared/model/inputs.py:33-85). One call before the host's one read
+ * (ir_varlen_form_tables only when the tables did not fit):
  *   ir_varlen_form_scan: reads every mask element once (element (r, k) at
  *     mask + r*mask_q_stride + k*mask_k_stride; a contiguous 16-byte-aligned
  *     mask as one flat array) and every key's slot; writes cu_seqlens_q
  *     [num_q + 1], q_start [num_q] and seq_k_offsets [num_q] for the sequences
- *     found, and info[0..3] (no clearing needed): info[1..3] = sequence count,
+ *     found, and info[0..5] (no clearing needed): info[1..3] = sequence count,
  *     longest chunk, widest block table (blocks); info[0] = 0 if each row's
  *     visible keys are one contiguous range, every other value <= -6e4, the
  *     rows of a sequence each see one key more than the last, the sequences'
  *     key ranges tile [0, num_k) in order, and every slot
  *     gather_slots[k_off_i + p] (stride gs_k_stride) has the closed form with a
- *     block id in [0, num_blocks); else 1. row_records: [4*num_q] int32
+ *     block id in [0, num_blocks); else 1. info[5] is working space. info[4]
+ *     = 1 when the call also wrote the block tables: block_tables (null or
+ *     int32 [tables_capacity]) holds them as [info[1], W] with
+ *     W = max(info[3], 1) when info[0] is clear and info[1] * W <=
+ *     tables_capacity. host_record (null, or pinned host memory
+ *     from the HIP host allocator, at least 2*num_q + 9 int32) receives, from
+ *     the device at the end of the call, info[0..4] at [0..4], then
+ *     cu_seqlens_q[0..n] at [8..8+n] and q_start[0..n) at [9+n..9+2n)
+ *     (n = info[1]; written only when info[0] is clear): after a stream
+ *     synchronisation the host reads it in place. row_records: [4*num_q] int32
  *     scratch, 16-byte aligned, zero before the first call; every call leaves
  *     it zero (calls sharing it must be stream-ordered).
  *   ir_varlen_form_tables: block_tables[i, j] = gather_slots[k_off_i + j*bs] / bs
@@ -367,7 +376,8 @@ int ir_decode_form(const int64_t* gather_slots, int64_t gs_b_stride, int64_t gs_
 int ir_varlen_form_scan(const void* mask, int64_t mask_q_stride, int64_t mask_k_stride, int mask_dtype,
                         int num_q, int num_k, const int64_t* gather_slots, int64_t gs_k_stride, int block_size,
                         int64_t num_blocks, int32_t* row_records, int32_t* cu_seqlens_q, int32_t* q_start,
-                        int32_t* seq_k_offsets, int32_t* info, ir_stream_t stream);
+                        int32_t* seq_k_offsets, int32_t* info, int32_t* block_tables, int64_t tables_capacity,
+                        int32_t* host_record, int64_t host_capacity, ir_stream_t stream);
 int ir_varlen_form_tables(const int64_t* gather_slots, int64_t gs_k_stride, const int32_t* seq_k_offsets,
                           const int32_t* cu_seqlens_q, const int32_t* q_start, int num_seqs, int block_size,
                           int32_t* block_tables, int64_t bt_stride, int max_blocks_per_seq, ir_stream_t stream);

@@ -103,7 +103,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ir_varlen_form_scan": (
         _c_i32,
         [_c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i32, _c_i64, _c_p, _c_p, _c_p, _c_p,
-         _c_p, _c_p],
+         _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p],
     ),
     "ir_varlen_form_tables": (
         _c_i32,

@@ -19,10 +19,13 @@
 // verifies every slot of every sequence against the closed form and the pool,
 // on the device, before the host reads anything. Any violation sets
 // info[0]; the host then keeps the mask kernel, which reads the metadata as
-// given. With info[0] clear the host sizes the block tables from info and
-// ir_varlen_form_tables writes bt_i[j] = gather_slots[k_off_i + j bs] / bs; the
-// chunked-prefill kernel over them attends exactly the keys the mask allows.
-// One synchronising read per step: info, cu_seqlens_q and q_start together.
+// given. With info[0] clear, the same call writes the block tables
+// bt_i[j] = gather_slots[k_off_i + j bs] / bs into a buffer of the caller's
+// (stride: the widest table, read on the device) when they fit, and copies
+// the verdict, the sizes, cu_seqlens_q and q_start into pinned host memory
+// from the device; the chunked-prefill kernel over the tables attends exactly
+// the keys the mask allows. One synchronising read per step, no copy launched
+// and no launch after it (ir_varlen_form_tables writes tables that did not fit).
 #include <algorithm>
 
 #include "common.hpp"
@@ -74,6 +77,24 @@ struct RowRec {
 };
 constexpr int kFirstBias = 0x7fffffff;
 
+// Wavefront reduction with no LDS round trip: DPP permutations inside each
+// 16-lane row (lane ^ 1, lane ^ 2, then each 8-lane half mirrored, then the
+// row mirrored), then gfx950's row swaps (rows 0<->1 and 2<->3, then the two
+// 32-lane halves; both outputs of a swap are combined, so which carries which
+// does not matter for a symmetric op). Every lane ends with the result; all
+// 64 lanes must be active.
+template <typename Op>
+__device__ __forceinline__ int wave_fold(int x, Op op) {
+  x = op(x, __builtin_amdgcn_update_dpp(0, x, 0xb1, 0xf, 0xf, false));   // quad_perm [1, 0, 3, 2]
+  x = op(x, __builtin_amdgcn_update_dpp(0, x, 0x4e, 0xf, 0xf, false));   // quad_perm [2, 3, 0, 1]
+  x = op(x, __builtin_amdgcn_update_dpp(0, x, 0x141, 0xf, 0xf, false));  // row_half_mirror
+  x = op(x, __builtin_amdgcn_update_dpp(0, x, 0x140, 0xf, 0xf, false));  // row_mirror
+  const auto b = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+  x = op((int)b[0], (int)b[1]);
+  const auto a = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+  return op((int)a[0], (int)a[1]);
+}
+
 // A row's share of a run of visible keys [k_lo, k_hi] (count keys) and of
 // wrong values, added to its record.
 __device__ __forceinline__ void rec_add(RowRec* rec, int r, int k_lo, int k_hi, int count, int wrong) {
@@ -83,6 +104,16 @@ __device__ __forceinline__ void rec_add(RowRec* rec, int r, int k_lo, int k_hi, 
     atomicAdd(&rec[r].count, count);
   }
   if (wrong) atomicOr(&rec[r].wrong, 1);
+}
+
+// One row's part of a wavefront's pieces, folded over the wavefront and added
+// to the row's record by lane 0.
+__device__ __forceinline__ void wave_rec_add(RowRec* rec, int r, int f, int l, int n, int wr) {
+  f = wave_fold(f, [](int a, int b) { return min(a, b); });
+  l = wave_fold(l, [](int a, int b) { return max(a, b); });
+  n = wave_fold(n, [](int a, int b) { return a + b; });
+  const int any_wrong = __ballot(wr != 0) != 0ull;
+  if ((threadIdx.x & 63) == 0) rec_add(rec, r, f, l, n, any_wrong);
 }
 
 // Contiguous masks: the flat [Q * K] array as 16-byte pieces, grid-stride.
@@ -161,20 +192,8 @@ __global__ __launch_bounds__(kFlatThreads) void varlen_flat_kernel(const u32x4* 
         wr[0] |= (bad & in_a) != 0u;
         wr[1] |= (bad & ~in_a) != 0u;
       }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-#pragma unroll
-        for (int sl = 0; sl < 2; ++sl) {
-          f[sl] = min(f[sl], __shfl_xor(f[sl], o));
-          l[sl] = max(l[sl], __shfl_xor(l[sl], o));
-          n[sl] += __shfl_xor(n[sl], o);
-          wr[sl] |= __shfl_xor(wr[sl], o);
-        }
-      }
-      if (lane < 2 && r0 + lane <= r1) {
-        const bool one = lane == 1;  // lane 0 updates row r0, lane 1 row r0 + 1
-        rec_add(rec, r0 + lane, one ? f[1] : f[0], one ? l[1] : l[0], one ? n[1] : n[0], one ? wr[1] : wr[0]);
-      }
+      wave_rec_add(rec, r0, f[0], l[0], n[0], wr[0]);
+      if (r1 > r0) wave_rec_add(rec, r1, f[1], l[1], n[1], wr[1]);  // uniform
       continue;
     }
     // rows shorter than a span: each load instruction's 64 pieces on their own
@@ -231,20 +250,8 @@ __global__ __launch_bounds__(kFlatThreads) void varlen_flat_kernel(const u32x4* 
         }
         wr[1] |= wb;
       }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-#pragma unroll
-        for (int sl = 0; sl < 2; ++sl) {
-          f[sl] = min(f[sl], __shfl_xor(f[sl], o));
-          l[sl] = max(l[sl], __shfl_xor(l[sl], o));
-          n[sl] += __shfl_xor(n[sl], o);
-          wr[sl] |= __shfl_xor(wr[sl], o);
-        }
-      }
-      if (lane < 2 && r0 + lane <= r_end) {
-        const bool one = lane == 1;  // lane 0 updates row r0, lane 1 row r0 + 1
-        rec_add(rec, r0 + lane, one ? f[1] : f[0], one ? l[1] : l[0], one ? n[1] : n[0], one ? wr[1] : wr[0]);
-      }
+      wave_rec_add(rec, r0, f[0], l[0], n[0], wr[0]);
+      if (r_end > r0) wave_rec_add(rec, r0 + 1, f[1], l[1], n[1], wr[1]);  // uniform
     }
   }
 }
@@ -394,6 +401,7 @@ __global__ __launch_bounds__(kSegThreads) void varlen_segments_kernel(RowRec* re
     info[1] = nseq;
     info[2] = s_maxq;
     info[3] = s_maxb;
+    info[5] = 0;  // the check's workgroup ticket
   }
 }
 
@@ -402,37 +410,79 @@ __global__ __launch_bounds__(kSegThreads) void varlen_segments_kernel(RowRec* re
 // at position p = k - k_off_i must hold bt_i[p / bs] * bs + p % bs, where
 // bt_i[j] = gather_slots[k_off_i + j * bs] / bs is a block id in the pool.
 // ORs 1 into info[0] on any violation. The sequence count comes from info[1].
+// The same grid writes the block tables, entry e = i * W + j of [info[1], W]
+// (W = max(info[3], 1); zero past the sequence's keys), when they fit in
+// `cap`. The last workgroup to finish (a ticket in info[5], which the
+// segmentation zeroes) publishes info[4] (tables written) and, into the host
+// record, the verdict, the sizes, cu_seqlens_q and q_start, then fences at
+// system scope.
 constexpr int kCheckStage = 4096;
 __global__ __launch_bounds__(kScanThreads) void varlen_check_kernel(const int64_t* gs, int64_t gs_k,
-                                                                   const int32_t* seq_lo, int K, int bs,
-                                                                   int64_t num_blocks, int32_t* info) {
+                                                                   const int32_t* seq_lo, const int32_t* cu,
+                                                                   const int32_t* q_start, int K, int bs,
+                                                                   int64_t num_blocks, int32_t* info, int32_t* bt,
+                                                                   int cap, int32_t* host) {
   __shared__ int s_lo[kCheckStage];
-  __shared__ int s_bad;
+  __shared__ int s_bad, s_last;
   const int tid = threadIdx.x;
-  const int nseq = info[1];
-  if (info[0] != 0 || nseq <= 0) return;  // uniform: the scan already failed
+  const int nseq = info[1], maxq = info[2], width = info[3];
+  const bool go = info[0] == 0 && nseq > 0;  // uniform: otherwise the scan already failed
+  const int w = max(width, 1);
+  const bool fits = go && bt != nullptr && (int64_t)nseq * w <= cap;
   const bool staged = nseq <= kCheckStage;
   if (tid == 0) s_bad = 0;
-  if (staged)
+  if (go && staged)
     for (int i = tid; i < nseq; i += kScanThreads) s_lo[i] = seq_lo[i];
   __syncthreads();
-  const int k = blockIdx.x * kScanThreads + tid;
-  if (k < K) {
-    int lo = 0, hi = nseq - 1;  // the last sequence whose first key is <= k
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if ((staged ? s_lo[mid] : seq_lo[mid]) <= k) lo = mid;
-      else hi = mid - 1;
+  if (go) {
+    const int k = blockIdx.x * kScanThreads + tid;
+    if (k < K) {
+      int lo = 0, hi = nseq - 1;  // the last sequence whose first key is <= k
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if ((staged ? s_lo[mid] : seq_lo[mid]) <= k) lo = mid;
+        else hi = mid - 1;
+      }
+      const int64_t off = staged ? s_lo[lo] : seq_lo[lo];
+      const int p = (int)(k - off);
+      const int64_t head = gs[(off + (int64_t)(p / bs) * bs) * gs_k];
+      const int64_t id = head / bs;
+      if (p < 0 || head < 0 || head % bs != 0 || id >= num_blocks || gs[(int64_t)k * gs_k] != id * bs + p % bs)
+        s_bad = 1;
     }
-    const int64_t off = staged ? s_lo[lo] : seq_lo[lo];
-    const int p = (int)(k - off);
-    const int64_t head = gs[(off + (int64_t)(p / bs) * bs) * gs_k];
-    const int64_t id = head / bs;
-    if (p < 0 || head < 0 || head % bs != 0 || id >= num_blocks || gs[(int64_t)k * gs_k] != id * bs + p % bs)
-      s_bad = 1;
+    if (fits) {
+      // the segmentation found the sequences' key ranges tiling [0, K): sequence
+      // i's keys are [k_off_i, k_off_{i+1}), the last one's end at K
+      const unsigned n = (unsigned)(nseq * w);
+      for (unsigned e = blockIdx.x * kScanThreads + tid; e < n; e += gridDim.x * kScanThreads) {
+        const int i = (int)(e / (unsigned)w), j = (int)(e - (unsigned)i * w);
+        const int lo = staged ? s_lo[i] : seq_lo[i];
+        const int end = i + 1 < nseq ? (staged ? s_lo[i + 1] : seq_lo[i + 1]) : K;
+        const int p = j * bs;
+        bt[e] = p < end - lo ? (int32_t)(gs[(int64_t)(lo + p) * gs_k] / bs) : 0;
+      }
+    }
   }
   __syncthreads();
-  if (tid == 0 && s_bad) atomicOr(&info[0], 1);
+  if (tid == 0) {
+    if (s_bad) atomicOr(&info[0], 1);
+    __threadfence();
+    s_last = atomicAdd(&info[5], 1) == (int)gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  const int bad = atomicOr(&info[0], 0);  // every workgroup's verdict is in
+  const bool ok = bad == 0 && nseq > 0;
+  if (tid == 0) info[4] = ok && fits;
+  if (host == nullptr) return;
+  if (tid < 8)
+    host[tid] = tid == 0 ? bad : tid == 1 ? nseq : tid == 2 ? maxq : tid == 3 ? width : tid == 4 ? (int)(ok && fits) : 0;
+  if (ok) {
+    for (int i = tid; i <= nseq; i += kScanThreads) host[8 + i] = cu[i];
+    for (int i = tid; i < nseq; i += kScanThreads) host[9 + nseq + i] = q_start[i];
+  }
+  __threadfence_system();
 }
 
 // Workgroup (i, y): entries of sequence i's table whose first key lies in
@@ -453,6 +503,25 @@ __global__ __launch_bounds__(kScanThreads) void varlen_tables_kernel(const int64
   }
 }
 
+// The flat scan with no more workgroups than stay resident on the device at
+// once (occupancy queried once per instance): its grid-stride loop then never
+// waits for a second round of workgroups to start after the first.
+template <int DT, bool NARROW>
+void launch_flat(const u32x4* pc, int64_t whole, int K, RowRec* rec, hipStream_t s) {
+  static const int per_cu = [] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&varlen_flat_kernel<DT, NARROW>),
+                                                     kFlatThreads, 0) != hipSuccess || n < 1)
+      n = 1;
+    return n;
+  }();
+  constexpr int kWaves = kFlatThreads / 64;
+  const int64_t spans = (whole + 64 * kFlatPieces - 1) / (64 * kFlatPieces);
+  const int64_t wgs = std::min<int64_t>((spans + kWaves - 1) / kWaves, (int64_t)device_cus() * per_cu);
+  hipLaunchKernelGGL((varlen_flat_kernel<DT, NARROW>), dim3((unsigned)wgs), dim3(kFlatThreads), 0, s, pc, whole, K,
+                     rec);
+}
+
 }  // namespace
 }  // namespace ir
 
@@ -461,13 +530,25 @@ using namespace ir;
 extern "C" int ir_varlen_form_scan(const void* mask, int64_t mask_q_stride, int64_t mask_k_stride, int mask_dtype,
                                    int num_q, int num_k, const int64_t* gather_slots, int64_t gs_k_stride,
                                    int block_size, int64_t num_blocks, int32_t* row_records, int32_t* cu_seqlens_q,
-                                   int32_t* q_start, int32_t* seq_k_offsets, int32_t* info, ir_stream_t stream) {
+                                   int32_t* q_start, int32_t* seq_k_offsets, int32_t* info, int32_t* block_tables,
+                                   int64_t tables_capacity, int32_t* host_record, int64_t host_capacity,
+                                   ir_stream_t stream) {
   IR_REQUIRE(dtype_bytes(mask_dtype) > 0, "ir_varlen_form_scan: unknown mask dtype %d", mask_dtype);
-  IR_REQUIRE(num_q >= 0 && num_k >= 0 && block_size > 0 && num_blocks >= 0, "ir_varlen_form_scan: bad sizes");
+  IR_REQUIRE(num_q >= 0 && num_k >= 0 && block_size > 0 && num_blocks >= 0 && tables_capacity >= 0,
+             "ir_varlen_form_scan: bad sizes");
   if (num_q == 0) return ok();
   IR_REQUIRE(mask && gather_slots && row_records && cu_seqlens_q && q_start && seq_k_offsets && info,
              "ir_varlen_form_scan: null pointer");
   IR_REQUIRE(((uintptr_t)row_records & 15) == 0, "ir_varlen_form_scan: row_records must be 16-byte aligned");
+  IR_REQUIRE(host_record == nullptr || host_capacity >= 2 * (int64_t)num_q + 9,
+             "ir_varlen_form_scan: host_record holds %lld int32, needs %lld", (long long)host_capacity,
+             2 * (long long)num_q + 9);
+  int32_t* host_dev = nullptr;
+  if (host_record != nullptr) {
+    const hipError_t e = hipHostGetDevicePointer((void**)&host_dev, host_record, 0);
+    if (e != hipSuccess)
+      return fail(IR_EINVAL, "ir_varlen_form_scan: host_record is not pinned host memory: %s", hipGetErrorString(e));
+  }
   hipStream_t s = (hipStream_t)stream;
   RowRec* rec = (RowRec*)row_records;
   const int per = 16 / dtype_bytes(mask_dtype);
@@ -476,32 +557,17 @@ extern "C" int ir_varlen_form_scan(const void* mask, int64_t mask_q_stride, int6
   if (flat) {
     const int64_t elems = (int64_t)num_q * num_k, whole = elems / per;
     if (whole > 0) {
-      const int64_t spans = (whole + 64 * kFlatPieces - 1) / (64 * kFlatPieces);
-      const int64_t waves = std::min<int64_t>(spans, (int64_t)device_cus() * 32);
-      const dim3 grid((unsigned)((waves + kFlatThreads / 64 - 1) / (kFlatThreads / 64)));
       const bool narrow = elems + 64 * kFlatPieces * per < ((int64_t)1 << 31);
       const u32x4* pc = (const u32x4*)mask;
       if (mask_dtype == IR_DTYPE_F32) {
-        if (narrow)
-          hipLaunchKernelGGL((varlen_flat_kernel<IR_DTYPE_F32, true>), grid, dim3(kFlatThreads), 0, s, pc, whole,
-                             num_k, rec);
-        else
-          hipLaunchKernelGGL((varlen_flat_kernel<IR_DTYPE_F32, false>), grid, dim3(kFlatThreads), 0, s, pc, whole,
-                             num_k, rec);
+        if (narrow) launch_flat<IR_DTYPE_F32, true>(pc, whole, num_k, rec, s);
+        else launch_flat<IR_DTYPE_F32, false>(pc, whole, num_k, rec, s);
       } else if (mask_dtype == IR_DTYPE_BF16) {
-        if (narrow)
-          hipLaunchKernelGGL((varlen_flat_kernel<IR_DTYPE_BF16, true>), grid, dim3(kFlatThreads), 0, s, pc, whole,
-                             num_k, rec);
-        else
-          hipLaunchKernelGGL((varlen_flat_kernel<IR_DTYPE_BF16, false>), grid, dim3(kFlatThreads), 0, s, pc, whole,
-                             num_k, rec);
+        if (narrow) launch_flat<IR_DTYPE_BF16, true>(pc, whole, num_k, rec, s);
+        else launch_flat<IR_DTYPE_BF16, false>(pc, whole, num_k, rec, s);
       } else {
-        if (narrow)
-          hipLaunchKernelGGL((varlen_flat_kernel<IR_DTYPE_F16, true>), grid, dim3(kFlatThreads), 0, s, pc, whole,
-                             num_k, rec);
-        else
-          hipLaunchKernelGGL((varlen_flat_kernel<IR_DTYPE_F16, false>), grid, dim3(kFlatThreads), 0, s, pc, whole,
-                             num_k, rec);
+        if (narrow) launch_flat<IR_DTYPE_F16, true>(pc, whole, num_k, rec, s);
+        else launch_flat<IR_DTYPE_F16, false>(pc, whole, num_k, rec, s);
       }
     }
     if (whole * per < elems)
@@ -513,10 +579,10 @@ extern "C" int ir_varlen_form_scan(const void* mask, int64_t mask_q_stride, int6
   }
   hipLaunchKernelGGL(varlen_segments_kernel, dim3(1), dim3(kSegThreads), 0, s, rec, num_q, num_k, block_size,
                      cu_seqlens_q, q_start, seq_k_offsets, info);
-  if (num_k > 0)
-    hipLaunchKernelGGL(varlen_check_kernel, dim3((unsigned)((num_k + kScanThreads - 1) / kScanThreads)),
-                       dim3(kScanThreads), 0, s, gather_slots, gs_k_stride, seq_k_offsets, num_k, block_size,
-                       num_blocks, info);
+  hipLaunchKernelGGL(varlen_check_kernel, dim3((unsigned)std::max((num_k + kScanThreads - 1) / kScanThreads, 1)),
+                     dim3(kScanThreads), 0, s, gather_slots, gs_k_stride, seq_k_offsets, cu_seqlens_q, q_start,
+                     num_k, block_size, num_blocks, info, tables_capacity > 0 ? block_tables : nullptr,
+                     (int)std::min<int64_t>(tables_capacity, INT32_MAX), host_dev);
   return check_launch("ir_varlen_form_scan");
 }
 

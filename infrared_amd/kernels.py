@@ -658,20 +658,26 @@ class VarlenForm:
 
 
 def varlen_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int, num_blocks: int,
-                records: torch.Tensor | None = None, staging: torch.Tensor | None = None) -> VarlenForm | None:
+                records: torch.Tensor | None = None, staging: torch.Tensor | None = None,
+                tables_capacity: int | None = None) -> VarlenForm | None:
     """Prefill metadata from the reference's packed prefill / mixed-step frame
     (``gather_slots`` ``[1, K]`` int64, mask ``[1, 1, Q, K]``), or ``None``
-    unless it has that form exactly (``ir_varlen_form_scan`` /
-    ``ir_varlen_form_tables``). Synchronises once: the verdict (mask and every
-    slot checked on the device), the sizes and the derived chunk sizes and
-    prefixes (host copies for the caller) are read together; the block tables
-    are then written without a further read.
+    unless it has that form exactly (``ir_varlen_form_scan``). Synchronises
+    once: one call checks the mask and every slot on the device, derives the
+    sequences, writes their block tables (stride read on the device) and
+    publishes the verdict, the sizes, the chunk starts and the prefixes into
+    ``staging``; the host reads them there after one stream synchronisation
+    and launches nothing more (``ir_varlen_form_tables`` only for tables
+    beyond the call's table capacity).
 
     ``records``: int32 scratch of at least ``4 * Q`` elements, zero at rest
     (every call leaves it zero), 16-byte aligned; allocated zeroed when not
-    given. ``staging``: a pinned host int32 tensor the read lands in (at
-    least :func:`varlen_staging_size` ``(Q)`` elements); a pageable copy
-    otherwise."""
+    given. ``staging``: a pinned host int32 tensor of at least
+    :func:`varlen_staging_size` ``(Q)`` elements, written by the device;
+    without one the record is copied back from device memory.
+    ``tables_capacity``: block-table entries the call may write (default
+    ``max(2**17, 4 * (K // block_size + Q))``); wider tables are written by a
+    second launch after the read."""
     dev = require_device(gather_slots, mask)
     if gather_slots.dtype != torch.int64 or gather_slots.dim() != 2 or gather_slots.shape[0] != 1:
         raise RuntimeError("varlen_form: gather_slots must be int64 [1, K]")
@@ -686,48 +692,63 @@ def varlen_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int,
         records = torch.zeros(4 * q, **i32)
     if records.dtype != torch.int32 or records.numel() < 4 * q or records.data_ptr() % 16:
         raise RuntimeError(f"varlen_form: records must be int32 [>= {4 * q}], 16-byte aligned, zero at rest")
-    # one allocation: info | cu | q_start (read back together) | k_off
-    o_cu, o_qs, o_ko = _varlen_offsets(q)
-    buf = torch.empty(o_ko + q, **i32)
-    info, cu, q_start, k_off = buf[:4], buf[o_cu : o_cu + q + 1], buf[o_qs : o_qs + q], buf[o_ko : o_ko + q]
+    # one allocation: info | cu | q_start | k_off | block tables (up to `cap`
+    # entries); views are cut after the read, for what the form keeps
+    o_cu, o_qs, o_ko, o_bt = _varlen_offsets(q)
+    cap = max(1 << 17, 4 * (k // block_size + q)) if tables_capacity is None else max(int(tables_capacity), 0)
+    cap = min(cap, 2**31 - 1)
+    buf = torch.empty(o_bt + cap, **i32)
+    base = buf.data_ptr()
+    pinned = (staging is not None and staging.is_pinned() and staging.dtype == torch.int32
+              and staging.is_contiguous() and staging.numel() >= 2 * q + 9)
     rc = lib().ir_varlen_form_scan(
         ptr(mask), mask.stride(2), mask.stride(3), dtype_code(mask.dtype), q, k, ptr(gather_slots),
-        gather_slots.stride(1), block_size, num_blocks, ptr(records), ptr(cu), ptr(q_start), ptr(k_off), ptr(info),
-        stream_ptr(dev),
+        gather_slots.stride(1), block_size, num_blocks, ptr(records), base + 4 * o_cu, base + 4 * o_qs,
+        base + 4 * o_ko, base, base + 4 * o_bt, cap, ptr(staging) if pinned else None,
+        staging.numel() if pinned else 0, stream_ptr(dev),
     )
     check(rc, "ir_varlen_form_scan")
-    n = o_ko  # the verdict, the sizes and the split, one read
-    if staging is not None and staging.is_pinned() and staging.dtype == torch.int32 and staging.numel() >= n:
-        host = staging[:n]
-        host.copy_(buf[:n], non_blocking=True)
+    if pinned:
         torch.cuda.current_stream(dev).synchronize()
+        bad, nseq, max_q, width, written = staging[:5].tolist()
+        if bad or nseq <= 0:
+            return None
+        rec = staging[8 : 9 + 2 * nseq].tolist()
+        offs, prefixes = rec[: nseq + 1], rec[nseq + 1 :]
     else:
-        host = buf[:n].cpu()
-    bad, nseq, max_q, width = host[:4].tolist()
-    if bad or nseq <= 0:
-        return None
-    offs, prefixes = host[o_cu : o_cu + nseq + 1].tolist(), host[o_qs : o_qs + nseq].tolist()
+        host = buf[:o_ko].cpu()
+        bad, nseq, max_q, width, written = host[:5].tolist()
+        if bad or nseq <= 0:
+            return None
+        offs, prefixes = host[o_cu : o_cu + nseq + 1].tolist(), host[o_qs : o_qs + nseq].tolist()
     width = max(width, 1)
-    bt = torch.empty(nseq, width, **i32)
-    rc = lib().ir_varlen_form_tables(
-        ptr(gather_slots), gather_slots.stride(1), ptr(k_off), ptr(cu), ptr(q_start), nseq, block_size, ptr(bt),
-        bt.stride(0), width, stream_ptr(dev),
-    )
-    check(rc, "ir_varlen_form_tables")
+    cu, q_start = buf[o_cu : o_cu + nseq + 1], buf[o_qs : o_qs + nseq]
+    if written:
+        bt = buf[o_bt : o_bt + nseq * width].view(nseq, width)
+    else:
+        bt = torch.empty(nseq, width, **i32)
+        rc = lib().ir_varlen_form_tables(
+            ptr(gather_slots), gather_slots.stride(1), base + 4 * o_ko, ptr(cu), ptr(q_start), nseq, block_size,
+            ptr(bt), bt.stride(0), width, stream_ptr(dev),
+        )
+        check(rc, "ir_varlen_form_tables")
     q_lens = tuple(b - a_ for a_, b in zip(offs, offs[1:]))
-    return VarlenForm(bt, cu[: nseq + 1], q_start[:nseq], max_q, q_lens, tuple(prefixes))
+    return VarlenForm(bt, cu, q_start, max_q, q_lens, tuple(prefixes))
 
 
-def _varlen_offsets(q: int) -> tuple[int, int, int]:
-    """Element offsets of cu_seqlens_q, q_start and the key offsets in the
-    check's buffer (info at 0; 256-byte regions)."""
+def _varlen_offsets(q: int) -> tuple[int, int, int, int]:
+    """Element offsets of cu_seqlens_q, q_start, the key offsets and the block
+    tables in the check's buffer (info at 0; 256-byte regions)."""
     a = (q + 1 + 63) // 64 * 64
-    return 64, 64 + a, 64 + a + (q + 63) // 64 * 64
+    b = (q + 63) // 64 * 64
+    return 64, 64 + a, 64 + a + b, 64 + a + 2 * b
 
 
 def varlen_staging_size(q: int) -> int:
-    """int32 elements of the pinned host buffer :func:`varlen_form` reads into."""
-    return _varlen_offsets(q)[2]
+    """int32 elements of the pinned host record :func:`varlen_form` has the
+    device write (the verdict and sizes, then up to ``q + 1`` chunk starts and
+    ``q`` prefixes)."""
+    return (2 * q + 9 + 63) // 64 * 64
 
 
 def stream_capture_id(device: torch.device | str | int | None = None) -> int:

@@ -263,13 +263,13 @@ class PagedKVPool:
         closed form per sequence and the additive mask of
         ``build_attention_mask`` / ``build_varlen_mask``
         (``infrared/engine/paged_engine.py:194-206, 461-516``,
-        ``infrared/model/inputs.py:33-85``). ``ir_varlen_form_scan`` /
-        ``ir_varlen_form_tables`` recover ``cu_seqlens_q``, ``q_start`` and the
-        block tables on the device and verify the form exactly, so the
-        chunked-prefill kernel computes what the mask kernel would. The check
-        reads the mask once and synchronises twice; the result is cached for
-        the step's other layers (same ``gather_slots`` and ``mask`` tensors, not
-        modified in place since).
+        ``infrared/model/inputs.py:33-85``). ``ir_varlen_form_scan`` recovers
+        ``cu_seqlens_q``, ``q_start`` and the block tables on the device and
+        verifies the form exactly, so the chunked-prefill kernel computes what
+        the mask kernel would. The check reads the mask once and synchronises
+        once (the device writes the verdict and sizes into the pool's pinned
+        record); the result is cached for the step's other layers (same
+        ``gather_slots`` and ``mask`` tensors, not modified in place since).
         Under hipGraph capture ``None`` is returned and the mask kernel runs.
         """
         if torch.cuda.is_current_stream_capturing():

@@ -579,6 +579,16 @@ def test_packed_form_check_reads_every_mask_layout(dtype, layout):
         m[0, 0, r, k] = value
         return m
 
+    staging = torch.full((kernels.varlen_staging_size(Q),), -5, dtype=torch.int32, pin_memory=True)
+
+    def forms(g, m):
+        # the record copied back from device memory; written by the device into
+        # pinned memory, tables in the call's capacity; the same with tables
+        # wider than a capacity of one entry, written by the second launch
+        return [kernels.varlen_form(g, m, bs, sum(need) + 7),
+                kernels.varlen_form(g, m, bs, sum(need) + 7, staging=staging),
+                kernels.varlen_form(g, m, bs, sum(need) + 7, staging=staging, tables_capacity=1)]
+
     for m, accepted in (
         (base, True),
         (planted(0, 100, float("-inf")), True),
@@ -588,15 +598,17 @@ def test_packed_form_check_reads_every_mask_layout(dtype, layout):
         (planted(8, long_key, neg), False),
         (planted(5, 0, 0.0), False),
     ):
-        f = kernels.varlen_form(gs, on_device(m), bs, sum(need) + 7)
-        if not accepted:
-            assert f is None
-            continue
-        assert f is not None
-        assert f.q_lens == tuple(q_lens) and f.prefixes == tuple(num_cached) and f.max_q_len == max(q_lens)
-        assert f.cu_seqlens_q.tolist() == [0, 5, 8, 13] and f.q_start.tolist() == num_cached
-        for i, nb in enumerate(need):
-            assert f.block_tables[i, :nb].tolist() == tables[i]
+        for f in forms(gs, on_device(m)):
+            if not accepted:
+                assert f is None
+                continue
+            assert f is not None
+            assert f.q_lens == tuple(q_lens) and f.prefixes == tuple(num_cached) and f.max_q_len == max(q_lens)
+            assert f.cu_seqlens_q.tolist() == [0, 5, 8, 13] and f.q_start.tolist() == num_cached
+            assert f.block_tables.shape == (3, max(need))
+            for i, nb in enumerate(need):
+                assert f.block_tables[i, :nb].tolist() == tables[i]
+                assert f.block_tables[i, nb:].eq(0).all()
     # slots the device check rejects: one off its block's closed form deep in
     # sequence 2, and a block head outside the pool
     off_form = gs.clone()
@@ -604,7 +616,7 @@ def test_packed_form_check_reads_every_mask_layout(dtype, layout):
     outside = gs.clone()
     outside[0, 5 + 16 + 25008 : 5 + 16 + 25024] += (sum(need) + 7) * bs  # one whole block, ids past the pool
     for bad_gs in (off_form, outside):
-        assert kernels.varlen_form(bad_gs, on_device(base), bs, sum(need) + 7) is None
+        assert forms(bad_gs, on_device(base)) == [None, None, None]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
