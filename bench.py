@@ -850,9 +850,9 @@ def _bench_reference_form_prefill(args) -> dict:
         fresh.clear()
         fresh.append((ours.gather_slots.clone(), mask.clone()))
 
-    ms = _rows_ms({"ref": step_ref, "ours": step_ours}, 7, layers, prep=prep)
+    ms = _rows_ms({"ref": step_ref, "ours": step_ours}, 15, layers, prep=prep)
     ms_ref, ms_ours = ms["ref"], ms["ours"]
-    ms_check = _rows_ms({"check": check_only}, 7, 1, prep=prep)["check"]
+    ms_check = _rows_ms({"check": check_only}, 15, 1, prep=prep)["check"]
     form = pool._ref_varlen[1]
     ms_masked = _rows_ms({"masked": step_masked}, 1, layers, warm=False)["masked"]
     out_ref = paged_attention(q, k, v, RefContext(pool, ours.write_slots, ours.gather_slots), mask, 0, cfg.scale,
@@ -889,11 +889,14 @@ def _bench_reference_form(args) -> dict:
     """Unchanged reference callers at the Qwen2.5-7B decode shape: each step's
     metadata in the reference engine's own form (``gather_slots [B, T]`` +
     additive mask, ``infrared/engine/paged_engine.py:290-332``, no block
-    tables) through ``paged_attention`` for ``--layers`` layers (KV write +
-    attention per layer, eager launches). Rows: the seam recognising the decode
-    form (one check per step) and running the block-table kernels; the same
-    step with block-table fields filled by the caller; and the mask kernel
-    reading gather_slots + mask as given (``use_triton=False``)."""
+    tables; new tensors every step, made before the timed region) through
+    ``paged_attention`` for ``--layers`` layers (KV write + attention per
+    layer, eager launches). Rows: the seam recognising the decode form (one
+    check per step, no host wait) and running the block-table kernels; the
+    same layers captured as the reference's ``CudaGraphDecoder`` does; the
+    same step with block-table fields filled by the caller; and the mask kernel
+    reading gather_slots + mask as given (``use_triton=False``). The rows'
+    steps are interleaved."""
     from dataclasses import dataclass
 
     from infrared_amd import PagedContext, PagedKVPool, kernels, metadata, paged_attention
@@ -922,11 +925,17 @@ def _bench_reference_form(args) -> dict:
     q = torch.randn(b, 1, hq, d, generator=g, device="cuda").to(cfg.dtype)
     k = torch.randn(b, 1, hkv, d, generator=g, device="cuda").to(cfg.dtype)
     v = torch.randn(b, 1, hkv, d, generator=g, device="cuda").to(cfg.dtype)
-    layers, steps = args.layers, 7
+    layers, steps = args.layers, 15
+    fresh = []
+
+    def prep():
+        # a step's metadata arrives as new tensors, as the reference engine
+        # builds them (made before the timed region: the caller's work)
+        fresh.clear()
+        fresh.append((ours.gather_slots.clone(), mask.clone()))
 
     def step_ref():
-        # a step's metadata arrives as new tensors, as the reference engine builds them
-        gs, m = ours.gather_slots.clone(), mask.clone()
+        gs, m = fresh.pop()
         paged = RefContext(pool, ours.write_slots, gs)
         for _ in range(layers):
             paged_attention(q, k, v, paged, m, 0, cfg.scale, cfg.n_rep)
@@ -966,9 +975,11 @@ def _bench_reference_form(args) -> dict:
     def step_graph():
         graph.replay()
 
-    ms = _rows_ms({"ref": step_ref, "ours": step_ours, "graph": step_graph, "masked": step_masked}, steps, layers)
+    ms = _rows_ms({"ref": step_ref, "ours": step_ours, "graph": step_graph, "masked": step_masked}, steps, layers,
+                  prep=prep)
     ms_ref, ms_ours, ms_masked, ms_graph = ms["ref"], ms["ours"], ms["masked"], ms["graph"]
     form = pool._ref_form[1]
+    recognised = form is not None and form.verdict() is True  # (before another check takes the record)
     out_ref = paged_attention(q, k, v, RefContext(pool, ours.write_slots, ours.gather_slots), mask, 0, cfg.scale,
                               cfg.n_rep)
     out_ours = paged_attention(q, k, v, PagedContext(pool, ours.write_slots, ours.gather_slots, True,
@@ -983,7 +994,7 @@ def _bench_reference_form(args) -> dict:
         "config": {"workload": f"{cfg.name} decode in the reference's metadata form: {b} seqs, {hq}q/{hkv}kv heads, "
                    f"head_dim {d}, block {bs}, gather_slots {tuple(ours.gather_slots.shape)}, {layers} layers per step "
                    "(KV write + attention per layer), eager",
-                   "decode_form_recognised": form is not None,
+                   "decode_form_recognised": recognised,
                    "equal_to_block_table_path": bool(torch.equal(out_ref, out_ours)),
                    "graph_replay_equal_to_block_table_path": bool(torch.equal(out_graph, out_ours)),
                    "rows_us_per_call": {"reference form, recognised (one check per step)": round(ms_ref * 1e3, 2),

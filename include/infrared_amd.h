@@ -316,15 +316,20 @@ int ir_paged_attention_masked(const void* q, int64_t q_b_stride, int64_t q_s_str
  * (infrared/engine/paged_engine.py:306-314, :630-638, via PagedContext,
  * infrared/cache/paged_kv_cache.py:75-91). Writes context_lens[i] (the mask's
  * zeros) and block_tables[i, j] = gather_slots[i, j * bs] / bs (0 past the
- * context), and ORs 1 into *bad unless the metadata has exactly that form: the
- * zeros a prefix, later mask values <= -6e4, at least one zero, every slot
- * below ctx_i the closed form, every block id in [0, num_blocks). With *bad
- * clear the decode kernels over these tables compute what
- * ir_paged_attention_masked computes. *bad must be 0 before the call.
- *   flags: IR_FORM_CLEAR_ON_FAIL launches a second kernel that sets every
- *   context_lens[i] to 0 when the check failed (for graph capture, where the
- *   host cannot read *bad: the block-table decode then reads no key and the
- *   mask kernel, gated on *bad, computes the call).
+ * context), and sets bad[0] to 1 unless the metadata has exactly that form,
+ * else 0: the zeros a prefix, later mask values <= -6e4, at least one zero,
+ * every slot below ctx_i the closed form, every block id in [0, num_blocks).
+ * With bad[0] clear the decode kernels over these tables compute what
+ * ir_paged_attention_masked computes. bad: int32 [batch + 1], no clearing
+ * needed (bad[1..batch] is working space).
+ *   flags: IR_FORM_CLEAR_ON_FAIL also sets every context_lens[i] to 0 when the
+ *   check failed (for a caller that does not wait for bad[0], as under graph
+ *   capture: the block-table decode then reads no key and the mask kernel,
+ *   gated on bad[0], computes the call).
+ *   host_verdict: null, or pinned host memory from the HIP host allocator
+ *   (one uint64): receives (uint64)tag << 32 | bad[0] from the device at the
+ *   end of the call in one 8-byte store, so the host can read the verdict of
+ *   the call it tagged when it arrives, without synchronising.
  *   gather_slots: [batch, seq_k] int64 (strides b, t); mask: element (b, t) at
  *   mask + b*mask_b_stride + t*mask_t_stride, dtype mask_dtype.
  *   block_tables: [batch, bt_stride] int32, max_blocks_per_seq >= ceil(seq_k / bs).
@@ -333,7 +338,7 @@ int ir_decode_form(const int64_t* gather_slots, int64_t gs_b_stride, int64_t gs_
                    const void* mask, int64_t mask_b_stride, int64_t mask_t_stride, int mask_dtype,
                    int batch, int seq_k, int block_size, int64_t num_blocks, int32_t* block_tables,
                    int64_t bt_stride, int max_blocks_per_seq, int32_t* context_lens, int32_t* bad,
-                   int flags, ir_stream_t stream);
+                   int flags, uint64_t* host_verdict, uint32_t tag, ir_stream_t stream);
 
 /*
  * Prefill metadata from the reference engine's packed prefill / mixed-step

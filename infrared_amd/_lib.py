@@ -97,7 +97,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ir_decode_form": (
         _c_i32,
         [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_p, _c_i64,
-         _c_i32, _c_p, _c_p, _c_i32, _c_p],
+         _c_i32, _c_p, _c_p, _c_i32, _c_p, ctypes.c_uint32, _c_p],
     ),
     "ir_stream_capture_id": (_c_i32, [_c_p, ctypes.POINTER(ctypes.c_uint64)]),
     "ir_varlen_form_scan": (

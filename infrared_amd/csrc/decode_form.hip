@@ -10,14 +10,19 @@
 // finfo.min included), every slot below ctx_i follows the closed form and
 // every block id lies in the pool, and at least one key is visible (a row
 // masked entirely is the mask kernel's uniform average over its keys, not an
-// empty context). Any violation sets *bad; the host then keeps the mask
+// empty context). Each workgroup leaves its sequence's flag in bad[1 + i]; a
+// one-workgroup launch after it ORs them into bad[0] (so nothing needs clearing
+// before the call). A violation sets bad[0]; the caller then runs the mask
 // kernel, which reads the metadata as given.
 //
-// Under hipGraph capture the host cannot read the verdict, so both kernels are
-// recorded and the verdict gates them on the device: with IR_FORM_CLEAR_ON_FAIL
-// a second launch sets every context length to 0 when *bad is set (the
+// Where the host does not wait for the verdict -- under hipGraph capture, or
+// an eager caller that launches before the verdict is known -- both kernels
+// run and the verdict gates them on the device: with IR_FORM_CLEAR_ON_FAIL the
+// second launch also sets every context length to 0 when bad[0] is set (the
 // block-table decode then reads nothing and writes zero rows), and the mask
-// kernel, given *bad as its run_if gate, runs after it only in that case.
+// kernel, given bad[0] as its run_if gate, runs after it only in that case.
+// The second launch can also publish the verdict, tagged, into pinned host
+// memory, where the host reads it when it arrives without synchronising.
 #include "common.hpp"
 #include "status.hpp"
 
@@ -43,7 +48,7 @@ __global__ __launch_bounds__(kFormThreads) void decode_form_kernel(const int64_t
                                                                    const void* mask, int64_t m_b, int64_t m_t, int T,
                                                                    int bs, int64_t num_blocks, int32_t* bt,
                                                                    int64_t bt_stride, int width, int32_t* ctx_out,
-                                                                   int32_t* bad) {
+                                                                   int32_t* seq_bad) {
   __shared__ int s_zeros, s_first, s_bad;
   const int b = blockIdx.x, tid = threadIdx.x;
   if (tid == 0) {
@@ -115,14 +120,34 @@ __global__ __launch_bounds__(kFormThreads) void decode_form_kernel(const int64_t
   __syncthreads();
   if (tid == 0) {
     ctx_out[b] = ctx;
-    if (s_bad) atomicOr(bad, 1);
+    seq_bad[b] = s_bad;
   }
 }
 
-// After the check: when it failed, every context length becomes 0.
-__global__ __launch_bounds__(256) void decode_form_clear_kernel(const int32_t* bad, int32_t* ctx_out, int batch) {
-  if (*bad == 0) return;
-  for (int b = blockIdx.x * 256 + threadIdx.x; b < batch; b += gridDim.x * 256) ctx_out[b] = 0;
+// After the check, one workgroup: bad[0] = any sequence's flag; when asked,
+// every context length becomes 0 if the check failed; and, when given, the
+// host record receives tag << 32 | verdict in one 8-byte store, then a
+// system-scope fence.
+constexpr int kFinishThreads = 1024;
+__global__ __launch_bounds__(kFinishThreads) void decode_form_finish_kernel(int32_t* bad, int batch, int32_t* ctx_out,
+                                                                           int clear, uint64_t* host, uint32_t tag) {
+  __shared__ int s_bad;
+  if (threadIdx.x == 0) s_bad = 0;
+  __syncthreads();
+  int v = 0;
+  for (int b = threadIdx.x; b < batch; b += kFinishThreads) v |= bad[1 + b];
+  if (v) s_bad = 1;
+  __syncthreads();
+  const int verdict = s_bad;
+  if (threadIdx.x == 0) {
+    bad[0] = verdict;
+    if (host != nullptr) {
+      host[0] = (uint64_t)tag << 32 | (uint32_t)verdict;
+      __threadfence_system();
+    }
+  }
+  if (clear && verdict)
+    for (int b = threadIdx.x; b < batch; b += kFinishThreads) ctx_out[b] = 0;
 }
 
 }  // namespace
@@ -134,7 +159,7 @@ extern "C" int ir_decode_form(const int64_t* gather_slots, int64_t gs_b_stride, 
                               const void* mask, int64_t mask_b_stride, int64_t mask_t_stride, int mask_dtype,
                               int batch, int seq_k, int block_size, int64_t num_blocks, int32_t* block_tables,
                               int64_t bt_stride, int max_blocks_per_seq, int32_t* context_lens, int32_t* bad,
-                              int flags, ir_stream_t stream) {
+                              int flags, uint64_t* host_verdict, uint32_t tag, ir_stream_t stream) {
   IR_REQUIRE(dtype_bytes(mask_dtype) > 0, "ir_decode_form: unknown mask dtype %d", mask_dtype);
   IR_REQUIRE((flags & ~IR_FORM_CLEAR_ON_FAIL) == 0, "ir_decode_form: unknown flags %#x", flags);
   IR_REQUIRE(batch >= 0 && seq_k >= 0 && block_size > 0 && num_blocks >= 0, "ir_decode_form: bad sizes");
@@ -142,21 +167,29 @@ extern "C" int ir_decode_form(const int64_t* gather_slots, int64_t gs_b_stride, 
              "ir_decode_form: block tables of %d ids cannot hold %d keys", max_blocks_per_seq, seq_k);
   if (batch == 0) return ok();
   IR_REQUIRE(gather_slots && mask && block_tables && context_lens && bad, "ir_decode_form: null pointer");
+  uint64_t* host_dev = nullptr;
+  if (host_verdict != nullptr) {
+    const hipError_t e = hipHostGetDevicePointer((void**)&host_dev, host_verdict, 0);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();  // not left for the next launch check to report
+      return fail(IR_EINVAL, "ir_decode_form: host_verdict is not pinned host memory: %s", hipGetErrorString(e));
+    }
+  }
   hipStream_t s = (hipStream_t)stream;
+  int32_t* seq_bad = bad + 1;
   if (mask_dtype == IR_DTYPE_F32)
     hipLaunchKernelGGL(decode_form_kernel<IR_DTYPE_F32>, dim3(batch), dim3(kFormThreads), 0, s, gather_slots,
                        gs_b_stride, gs_t_stride, mask, mask_b_stride, mask_t_stride, seq_k, block_size, num_blocks,
-                       block_tables, bt_stride, max_blocks_per_seq, context_lens, bad);
+                       block_tables, bt_stride, max_blocks_per_seq, context_lens, seq_bad);
   else if (mask_dtype == IR_DTYPE_BF16)
     hipLaunchKernelGGL(decode_form_kernel<IR_DTYPE_BF16>, dim3(batch), dim3(kFormThreads), 0, s, gather_slots,
                        gs_b_stride, gs_t_stride, mask, mask_b_stride, mask_t_stride, seq_k, block_size, num_blocks,
-                       block_tables, bt_stride, max_blocks_per_seq, context_lens, bad);
+                       block_tables, bt_stride, max_blocks_per_seq, context_lens, seq_bad);
   else
     hipLaunchKernelGGL(decode_form_kernel<IR_DTYPE_F16>, dim3(batch), dim3(kFormThreads), 0, s, gather_slots,
                        gs_b_stride, gs_t_stride, mask, mask_b_stride, mask_t_stride, seq_k, block_size, num_blocks,
-                       block_tables, bt_stride, max_blocks_per_seq, context_lens, bad);
-  if (flags & IR_FORM_CLEAR_ON_FAIL)
-    hipLaunchKernelGGL(decode_form_clear_kernel, dim3((batch + 255) / 256), dim3(256), 0, s, bad, context_lens,
-                       batch);
+                       block_tables, bt_stride, max_blocks_per_seq, context_lens, seq_bad);
+  hipLaunchKernelGGL(decode_form_finish_kernel, dim3(1), dim3(kFinishThreads), 0, s, bad, batch, context_lens,
+                     (flags & IR_FORM_CLEAR_ON_FAIL) ? 1 : 0, host_dev, tag);
   return check_launch("ir_decode_form");
 }

@@ -546,8 +546,10 @@ extern "C" int ir_varlen_form_scan(const void* mask, int64_t mask_q_stride, int6
   int32_t* host_dev = nullptr;
   if (host_record != nullptr) {
     const hipError_t e = hipHostGetDevicePointer((void**)&host_dev, host_record, 0);
-    if (e != hipSuccess)
+    if (e != hipSuccess) {
+      (void)hipGetLastError();  // not left for the next launch check to report
       return fail(IR_EINVAL, "ir_varlen_form_scan: host_record is not pinned host memory: %s", hipGetErrorString(e));
+    }
   }
   hipStream_t s = (hipStream_t)stream;
   RowRec* rec = (RowRec*)row_records;

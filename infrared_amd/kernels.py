@@ -614,30 +614,39 @@ FORM_CLEAR_ON_FAIL = 1  # IR_FORM_CLEAR_ON_FAIL
 
 
 def decode_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int, num_blocks: int,
-                clear_on_fail: bool = False) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+                clear_on_fail: bool = False, host_verdict: torch.Tensor | None = None,
+                tag: int = 0) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Block tables ``[B, ceil(T / bs)]`` int32 and context lengths ``[B]`` int32
     from the reference's decode metadata (``gather_slots`` ``[B, T]`` int64, mask
-    ``[B, 1, 1, T]``), plus an int32 flag, nonzero unless the metadata has the
-    reference engine's decode form exactly (``ir_decode_form``).
+    ``[B, 1, 1, T]``), plus an int32 flag ``[1]``, nonzero unless the metadata
+    has the reference engine's decode form exactly (``ir_decode_form``).
     ``clear_on_fail``: when the check fails, every context length is set to 0
-    on the device (for capture, where the flag cannot be read on the host)."""
+    on the device (for a caller that does not wait for the flag).
+    ``host_verdict``: a pinned int64 ``[1]`` host tensor the device writes
+    ``tag << 32 | flag`` into at the end of the call."""
     dev = require_device(gather_slots, mask)
     if gather_slots.dtype != torch.int64 or gather_slots.dim() != 2:
         raise RuntimeError("decode_form: gather_slots must be int64 [B, T]")
     b, t = gather_slots.shape
     if mask.dim() != 4 or mask.shape[0] != b or mask.shape[1] != 1 or mask.shape[2] != 1 or mask.shape[3] != t:
         raise RuntimeError(f"decode_form: mask must be [B, 1, 1, T], got {tuple(mask.shape)}")
+    if host_verdict is not None and (host_verdict.dtype != torch.int64 or host_verdict.numel() < 1
+                                     or host_verdict.is_cuda):
+        # (ir_decode_form refuses memory that is not pinned)
+        raise RuntimeError("decode_form: host_verdict must be a pinned int64 host tensor")
     width = max(-(-t // block_size), 1)
-    bt = torch.empty(b, width, dtype=torch.int32, device=dev)
-    ctx = torch.empty(b, dtype=torch.int32, device=dev)
-    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    # one allocation: block tables | context lengths | flag and per-sequence flags
+    n_bt = b * width
+    buf = torch.empty(n_bt + 2 * b + 1, dtype=torch.int32, device=dev)
+    base = buf.data_ptr()
     rc = lib().ir_decode_form(
         ptr(gather_slots), gather_slots.stride(0), gather_slots.stride(1), ptr(mask), mask.stride(0),
-        mask.stride(3), dtype_code(mask.dtype), b, t, block_size, num_blocks, ptr(bt), bt.stride(0), width,
-        ptr(ctx), ptr(bad), FORM_CLEAR_ON_FAIL if clear_on_fail else 0, stream_ptr(dev),
+        mask.stride(3), dtype_code(mask.dtype), b, t, block_size, num_blocks, base, width, width,
+        base + 4 * n_bt, base + 4 * (n_bt + b), FORM_CLEAR_ON_FAIL if clear_on_fail else 0, ptr(host_verdict),
+        int(tag) & 0xFFFFFFFF, stream_ptr(dev),
     )
     check(rc, "ir_decode_form")
-    return bt, ctx, bad
+    return buf[:n_bt].view(b, width), buf[n_bt : n_bt + b], buf[n_bt + b : n_bt + b + 1]
 
 
 @dataclass(slots=True)
@@ -699,8 +708,11 @@ def varlen_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int,
     cap = min(cap, 2**31 - 1)
     buf = torch.empty(o_bt + cap, **i32)
     base = buf.data_ptr()
-    pinned = (staging is not None and staging.is_pinned() and staging.dtype == torch.int32
-              and staging.is_contiguous() and staging.numel() >= 2 * q + 9)
+    pinned = staging is not None
+    if pinned and (staging.dtype != torch.int32 or staging.is_cuda or not staging.is_contiguous()
+                   or staging.numel() < 2 * q + 9):
+        # (ir_varlen_form_scan refuses memory that is not pinned)
+        raise RuntimeError(f"varlen_form: staging must be a pinned contiguous int32 host tensor of >= {2 * q + 9}")
     rc = lib().ir_varlen_form_scan(
         ptr(mask), mask.stride(2), mask.stride(3), dtype_code(mask.dtype), q, k, ptr(gather_slots),
         gather_slots.stride(1), block_size, num_blocks, ptr(records), base + 4 * o_cu, base + 4 * o_qs,

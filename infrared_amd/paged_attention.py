@@ -24,9 +24,10 @@ calls once per layer (``infrared/model/layers.py:178-180``):
      bs + p % bs`` and mask 0 then ``finfo.min``,
      ``infrared/engine/paged_engine.py:306-314, 630-638``): the same decode
      kernels over block tables derived from them on the device (checked once
-     per step, ``PagedKVPool.reference_decode_form``; under graph capture the
-     check is recorded and gates, on the device, a mask kernel recorded after
-     the decode, so each replay takes the path its own metadata allows);
+     per step, ``PagedKVPool.reference_decode_form``, with no host wait: until
+     the check's verdict reaches the host -- under graph capture, never -- its
+     flag gates, on the device, a mask kernel run after the decode, so each
+     call or replay takes the path its own metadata allows);
    - otherwise, for the reference engine's packed prefill / mixed-step frame
      (batch 1: every scheduled sequence's query tokens, a key axis
      concatenating their histories in order, ``gather_slots`` with the closed
@@ -158,13 +159,22 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
             # the reference's packed prefill / mixed-step frame: when it has
             # that form, run the chunked-prefill kernel over derived metadata
             vform = pool.reference_varlen_form(paged.gather_slots, mask)
-        if form is not None:
+        verdict = form.verdict() if form is not None else None
+        if form is not None and verdict is False:
+            # the check's published verdict: not the decode form
+            out = kernels.paged_attention_masked(
+                q, k_layer, v_layer, paged.gather_slots, mask, scale, err_flags=err
+            )
+        elif form is not None:
             out = _decode(q, pool, layer_idx, form.block_tables, form.context_lens, form, scale, err)
-            if form.gate is not None:
-                # recorded under graph capture: the replay's own check decides,
-                # on the device, whether this mask kernel overwrites the rows
+            verdict = form.verdict()  # (it may have arrived while the decode was launched)
+            if form.gate is not None and verdict is not True:
+                # verdict not known on the host (under capture, never): the
+                # check's flag decides, on the device, whether this mask kernel
+                # overwrites the rows; known to fail: it does
                 kernels.paged_attention_masked(
-                    q, k_layer, v_layer, paged.gather_slots, mask, scale, out=out, err_flags=err, run_if=form.gate
+                    q, k_layer, v_layer, paged.gather_slots, mask, scale, out=out, err_flags=err,
+                    run_if=form.gate if verdict is None else None,
                 )
         elif vform is not None and vform.row_split is not None:
             out = _split_step(q, pool, layer_idx, vform.row_split, scale, err)

@@ -120,6 +120,11 @@ class PagedKVPool:
         # the packed-form check's row records (zero at rest) and pinned read buffer
         self._varlen_records: torch.Tensor | None = None
         self._varlen_staging: torch.Tensor | None = None
+        # the eager decode-form check's verdict, written by the device into
+        # pinned memory as tag << 32 | flag (read without synchronising)
+        self._verdict: torch.Tensor | None = None
+        self._verdict_np = None
+        self._verdict_tag = 0
 
     # --- reference surface ------------------------------------------------
 
@@ -206,22 +211,28 @@ class PagedKVPool:
         dtype, fp16's ``finfo.min`` included), so the decode kernels compute
         what the mask kernel would.
 
-        Eager: the check costs one launch and one synchronising read of its
-        flag; the result is cached for the step's other layers (same
-        ``gather_slots`` and ``mask`` tensors, not modified in place since).
+        The host never waits for the check. It runs with
+        ``IR_FORM_CLEAR_ON_FAIL`` and the returned form carries its device flag
+        as ``gate``: until the verdict is known the caller runs the block-table
+        decode followed by the mask kernel gated on the flag (each replay, or
+        each call, then computes what the mask kernel would). Eagerly the
+        device also writes the verdict, tagged, into the pool's pinned record;
+        :meth:`_DecodeForm.verdict` reads it there when it has arrived (by the
+        step's second layer, typically), and later layers then run only the
+        kernels it selects. The eager result is cached for the step's other
+        layers (same ``gather_slots`` and ``mask`` tensors, not modified in
+        place since).
 
         Under hipGraph capture (the reference's ``CudaGraphDecoder`` captures
         its decode forward on static ``gather_slots`` / ``mask`` buffers that
-        each replay refills, ``infrared/engine/cuda_graph.py:231-285``) no read
-        is possible, so the check itself is recorded, once per capture and
-        metadata pair, with ``IR_FORM_CLEAR_ON_FAIL``; the returned form
-        carries the flag as ``gate``, and the caller records the block-table
-        decode followed by the mask kernel gated on the flag. Each replay then
-        checks its own metadata: in the decode form it runs the block-table
-        kernels, otherwise the mask kernel. The eager cache is never consulted
-        under capture. The form holds the buffers its graph addresses (its own
-        plan buffer, the decode workspace and counters) for as long as the
-        captured ``gather_slots`` tensor lives.
+        each replay refills, ``infrared/engine/cuda_graph.py:231-285``) the
+        check itself is recorded, once per capture and metadata pair, and its
+        form never reads a verdict: each replay checks its own metadata and
+        runs the block-table kernels in the decode form, otherwise the mask
+        kernel. The eager cache is never consulted under capture. The form
+        holds the buffers its graph addresses (its own plan buffer, the decode
+        workspace and counters) for as long as the captured ``gather_slots``
+        tensor lives.
         """
         if not (gather_slots.dim() == 2 and gather_slots.dtype == torch.int64 and gather_slots.is_cuda
                 and mask.is_cuda and mask.dim() == 4 and tuple(mask.shape[:3]) == (gather_slots.shape[0], 1, 1)
@@ -232,10 +243,13 @@ class PagedKVPool:
         c = self._ref_form
         if c is not None and _same_metadata(c[0], gather_slots, mask):
             return c[1]
-        form = None
-        bt, ctx, bad = kernels.decode_form(gather_slots, mask, self.block_size, self.num_blocks)
-        if int(bad.item()) == 0:
-            form = _DecodeForm(bt, ctx)
+        if self._verdict is None:
+            self._verdict = torch.zeros(1, dtype=torch.int64, pin_memory=True)
+            self._verdict_np = self._verdict.numpy()  # the same pinned memory, read without torch
+        self._verdict_tag = (self._verdict_tag + 1) & 0x7FFFFFFF
+        bt, ctx, bad = kernels.decode_form(gather_slots, mask, self.block_size, self.num_blocks,
+                                           clear_on_fail=True, host_verdict=self._verdict, tag=self._verdict_tag)
+        form = _DecodeForm(bt, ctx, gate=bad, peek=(self._verdict_np, self._verdict_tag))
         self._ref_form = (_metadata_key(gather_slots, mask), form)
         return form
 
@@ -328,10 +342,11 @@ class _DecodeForm:
     """Block tables and context lengths derived from reference decode metadata,
     with the step's decode plan once built.
 
-    A form recorded under graph capture has ``gate`` (the check's int32 flag
-    on the device, nonzero when the metadata is not in the decode form; the
-    context lengths are then 0) and its own ``plan_buf``; ``held`` keeps the
-    pool buffers its graph's kernels address alive."""
+    ``gate`` is the check's int32 flag on the device, nonzero when the
+    metadata is not in the decode form (the context lengths are then 0); a
+    form with a gate has its own ``plan_buf``. ``peek`` (eager forms): the
+    pinned record the device writes the tagged verdict into, and the tag;
+    ``held`` keeps the pool buffers a captured graph's kernels address alive."""
 
     block_tables: torch.Tensor
     context_lens: torch.Tensor
@@ -339,6 +354,19 @@ class _DecodeForm:
     gate: torch.Tensor | None = None
     plan_buf: torch.Tensor | None = None
     held: list = field(default_factory=list)
+    peek: tuple | None = None
+
+    def verdict(self) -> bool | None:
+        """True / False once the device has published this form's check (the
+        metadata is / is not in the decode form), None before (or for a form
+        recorded under capture, which never reads one)."""
+        if self.peek is None:
+            return None
+        record, tag = self.peek
+        v = int(record[0])
+        if v >> 32 != tag:
+            return None
+        return (v & 0xFFFFFFFF) == 0
 
 
 @dataclass(slots=True)

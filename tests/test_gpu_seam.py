@@ -316,6 +316,7 @@ def test_reference_decode_metadata_runs_the_block_table_kernels(num_seqs):
                                     ours.block_tables.cpu(), ours.context_lens.cpu(), bs, d**-0.5)
         assert (got[:, 0].float().cpu() - expect).abs().max().item() <= 2e-2
     assert forms[0] is not None and all(f is forms[0] for f in forms)
+    assert forms[0].verdict() is True  # later layers ran the block-table kernels alone
     assert torch.equal(forms[0].context_lens, ours.context_lens)
     for i, c in enumerate(ours.context_lens.tolist()):  # (entries past a context are never read)
         n = -(-c // bs)
@@ -348,9 +349,15 @@ def test_decode_form_check_over_mask_dtypes(dtype, num_blocks):
         mask[i, 0, 0, : nc + 1] = 0
     ctx_want = [nc + 1 for nc in num_cached]
 
+    record = torch.zeros(1, dtype=torch.int64, pin_memory=True)
+    tags = iter(range(7, 100))
+
     def run(gs_, mask_):
-        bt, ctx, bad = kernels.decode_form(gs_.to(DEV), mask_.to(DEV), bs, num_blocks)
+        tag = next(tags)
+        bt, ctx, bad = kernels.decode_form(gs_.to(DEV), mask_.to(DEV), bs, num_blocks, host_verdict=record, tag=tag)
         torch.cuda.synchronize()
+        # the verdict the device published into pinned memory, under this call's tag
+        assert int(record[0]) == (tag << 32 | int(bad.item()))
         return bt.cpu(), ctx.cpu(), int(bad.item())
 
     bt, ctx, bad = run(gs, mask)
@@ -400,7 +407,10 @@ def test_reference_metadata_outside_the_decode_form_takes_the_mask_kernel():
         v = torch.randn(3, 1, h_kv, d, device=DEV)
         got = paged_attention(q, k, v, ref, m, 0, d**-0.5, n_rep)
         torch.cuda.synchronize()
-        assert pool._ref_form[1] is None
+        assert pool._ref_form[1].verdict() is False  # published by the device, read without a wait
+        again = paged_attention(q, k, v, ref, m, 0, d**-0.5, n_rep)  # the mask kernel alone now
+        torch.cuda.synchronize()
+        assert torch.equal(again, got)
         expect = O.paged_attention_naive(q.cpu(), pool.k[0].cpu(), pool.v[0].cpu(), gs.cpu(), m.cpu(), d**-0.5, n_rep)
         assert (got.cpu() - expect).abs().max().item() <= 1e-4
 
@@ -640,6 +650,23 @@ def test_packed_form_check_on_tiny_frames(dtype, case):
     assert f is not None
     assert f.q_lens == tuple(q_lens) and f.prefixes == tuple(num_cached)
     assert f.block_tables[:, 0].tolist() == [t[0] for t in tables]
+
+
+def test_host_records_must_be_pinned():
+    """The checks' host records are written by the device, so pageable memory
+    is refused with an error (and the refusal is not left behind for the next
+    call's launch check)."""
+    gs = torch.tensor([[0, 1, 2]], dtype=torch.int64, device=DEV)
+    m = torch.tensor([[[[0.0, 0.0, 0.0]]]], device=DEV)
+    with pytest.raises(RuntimeError, match="not pinned host memory"):
+        kernels.decode_form(gs, m, 16, 4, host_verdict=torch.zeros(1, dtype=torch.int64))
+    bt, ctx, bad = kernels.decode_form(gs, m, 16, 4, host_verdict=torch.zeros(1, dtype=torch.int64, pin_memory=True))
+    assert int(bad.item()) == 0 and ctx.tolist() == [3] and bt.tolist() == [[0]]
+    frame = torch.zeros(1, 1, 1, 3, device=DEV)
+    with pytest.raises(RuntimeError, match="not pinned host memory"):
+        kernels.varlen_form(gs, frame, 16, 4, staging=torch.zeros(64, dtype=torch.int32))
+    f = kernels.varlen_form(gs, frame, 16, 4, staging=torch.zeros(64, dtype=torch.int32, pin_memory=True))
+    assert f is not None and f.q_lens == (1,) and f.prefixes == (2,)
 
 
 def test_reference_metadata_refilled_in_place_is_checked_again():
