@@ -351,7 +351,8 @@ def _bench_prefill(args) -> dict:
     # the work plan (the seam's choice unless --schedule forces it), rebuilt
     # every --layers calls as an engine step would
     planned = args.schedule == "planned" or (args.schedule == "auto" and kernels.prefill_plan_pays(
-        cfg.num_seqs, cfg.chunk, cfg.num_q_heads, cfg.num_kv_heads))
+        cfg.num_seqs, cfg.chunk, cfg.num_q_heads, cfg.num_kv_heads,
+        max_keys=case.block_tables[0].shape[1] * cfg.block_size))
     plan_buf = torch.empty(max(256, kernels.prefill_plan_bytes(cfg.num_seqs, cfg.chunk, cfg.num_q_heads,
                                                                cfg.num_kv_heads, cfg.head_dim)),
                            dtype=torch.uint8, device="cuda")

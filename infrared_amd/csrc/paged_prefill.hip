@@ -987,10 +987,12 @@ struct PrefillKnobs {
   int waves = 0;   // 0: 4, or 8 when 4 cannot hold a token's query heads
   int ring2 = -1;  // -1: the default (2-deep)
   bool cuts = true;
+  bool split = true;  // a grid no larger than the CUs: 8 wavefronts of one column tile
   PrefillKnobs() {
     if (const char* e = getenv("IR_PREFILL_WAVES")) waves = atoi(e) == 8 ? 8 : 4;
     if (const char* e = getenv("IR_PREFILL_RING2")) ring2 = atoi(e) == 1 ? 1 : 0;
     if (const char* e = getenv("IR_PREFILL_CUTS")) cuts = atoi(e) != 0;
+    if (const char* e = getenv("IR_PREFILL_SPLIT")) split = atoi(e) != 0;
   }
 };
 
@@ -1069,7 +1071,14 @@ int launch_prefill(const PrefillArgs& a, int sched, hipStream_t s) {
   const bool fast = a.bs_shift >= 0 && slots < (1 << 23) && a.c_slot < (1 << 23) &&
                     (slots * a.c_slot + a.c_head * a.num_kv_heads) < ((int64_t)1 << 31);
   const dim3 g((unsigned)grid);
-  if (a.nw == 4) {
+  if (a.nw == 4 && !a.items && grid <= device_cus() && prefill_knobs().split) {
+    // every workgroup alone on its CU: its 128 columns on 8 wavefronts of one
+    // 16-column tile (two per SIMD) rather than 4 of two, so each walks its
+    // keys with half the per-wavefront work (the same arithmetic per column)
+    const dim3 block(PShape<D, 8, 1>::NT);
+    if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 1, kRing2>), g, block, 0, s, a);
+    else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 1, kRing2>), g, block, 0, s, a);
+  } else if (a.nw == 4) {
     const dim3 block(PShape<D, 4>::NT);
     if (sched == kRing2) {
       if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 4, 2, kRing2>), g, block, 0, s, a);

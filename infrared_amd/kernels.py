@@ -486,14 +486,24 @@ def prefill_plan_xcds() -> int:
     return int(lib().ir_paged_prefill_plan_xcds())
 
 
+PLAN_CUT_KEYS = 1024  # a call whose longest context exceeds this many keys is planned (its items get cut)
+
+
 def prefill_plan_pays(num_seqs: int, max_q_len: int, num_q_heads: int, num_kv_heads: int,
-                      device: torch.device | str | int | None = None) -> bool:
+                      device: torch.device | str | int | None = None, max_keys: int = 0) -> bool:
     """Whether a plan can shorten the call: its workgroups outnumber the CUs,
     so the dispatch order -- and cutting the heaviest items -- decides which
-    CU finishes last. Below that every workgroup starts at once. (Items are
-    (sequence, block of 128 // n_rep query tokens), 4-wavefront workgroups.)"""
+    CU finishes last; or its longest context (``max_keys``, e.g. the block
+    tables' width times the block size) exceeds ``PLAN_CUT_KEYS``, so cutting
+    the long items into key ranges shortens the longest walk even when every
+    workgroup starts at once (one 512-token chunk after 4,096 cached: 68 vs
+    110 us; two 128-token chunks after 1,024: 26 vs 32 us). Otherwise every
+    workgroup starts at once with nothing worth cutting. (Items are (sequence,
+    block of 128 // n_rep query tokens), 4-wavefront workgroups.)"""
     if num_seqs <= 0 or max_q_len <= 0 or num_kv_heads <= 0 or num_q_heads % num_kv_heads:
         return False
+    if max_keys > PLAN_CUT_KEYS:
+        return True
     n_rep = num_q_heads // num_kv_heads
     tq = (128 if n_rep <= 128 else 256) // n_rep
     idx = torch.device(device if device is not None else "cuda").index

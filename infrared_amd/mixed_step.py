@@ -172,7 +172,8 @@ class MixedStep:
             self.plan_buf = None
         self.plan: kernels.DecodePlan | None = None
         npre = batch.q_start.shape[0]
-        self.ordered = kernels.prefill_plan_pays(npre, batch.max_q_len, hq, pool.num_kv_heads, dev)
+        self.ordered = kernels.prefill_plan_pays(npre, batch.max_q_len, hq, pool.num_kv_heads, dev,
+                                                 max_keys=batch.pre_tables.shape[1] * pool.block_size)
         self.plan_pre_buf = (torch.empty(kernels.prefill_plan_bytes(npre, batch.max_q_len, hq, pool.num_kv_heads, d),
                                          dtype=torch.uint8, device=dev) if self.ordered else None)
         self.plan_pre: kernels.PrefillPlan | None = None

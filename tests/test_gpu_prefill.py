@@ -386,6 +386,11 @@ _SCHED_CASES = {
     # fp16, head_dim 64, a 12-token block (general addressing path)
     "f16-bs12": (PrefillConfig("pf-s-f16", 8, 0, 32, 8, 64, 12, torch.float16, 0, seed=31),
                  [0, 100, 7, 300, 12, 0, 50, 1], [300, 256, 290, 200, 310, 280, 260, 299]),
+    # grids no larger than the CUs (240 and 48 workgroups): 8 wavefronts of one column tile by default
+    "small": (PrefillConfig("pf-small", 4, 256, 28, 4, 128, 16, torch.bfloat16, 0, seed=7),
+              [0, 100, 700, 33], [256, 256, 256, 256]),
+    "small-f16": (PrefillConfig("pf-small-f16", 3, 64, 32, 8, 64, 12, torch.float16, 0, seed=9),
+                  [0, 50, 300], [64, 1, 40]),
 }
 
 
@@ -393,9 +398,11 @@ _SCHED_CASES = {
 def test_prefill_schedules_agree_bit_for_bit(key, tmp_path):
     """Every workgroup shape and schedule does each column's arithmetic in the
     same order: 4-wavefront workgroups on the 2-deep ring, on the 3-deep ring
-    (next tile's scores beside this tile's exponentials) and 8-wavefront
-    workgroups give identical outputs, within the bar of the oracle. The knobs
-    are read once per process, so each shape runs in a child process."""
+    (next tile's scores beside this tile's exponentials), 8-wavefront
+    workgroups, and -- on grids no larger than the CUs, where it is the
+    default -- 8 wavefronts of one column tile give identical outputs, within
+    the bar of the oracle. The knobs are read once per process, so each shape
+    runs in a child process."""
     import os
     import subprocess
     import sys
@@ -403,7 +410,9 @@ def test_prefill_schedules_agree_bit_for_bit(key, tmp_path):
     name, prefixes, q_lens = _SCHED_CASES[key]
     tests = os.path.dirname(os.path.abspath(__file__))
     outs = []
-    for i, env in enumerate(({"IR_PREFILL_RING2": "1"}, {"IR_PREFILL_RING2": "0"}, {"IR_PREFILL_WAVES": "8"})):
+    envs = ({"IR_PREFILL_RING2": "1"}, {"IR_PREFILL_RING2": "0", "IR_PREFILL_SPLIT": "0"}, {"IR_PREFILL_WAVES": "8"},
+            {"IR_PREFILL_SPLIT": "0"})
+    for i, env in enumerate(envs):
         path = str(tmp_path / f"s{i}.pt")
         res = subprocess.run(
             [sys.executable, "-c", _SCHED_CHILD.format(root=os.path.dirname(tests), tests=tests, key=key, path=path)],
@@ -411,7 +420,7 @@ def test_prefill_schedules_agree_bit_for_bit(key, tmp_path):
         )
         assert res.returncode == 0 and "SCHED OK" in res.stdout, str(env) + res.stdout + res.stderr[-2000:]
         outs.append(torch.load(path, weights_only=True))
-    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
     case = make_prefill_case(name, DEV, prefixes=prefixes, q_lens=q_lens)
     cfg = case.config
     ref = O.prefill_reference(

@@ -101,16 +101,24 @@ def test_packed_prefill_and_decode_step_through_seam(use_triton):
     assert (out[0].float().cpu() - ref).abs().max().item() <= 2e-2
 
 
-def test_prefill_step_builds_its_work_plan_once():
-    """A prefill step whose workgroups outnumber the CUs: the first layer builds
-    the work plan and caches it on the context, the second reuses it, and both
-    layers' outputs equal the unplanned kernel (within the fp32 rounding of a
-    cut item's merge) and match the oracle."""
+@pytest.mark.parametrize("case", ["many-workgroups", "few-long"])
+def test_prefill_step_builds_its_work_plan_once(case):
+    """A prefill step whose workgroups outnumber the CUs, or one of few
+    workgroups over a long context (one 200-token chunk after 3,000 cached: 48
+    workgroups, items worth cutting): the first layer builds the work plan and
+    caches it on the context, the second reuses it, and both layers' outputs
+    equal the unplanned kernel (within the fp32 rounding of a cut item's merge)
+    and match the oracle."""
     g = torch.Generator().manual_seed(9)
     bs, h_kv, n_rep, d = 16, 4, 7, 128
-    num_cached = [0, 2000, 160, 3000, 40, 40, 900, 1200]
-    q_lens = [300, 300, 280, 300, 64, 300, 2, 250]
-    assert kernels.prefill_plan_pays(len(q_lens), max(q_lens), h_kv * n_rep, h_kv, DEV)
+    if case == "many-workgroups":
+        num_cached = [0, 2000, 160, 3000, 40, 40, 900, 1200]
+        q_lens = [300, 300, 280, 300, 64, 300, 2, 250]
+        assert kernels.prefill_plan_pays(len(q_lens), max(q_lens), h_kv * n_rep, h_kv, DEV)
+    else:
+        num_cached, q_lens = [3000], [200]
+        assert not kernels.prefill_plan_pays(1, 200, h_kv * n_rep, h_kv, DEV)
+        assert kernels.prefill_plan_pays(1, 200, h_kv * n_rep, h_kv, DEV, max_keys=3200)
     nblk = sum(metadata.blocks_for(c + n, bs) for c, n in zip(num_cached, q_lens))
     perm = torch.randperm(nblk + 10, generator=g).tolist()
     tables, off = [], 0
