@@ -94,6 +94,9 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--layout", choices=("head_major", "slot_major"), default="head_major",
                    help="decode: the pool's physical layout -- head-major (default: a KV head's block is one "
                    "contiguous run) or the reference's contiguous [slots, H_kv, D] storage")
+    p.add_argument("--separate-write", action="store_true",
+                   help="mixed: the step's K/V write as its own launch (ir_kv_scatter) instead of inside the "
+                        "prefill launch")
     p.add_argument("--overlap", action="store_true",
                    help="mixed: decode and prefill on two streams (default: one stream, measured faster)")
     p.add_argument("--copy-calib-mib", type=int, default=0,
@@ -415,11 +418,11 @@ def _bench_prefill(args) -> dict:
 
 
 def _bench_mixed(args) -> dict:
-    """One 28-layer mixed step (scatter + decode + prefill per layer) per graph replay."""
+    """One 28-layer mixed step (K/V write, prefill and decode per layer) per graph replay."""
     from infrared_amd.mixed_step import MixedStep, make_mixed_case
 
     cfg, pool, batch, inputs = make_mixed_case("qwen7b-mixed", "cuda")
-    step = MixedStep(pool, batch, inputs, cfg.scale, overlap=args.overlap)
+    step = MixedStep(pool, batch, inputs, cfg.scale, overlap=args.overlap, fused=not args.separate_write)
     step.capture()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     warm_ms, warm = 0.0, 0
@@ -482,6 +485,7 @@ def _bench_mixed(args) -> dict:
                    f"{cfg.num_q_heads}q/{cfg.num_kv_heads}kv heads, head_dim {cfg.head_dim}, block {cfg.block_size}",
                    "decode_kv_bytes_per_step": dec_bytes, "prefill_flops_per_step": pre_flops,
                    "scatter_bytes_per_step": scatter_bytes, "overlap_streams": args.overlap,
+                   "kv_write": "own launch" if not step.fused else "inside the prefill launch",
                    "replays": n},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "measured_peak": _measured_peak("hbm"),

@@ -52,8 +52,10 @@ enum {
   IR_ERR_BLOCK_RANGE = 2,    /* block id outside [0, num_blocks) (block masked) */
   IR_ERR_CONTEXT_RANGE = 4,  /* context_len > max_blocks*block_size (clamped) or < 0 */
   IR_ERR_GATHER_RANGE = 8,   /* gather slot outside [0, num_slots) (key masked) */
-  IR_ERR_PLAN = 16           /* a decode plan with sequence pairs run without IR_PLAN_SHARE_GROUPS
+  IR_ERR_PLAN = 16,          /* a decode plan with sequence pairs run without IR_PLAN_SHARE_GROUPS
                                 (nothing written) */
+  IR_ERR_WRITE_SLOT = 32     /* a fused prefill's new token written elsewhere than its block-table
+                                slot (the call attended the new row itself) */
 };
 
 /* flags of ir_paged_prefill_plan, ir_paged_decode_plan and ir_paged_decode_planned */
@@ -417,6 +419,17 @@ int ir_varlen_form_tables(const int64_t* gather_slots, int64_t gs_k_stride, cons
  * IR_ERR_CONTEXT_RANGE and are clamped; a bad block id sets IR_ERR_BLOCK_RANGE and
  * that block's keys read as zeros. head_dim in {64, 128}; dtype bf16 or f16 (fp32 returns
  * IR_EUNSUPPORTED: use ir_paged_attention_masked).
+ * Fused K/V write (the step's PagedKVPool.write folded into the call; k_new null: none):
+ *   k_new, v_new: [n_write, num_kv_heads, head_dim] (strides token, head in elements;
+ *                 16-byte aligned, 16-byte strides), rows written to the caches at
+ *                 write_slots[row] (int64 [n_write]; a negative slot is skipped, one
+ *                 past the pool is flagged IR_ERR_SLOT_RANGE), as ir_kv_scatter would --
+ *                 by workgroups of the same launch, so the caches are written here.
+ *   src_row0:     rows src_row0 .. src_row0 + total_q - 1 are this call's query tokens
+ *                 in packed order; their keys (positions >= q_start[b]) are read from
+ *                 those rows, not from the pool. Equal to ir_kv_scatter followed by the
+ *                 unfused call when each such row's write slot is its block-table slot;
+ *                 a row whose slot differs sets IR_ERR_WRITE_SLOT.
  */
 int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
                      const void* k_cache, const void* v_cache, int64_t cache_slot_stride,
@@ -426,6 +439,9 @@ int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
                      int total_q, int max_q_len, void* out, int64_t out_tok_stride,
                      int64_t out_head_stride, int num_q_heads, int num_kv_heads, int head_dim,
                      float scale, int dtype, void* plan, int64_t plan_bytes,
+                     const void* k_new, int64_t k_new_tok_stride, int64_t k_new_head_stride,
+                     const void* v_new, int64_t v_new_tok_stride, int64_t v_new_head_stride,
+                     const int64_t* write_slots, int64_t n_write, int64_t src_row0,
                      int32_t* err_flags, ir_stream_t stream);
 
 /*

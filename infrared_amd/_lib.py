@@ -25,6 +25,7 @@ ERR_BLOCK_RANGE = 2
 ERR_CONTEXT_RANGE = 4
 ERR_GATHER_RANGE = 8
 ERR_PLAN = 16
+ERR_WRITE_SLOT = 32
 
 _c_i32, _c_i64, _c_f32, _c_p = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
@@ -92,7 +93,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_i32,
         [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i64, _c_i32,
          _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_f32,
-         _c_i32, _c_p, _c_i64, _c_p, _c_p],
+         _c_i32, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p],
     ),
     "ir_decode_form": (
         _c_i32,

@@ -109,7 +109,58 @@ struct PrefillArgs {
   float* ws_o;        // partial rows [piece][kv head][column][D]
   float* ws_ml;       // (max, sum) of each partial row
   int64_t n_items_grid;  // workgroups of a planned call (plan entries)
+  // Fused K/V write (k_new null: none). Workgroups n_work, n_work + 1, ... of
+  // the grid copy rows [0, n_write) of k_new / v_new ([rows, H_kv, D], strides
+  // in elements) to the pool at write_slots[row]; the attending workgroups read
+  // a sequence's own new keys (positions >= q_start[b]) from row src_row0 +
+  // cu_q[b] + (position - q_start[b]) of k_new / v_new instead of the pool.
+  const void* k_new;
+  const void* v_new;
+  int64_t kn_tok, kn_head, vn_tok, vn_head;
+  const int64_t* write_slots;
+  int64_t n_write, src_row0;
+  int64_t n_work;  // attending workgroups (the grid less the writers)
 };
+
+// 16-byte pieces a writer lane moves, all loads in flight before any store.
+constexpr int kWritePieces = 4;
+
+// A writer workgroup of a fused call: its share of the rows x KV heads x
+// 16-byte pieces, copied from k_new / v_new to the pool (kv_scatter's rules:
+// a negative slot is skipped, a slot past the pool is flagged and skipped).
+template <int D, int NT>
+__device__ __forceinline__ void prefill_write_rows(const PrefillArgs& a, int64_t wg) {
+  constexpr int P = D / 8;  // 16-byte pieces of one (row, head) of 16-bit elements
+  const int64_t per_row = (int64_t)a.num_kv_heads * P;
+  const int64_t total = a.n_write * per_row;
+  const int64_t num_slots = a.num_blocks * a.bs;
+  const int64_t first = wg * (NT * kWritePieces) + threadIdx.x;
+  int64_t slot[kWritePieces], coff[kWritePieces];
+  u32x4 kx[kWritePieces], vx[kWritePieces];
+#pragma unroll
+  for (int u = 0; u < kWritePieces; ++u) {
+    const int64_t i = first + (int64_t)u * NT;
+    const bool in = i < total;
+    const int64_t ii = in ? i : 0;  // row 0 exists (n_write >= 1): loaded, never stored
+    const int64_t row = ii / per_row;
+    const int rem = (int)(ii - row * per_row);
+    const int h = rem / P, part = rem - h * P;
+    slot[u] = in ? a.write_slots[row] : -1;
+    kx[u] = *(const u32x4*)((const uint16_t*)a.k_new + row * a.kn_tok + h * a.kn_head + part * 8);
+    vx[u] = *(const u32x4*)((const uint16_t*)a.v_new + row * a.vn_tok + h * a.vn_head + part * 8);
+    coff[u] = h * a.c_head + part * 8;
+  }
+#pragma unroll
+  for (int u = 0; u < kWritePieces; ++u) {
+    if (slot[u] < 0) continue;  // padding sentinel
+    if (slot[u] >= num_slots) {
+      flag_error(a.err, IR_ERR_SLOT_RANGE);
+      continue;
+    }
+    *(u32x4*)((uint16_t*)a.kc + slot[u] * a.c_slot + coff[u]) = kx[u];
+    *(u32x4*)((uint16_t*)a.vc + slot[u] * a.c_slot + coff[u]) = vx[u];
+  }
+}
 
 template <int D, int NW_ = 8, int CT_ = 2>
 struct PShape {
@@ -135,7 +186,7 @@ struct PShape {
 // and <= 256 registers, so two 4-wavefront workgroups share a CU).
 constexpr int kLockstep = 0, kRing2 = 2;
 
-template <int DT, int D, bool FAST, int NW, int CTW, int SCHED>
+template <int DT, int D, bool FAST, int NW, int CTW, int SCHED, bool FUSED = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 8 || SCHED == kRing2 ? 2 : 1)))
 void paged_prefill_kernel(PrefillArgs a) {
   typedef PShape<D, NW, CTW> S;
@@ -149,6 +200,11 @@ void paged_prefill_kernel(PrefillArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
   const int TQ = a.tq;
+
+  if (FUSED && blockIdx.x >= a.n_work) {  // a writer of a fused call
+    prefill_write_rows<D, NT>(a, blockIdx.x - a.n_work);
+    return;
+  }
 
   // ---- which (query block, KV head, sequence) and which piece of its keys:
   // plan entry i when a plan is given, else the last query blocks (most keys
@@ -275,11 +331,36 @@ void paged_prefill_kernel(PrefillArgs a) {
   // through the next tile's math instead of being waited for at once
   bool kuse[S::KPT];
   // Global loads of key tile kb into registers (whole workgroup, uniform call).
+  // In a fused call, a tile holding the sequence's new keys reads those keys
+  // from the call's new rows (the writers fill their slots concurrently).
+  const uint16_t* kn = a.k_new ? (const uint16_t*)a.k_new + (int64_t)kvh * a.kn_head : nullptr;
+  const uint16_t* vn = a.v_new ? (const uint16_t*)a.v_new + (int64_t)kvh * a.vn_head : nullptr;
+  const int64_t new_row0 = a.src_row0 + q_lo - p0;  // row of new key k: new_row0 + k
   auto load_regs = [&](int kb) {
     const int k0 = kb * BN;
     const int k_last = min(k0 + BN, kmax) - 1;
     const int last_blk = FAST ? k_last >> a.bs_shift : k_last / a.bs;
     if (last_blk >= bt_base + kBtCache) fill_bt(FAST ? k0 >> a.bs_shift : k0 / a.bs);
+    if (FUSED && k0 + BN > p0) {  // uniform: new keys in this tile
+#pragma unroll
+      for (int i = 0; i < S::KPT; ++i) {
+        const int q = tid + NT * i;
+        if (S::KCH % NT == 0 || q < S::KCH) {
+          const int key = q / (D / 8), part = q % (D / 8);
+          const int kk = k0 + key;
+          bool use;
+          const int64_t sl = slot_of(kk, use);
+          const bool fresh = kk >= p0 && kk < kmax;
+          const int64_t row = new_row0 + kk;
+          const uint16_t* kp = fresh ? kn + row * a.kn_tok + part * 8 : kc + sl + part * 8;
+          const uint16_t* vp = fresh ? vn + row * a.vn_tok + part * 8 : vc + sl + part * 8;
+          kreg[i] = *(const u32x4*)kp;
+          vreg[i] = *(const u32x4*)vp;
+          kuse[i] = use;
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < S::KPT; ++i) {
       const int q = tid + NT * i;
@@ -532,6 +613,18 @@ void paged_prefill_kernel(PrefillArgs a) {
     }
   }
   if (bad) flag_error(a.err, IR_ERR_BLOCK_RANGE);
+  if (FUSED && kvh == 0 && part == 0 && tid < TQ && tq0 + tid < q_len) {
+    // this block's new tokens (checked once, by the KV head 0 workgroups):
+    // each one's write slot must be the slot its block table gives it, which
+    // the workgroups that read it as a key took it to be (a check after the
+    // walk, off its loads' path)
+    const int pos = p0 + tq0 + tid;
+    const int blk = pos / a.bs;
+    const int32_t bid = blk < a.max_blocks ? bt_row[blk] : -1;
+    const int64_t ws = a.write_slots[a.src_row0 + q_lo + tq0 + tid];
+    if (bid >= 0 && (int64_t)bid < a.num_blocks && ws != (int64_t)bid * a.bs + (pos - blk * a.bs))
+      flag_error(a.err, IR_ERR_WRITE_SLOT);
+  }
 
   if (nparts == 1) {
     // ---- normalise and store: lane (g, c) register r of d tile dt = output
@@ -1061,37 +1154,63 @@ PlanLayout plan_layout(const PrefillGeometry& g, int num_seqs, int num_kv_heads,
 }
 
 template <int DT, int D>
-int launch_prefill(const PrefillArgs& a, int sched, hipStream_t s) {
+int launch_prefill(PrefillArgs a, int sched, hipStream_t s) {
   const int64_t grid = a.items ? a.n_items_grid : (int64_t)a.n_qblocks * a.num_kv_heads * a.num_seqs;
   if (grid <= 0) return ok();
   if (grid > 0x7fffffff) return fail(IR_EINVAL, "ir_paged_prefill: grid of %lld workgroups too large", (long long)grid);
+  a.n_work = grid;
+  // a fused call's writers follow the attending workgroups (so the plan's
+  // placement of those is unchanged): enough for every row x head x piece
+  auto writers = [&](int nt) -> int64_t {
+    if (a.k_new == nullptr) return 0;
+    const int64_t pieces = a.n_write * a.num_kv_heads * (D / 8);
+    return (pieces + (int64_t)nt * kWritePieces - 1) / ((int64_t)nt * kWritePieces);
+  };
   // fast addressing: slot and stride below 2^23 (24-bit products) and every
   // element offset of the layer below 2^31
   const int64_t slots = a.num_blocks * a.bs;
   const bool fast = a.bs_shift >= 0 && slots < (1 << 23) && a.c_slot < (1 << 23) &&
                     (slots * a.c_slot + a.c_head * a.num_kv_heads) < ((int64_t)1 << 31);
-  const dim3 g((unsigned)grid);
-  if (a.nw == 4 && !a.items && grid <= device_cus() && prefill_knobs().split) {
+  if (grid + writers(256) > 0x7fffffff) return fail(IR_EINVAL, "ir_paged_prefill: too many rows to write");
+  const bool split = a.nw == 4 && !a.items && grid <= device_cus() && prefill_knobs().split;
+  if (a.k_new != nullptr && !split) {
+    // The write as its own launch first: a fused instance of the 4- and
+    // 8-wavefront loops needs more registers than they have to spare (the
+    // 4-wavefront one measured 10% slower, its spilling variant more).
+    const int rc = ir_kv_scatter(a.k_new, a.kn_tok, a.kn_head, a.v_new, a.vn_tok, a.vn_head, (void*)a.kc,
+                                 (void*)a.vc, a.c_slot, a.c_head, a.num_blocks * a.bs, a.write_slots, a.n_write,
+                                 a.num_kv_heads, D, DT, a.err, (ir_stream_t)s);
+    if (rc != IR_OK) return rc;
+    a.k_new = a.v_new = nullptr;
+  }
+  const bool fused = a.k_new != nullptr;
+#define IR_PREFILL_LAUNCH(NW_, CT_, SCHED_, NT_)                                                            \
+  do {                                                                                                     \
+    const dim3 block(NT_), g((unsigned)(grid + writers(NT_)));                                              \
+    if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, NW_, CT_, SCHED_>), g, block, 0, s, a);  \
+    else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, NW_, CT_, SCHED_>), g, block, 0, s, a);      \
+  } while (0)
+  if (split) {
     // every workgroup alone on its CU: its 128 columns on 8 wavefronts of one
     // 16-column tile (two per SIMD) rather than 4 of two, so each walks its
-    // keys with half the per-wavefront work (the same arithmetic per column)
-    const dim3 block(PShape<D, 8, 1>::NT);
-    if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 1, kRing2>), g, block, 0, s, a);
-    else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 1, kRing2>), g, block, 0, s, a);
-  } else if (a.nw == 4) {
-    const dim3 block(PShape<D, 4>::NT);
-    if (sched == kRing2) {
-      if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 4, 2, kRing2>), g, block, 0, s, a);
-      else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 4, 2, kRing2>), g, block, 0, s, a);
+    // keys with half the per-wavefront work (the same arithmetic per column);
+    // a fused call's writers and new-key loads fit its registers
+    const dim3 block(PShape<D, 8, 1>::NT), g((unsigned)(grid + writers(PShape<D, 8, 1>::NT)));
+    if (fused) {
+      if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 1, kRing2, true>), g, block, 0, s, a);
+      else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 1, kRing2, true>), g, block, 0, s, a);
     } else {
-      if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 4, 2, kLockstep>), g, block, 0, s, a);
-      else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 4, 2, kLockstep>), g, block, 0, s, a);
+      if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 1, kRing2>), g, block, 0, s, a);
+      else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 1, kRing2>), g, block, 0, s, a);
     }
+  } else if (a.nw == 4 && sched == kRing2) {
+    IR_PREFILL_LAUNCH(4, 2, kRing2, (PShape<D, 4>::NT));
+  } else if (a.nw == 4) {
+    IR_PREFILL_LAUNCH(4, 2, kLockstep, (PShape<D, 4>::NT));
   } else {
-    const dim3 block(PShape<D, 8>::NT);
-    if (fast) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, true, 8, 2, kRing2>), g, block, 0, s, a);
-    else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, false, 8, 2, kRing2>), g, block, 0, s, a);
+    IR_PREFILL_LAUNCH(8, 2, kRing2, (PShape<D, 8>::NT));
   }
+#undef IR_PREFILL_LAUNCH
   return check_launch("ir_paged_prefill");
 }
 
@@ -1117,7 +1236,10 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
                                 int max_blocks_per_seq, const int32_t* cu_seqlens_q, const int32_t* q_start,
                                 int num_seqs, int total_q, int max_q_len, void* out, int64_t out_tok_stride,
                                 int64_t out_head_stride, int num_q_heads, int num_kv_heads, int head_dim, float scale,
-                                int dtype, void* plan, int64_t plan_bytes, int32_t* err_flags, ir_stream_t stream) {
+                                int dtype, void* plan, int64_t plan_bytes, const void* k_new,
+                                int64_t k_new_tok_stride, int64_t k_new_head_stride, const void* v_new,
+                                int64_t v_new_tok_stride, int64_t v_new_head_stride, const int64_t* write_slots,
+                                int64_t n_write, int64_t src_row0, int32_t* err_flags, ir_stream_t stream) {
   IR_REQUIRE(dtype == IR_DTYPE_BF16 || dtype == IR_DTYPE_F16 || dtype == IR_DTYPE_F32,
              "ir_paged_prefill: unknown dtype %d", dtype);
   if (dtype == IR_DTYPE_F32)
@@ -1181,6 +1303,25 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
     a.ws_ml = (float*)(pl + ly.off_ml);
     a.ws_o = (float*)(pl + ly.off_o);
     a.n_items_grid = ly.entries;
+  }
+  if (k_new != nullptr) {
+    IR_REQUIRE(v_new && write_slots, "ir_paged_prefill: k_new given without v_new or write_slots");
+    IR_REQUIRE(n_write >= 1 && src_row0 >= 0 && src_row0 + total_q <= n_write,
+               "ir_paged_prefill: the new rows [%lld, %lld) must lie within the %lld rows written",
+               (long long)src_row0, (long long)src_row0 + total_q, (long long)n_write);
+    IR_REQUIRE(aligned16(k_new) && aligned16(v_new) && (k_new_tok_stride * 2) % 16 == 0 &&
+                   (k_new_head_stride * 2) % 16 == 0 && (v_new_tok_stride * 2) % 16 == 0 &&
+                   (v_new_head_stride * 2) % 16 == 0,
+               "ir_paged_prefill: k_new / v_new must be 16-byte aligned with 16-byte strides");
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.kn_tok = k_new_tok_stride;
+    a.kn_head = k_new_head_stride;
+    a.vn_tok = v_new_tok_stride;
+    a.vn_head = v_new_head_stride;
+    a.write_slots = write_slots;
+    a.n_write = n_write;
+    a.src_row0 = src_row0;
   }
   a.out = out;
   a.o_tok = out_tok_stride;

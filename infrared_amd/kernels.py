@@ -574,6 +574,8 @@ def paged_prefill(
     out: torch.Tensor | None = None,
     err_flags: torch.Tensor | None = None,
     plan: PrefillPlan | None = None,
+    new_kv: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
+    src_row0: int = 0,
 ) -> torch.Tensor:
     """Causal paged attention for packed query chunks: ``q`` ``[total_q, H_q, D]``.
 
@@ -583,6 +585,12 @@ def paged_prefill(
     bounds the per-sequence query counts (host value, sizes the grid).
     ``plan``: the :func:`prefill_plan` of this metadata and shapes (heaviest
     work first, the heaviest items cut into merged key-range pieces).
+    ``new_kv``: ``(k, v, slots)`` -- the step's new rows ``[N, H_kv, D]`` and
+    their int64 write slots ``[N]`` -- written into the caches by the same
+    launch (what :func:`kv_scatter` would do first); rows ``src_row0 ..
+    src_row0 + total_q - 1`` are this call's query tokens, whose keys are then
+    read from those rows (``ERR_WRITE_SLOT`` is flagged where a token's write
+    slot is not its block-table slot).
     """
     dev = require_device(q, k_cache, v_cache, block_tables, cu_seqlens_q, q_start)
     _cache_layer("paged_prefill", k_cache)
@@ -608,13 +616,27 @@ def paged_prefill(
             raise RuntimeError("paged_prefill: the plan was built for other shapes")
     if out is None:
         out = torch.empty(total_q, hq, d, dtype=q.dtype, device=dev)
+    kn = vn = slots = None
+    n_write = 0
+    if new_kv is not None:
+        kn, vn, slots = new_kv
+        require_device(q, kn, vn, slots)
+        n_write = kn.shape[0]
+        if (kn.shape != (n_write, h_kv, d) or vn.shape != kn.shape or kn.dtype != q.dtype or vn.dtype != q.dtype
+                or slots.dtype != torch.int64 or slots.shape != (n_write,)):
+            raise RuntimeError("paged_prefill: new_kv must be (k, v [N, H_kv, D] of q's dtype, slots int64 [N])")
+        _last_dim_contiguous("paged_prefill new k", kn)
+        _last_dim_contiguous("paged_prefill new v", vn)
+        slots = slots.contiguous()
     rc = lib().ir_paged_prefill(
         ptr(q), q.stride(0), q.stride(1), ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
         k_cache.shape[0] // block_size, block_size, ptr(block_tables), block_tables.stride(0),
         block_tables.shape[1], ptr(cu_seqlens_q), ptr(q_start), b, total_q, int(max_q_len), ptr(out),
         out.stride(0), out.stride(1), hq, h_kv, d, float(scale), dtype_code(q.dtype),
-        None if plan is None else ptr(plan.buf), 0 if plan is None else plan.buf.numel(), ptr(err_flags),
-        stream_ptr(dev),
+        None if plan is None else ptr(plan.buf), 0 if plan is None else plan.buf.numel(),
+        ptr(kn), 0 if kn is None else kn.stride(0), 0 if kn is None else kn.stride(1),
+        ptr(vn), 0 if vn is None else vn.stride(0), 0 if vn is None else vn.stride(1),
+        ptr(slots), n_write, int(src_row0), ptr(err_flags), stream_ptr(dev),
     )
     check(rc, "ir_paged_prefill")
     return out

@@ -5,18 +5,22 @@ The reference's mixed step (``infrared/engine/paged_engine.py:461-516``) packs
 all scheduled query tokens into one ``B = 1`` frame and attends with a
 quadratic varlen mask (``infrared/model/inputs.py:57-85``) through the paged
 seam (``infrared/model/triton_attention.py:81-107``), layer after layer. Here
-each layer's attention work is three kernel launches on the step's own
+each layer's attention work is two kernel launches on the step's own
 metadata:
 
-1. ``ir_kv_scatter`` of the step's new K/V rows (decode tokens first, then the
-   chunk tokens) into the pool at ``write_slots``;
+1. ``ir_paged_prefill`` for the chunks (causal after their cached prefix),
+   whose launch also writes the step's new K/V rows (decode tokens first, then
+   the chunk tokens) into the pool at ``write_slots`` -- the K/V write of the
+   reference's ``PagedKVPool.write`` -- while its attending workgroups read
+   the chunks' own new keys from those rows;
 2. the decode of the one-token rows over their block tables: on the balanced
    plan that ``ir_paged_decode_plan`` builds once at the start of the step
    (``ir_paged_decode_planned`` per layer) when the rows fill the device, else
-   ``ir_paged_decode``'s fixed split-KV partitions;
-3. ``ir_paged_prefill`` for the chunks (causal after their cached prefix).
+   ``ir_paged_decode``'s fixed split-KV partitions. It follows the prefill,
+   which has written its rows' new tokens.
 
-By default the three run on one stream. With ``overlap=True`` the decode
+With ``fused=False`` the write is its own launch (``ir_kv_scatter``) ahead of
+the decode and then the prefill. With ``overlap=True`` (unfused) the decode
 rows' scatter runs first, then the stream forks: the decode (HBM-bound) on
 one branch, the chunks' scatter and prefill (MFMA-bound) on the other, joined
 before the next layer; captured, they become parallel graph branches (both
@@ -152,9 +156,10 @@ class MixedStep:
     """
 
     def __init__(self, pool: PagedKVPool, batch: MixedBatch, inputs: MixedInputs, scale: float, *,
-                 overlap: bool = False) -> None:
+                 overlap: bool = False, fused: bool = True) -> None:
         self.pool, self.batch, self.inputs, self.scale = pool, batch, inputs, scale
         self.overlap = overlap
+        self.fused = fused and not overlap
         dev = pool.device
         self.out_dec = torch.empty_like(inputs.q_dec)
         self.out_pre = torch.empty_like(inputs.q_pre)
@@ -197,15 +202,23 @@ class MixedStep:
             out=self.out_dec[layer], workspace=self.workspace, err_flags=self.err, counters=self.counters,
         )
 
-    def _prefill(self, layer: int) -> None:
+    def _prefill(self, layer: int, fused: bool = False) -> None:
         b, inp, pool = self.batch, self.inputs, self.pool
         kernels.paged_prefill(
             inp.q_pre[layer], pool.k[layer], pool.v[layer], b.pre_tables, b.cu_seqlens_q, b.q_start, b.max_q_len,
             pool.block_size, self.scale, out=self.out_pre[layer], err_flags=self.err, plan=self.plan_pre,
+            new_kv=(inp.k_new[layer], inp.v_new[layer], b.write_slots) if fused else None,
+            src_row0=inp.q_dec.shape[1],
         )
 
     def _layer(self, layer: int) -> None:
         b, inp, pool = self.batch, self.inputs, self.pool
+        if self.fused:
+            # the prefill launch writes every new row (the decode rows' too)
+            # and reads the chunks' own keys from them; the decode follows
+            self._prefill(layer, fused=True)
+            self._decode(layer)
+            return
         if self._side is None:
             kernels.kv_scatter(pool.k[layer], pool.v[layer], inp.k_new[layer], inp.v_new[layer], b.write_slots,
                                self.err)

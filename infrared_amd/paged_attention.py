@@ -67,17 +67,19 @@ def paged_attention(
 
     ``q`` ``[B, Sq, H, D]`` (RoPE applied); ``k``/``v`` ``[B, Sq, H_kv, D]``;
     ``mask`` ``[B, 1, Sq, T]`` additive (may be ``None`` on the block-table path).
-    Returns ``[B, Sq, H, D]``.
+    Returns ``[B, Sq, H, D]``. Where the call runs the chunked-prefill kernel
+    the write is part of that launch (``ir_paged_prefill``'s fused write: the
+    kernel reads its own new keys from ``k`` / ``v``); elsewhere
+    ``pool.write`` runs first.
     """
-    pool = paged.pool
     h_kv, d = k.shape[-2], k.shape[-1]
     b, sq, hq, dq = q.shape
     if dq != d or hq != h_kv * n_rep:
         raise RuntimeError(
             f"paged_attention: q {tuple(q.shape)} inconsistent with k {tuple(k.shape)} and n_rep={n_rep}"
         )
-    pool.write(layer_idx, k.reshape(-1, h_kv, d), v.reshape(-1, h_kv, d), paged.write_slots)
-    return _attend(q, paged, mask, layer_idx, scale)
+    return _attend(q, paged, mask, layer_idx, scale,
+                   new_kv=(k.reshape(-1, h_kv, d), v.reshape(-1, h_kv, d), paged.write_slots))
 
 
 def rope_paged_attention(
@@ -115,12 +117,20 @@ def rope_paged_attention(
     return _attend(q_rot, paged, mask, layer_idx, scale)
 
 
-def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, scale: float) -> torch.Tensor:
-    """Attention over the pool (this step's K/V already written)."""
+def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, scale: float,
+            new_kv: tuple | None = None) -> torch.Tensor:
+    """Attention over the pool. ``new_kv`` = (k rows, v rows, write slots) of
+    this step, not yet written: the chunked-prefill paths fold the write into
+    their launch, every other path writes them first (``pool.write``)."""
     pool = paged.pool
     b, sq = q.shape[:2]
     k_layer, v_layer = pool.k[layer_idx], pool.v[layer_idx]
     err = getattr(pool, "err_flags", None)
+    fusable = new_kv is not None and _fusable(pool, layer_idx, new_kv)
+
+    def write():
+        if new_kv is not None:
+            pool.write(layer_idx, *new_kv)
 
     block_tables = getattr(paged, "block_tables", None)
     context_lens = getattr(paged, "context_lens", None)
@@ -134,12 +144,16 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
         and q.dtype in (torch.bfloat16, torch.float16)
     ):
         split = getattr(paged, "row_split", None)
+        if not fusable:
+            write()
         if split is not None:
-            out = _split_step(q, pool, layer_idx, split, scale, err)
+            out = _split_step(q, pool, layer_idx, split, scale, err, new_kv if fusable else None)
         else:
             max_q = getattr(paged, "max_q_len", 0) or b * sq
-            out = _prefill(q, pool, layer_idx, block_tables, cu_seqlens_q, q_start, max_q, paged, scale, err)
+            out = _prefill(q, pool, layer_idx, block_tables, cu_seqlens_q, q_start, max_q, paged, scale, err,
+                           new_kv=new_kv if fusable else None)
     elif paged.use_triton and block_tables is not None and context_lens is not None and sq == 1:
+        write()
         out = _decode(q, pool, layer_idx, block_tables, context_lens, paged, scale, err)
     else:
         if paged.gather_slots is None or mask is None:
@@ -159,6 +173,9 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
             # the reference's packed prefill / mixed-step frame: when it has
             # that form, run the chunked-prefill kernel over derived metadata
             vform = pool.reference_varlen_form(paged.gather_slots, mask)
+        if vform is None or not fusable:
+            write()
+            fusable = False
         verdict = form.verdict() if form is not None else None
         if form is not None and verdict is False:
             # the check's published verdict: not the decode form
@@ -177,10 +194,10 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
                     run_if=form.gate if verdict is None else None,
                 )
         elif vform is not None and vform.row_split is not None:
-            out = _split_step(q, pool, layer_idx, vform.row_split, scale, err)
+            out = _split_step(q, pool, layer_idx, vform.row_split, scale, err, new_kv if fusable else None)
         elif vform is not None:
             out = _prefill(q, pool, layer_idx, vform.block_tables, vform.cu_seqlens_q, vform.q_start,
-                           vform.max_q_len, vform, scale, err)
+                           vform.max_q_len, vform, scale, err, new_kv=new_kv if fusable else None)
         else:
             out = kernels.paged_attention_masked(
                 q, k_layer, v_layer, paged.gather_slots, mask, scale, err_flags=err
@@ -190,30 +207,55 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
     return out
 
 
-def _split_step(q, pool, layer_idx: int, split, scale: float, err) -> torch.Tensor:
+def _split_step(q, pool, layer_idx: int, split, scale: float, err, new_kv: tuple | None = None) -> torch.Tensor:
     """A packed step whose one-token rows (decodes) form one block of rows:
     those rows through the decode kernels (the balanced schedule when the batch
     fills the device), the other block through the prefill kernel, each kernel
     reading its rows of ``q`` and writing its rows of the output in place. A
     one-token row is a decode: it attends its whole history, as the prefill
-    kernel would. Returns ``q``'s shape."""
+    kernel would. ``new_kv`` (the step's rows, not yet written): the prefill
+    launch writes every row, the decode rows' included, and runs first.
+    Returns ``q``'s shape."""
     b, sq, hq, d = q.shape
     qf = q.reshape(b * sq, hq, d)
     out = torch.empty_like(qf)
     (d0, d1), (p0, p1) = split.dec_range, split.pre_range
+    if new_kv is not None and p1 <= p0:
+        pool.write(layer_idx, *new_kv)
+        new_kv = None
+    if new_kv is not None:
+        _prefill(qf[p0:p1].unsqueeze(0), pool, layer_idx, split.pre_tables, split.pre_cu, split.pre_q_start,
+                 split.pre_max_q, split, scale, err, out=out[p0:p1], new_kv=new_kv, src_row0=p0)
     _decode(qf[d0:d1].unsqueeze(1), pool, layer_idx, split.dec_tables, split.dec_ctx, split, scale, err,
             out=out[d0:d1])
-    if p1 > p0:
+    if new_kv is None and p1 > p0:
         _prefill(qf[p0:p1].unsqueeze(0), pool, layer_idx, split.pre_tables, split.pre_cu, split.pre_q_start,
                  split.pre_max_q, split, scale, err, out=out[p0:p1])
     return out.view(b, sq, hq, d)
 
 
+def _fusable(pool, layer_idx: int, new_kv: tuple) -> bool:
+    """Whether ``ir_paged_prefill`` can take the step's write: this package's
+    pool (the kernels address its layers), write slots present, rows of the
+    pool's dtype in 16-byte-aligned pieces."""
+    k, v, slots = new_kv
+    if slots is None or not hasattr(pool, "reference_varlen_form") or not torch.is_tensor(slots):
+        return False
+    kc = pool.k[layer_idx]
+    if k.dtype != kc.dtype or v.dtype != kc.dtype or kc.dtype not in (torch.bfloat16, torch.float16):
+        return False
+    if slots.dtype != torch.int64 or slots.dim() != 1 or slots.shape[0] != k.shape[0]:
+        return False
+    return all(t.stride(-1) == 1 and t.stride(0) % 8 == 0 and t.stride(1) % 8 == 0 and t.data_ptr() % 16 == 0
+               for t in (k, v))
+
+
 def _prefill(q, pool, layer_idx: int, block_tables, cu_seqlens_q, q_start, max_q: int, holder, scale: float,
-             err, out: torch.Tensor | None = None) -> torch.Tensor:
+             err, out: torch.Tensor | None = None, new_kv: tuple | None = None, src_row0: int = 0) -> torch.Tensor:
     """Packed query chunks over block tables: the chunked-prefill kernel with
-    the step's work plan (built by the first layer, cached on ``holder``).
-    Returns ``q``'s shape."""
+    the step's work plan (built by the first layer, cached on ``holder``) and,
+    given ``new_kv``, the step's K/V write in the same launch (``q``'s rows are
+    rows ``src_row0..`` of it). Returns ``q``'s shape."""
     b, sq, hq, d = q.shape
     h_kv = pool.k.shape[-2]
     nseq = q_start.shape[0]
@@ -229,7 +271,7 @@ def _prefill(q, pool, layer_idx: int, block_tables, cu_seqlens_q, q_start, max_q
             pass
     return kernels.paged_prefill(
         q.reshape(b * sq, hq, d), pool.k[layer_idx], pool.v[layer_idx], block_tables, cu_seqlens_q, q_start, max_q,
-        pool.block_size, scale, out=out, err_flags=err, plan=plan,
+        pool.block_size, scale, out=out, err_flags=err, plan=plan, new_kv=new_kv, src_row0=src_row0,
     ).view(b, sq, hq, d)
 
 

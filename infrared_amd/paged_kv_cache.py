@@ -46,6 +46,7 @@ from infrared_amd._lib import (
     ERR_GATHER_RANGE,
     ERR_PLAN,
     ERR_SLOT_RANGE,
+    ERR_WRITE_SLOT,
 )
 
 _ERR_NAMES = {
@@ -54,6 +55,7 @@ _ERR_NAMES = {
     ERR_CONTEXT_RANGE: "context length outside the block table",
     ERR_GATHER_RANGE: "gather slot outside the pool",
     ERR_PLAN: "decode plan with sequence pairs run without share groups",
+    ERR_WRITE_SLOT: "new token written elsewhere than its block-table slot",
 }
 
 

@@ -33,14 +33,17 @@ def _oracle_step(cfg, pool_k, pool_v, batch, inputs):
 
 
 @pytest.mark.parametrize("config,planned", [(SMALL, False), (WIDE, True)])
-@pytest.mark.parametrize("overlap", [False, True])
-def test_mixed_step_eager_matches_oracle_and_graph_replays(overlap, config, planned):
+@pytest.mark.parametrize("mode", ["fused-write", "separate-write", "overlap"])
+def test_mixed_step_eager_matches_oracle_and_graph_replays(mode, config, planned):
     """Both decode schedules inside the step: the fixed partitions (12 rows) and
-    the plan built once per step and captured with the layers (72 rows)."""
+    the plan built once per step and captured with the layers (72 rows); the
+    step's K/V write inside the prefill launch (the default), as its own
+    launch, and with the chunks on a second stream."""
     cfg, pool, batch, inputs = make_mixed_case(config, DEV)
     pk = [pool.k[i].cpu().clone() for i in range(cfg.num_layers)]
     pv = [pool.v[i].cpu().clone() for i in range(cfg.num_layers)]
-    step = MixedStep(pool, batch, inputs, cfg.scale, overlap=overlap)
+    step = MixedStep(pool, batch, inputs, cfg.scale, overlap=mode == "overlap", fused=mode == "fused-write")
+    assert step.fused == (mode == "fused-write")
     assert step.planned == planned
     step.eager()
     torch.cuda.synchronize()
