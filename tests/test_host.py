@@ -149,3 +149,48 @@ def test_block_tables_tensor_pads_with_block_zero():
     assert bt.dtype == torch.int32 and bt.tolist() == [[5, 6, 7, 0], [0, 0, 0, 0], [9, 0, 0, 0]]
     with pytest.raises(ValueError, match="longer than width"):
         metadata.block_tables_tensor([[1, 2, 3]], "cpu", 2)
+
+
+def test_prefill_plan_pays_for_long_contexts_on_any_grid():
+    """A call whose longest context exceeds PLAN_CUT_KEYS is planned whatever
+    its workgroup count (decided before the device is asked for its CUs)."""
+    from infrared_amd import kernels
+
+    keys = kernels.PLAN_CUT_KEYS
+    assert kernels.prefill_plan_pays(1, 200, 28, 4, "cpu", max_keys=keys + 1)
+    assert not kernels.prefill_plan_pays(0, 200, 28, 4, "cpu", max_keys=keys + 1)  # nothing to plan
+    assert not kernels.prefill_plan_pays(1, 200, 28, 5, "cpu", max_keys=keys + 1)  # heads not grouped
+
+
+def test_seam_folds_the_write_only_for_rows_the_prefill_kernel_can_take():
+    """The seam hands the step's rows to the prefill launch only for this
+    package's pool, 16-bit rows of the pool's dtype in 16-byte pieces and
+    int64 write slots; anything else is written by pool.write first."""
+    from infrared_amd.paged_attention import _fusable
+
+    class Pool:  # the attributes the check reads
+        def __init__(self, dtype):
+            self.k = torch.zeros(2, 64, 4, 128, dtype=dtype)
+
+        def reference_varlen_form(self):  # pragma: no cover - presence is what counts
+            pass
+
+    k = torch.zeros(10, 4, 128, dtype=torch.bfloat16)
+    v = torch.zeros_like(k)
+    slots = torch.arange(10, dtype=torch.int64)
+    pool = Pool(torch.bfloat16)
+    assert _fusable(pool, 1, (k, v, slots))
+    assert not _fusable(pool, 1, (k, v, None))
+    assert not _fusable(pool, 1, (k, v, slots.int()))
+    assert not _fusable(pool, 1, (k, v, slots[:9]))
+    assert not _fusable(pool, 1, (k.float(), v.float(), slots))
+    assert not _fusable(Pool(torch.float32), 1, (k.float(), v.float(), slots))
+    wide = torch.zeros(10, 4, 130, dtype=torch.bfloat16)[..., :128]  # rows 260 elements apart
+    assert not _fusable(pool, 1, (wide, wide, slots))
+    shifted = torch.zeros(10 * 512 + 1, dtype=torch.bfloat16)[1:].view(10, 4, 128)  # 2-byte aligned
+    assert not _fusable(pool, 1, (shifted, shifted, slots))
+
+    class ForeignPool:  # a pool without this package's kernels
+        k = pool.k
+
+    assert not _fusable(ForeignPool(), 1, (k, v, slots))
