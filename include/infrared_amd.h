@@ -371,8 +371,11 @@ int ir_decode_form(const int64_t* gather_slots, int64_t gs_b_stride, int64_t gs_
  *     from the HIP host allocator, at least 2*num_q + 9 int32) receives, from
  *     the device at the end of the call, info[0..4] at [0..4], then
  *     cu_seqlens_q[0..n] at [8..8+n] and q_start[0..n) at [9+n..9+2n)
- *     (n = info[1]; written only when info[0] is clear): after a stream
- *     synchronisation the host reads it in place. row_records: [4*num_q] int32
+ *     (n = info[1]; written only when info[0] is clear) and, last, once the
+ *     rest is visible to the host, `tag` at [7]: a host that waits for word 7
+ *     to hold a tag its earlier calls did not pass reads the whole record
+ *     without synchronising the stream (a stream synchronisation works too;
+ *     nothing is written when num_q is 0). row_records: [4*num_q] int32
  *     scratch, 16-byte aligned, zero before the first call; every call leaves
  *     it zero (calls sharing it must be stream-ordered).
  *   ir_varlen_form_tables: block_tables[i, j] = gather_slots[k_off_i + j*bs] / bs
@@ -384,7 +387,7 @@ int ir_varlen_form_scan(const void* mask, int64_t mask_q_stride, int64_t mask_k_
                         int num_q, int num_k, const int64_t* gather_slots, int64_t gs_k_stride, int block_size,
                         int64_t num_blocks, int32_t* row_records, int32_t* cu_seqlens_q, int32_t* q_start,
                         int32_t* seq_k_offsets, int32_t* info, int32_t* block_tables, int64_t tables_capacity,
-                        int32_t* host_record, int64_t host_capacity, ir_stream_t stream);
+                        int32_t* host_record, int64_t host_capacity, int32_t tag, ir_stream_t stream);
 int ir_varlen_form_tables(const int64_t* gather_slots, int64_t gs_k_stride, const int32_t* seq_k_offsets,
                           const int32_t* cu_seqlens_q, const int32_t* q_start, int num_seqs, int block_size,
                           int32_t* block_tables, int64_t bt_stride, int max_blocks_per_seq, ir_stream_t stream);

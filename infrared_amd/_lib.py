@@ -104,7 +104,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ir_varlen_form_scan": (
         _c_i32,
         [_c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i32, _c_i64, _c_p, _c_p, _c_p, _c_p,
-         _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p],
+         _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_p],
     ),
     "ir_varlen_form_tables": (
         _c_i32,
@@ -160,8 +160,17 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 
 def stream_ptr(device: torch.device) -> int:
-    """Raw handle of torch's current stream on ``device`` (captured under hipGraph capture)."""
-    return torch.cuda.current_stream(device).cuda_stream
+    """Raw handle of torch's current stream on ``device`` (the capturing stream
+    under hipGraph capture): the same handle as
+    ``torch.cuda.current_stream(device).cuda_stream``, read without building a
+    stream object."""
+    if _raw_stream is None:
+        return torch.cuda.current_stream(device).cuda_stream
+    index = device.index
+    return _raw_stream(torch.cuda.current_device() if index is None else index)
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -21,11 +21,13 @@
 // info[0]; the host then keeps the mask kernel, which reads the metadata as
 // given. With info[0] clear, the same call writes the block tables
 // bt_i[j] = gather_slots[k_off_i + j bs] / bs into a buffer of the caller's
-// (stride: the widest table, read on the device) when they fit, and copies
+// (stride: the widest table, read on the device) when they fit, and writes
 // the verdict, the sizes, cu_seqlens_q and q_start into pinned host memory
-// from the device; the chunked-prefill kernel over the tables attends exactly
-// the keys the mask allows. One synchronising read per step, no copy launched
-// and no launch after it (ir_varlen_form_tables writes tables that did not fit).
+// from the device, a caller's tag last; the chunked-prefill kernel over the
+// tables attends exactly the keys the mask allows. Two launches for frames of
+// up to 4,096 rows (the pass over the mask, then one that segments and checks),
+// three beyond; the host waits once, for the tag, and launches nothing after
+// it (ir_varlen_form_tables writes tables that did not fit).
 #include <algorithm>
 
 #include "common.hpp"
@@ -116,6 +118,13 @@ __device__ __forceinline__ void wave_rec_add(RowRec* rec, int r, int f, int l, i
   if ((threadIdx.x & 63) == 0) rec_add(rec, r, f, l, n, any_wrong);
 }
 
+// The scan's first kernel clears the verdict word and the workgroup ticket
+// the verification counts on (the kernels after it read them).
+__device__ __forceinline__ void clear_verdict(int32_t* info) {
+  info[0] = 0;
+  info[5] = 0;
+}
+
 // Contiguous masks: the flat [Q * K] array as 16-byte pieces, grid-stride.
 // A wavefront takes 64 * kFlatPieces consecutive pieces per pass (each load
 // instruction 1 KiB contiguous), all in flight before any is inspected. A
@@ -131,8 +140,10 @@ constexpr int kFlatThreads = 256;
 constexpr int kFlatPieces = 8;
 
 template <int DT, bool NARROW>
-__global__ __launch_bounds__(kFlatThreads) void varlen_flat_kernel(const u32x4* pieces, int64_t whole, int K, RowRec* rec) {
+__global__ __launch_bounds__(kFlatThreads) void varlen_flat_kernel(const u32x4* pieces, int64_t whole, int K, RowRec* rec,
+                                                                  int32_t* info) {
   constexpr int PER = DT == IR_DTYPE_F32 ? 4 : 8;
+  if (blockIdx.x == 0 && threadIdx.x == 0) clear_verdict(info);
   constexpr uint32_t M = kMinWord<DT>;
   const int lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * (kFlatThreads / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -259,7 +270,8 @@ __global__ __launch_bounds__(kFlatThreads) void varlen_flat_kernel(const u32x4* 
 // The array's last partial piece (Q * K not a multiple of a piece), element by
 // element, and strided masks: one workgroup per row.
 __global__ __launch_bounds__(64) void varlen_tail_kernel(const void* mask, int dtype, int64_t e_from, int64_t e_to,
-                                                          int K, RowRec* rec) {
+                                                          int K, RowRec* rec, int32_t* info) {
+  if (threadIdx.x == 0) clear_verdict(info);
   for (int64_t e = e_from + threadIdx.x; e < e_to; e += 64) {
     const float x = mask_value(mask, dtype, e);
     const int r = (int)(e / K), k = (int)(e - (int64_t)r * K);
@@ -269,9 +281,11 @@ __global__ __launch_bounds__(64) void varlen_tail_kernel(const void* mask, int d
 }
 
 __global__ __launch_bounds__(kScanThreads) void varlen_rows_strided_kernel(const void* mask, int dtype, int64_t m_q,
-                                                                          int64_t m_k, int K, RowRec* rec) {
+                                                                          int64_t m_k, int K, RowRec* rec,
+                                                                          int32_t* info) {
   __shared__ int s_first, s_last, s_count, s_wrong;
   const int r = blockIdx.x, tid = threadIdx.x;
+  if (r == 0 && tid == 0) clear_verdict(info);
   if (tid == 0) {
     s_first = K;
     s_last = -1;
@@ -336,7 +350,8 @@ __global__ __launch_bounds__(kSegThreads) void varlen_segments_kernel(RowRec* re
 #pragma unroll
     for (int j = 0; j <= kSegRows; ++j) {
       const int r = r0 - 1 + j;
-      x[j] = r >= 0 && r < Q ? rec[r] : RowRec{0, 0, 0, 0};
+      const RowRec y = rec[min(max(r, 0), Q - 1)];  // unconditional: the loads stay in flight together
+      x[j] = r >= 0 && r < Q ? y : RowRec{0, 0, 0, 0};
     }
     int lo[kSegRows + 1], hi[kSegRows + 1], start[kSegRows];
     range(x[0], lo[0], hi[0]);
@@ -414,14 +429,37 @@ __global__ __launch_bounds__(kSegThreads) void varlen_segments_kernel(RowRec* re
 // (W = max(info[3], 1); zero past the sequence's keys), when they fit in
 // `cap`. The last workgroup to finish (a ticket in info[5], which the
 // segmentation zeroes) publishes info[4] (tables written) and, into the host
-// record, the verdict, the sizes, cu_seqlens_q and q_start, then fences at
-// system scope.
+// record, the verdict, the sizes, cu_seqlens_q and q_start, then, after a
+// system-scope fence, the caller's tag, so a host that polls the tag reads a
+// whole record without synchronising the stream.
 constexpr int kCheckStage = 4096;
+
+// The host record, by the first wavefront of the (last) workgroup: the
+// verdict and the sizes at [0..4], cu_seqlens_q at [8..8+n] and q_start at
+// [9+n..9+2n) when the form holds, then, after a system-scope fence (the
+// wavefront's stores all complete before it goes on), `tag` at [7], so a host
+// that polls the tag reads a whole record. cu / q_start may point at LDS. The
+// other wavefronts return at once.
+__device__ void publish_record(int32_t* host, int bad, int nseq, int maxq, int width, bool written, const int32_t* cu,
+                               const int32_t* q_start, int32_t tag) {
+  const int lane = threadIdx.x;
+  if (lane >= 64) return;
+  if (lane < 7)
+    host[lane] = lane == 0 ? bad : lane == 1 ? nseq : lane == 2 ? maxq : lane == 3 ? width : lane == 4 ? (int)written : 0;
+  if (bad == 0 && nseq > 0) {
+    for (int i = lane; i <= nseq; i += 64) host[8 + i] = cu[i];
+    for (int i = lane; i < nseq; i += 64) host[9 + nseq + i] = q_start[i];
+  }
+  __threadfence_system();
+  __builtin_amdgcn_wave_barrier();
+  if (lane == 0) *(volatile int32_t*)&host[7] = tag;
+}
+
 __global__ __launch_bounds__(kScanThreads) void varlen_check_kernel(const int64_t* gs, int64_t gs_k,
                                                                    const int32_t* seq_lo, const int32_t* cu,
                                                                    const int32_t* q_start, int K, int bs,
                                                                    int64_t num_blocks, int32_t* info, int32_t* bt,
-                                                                   int cap, int32_t* host) {
+                                                                   int cap, int32_t* host, int32_t tag) {
   __shared__ int s_lo[kCheckStage];
   __shared__ int s_bad, s_last;
   const int tid = threadIdx.x;
@@ -475,14 +513,235 @@ __global__ __launch_bounds__(kScanThreads) void varlen_check_kernel(const int64_
   const int bad = atomicOr(&info[0], 0);  // every workgroup's verdict is in
   const bool ok = bad == 0 && nseq > 0;
   if (tid == 0) info[4] = ok && fits;
-  if (host == nullptr) return;
-  if (tid < 8)
-    host[tid] = tid == 0 ? bad : tid == 1 ? nseq : tid == 2 ? maxq : tid == 3 ? width : tid == 4 ? (int)(ok && fits) : 0;
-  if (ok) {
-    for (int i = tid; i <= nseq; i += kScanThreads) host[8 + i] = cu[i];
-    for (int i = tid; i < nseq; i += kScanThreads) host[9 + nseq + i] = q_start[i];
+  if (host != nullptr) publish_record(host, bad, nseq, maxq, width, ok && fits, cu, q_start, tag);
+}
+
+// Frames of at most kVerifyRows rows: the segmentation and the slot check in
+// one launch. Every workgroup segments the rows itself, in LDS, from the row
+// records (64 KiB at most, read by each), so no workgroup waits for another:
+// workgroup 0 writes cu_seqlens_q, q_start, the sequences' first keys and
+// info[1..3]; each workgroup checks its keys (grid-stride, at most one
+// workgroup per CU) and writes their block-table entries. The workgroups
+// count themselves, and the failed ones, in one ticket word (info[5], cleared
+// by the scan): the last to arrive knows the verdict from its ticket, writes
+// info[0] and info[4], zeroes the row records for the next call and publishes
+// the host record.
+//
+// The rules are the segmentation kernel's, and the check kernel's closed form
+// stated key by key, so that every slot a thread needs is loaded before the
+// segmentation is known: key k at position p of its sequence holds a block
+// head (>= 0, a multiple of bs, block id < num_blocks) when p % bs == 0 and
+// gather_slots[k - 1] + 1 otherwise -- by induction over each block, the same
+// as gather_slots[k] = bt[p / bs] * bs + p % bs with bt[j] the block id of the
+// sequence's key j * bs. A key at a block head writes that table entry.
+// Loads and LDS reads are issued unconditionally (indices clamped into range,
+// results selected after): a load under a per-lane condition ends in a wait for
+// it, which would serialise the record reads.
+constexpr int kVerifyThreads = 1024;
+constexpr int kVerifyRowsPer = 4;
+constexpr int kVerifyRows = kVerifyThreads * kVerifyRowsPer;
+constexpr int kTicketBad = 1 << 16;  // a failed workgroup's share of the ticket (grids of < 2^16)
+
+// slot / bs and slot % bs, in 32 bits when the slot allows
+__device__ __forceinline__ void slot_divmod(int64_t g, int bs, int64_t& q, int& r) {
+  if ((uint64_t)g < 0x80000000ull) {
+    const uint32_t u = (uint32_t)g, d = u / (uint32_t)bs;
+    q = d;
+    r = (int)(u - d * (uint32_t)bs);
+  } else {
+    q = g / bs;
+    r = (int)(g - q * bs);
   }
-  __threadfence_system();
+}
+
+__global__ __launch_bounds__(kVerifyThreads) void varlen_verify_kernel(RowRec* rec, int Q, const int64_t* gs,
+                                                                    int64_t gs_k, int K, int bs, int64_t num_blocks,
+                                                                    int32_t* cu, int32_t* q_start, int32_t* seq_lo,
+                                                                    int32_t* info, int32_t* bt, int cap,
+                                                                    int32_t* host, int32_t tag) {
+  constexpr int NW = kVerifyThreads / 64;
+  // rows' visible ranges (-1 when unusable), then the sequences' first rows and keys
+  __shared__ int32_t s_rlo[kVerifyRows], s_rhi[kVerifyRows], s_cu[kVerifyRows + 1], s_lo[kVerifyRows];
+  __shared__ int32_t s_qs[kVerifyRows];
+  __shared__ __align__(16) int s_cnt[kVerifyRowsPer * NW];
+  __shared__ int s_rows_bad, s_keys_bad, s_maxq, s_maxb, s_ticket;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // every load first: rows c * 256 + tid, and this thread's first key and the one before it
+  RowRec x[kVerifyRowsPer];
+#pragma unroll
+  for (int c = 0; c < kVerifyRowsPer; ++c) x[c] = rec[min(c * kVerifyThreads + tid, Q - 1)];
+  const int k_first = blockIdx.x * kVerifyThreads + tid;
+  int64_t g_here = -1, g_prev = -1;
+  if (K > 0) {  // uniform
+    const int kc = min(k_first, K - 1);
+    g_here = gs[(int64_t)kc * gs_k];
+    g_prev = gs[(int64_t)max(kc - 1, 0) * gs_k];
+  }
+  if (tid == 0) {
+    s_rows_bad = 0;
+    s_keys_bad = 0;
+    s_maxq = 0;
+    s_maxb = 0;
+  }
+#pragma unroll
+  for (int c = 0; c < kVerifyRowsPer; ++c) {
+    const int r = c * kVerifyThreads + tid;
+    const int first = kFirstBias - x[c].first_c, last = x[c].last1 - 1;
+    const bool unusable = x[c].wrong || x[c].count == 0 || last - first + 1 != x[c].count;
+    if (r < Q) {
+      s_rlo[r] = unusable ? -1 : first;
+      s_rhi[r] = unusable ? -1 : last;
+    }
+  }
+  __syncthreads();
+  // sequence starts, row by row against the row before; numbered in row order.
+  // Every range is read first and the rules are evaluated without branches.
+  int lo[kVerifyRowsPer], hi[kVerifyRowsPer];
+  uint32_t starts = 0;
+  int bad = 0, rank[kVerifyRowsPer];
+  {
+    int lo_p[kVerifyRowsPer], hi_p[kVerifyRowsPer];
+#pragma unroll
+    for (int c = 0; c < kVerifyRowsPer; ++c) {
+      const int rc = min(c * kVerifyThreads + tid, Q - 1), rp = max(rc - 1, 0);
+      lo[c] = s_rlo[rc];
+      hi[c] = s_rhi[rc];
+      lo_p[c] = s_rlo[rp];
+      hi_p[c] = s_rhi[rp];
+    }
+    const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int c = 0; c < kVerifyRowsPer; ++c) {
+      const int r = c * kVerifyThreads + tid;
+      const int in = r < Q, first = r == 0;
+      const int lp = first ? -1 : lo_p[c], hp = first ? -1 : hi_p[c];
+      const int st = in & (first | (lo[c] != lp));
+      // a row whose own scan failed; a new sequence's keys follow the last
+      // one's; a row of the same sequence sees one key more than the row before;
+      // the key axis ends with the last sequence
+      const int broken = st ? lo[c] != hp + 1 : hi[c] != hp + 1;
+      bad |= in & ((lo[c] < 0) | broken | ((r == Q - 1) & (hi[c] != K - 1)));
+      const uint64_t m = __ballot(st);
+      rank[c] = __popcll(m & below);
+      starts |= (uint32_t)st << c;
+      if (lane == 0) s_cnt[c * NW + wv] = __popcll(m);
+    }
+  }
+  if (bad) s_rows_bad = 1;
+  __syncthreads();
+  int cnt[kVerifyRowsPer * NW];
+#pragma unroll
+  for (int e = 0; e < kVerifyRowsPer * NW; e += 4) {
+    const int4 v = *(const int4*)&s_cnt[e];
+    cnt[e] = v.x;
+    cnt[e + 1] = v.y;
+    cnt[e + 2] = v.z;
+    cnt[e + 3] = v.w;
+  }
+  int nseq = 0;
+#pragma unroll
+  for (int c = 0; c < kVerifyRowsPer; ++c) {
+    int before = 0;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) before += v < wv ? cnt[c * NW + v] : 0;
+    if ((starts >> c) & 1u) {
+      const int i = nseq + before + rank[c];
+      s_cu[i] = c * kVerifyThreads + tid;
+      s_lo[i] = lo[c];
+      s_qs[i] = hi[c] - lo[c];
+    }
+#pragma unroll
+    for (int v = 0; v < NW; ++v) nseq += cnt[c * NW + v];
+  }
+  if (tid == 0) s_cu[nseq] = Q;
+  __syncthreads();
+  // the longest chunk and the widest table
+  int mq = 0, mb = 0;
+  for (int e = tid; e < nseq; e += kVerifyThreads) {
+    const int q = s_cu[e + 1] - s_cu[e];
+    mq = max(mq, q);
+    mb = max(mb, (s_qs[e] + q + bs - 1) / bs);
+  }
+  mq = wave_fold(mq, [](int a, int b) { return max(a, b); });
+  mb = wave_fold(mb, [](int a, int b) { return max(a, b); });
+  if (lane == 0) {
+    atomicMax(&s_maxq, mq);
+    atomicMax(&s_maxb, mb);
+  }
+  __syncthreads();
+  const int maxq = s_maxq, width = s_maxb;
+  const bool rows_ok = s_rows_bad == 0;  // uniform
+  if (blockIdx.x == 0) {
+    for (int e = tid; e <= nseq; e += kVerifyThreads) cu[e] = s_cu[e];
+    for (int e = tid; e < nseq; e += kVerifyThreads) {
+      q_start[e] = s_qs[e];
+      seq_lo[e] = s_lo[e];
+    }
+    if (tid == 0) {
+      info[1] = nseq;
+      info[2] = maxq;
+      info[3] = width;
+    }
+  }
+  const int w = max(width, 1);
+  const bool fits = rows_ok && bt != nullptr && (int64_t)nseq * w <= cap;
+  if (rows_ok) {
+    int keys_bad = 0;
+    for (int k = k_first; k < K; k += gridDim.x * kVerifyThreads) {
+      if (k != k_first) {
+        g_here = gs[(int64_t)k * gs_k];
+        g_prev = gs[(int64_t)(k - 1) * gs_k];
+      }
+      int a = 0, b = nseq - 1;  // the last sequence whose first key is <= k
+      while (a < b) {
+        const int mid = (a + b + 1) >> 1;
+        if (s_lo[mid] <= k) a = mid;
+        else b = mid - 1;
+      }
+      const int p = k - s_lo[a];
+      if (p < 0) {
+        keys_bad = 1;
+      } else if (p % bs == 0) {
+        int64_t id;
+        int off;
+        slot_divmod(g_here, bs, id, off);
+        if (g_here < 0 || off != 0 || id >= num_blocks) keys_bad = 1;
+        if (fits) bt[a * w + p / bs] = (int32_t)id;
+      } else if (g_here != g_prev + 1) {
+        keys_bad = 1;
+      }
+    }
+    if (keys_bad) s_keys_bad = 1;
+    if (fits) {
+      // entries past each sequence's last block
+      const unsigned n = (unsigned)(nseq * w);
+      for (unsigned e = blockIdx.x * kVerifyThreads + tid; e < n; e += gridDim.x * kVerifyThreads) {
+        const int sq = (int)(e / (unsigned)w), j = (int)(e - (unsigned)sq * w);
+        const int end = sq + 1 < nseq ? s_lo[sq + 1] : K;
+        if (j * bs >= end - s_lo[sq]) bt[e] = 0;
+      }
+    }
+  }
+  __syncthreads();
+  const bool failed = !rows_ok || s_keys_bad != 0;  // uniform
+  if (tid == 0) {
+    __threadfence();
+    s_ticket = atomicAdd(&info[5], 1 + (failed ? kTicketBad : 0)) + 1 + (failed ? kTicketBad : 0);
+  }
+  __syncthreads();
+  const int ticket = s_ticket;
+  if ((ticket & (kTicketBad - 1)) != (int)gridDim.x) return;
+  __threadfence();
+  const int verdict = ticket >= kTicketBad;  // some workgroup failed
+  const bool ok = verdict == 0 && nseq > 0;
+  if (tid == 0) {
+    info[0] = verdict;
+    info[4] = ok && fits;
+  }
+  if (host != nullptr) publish_record(host, verdict, nseq, maxq, width, ok && fits, s_cu, s_qs, tag);
+  // every workgroup has read the row records: leave them zero for the next
+  // scan (after the record, which the host may be waiting for)
+  for (int r = tid; r < Q; r += kVerifyThreads) rec[r] = RowRec{0, 0, 0, 0};
 }
 
 // Workgroup (i, y): entries of sequence i's table whose first key lies in
@@ -507,7 +766,7 @@ __global__ __launch_bounds__(kScanThreads) void varlen_tables_kernel(const int64
 // once (occupancy queried once per instance): its grid-stride loop then never
 // waits for a second round of workgroups to start after the first.
 template <int DT, bool NARROW>
-void launch_flat(const u32x4* pc, int64_t whole, int K, RowRec* rec, hipStream_t s) {
+void launch_flat(const u32x4* pc, int64_t whole, int K, RowRec* rec, int32_t* info, hipStream_t s) {
   static const int per_cu = [] {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&varlen_flat_kernel<DT, NARROW>),
@@ -519,7 +778,7 @@ void launch_flat(const u32x4* pc, int64_t whole, int K, RowRec* rec, hipStream_t
   const int64_t spans = (whole + 64 * kFlatPieces - 1) / (64 * kFlatPieces);
   const int64_t wgs = std::min<int64_t>((spans + kWaves - 1) / kWaves, (int64_t)device_cus() * per_cu);
   hipLaunchKernelGGL((varlen_flat_kernel<DT, NARROW>), dim3((unsigned)wgs), dim3(kFlatThreads), 0, s, pc, whole, K,
-                     rec);
+                     rec, info);
 }
 
 }  // namespace
@@ -532,7 +791,7 @@ extern "C" int ir_varlen_form_scan(const void* mask, int64_t mask_q_stride, int6
                                    int block_size, int64_t num_blocks, int32_t* row_records, int32_t* cu_seqlens_q,
                                    int32_t* q_start, int32_t* seq_k_offsets, int32_t* info, int32_t* block_tables,
                                    int64_t tables_capacity, int32_t* host_record, int64_t host_capacity,
-                                   ir_stream_t stream) {
+                                   int32_t tag, ir_stream_t stream) {
   IR_REQUIRE(dtype_bytes(mask_dtype) > 0, "ir_varlen_form_scan: unknown mask dtype %d", mask_dtype);
   IR_REQUIRE(num_q >= 0 && num_k >= 0 && block_size > 0 && num_blocks >= 0 && tables_capacity >= 0,
              "ir_varlen_form_scan: bad sizes");
@@ -562,29 +821,38 @@ extern "C" int ir_varlen_form_scan(const void* mask, int64_t mask_q_stride, int6
       const bool narrow = elems + 64 * kFlatPieces * per < ((int64_t)1 << 31);
       const u32x4* pc = (const u32x4*)mask;
       if (mask_dtype == IR_DTYPE_F32) {
-        if (narrow) launch_flat<IR_DTYPE_F32, true>(pc, whole, num_k, rec, s);
-        else launch_flat<IR_DTYPE_F32, false>(pc, whole, num_k, rec, s);
+        if (narrow) launch_flat<IR_DTYPE_F32, true>(pc, whole, num_k, rec, info, s);
+        else launch_flat<IR_DTYPE_F32, false>(pc, whole, num_k, rec, info, s);
       } else if (mask_dtype == IR_DTYPE_BF16) {
-        if (narrow) launch_flat<IR_DTYPE_BF16, true>(pc, whole, num_k, rec, s);
-        else launch_flat<IR_DTYPE_BF16, false>(pc, whole, num_k, rec, s);
+        if (narrow) launch_flat<IR_DTYPE_BF16, true>(pc, whole, num_k, rec, info, s);
+        else launch_flat<IR_DTYPE_BF16, false>(pc, whole, num_k, rec, info, s);
       } else {
-        if (narrow) launch_flat<IR_DTYPE_F16, true>(pc, whole, num_k, rec, s);
-        else launch_flat<IR_DTYPE_F16, false>(pc, whole, num_k, rec, s);
+        if (narrow) launch_flat<IR_DTYPE_F16, true>(pc, whole, num_k, rec, info, s);
+        else launch_flat<IR_DTYPE_F16, false>(pc, whole, num_k, rec, info, s);
       }
     }
     if (whole * per < elems)
       hipLaunchKernelGGL(varlen_tail_kernel, dim3(1), dim3(64), 0, s, mask, mask_dtype, whole * per, elems, num_k,
-                         rec);
+                         rec, info);
   } else {
     hipLaunchKernelGGL(varlen_rows_strided_kernel, dim3(num_q), dim3(kScanThreads), 0, s, mask, mask_dtype,
-                       mask_q_stride, mask_k_stride, num_k, rec);
+                       mask_q_stride, mask_k_stride, num_k, rec, info);
   }
-  hipLaunchKernelGGL(varlen_segments_kernel, dim3(1), dim3(kSegThreads), 0, s, rec, num_q, num_k, block_size,
-                     cu_seqlens_q, q_start, seq_k_offsets, info);
-  hipLaunchKernelGGL(varlen_check_kernel, dim3((unsigned)std::max((num_k + kScanThreads - 1) / kScanThreads, 1)),
-                     dim3(kScanThreads), 0, s, gather_slots, gs_k_stride, seq_k_offsets, cu_seqlens_q, q_start,
-                     num_k, block_size, num_blocks, info, tables_capacity > 0 ? block_tables : nullptr,
-                     (int)std::min<int64_t>(tables_capacity, INT32_MAX), host_dev);
+  int32_t* tables = tables_capacity > 0 ? block_tables : nullptr;
+  const int cap = (int)std::min<int64_t>(tables_capacity, INT32_MAX);
+  if (num_q <= kVerifyRows) {
+    const int wgs = std::min(std::max((num_k + kVerifyThreads - 1) / kVerifyThreads, 1), device_cus());
+    hipLaunchKernelGGL(varlen_verify_kernel, dim3((unsigned)wgs), dim3(kVerifyThreads), 0, s, rec, num_q,
+                       gather_slots, gs_k_stride, num_k, block_size, num_blocks, cu_seqlens_q, q_start, seq_k_offsets,
+                       info, tables, cap, host_dev, tag);
+  } else {
+    const int key_wgs = std::max((num_k + kScanThreads - 1) / kScanThreads, 1);
+    hipLaunchKernelGGL(varlen_segments_kernel, dim3(1), dim3(kSegThreads), 0, s, rec, num_q, num_k, block_size,
+                       cu_seqlens_q, q_start, seq_k_offsets, info);
+    hipLaunchKernelGGL(varlen_check_kernel, dim3((unsigned)key_wgs), dim3(kScanThreads), 0, s, gather_slots,
+                       gs_k_stride, seq_k_offsets, cu_seqlens_q, q_start, num_k, block_size, num_blocks, info, tables,
+                       cap, host_dev, tag);
+  }
   return check_launch("ir_varlen_form_scan");
 }
 

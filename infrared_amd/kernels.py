@@ -8,6 +8,7 @@ capture.
 
 from __future__ import annotations
 
+import itertools
 from dataclasses import dataclass
 
 import torch
@@ -703,19 +704,21 @@ def varlen_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int,
                 tables_capacity: int | None = None) -> VarlenForm | None:
     """Prefill metadata from the reference's packed prefill / mixed-step frame
     (``gather_slots`` ``[1, K]`` int64, mask ``[1, 1, Q, K]``), or ``None``
-    unless it has that form exactly (``ir_varlen_form_scan``). Synchronises
-    once: one call checks the mask and every slot on the device, derives the
+    unless it has that form exactly (``ir_varlen_form_scan``). Waits once:
+    one call checks the mask and every slot on the device, derives the
     sequences, writes their block tables (stride read on the device) and
     publishes the verdict, the sizes, the chunk starts and the prefixes into
-    ``staging``; the host reads them there after one stream synchronisation
-    and launches nothing more (``ir_varlen_form_tables`` only for tables
-    beyond the call's table capacity).
+    ``staging``, tagged; the host polls the tag there (no stream
+    synchronisation unless the wait runs long) and launches nothing more
+    (``ir_varlen_form_tables`` only for tables beyond the call's table
+    capacity).
 
     ``records``: int32 scratch of at least ``4 * Q`` elements, zero at rest
     (every call leaves it zero), 16-byte aligned; allocated zeroed when not
     given. ``staging``: a pinned host int32 tensor of at least
-    :func:`varlen_staging_size` ``(Q)`` elements, written by the device;
-    without one the record is copied back from device memory.
+    :func:`varlen_staging_size` ``(Q)`` elements, written by the device (one
+    caller at a time); without one the record is copied back from device
+    memory after a stream synchronisation.
     ``tables_capacity``: block-table entries the call may write (default
     ``max(2**17, 4 * (K // block_size + Q))``); wider tables are written by a
     second launch after the read."""
@@ -728,56 +731,87 @@ def varlen_form(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int,
     q = mask.shape[2]
     if q == 0 or k == 0 or q >= 2**31 or k >= 2**31:
         return None
-    i32 = dict(dtype=torch.int32, device=dev)
     if records is None:
-        records = torch.zeros(4 * q, **i32)
+        records = torch.zeros(4 * q, dtype=torch.int32, device=dev)
     if records.dtype != torch.int32 or records.numel() < 4 * q or records.data_ptr() % 16:
         raise RuntimeError(f"varlen_form: records must be int32 [>= {4 * q}], 16-byte aligned, zero at rest")
+    if staging is not None and (staging.dtype != torch.int32 or staging.is_cuda or not staging.is_contiguous()
+                                or staging.numel() < 2 * q + 9):
+        # (ir_varlen_form_scan refuses memory that is not pinned)
+        raise RuntimeError(f"varlen_form: staging must be a pinned contiguous int32 host tensor of >= {2 * q + 9}")
+    return varlen_form_checked(gather_slots, mask, block_size, num_blocks, records, staging,
+                               None if staging is None else staging.numpy(), tables_capacity)
+
+
+def varlen_form_checked(gather_slots: torch.Tensor, mask: torch.Tensor, block_size: int, num_blocks: int,
+                        records: torch.Tensor, staging: torch.Tensor | None, host=None,
+                        tables_capacity: int | None = None) -> VarlenForm | None:
+    """:func:`varlen_form` once its checks have passed: the frame's shapes and
+    dtypes (Q and K in [1, 2**31)), ``records`` and ``staging`` as that
+    function requires them, and ``host`` a numpy view of ``staging`` (``None``
+    without one). For a caller that holds its buffers across steps."""
+    dev = mask.device
+    q, k = mask.shape[2], mask.shape[3]
     # one allocation: info | cu | q_start | k_off | block tables (up to `cap`
     # entries); views are cut after the read, for what the form keeps
     o_cu, o_qs, o_ko, o_bt = _varlen_offsets(q)
     cap = max(1 << 17, 4 * (k // block_size + q)) if tables_capacity is None else max(int(tables_capacity), 0)
     cap = min(cap, 2**31 - 1)
-    buf = torch.empty(o_bt + cap, **i32)
+    buf = torch.empty(o_bt + cap, dtype=torch.int32, device=dev)
     base = buf.data_ptr()
     pinned = staging is not None
-    if pinned and (staging.dtype != torch.int32 or staging.is_cuda or not staging.is_contiguous()
-                   or staging.numel() < 2 * q + 9):
-        # (ir_varlen_form_scan refuses memory that is not pinned)
-        raise RuntimeError(f"varlen_form: staging must be a pinned contiguous int32 host tensor of >= {2 * q + 9}")
+    tag = (next(_record_tags) & 0x7FFFFFFF) or 1
     rc = lib().ir_varlen_form_scan(
-        ptr(mask), mask.stride(2), mask.stride(3), dtype_code(mask.dtype), q, k, ptr(gather_slots),
-        gather_slots.stride(1), block_size, num_blocks, ptr(records), base + 4 * o_cu, base + 4 * o_qs,
-        base + 4 * o_ko, base, base + 4 * o_bt, cap, ptr(staging) if pinned else None,
-        staging.numel() if pinned else 0, stream_ptr(dev),
+        mask.data_ptr(), mask.stride(2), mask.stride(3), dtype_code(mask.dtype), q, k, gather_slots.data_ptr(),
+        gather_slots.stride(1), block_size, num_blocks, records.data_ptr(), base + 4 * o_cu, base + 4 * o_qs,
+        base + 4 * o_ko, base, base + 4 * o_bt, cap, staging.data_ptr() if pinned else None,
+        staging.numel() if pinned else 0, tag, stream_ptr(dev),
     )
     check(rc, "ir_varlen_form_scan")
     if pinned:
-        torch.cuda.current_stream(dev).synchronize()
-        bad, nseq, max_q, width, written = staging[:5].tolist()
-        if bad or nseq <= 0:
-            return None
-        rec = staging[8 : 9 + 2 * nseq].tolist()
-        offs, prefixes = rec[: nseq + 1], rec[nseq + 1 :]
-    else:
-        host = buf[:o_ko].cpu()
+        await_record(host, 7, tag, dev)
         bad, nseq, max_q, width, written = host[:5].tolist()
         if bad or nseq <= 0:
             return None
-        offs, prefixes = host[o_cu : o_cu + nseq + 1].tolist(), host[o_qs : o_qs + nseq].tolist()
-    width = max(width, 1)
-    cu, q_start = buf[o_cu : o_cu + nseq + 1], buf[o_qs : o_qs + nseq]
-    if written:
-        bt = buf[o_bt : o_bt + nseq * width].view(nseq, width)
+        rec = host[8 : 9 + 2 * nseq].tolist()
+        offs, prefixes = rec[: nseq + 1], rec[nseq + 1 :]
     else:
-        bt = torch.empty(nseq, width, **i32)
+        rec = buf[:o_ko].cpu()
+        bad, nseq, max_q, width, written = rec[:5].tolist()
+        if bad or nseq <= 0:
+            return None
+        offs, prefixes = rec[o_cu : o_cu + nseq + 1].tolist(), rec[o_qs : o_qs + nseq].tolist()
+    width = max(width, 1)
+    cu = buf.as_strided((nseq + 1,), (1,), o_cu)
+    q_start = buf.as_strided((nseq,), (1,), o_qs)
+    if written:
+        bt = buf.as_strided((nseq, width), (width, 1), o_bt)
+    else:
+        bt = torch.empty(nseq, width, dtype=torch.int32, device=dev)
         rc = lib().ir_varlen_form_tables(
-            ptr(gather_slots), gather_slots.stride(1), base + 4 * o_ko, ptr(cu), ptr(q_start), nseq, block_size,
-            ptr(bt), bt.stride(0), width, stream_ptr(dev),
+            gather_slots.data_ptr(), gather_slots.stride(1), base + 4 * o_ko, cu.data_ptr(), q_start.data_ptr(),
+            nseq, block_size, bt.data_ptr(), bt.stride(0), width, stream_ptr(dev),
         )
         check(rc, "ir_varlen_form_tables")
     q_lens = tuple(b - a_ for a_, b in zip(offs, offs[1:]))
     return VarlenForm(bt, cu, q_start, max_q, q_lens, tuple(prefixes))
+
+
+_record_tags = itertools.count(1)  # tags of the device-written host records, never reused in a process
+RECORD_POLLS = 30_000  # polls of a host record (~2 ms) before a stream synchronisation instead
+
+
+def await_record(host, word: int, tag: int, dev: torch.device) -> None:
+    """Waits until ``host[word]`` (a numpy view of pinned memory the device
+    writes, the tag word last) holds ``tag``: polls it up to ``RECORD_POLLS``
+    times, which sees the record as soon as the device has written it, then
+    synchronises the stream; raises if the record is still not there."""
+    for _ in range(RECORD_POLLS):
+        if host[word] == tag:
+            return
+    torch.cuda.current_stream(dev).synchronize()
+    if host[word] != tag:
+        raise RuntimeError("the device wrote no record for this call")
 
 
 def _varlen_offsets(q: int) -> tuple[int, int, int, int]:

@@ -119,9 +119,10 @@ class PagedKVPool:
         # id(gather_slots), id(mask)): each holds the buffers its graph's
         # replays address and lives as long as the captured gather_slots
         self._captured_forms: dict[tuple, tuple] = {}
-        # the packed-form check's row records (zero at rest) and pinned read buffer
+        # the packed-form check's row records (zero at rest), pinned record and its numpy view
         self._varlen_records: torch.Tensor | None = None
         self._varlen_staging: torch.Tensor | None = None
+        self._varlen_host = None
         # the eager decode-form check's verdict, written by the device into
         # pinned memory as tag << 32 | flag (read without synchronising)
         self._verdict: torch.Tensor | None = None
@@ -282,9 +283,10 @@ class PagedKVPool:
         ``infrared/model/inputs.py:33-85``). ``ir_varlen_form_scan`` recovers
         ``cu_seqlens_q``, ``q_start`` and the block tables on the device and
         verifies the form exactly, so the chunked-prefill kernel computes what
-        the mask kernel would. The check reads the mask once and synchronises
-        once (the device writes the verdict and sizes into the pool's pinned
-        record); the result is cached for the step's other layers (same
+        the mask kernel would. The check reads the mask once and the host
+        waits once, polling the pool's pinned record, which the device writes
+        (verdict, sizes, chunk starts and prefixes, then a tag) at the end of
+        the call; the result is cached for the step's other layers (same
         ``gather_slots`` and ``mask`` tensors, not modified in place since).
         Under hipGraph capture ``None`` is returned and the mask kernel runs.
         """
@@ -295,15 +297,17 @@ class PagedKVPool:
             return c[1]
         form = None
         if (gather_slots.dim() == 2 and gather_slots.shape[0] == 1 and gather_slots.dtype == torch.int64
-                and gather_slots.is_cuda and mask.is_cuda and mask.dim() == 4 and tuple(mask.shape[:2]) == (1, 1)
-                and mask.shape[3] == gather_slots.shape[1]):
+                and gather_slots.is_cuda and mask.device == gather_slots.device and mask.dim() == 4
+                and tuple(mask.shape[:2]) == (1, 1) and mask.shape[3] == gather_slots.shape[1]
+                and 0 < mask.shape[2] < 2**31 and 0 < mask.shape[3] < 2**31):
             q = mask.shape[2]
             if self._varlen_records is None or self._varlen_records.numel() < 4 * q:
                 self._varlen_records = torch.zeros(max(4 * q, 1024), dtype=torch.int32, device=self.device)
-                self._varlen_staging = torch.empty(kernels.varlen_staging_size(max(q, 256)), dtype=torch.int32,
+                self._varlen_staging = torch.zeros(kernels.varlen_staging_size(max(q, 256)), dtype=torch.int32,
                                                    pin_memory=True)
-            form = kernels.varlen_form(gather_slots, mask, self.block_size, self.num_blocks,
-                                       records=self._varlen_records, staging=self._varlen_staging)
+                self._varlen_host = self._varlen_staging.numpy()  # the same pinned memory
+            form = kernels.varlen_form_checked(gather_slots, mask, self.block_size, self.num_blocks,
+                                               self._varlen_records, self._varlen_staging, self._varlen_host)
             if form is not None:
                 # the reference packs decodes first (infrared/engine/scheduler.py:104-115)
                 form.row_split = row_split(form.block_tables, form.prefixes, form.q_lens)

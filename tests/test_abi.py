@@ -75,17 +75,21 @@ def test_validation_errors_report_codes_and_messages():
     )
     assert rc == -1 and b"null" in lib.ir_last_error()
     # the packed-form check: unknown mask dtype, empty frame (no-op), null pointers
-    rc = lib.ir_varlen_form_scan(None, 8, 1, 99, 4, 8, None, 1, 16, 100, None, None, None, None, None, None, 0, None, 0, None)
+    rc = lib.ir_varlen_form_scan(None, 8, 1, 99, 4, 8, None, 1, 16, 100,
+                                 None, None, None, None, None, None, 0, None, 0, 0, None)
     assert rc == -1 and b"dtype" in lib.ir_last_error()
-    rc = lib.ir_varlen_form_scan(None, 8, 1, 2, 0, 8, None, 1, 16, 100, None, None, None, None, None, None, 0, None, 0, None)
+    rc = lib.ir_varlen_form_scan(None, 8, 1, 2, 0, 8, None, 1, 16, 100,
+                                 None, None, None, None, None, None, 0, None, 0, 0, None)
     assert rc == 0 and lib.ir_last_error() == b""
-    rc = lib.ir_varlen_form_scan(None, 8, 1, 2, 4, 8, None, 1, 16, 100, None, None, None, None, None, None, 0, None, 0, None)
+    rc = lib.ir_varlen_form_scan(None, 8, 1, 2, 4, 8, None, 1, 16, 100,
+                                 None, None, None, None, None, None, 0, None, 0, 0, None)
     assert rc == -1 and b"null" in lib.ir_last_error()
-    rc = lib.ir_varlen_form_scan(None, 8, 1, 2, 4, 8, None, 1, 16, -1, None, None, None, None, None, None, 0, None, 0, None)
+    rc = lib.ir_varlen_form_scan(None, 8, 1, 2, 4, 8, None, 1, 16, -1,
+                                 None, None, None, None, None, None, 0, None, 0, 0, None)
     assert rc == -1 and b"bad sizes" in lib.ir_last_error()
     # a host record too small for 4 rows' chunk starts and prefixes (checked before any pointer is used)
     p = 256
-    rc = lib.ir_varlen_form_scan(p, 8, 1, 2, 4, 8, p, 1, 16, 100, p, p, p, p, p, p, 64, p, 16, None)
+    rc = lib.ir_varlen_form_scan(p, 8, 1, 2, 4, 8, p, 1, 16, 100, p, p, p, p, p, p, 64, p, 16, 0, None)
     assert rc == -1 and b"host_record holds 16 int32, needs 17" in lib.ir_last_error()
     # block tables narrower than their stride allows, and a table pass with no tables
     rc = lib.ir_varlen_form_tables(None, 1, None, None, None, 2, 16, None, 4, 8, None)

@@ -10,6 +10,7 @@ import pytest
 import torch
 
 from infrared_amd import PagedContext, PagedKVPool, kernels, metadata, paged_attention
+from infrared_amd._lib import stream_ptr
 from infrared_amd.hip_graph import HipGraphDecoder, build_decode_static_inputs, pick_bucket
 from oracle import naive as O
 
@@ -675,6 +676,60 @@ def test_host_records_must_be_pinned():
         kernels.varlen_form(gs, frame, 16, 4, staging=torch.zeros(64, dtype=torch.int32))
     f = kernels.varlen_form(gs, frame, 16, 4, staging=torch.zeros(64, dtype=torch.int32, pin_memory=True))
     assert f is not None and f.q_lens == (1,) and f.prefixes == (2,)
+
+
+def test_stream_handle_is_torchs_current_stream():
+    """The launches' stream handle is torch's current stream: the default one,
+    a side stream made current, and again the default one after it."""
+    dev = torch.device(DEV, torch.cuda.current_device())
+    assert stream_ptr(dev) == torch.cuda.current_stream(dev).cuda_stream
+    side = torch.cuda.Stream(dev)
+    with torch.cuda.stream(side):
+        assert stream_ptr(dev) == side.cuda_stream != torch.cuda.default_stream(dev).cuda_stream
+        assert stream_ptr(torch.device(DEV)) == side.cuda_stream
+    assert stream_ptr(dev) == torch.cuda.current_stream(dev).cuda_stream
+
+
+def test_packed_form_check_around_the_one_launch_row_limit():
+    """Frames of 4,096 query rows (segmentation and slot check in one launch)
+    and 4,097 rows (two launches): the derived metadata matches the frame in
+    both, a leaked key rejects each, and so does a slot off its block's closed
+    form; the host record of each call is that call's (one pinned record, the
+    verdicts alternating)."""
+    bs = 16
+    staging = torch.zeros(kernels.varlen_staging_size(4097), dtype=torch.int32, pin_memory=True)
+    for q_lens in ([2000, 1, 1595, 500], [2000, 1, 1596, 500]):
+        num_cached = [0, 37, 5, 333]
+        need = [metadata.blocks_for(c + n, bs) for c, n in zip(num_cached, q_lens)]
+        perm = torch.randperm(sum(need) + 3, generator=torch.Generator().manual_seed(len(q_lens))).tolist()
+        tables = [perm[sum(need[:i]) : sum(need[: i + 1])] for i in range(len(q_lens))]
+        q_seq, q_pos, k_seq, k_pos, gather = [], [], [], [], []
+        for i, (bt, c, n) in enumerate(zip(tables, num_cached, q_lens)):
+            q_seq += [i] * n
+            q_pos += list(range(c, c + n))
+            k_seq += [i] * (c + n)
+            k_pos += list(range(c + n))
+            gather += [O.slot(bt, p, bs) for p in range(c + n)]
+        mask = O.varlen_mask(torch.tensor(q_seq), torch.tensor(q_pos), torch.tensor(k_seq), torch.tensor(k_pos),
+                             torch.bfloat16).to(DEV)
+        assert mask.shape[2] == sum(q_lens) in (4096, 4097)
+        gs = torch.tensor([gather], dtype=torch.int64, device=DEV)
+        leaked = mask.clone()
+        leaked[0, 0, 2500, 0] = 0.0  # a row of sequence 2 sees sequence 0's first key
+        off_form = gs.clone()
+        off_form[0, 2040] += 1
+        for g, m, accepted in ((gs, mask, True), (gs, leaked, False), (off_form, mask, False), (gs, mask, True)):
+            f = kernels.varlen_form(g, m, bs, sum(need) + 3, staging=staging)
+            if not accepted:
+                assert f is None
+                continue
+            assert f is not None and f.q_lens == tuple(q_lens) and f.prefixes == tuple(num_cached)
+            assert f.max_q_len == max(q_lens)
+            assert f.cu_seqlens_q.tolist() == [0, 2000, 2001, 2001 + q_lens[2], sum(q_lens)]
+            assert f.q_start.tolist() == num_cached
+            for i, nb in enumerate(need):
+                assert f.block_tables[i, :nb].tolist() == tables[i]
+                assert f.block_tables[i, nb:].eq(0).all()
 
 
 def test_reference_metadata_refilled_in_place_is_checked_again():
