@@ -270,7 +270,11 @@ void paged_prefill_kernel(PrefillArgs a) {
 
   // ---- Q^T operands: lane (g, c) holds d = 32 ks + 8 g .. +7 of its column,
   // multiplied by scale * log2(e) and rounded back to the input dtype, so the
-  // score MFMA yields base-2 exponents directly
+  // score MFMA yields base-2 exponents directly. The small-grid shape (every
+  // workgroup alone on its CU: each one's latency is the call's) loads Q raw
+  // and scales it once its first key tile is staged, so Q's round trip
+  // overlaps the block ids' and the first tile's instead of preceding them.
+  constexpr bool EARLY = NW == 8 && CT == 1 && SCHED == kRing2;
   u32x4 qreg[CT][S::KS];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
@@ -279,10 +283,15 @@ void paged_prefill_kernel(PrefillArgs a) {
                            (int64_t)(col.ok ? col.head : 0) * a.q_head;
 #pragma unroll
     for (int ks = 0; ks < S::KS; ++ks) {
-      const u32x4 x = col.ok ? *(const u32x4*)(qrow + ks * 32 + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+      if constexpr (EARLY) {
+        const u32x4 x = *(const u32x4*)(qrow + ks * 32 + 8 * g);  // (a valid row when !col.ok)
+        qreg[ct][ks] = col.ok ? x : u32x4{0u, 0u, 0u, 0u};
+      } else {
+        const u32x4 x = col.ok ? *(const u32x4*)(qrow + ks * 32 + 8 * g) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        qreg[ct][ks][e] = Elem<DT>::pack2(Elem<DT>::lo(x[e]) * a.scale_log2, Elem<DT>::hi(x[e]) * a.scale_log2);
+        for (int e = 0; e < 4; ++e)
+          qreg[ct][ks][e] = Elem<DT>::pack2(Elem<DT>::lo(x[e]) * a.scale_log2, Elem<DT>::hi(x[e]) * a.scale_log2);
+      }
     }
   }
 
@@ -336,7 +345,7 @@ void paged_prefill_kernel(PrefillArgs a) {
   const uint16_t* kn = a.k_new ? (const uint16_t*)a.k_new + (int64_t)kvh * a.kn_head : nullptr;
   const uint16_t* vn = a.v_new ? (const uint16_t*)a.v_new + (int64_t)kvh * a.vn_head : nullptr;
   const int64_t new_row0 = a.src_row0 + q_lo - p0;  // row of new key k: new_row0 + k
-  auto load_regs = [&](int kb) {
+  auto load_into = [&](int kb, u32x4 (&kr)[S::KPT], u32x4 (&vr)[S::KPT], bool (&ku)[S::KPT]) {
     const int k0 = kb * BN;
     const int k_last = min(k0 + BN, kmax) - 1;
     const int last_blk = FAST ? k_last >> a.bs_shift : k_last / a.bs;
@@ -348,15 +357,19 @@ void paged_prefill_kernel(PrefillArgs a) {
         if (S::KCH % NT == 0 || q < S::KCH) {
           const int key = q / (D / 8), part = q % (D / 8);
           const int kk = k0 + key;
-          bool use;
-          const int64_t sl = slot_of(kk, use);
+          // a new key is read from the call's rows and needs no block id (the
+          // check after the walk flags a bad one): a tile of new keys only
+          // may be loaded before the block ids are
           const bool fresh = kk >= p0 && kk < kmax;
+          bool use = fresh;
+          int64_t sl = 0;
+          if (!fresh) sl = slot_of(kk, use);
           const int64_t row = new_row0 + kk;
           const uint16_t* kp = fresh ? kn + row * a.kn_tok + part * 8 : kc + sl + part * 8;
           const uint16_t* vp = fresh ? vn + row * a.vn_tok + part * 8 : vc + sl + part * 8;
-          kreg[i] = *(const u32x4*)kp;
-          vreg[i] = *(const u32x4*)vp;
-          kuse[i] = use;
+          kr[i] = *(const u32x4*)kp;
+          vr[i] = *(const u32x4*)vp;
+          ku[i] = use;
         }
       }
       return;
@@ -368,25 +381,27 @@ void paged_prefill_kernel(PrefillArgs a) {
         const int key = q / (D / 8), part = q % (D / 8);
         bool use;
         const int64_t sl = slot_of(k0 + key, use);
-        kreg[i] = *(const u32x4*)(kc + sl + part * 8);
-        vreg[i] = *(const u32x4*)(vc + sl + part * 8);
-        kuse[i] = use;
+        kr[i] = *(const u32x4*)(kc + sl + part * 8);
+        vr[i] = *(const u32x4*)(vc + sl + part * 8);
+        ku[i] = use;
       }
     }
   };
+  auto load_regs = [&](int kb) { load_into(kb, kreg, vreg, kuse); };
   // Registers -> LDS buffer `buf`: K and V tiles both row-major [64 keys][D]
   // (+32 bytes a row).
-  auto store_regs = [&](int buf) {
+  auto store_from = [&](int buf, const u32x4 (&kr)[S::KPT], const u32x4 (&vr)[S::KPT], const bool (&ku)[S::KPT]) {
 #pragma unroll
     for (int i = 0; i < S::KPT; ++i) {
       const int q = tid + NT * i;
       if (q < S::KCH) {
         const int key = q / (D / 8), part = q % (D / 8);
-        *(u32x4*)&ks_lds[buf][key * S::KROW + part * 8] = zero_unless(kreg[i], kuse[i]);
-        *(u32x4*)&vs_lds[buf][key * S::KROW + part * 8] = zero_unless(vreg[i], kuse[i]);
+        *(u32x4*)&ks_lds[buf][key * S::KROW + part * 8] = zero_unless(kr[i], ku[i]);
+        *(u32x4*)&vs_lds[buf][key * S::KROW + part * 8] = zero_unless(vr[i], ku[i]);
       }
     }
   };
+  auto store_regs = [&](int buf) { store_from(buf, kreg, vreg, kuse); };
   // V^T operand of PV step t (d tile t % DTL, 32-key step t / DTL) from the
   // row-major V tile at vb: lane (g, c) needs V[32 st + 4 g + e][16 dt + c]
   // (k-slots 0..3) and V[32 st + 16 + 4 g + e][..] (4..7), e = 0..3: the
@@ -550,7 +565,67 @@ void paged_prefill_kernel(PrefillArgs a) {
   };
 
   // ---- walk key tiles [t_lo, t_hi)
-  if constexpr (SCHED == kRing2) {
+  if constexpr (EARLY) {
+    // The small-grid shape: a workgroup's walk is short and alone on its CU,
+    // so its steps wait on load latency, not on the pipes. A register ring of
+    // R tiles keeps R - 1 tiles' loads in flight behind the one being staged
+    // (all of a short walk's at once); LDS stays a 2-deep ring. Tile t_lo + i
+    // lives in ring slot i % R, the walk unrolled by R so every slot index is
+    // fixed. The first tile, when it holds new keys only, is loaded before the
+    // block ids are, with Q's loads.
+    constexpr int R = 4;
+    if (t_lo < t_hi) {
+      u32x4 kr[R][S::KPT], vr[R][S::KPT];
+      bool ku[R][S::KPT];
+      const int bt0 = FAST ? (t_lo * BN) >> a.bs_shift : (t_lo * BN) / a.bs;
+      if (FUSED && t_lo * BN >= p0) {  // uniform
+        load_into(t_lo, kr[0], vr[0], ku[0]);
+        fill_bt(bt0);
+      } else {
+        fill_bt(bt0);
+        load_into(t_lo, kr[0], vr[0], ku[0]);
+      }
+#pragma unroll
+      for (int j = 1; j < R; ++j)
+        if (t_lo + j < t_hi) load_into(t_lo + j, kr[j], vr[j], ku[j]);
+      store_from(t_lo & 1, kr[0], vr[0], ku[0]);
+      __syncthreads();
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int ks = 0; ks < S::KS; ++ks) {
+          const u32x4 x = qreg[ct][ks];
+          u32x4 y;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            y[e] = Elem<DT>::pack2(Elem<DT>::lo(x[e]) * a.scale_log2, Elem<DT>::hi(x[e]) * a.scale_log2);
+          qreg[ct][ks] = y;
+        }
+      f32x4 sc[CT][4];
+      // tile kb (slot J): its scores, softmax and PV product from LDS buffer
+      // kb % 2; tile kb + 1 staged from slot J + 1; tile kb + R's loads into slot J
+      auto sub = [&](auto slot, int kb) {
+        constexpr int J = decltype(slot)::value;
+        if (kb >= t_hi) return;  // uniform
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int kt = 0; kt < 4; ++kt) sc[ct][kt] = negm[ct];
+#pragma unroll
+        for (int t = 0; t < 4 * S::KS; ++t) qk_step(ks_lds[kb & 1], t % 4, t / 4, sc);
+        step(std::false_type{}, kb, sc, sc);
+        if (kb + 1 < t_hi) store_from((kb + 1) & 1, kr[(J + 1) % R], vr[(J + 1) % R], ku[(J + 1) % R]);
+        if (kb + R < t_hi) load_into(kb + R, kr[J], vr[J], ku[J]);
+        __syncthreads();
+      };
+      for (int kb = t_lo; kb < t_hi; kb += R) {
+        sub(std::integral_constant<int, 0>{}, kb);
+        sub(std::integral_constant<int, 1>{}, kb + 1);
+        sub(std::integral_constant<int, 2>{}, kb + 2);
+        sub(std::integral_constant<int, 3>{}, kb + 3);
+      }
+    }
+  } else if constexpr (SCHED == kRing2) {
     // one tile per step: its scores (from -m), softmax and PV product read
     // buffer kb % 2 while tile kb + 1 is written to the other buffer from the
     // registers its loads filled a step earlier and tile kb + 2's loads go
@@ -622,8 +697,11 @@ void paged_prefill_kernel(PrefillArgs a) {
     const int blk = pos / a.bs;
     const int32_t bid = blk < a.max_blocks ? bt_row[blk] : -1;
     const int64_t ws = a.write_slots[a.src_row0 + q_lo + tq0 + tid];
-    if (bid >= 0 && (int64_t)bid < a.num_blocks && ws != (int64_t)bid * a.bs + (pos - blk * a.bs))
+    if (bid < 0 || (int64_t)bid >= a.num_blocks) {
+      if (blk < a.max_blocks) flag_error(a.err, IR_ERR_BLOCK_RANGE);  // (read from its row all the same)
+    } else if (ws != (int64_t)bid * a.bs + (pos - blk * a.bs)) {
       flag_error(a.err, IR_ERR_WRITE_SLOT);
+    }
   }
 
   if (nparts == 1) {

@@ -690,6 +690,17 @@ def test_stream_handle_is_torchs_current_stream():
     assert stream_ptr(dev) == torch.cuda.current_stream(dev).cuda_stream
 
 
+def test_a_host_record_that_never_arrives_raises(monkeypatch):
+    """A record whose tag never comes (no call wrote it): the wait stops
+    polling, synchronises the stream and raises rather than spinning on."""
+    import numpy as np
+
+    monkeypatch.setattr(kernels, "RECORD_POLLS", 50)
+    host = np.zeros(16, dtype=np.int32)
+    with pytest.raises(RuntimeError, match="wrote no record"):
+        kernels.await_record(host, 7, 77, torch.device(DEV))
+
+
 def test_packed_form_check_around_the_one_launch_row_limit():
     """Frames of 4,096 query rows (segmentation and slot check in one launch)
     and 4,097 rows (two launches): the derived metadata matches the frame in

@@ -194,3 +194,16 @@ def test_seam_folds_the_write_only_for_rows_the_prefill_kernel_can_take():
         k = pool.k
 
     assert not _fusable(ForeignPool(), 1, (k, v, slots))
+
+
+def test_record_wait_returns_once_the_tag_is_there():
+    """A device-written host record already carrying the call's tag is read at
+    once: no poll runs out and the stream is never synchronised (which needs a
+    device, absent here)."""
+    import numpy as np
+
+    from infrared_amd import kernels
+
+    host = np.zeros(16, dtype=np.int32)
+    host[7] = 12345
+    kernels.await_record(host, 7, 12345, torch.device("cuda"))
