@@ -107,6 +107,24 @@ def test_fused_write_flags_a_token_written_elsewhere():
     assert torch.equal(case.k_cache[spare], k_new[row0 + 300])
 
 
+def test_fused_write_flags_a_bad_block_id_of_a_new_token():
+    """A chunk with no cached prefix whose block table holds an id outside the
+    pool: its new keys are read from the given rows (no block id is looked up
+    for them), and the check after the walk flags the bad id."""
+    from infrared_amd._lib import ERR_BLOCK_RANGE
+
+    case, bt, slots, k_new, v_new, row0, plan, _ = _frame("small")
+    cfg = case.config
+    assert CASES["small"][1][0] == 0  # sequence 0: all its keys new
+    bad_bt = bt.clone()
+    bad_bt[0, 3] = case.k_cache.shape[0] // cfg.block_size + 5
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    kernels.paged_prefill(case.q, case.k_cache, case.v_cache, bad_bt, case.cu_seqlens_q, case.q_start, 256,
+                          cfg.block_size, cfg.scale, err_flags=err, new_kv=(k_new, v_new, slots), src_row0=row0)
+    torch.cuda.synchronize()
+    assert err.item() & ERR_BLOCK_RANGE
+
+
 def test_fused_write_refuses_rows_outside_the_written_range():
     case, bt, slots, k_new, v_new, row0, plan, _ = _frame("small")
     cfg = case.config
