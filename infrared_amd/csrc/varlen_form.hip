@@ -566,7 +566,7 @@ __global__ __launch_bounds__(kVerifyThreads) void varlen_verify_kernel(RowRec* r
   __shared__ __align__(16) int s_cnt[kVerifyRowsPer * NW];
   __shared__ int s_rows_bad, s_keys_bad, s_maxq, s_maxb, s_ticket;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  // every load first: rows c * 256 + tid, and this thread's first key and the one before it
+  // every load first: rows c * kVerifyThreads + tid, and this thread's first key and the one before it
   RowRec x[kVerifyRowsPer];
 #pragma unroll
   for (int c = 0; c < kVerifyRowsPer; ++c) x[c] = rec[min(c * kVerifyThreads + tid, Q - 1)];
