@@ -743,6 +743,31 @@ def test_packed_form_check_around_the_one_launch_row_limit():
                 assert f.block_tables[i, nb:].eq(0).all()
 
 
+def test_packed_form_check_on_a_key_axis_longer_than_one_pass_of_the_grid():
+    """Two query rows over 300,000 keys (more keys than the verification's
+    grid holds threads, so each thread checks several): the form is derived,
+    its one table matches, and a slot off its closed form near the end of the
+    axis -- in a later pass -- rejects the frame."""
+    bs, prefix, q = 16, 299_998, 2
+    k = prefix + q
+    nb = -(-k // bs)
+    table = torch.randperm(nb + 5, generator=torch.Generator().manual_seed(8))[:nb]
+    pos = torch.arange(k)
+    gs = (table[pos // bs] * bs + pos % bs).view(1, k).to(DEV)
+    m = torch.full((1, 1, q, k), torch.finfo(torch.bfloat16).min, dtype=torch.bfloat16)
+    m[0, 0, 0, : prefix + 1] = 0
+    m[0, 0, 1, :] = 0
+    m = m.to(DEV)
+    staging = torch.zeros(kernels.varlen_staging_size(q), dtype=torch.int32, pin_memory=True)
+    f = kernels.varlen_form(gs, m, bs, nb + 5, staging=staging)
+    assert f is not None and f.q_lens == (q,) and f.prefixes == (prefix,)
+    assert f.block_tables.shape == (1, nb) and torch.equal(f.block_tables[0].cpu(), table.to(torch.int32))
+    bad = gs.clone()
+    bad[0, k - 7] += 1
+    assert kernels.varlen_form(bad, m, bs, nb + 5, staging=staging) is None
+    assert kernels.varlen_form(gs, m, bs, nb + 5, staging=staging) is not None
+
+
 def test_reference_metadata_refilled_in_place_is_checked_again():
     """A caller that reuses its gather_slots and mask tensors, refilling them in
     place for the next step, gets that step's form derived again (the cache of
