@@ -566,10 +566,10 @@ void paged_prefill_kernel(PrefillArgs a) {
 
   // ---- walk key tiles [t_lo, t_hi)
   if constexpr (EARLY) {
-    // The small-grid shape: a workgroup's walk is short and alone on its CU,
-    // so its steps wait on load latency, not on the pipes. A register ring of
-    // R tiles keeps R - 1 tiles' loads in flight behind the one being staged
-    // (all of a short walk's at once); LDS stays a 2-deep ring. Tile t_lo + i
+    // The small-grid shape: a workgroup alone on its CU has no other one to
+    // cover its loads' latency, so a register ring of R tiles keeps R - 1
+    // tiles' loads in flight behind the one being staged (all of a short
+    // walk's at once); LDS stays a 2-deep ring. Tile t_lo + i
     // lives in ring slot i % R, the walk unrolled by R so every slot index is
     // fixed. The first tile, when it holds new keys only, is loaded before the
     // block ids are, with Q's loads.
