@@ -420,8 +420,12 @@ int ir_varlen_form_tables(const int64_t* gather_slots, int64_t gs_k_stride, cons
  *                 fp32 rounding of the merge (identical when nothing is cut).
  * Keys q_start[b] + q_len_b beyond the table (max_blocks_per_seq * block_size) set
  * IR_ERR_CONTEXT_RANGE and are clamped; a bad block id sets IR_ERR_BLOCK_RANGE and
- * that block's keys read as zeros. head_dim in {64, 128}; dtype bf16 or f16 (fp32 returns
- * IR_EUNSUPPORTED: use ir_paged_attention_masked).
+ * that block's keys read as zeros. head_dim in {64, 128}; dtype bf16, f16 or fp32. fp32
+ * (the reference's fp32 path: fp32 scores, softmax and PV product) runs on its own
+ * kernel of 64-column workgroups: at most 64 query heads per KV head (more returns
+ * IR_EUNSUPPORTED), unplanned (a plan is accepted and not read), the fused write as
+ * its own launch first; its q, out, cache and new-row strides are multiples of 16 bytes
+ * and out 16-byte aligned.
  * Fused K/V write (the step's PagedKVPool.write folded into the call; k_new null: none):
  *   k_new, v_new: [n_write, num_kv_heads, head_dim] (strides token, head in elements;
  *                 16-byte aligned, 16-byte strides), rows written to the caches at

@@ -810,6 +810,258 @@ void paged_prefill_kernel(PrefillArgs a) {
   if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---------------------------------------------------------------- fp32
+//
+// fp32 chunked prefill, the reference's fp32 path (fp32 scores, softmax and
+// PV product), with 16x16x4 fp32 MFMAs: lane (g, c) of a product supplies
+// element (row c, k-slot g) of A and (k-slot g, column c) of B and receives
+// rows 4g..4g+3 of column c. A workgroup is 4 wavefronts of one 16-column
+// tile: 64 columns, tq = 64 / n_rep tokens of one KV head's query heads, in
+// the 16-bit kernel's unplanned order (last query blocks first). Keys walk in
+// 64-key tiles through LDS -- K row-major, V transposed, so both operands are
+// 16-byte reads -- with the next tile's loads in flight in registers. The
+// score product's k-slot g of step (m, r) is d = 16 m + 4 g + r (a lane's K
+// read covers its four steps); the PV product's k-slot g of step (kt, r) is
+// key 16 kt + 4 g + r, the lane's own probability of that key. Same masking,
+// lazy rescale and flags as the 16-bit kernel.
+constexpr int kF32Threads = 256;
+constexpr int kF32Cols = 64;
+
+template <int D, bool FAST>
+__global__ __launch_bounds__(kF32Threads) __attribute__((amdgpu_waves_per_eu(2)))
+void paged_prefill_f32_kernel(PrefillArgs a) {
+  constexpr int NT = kF32Threads, BN = 64, MT = D / 16, DT4 = D / 4;
+  constexpr int KROW = D + 4;           // floats per K row in LDS
+  constexpr int VROW = BN + 4;          // floats per V^T row (one d, 64 keys)
+  constexpr int BPT = (BN / 4) * DT4 / NT;  // 4-key x 4-d blocks of a tile per thread
+  static_assert((BN / 4) * DT4 % NT == 0 && BPT >= 1, "a tile's blocks must divide among the threads");
+  __shared__ __attribute__((aligned(16))) float ks[BN * KROW];
+  __shared__ __attribute__((aligned(16))) float vt[D * VROW];
+  __shared__ int32_t bt_lds[kBtCache];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
+  const int TQ = a.tq;
+  const int per_tb = a.num_kv_heads * a.num_seqs;
+  const int tb = a.n_qblocks - 1 - (int)(blockIdx.x / per_tb);
+  const int rest = (int)(blockIdx.x % per_tb);
+  const int seq = rest % a.num_seqs, kvh = rest / a.num_seqs;
+  const int q_lo = a.cu_q[seq];
+  const int q_len = a.cu_q[seq + 1] - q_lo;
+  if (q_lo < 0 || q_len < 0 || (int64_t)q_lo + q_len > a.total_q) {
+    if (tid == 0 && tb == 0 && kvh == 0) flag_error(a.err, IR_ERR_CONTEXT_RANGE);
+    return;
+  }
+  const int tq0 = tb * TQ;
+  if (tb == a.n_qblocks - 1 && kvh == 0 && tid == 0 && q_len > a.n_qblocks * TQ)
+    flag_error(a.err, IR_ERR_CONTEXT_RANGE);
+  if (tq0 >= q_len) return;
+  int p0 = a.q_start[seq];
+  const int cap = a.max_blocks * a.bs;
+  if (p0 < 0 || (int64_t)p0 + q_len > cap) {
+    if (tid == 0 && tb == 0 && kvh == 0) flag_error(a.err, IR_ERR_CONTEXT_RANGE);
+    p0 = p0 < 0 ? 0 : min(p0, cap);
+  }
+  const int kmax = min(cap, p0 + min(q_len, tq0 + TQ));
+  const int nkb = kmax > 0 && a.num_blocks > 0 ? (kmax + BN - 1) / BN : 0;
+
+  // this lane's column j = 16 w + c: token tq0 + j / n_rep, query head
+  // kvh * n_rep + j % n_rep
+  const int j = w * 16 + c, jt = j / a.n_rep;
+  const bool col_ok = jt < TQ && tq0 + jt < q_len;
+  const int col_tok = tq0 + jt, col_head = kvh * a.n_rep + (j - jt * a.n_rep);
+  // Q^T operand of score step (m, r): q[16 m + 4 g + r] of the column, times
+  // scale * log2(e), so the scores come out as base-2 exponents
+  float qreg[MT][4];
+  {
+    const float* qrow = (const float*)a.q + (int64_t)(q_lo + (col_ok ? col_tok : tq0)) * a.q_tok +
+                        (int64_t)(col_ok ? col_head : kvh * a.n_rep) * a.q_head;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const f32x4 x = *(const f32x4*)(qrow + 16 * m + 4 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) qreg[m][r] = col_ok ? x[r] * a.scale_log2 : 0.f;
+    }
+  }
+
+  const int32_t* bt_row = a.bt + (int64_t)seq * a.bt_stride;
+  const float* kc = (const float*)a.kc + (int64_t)kvh * a.c_head;
+  const float* vc = (const float*)a.vc + (int64_t)kvh * a.c_head;
+  const int nblk_needed = (kmax + a.bs - 1) / a.bs;
+  int bt_base = 0;
+  auto fill_bt = [&](int base) {
+    __syncthreads();
+    for (int i = tid; i < kBtCache && base + i < nblk_needed; i += NT) bt_lds[i] = bt_row[base + i];
+    __syncthreads();
+    bt_base = base;
+  };
+  bool bad = false;
+  // element offset of key k's row in the pool and whether it may be used
+  // (keys past kmax are masked; a bad block id is flagged and reads as zeros)
+  auto slot_of = [&](int k, bool& use) -> int64_t {
+    const bool in = k < kmax;
+    const int kk = in ? k : bt_base * a.bs;
+    if constexpr (FAST) {
+      const int blk = kk >> a.bs_shift;
+      const int32_t bid = bt_lds[blk - bt_base];
+      use = in && (uint32_t)bid < (uint32_t)a.num_blocks;
+      bad |= in && !use;
+      const int sl = use ? (bid << a.bs_shift) | (kk & (a.bs - 1)) : 0;
+      return (int64_t)(uint32_t)__mul24(sl, a.c_slot32);
+    } else {
+      const int blk = kk / a.bs;
+      const int32_t bid = bt_lds[blk - bt_base];
+      use = in && bid >= 0 && (int64_t)bid < a.num_blocks;
+      bad |= in && !use;
+      return use ? ((int64_t)bid * a.bs + (kk - blk * a.bs)) * a.c_slot : 0;
+    }
+  };
+  // a tile's 4-key x 4-d blocks: block b = tid + NT i holds keys 4 (b / DT4)
+  // .. +3 at d = 4 (b % DT4) .. +3
+  f32x4 kr[BPT][4], vr[BPT][4];
+  bool ku[BPT][4];
+  auto load_tile = [&](int kb) {
+    const int k0 = kb * BN;
+    const int k_last = min(k0 + BN, kmax) - 1;
+    const int last_blk = FAST ? k_last >> a.bs_shift : k_last / a.bs;
+    if (last_blk >= bt_base + kBtCache) fill_bt(FAST ? k0 >> a.bs_shift : k0 / a.bs);
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      const int b = tid + NT * i, key4 = b / DT4, d4 = b - key4 * DT4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bool use;
+        const int64_t sl = slot_of(k0 + 4 * key4 + e, use);
+        kr[i][e] = *(const f32x4*)(kc + sl + 4 * d4);
+        vr[i][e] = *(const f32x4*)(vc + sl + 4 * d4);
+        ku[i][e] = use;
+      }
+    }
+  };
+  auto store_tile = [&]() {
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      const int b = tid + NT * i, key4 = b / DT4, d4 = b - key4 * DT4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) *(f32x4*)&ks[(4 * key4 + e) * KROW + 4 * d4] = ku[i][e] ? kr[i][e] : zero;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *(f32x4*)&vt[(4 * d4 + r) * VROW + 4 * key4] =
+            f32x4{ku[i][0] ? vr[i][0][r] : 0.f, ku[i][1] ? vr[i][1][r] : 0.f, ku[i][2] ? vr[i][2][r] : 0.f,
+                  ku[i][3] ? vr[i][3][r] : 0.f};
+    }
+  };
+
+  // online softmax of this lane's column: -m (running base-2 max, 0 before
+  // the first tile), the lane's share of the sum, O^T rows 16 dt + 4 g + i
+  float negm = 0.f, l = 0.f;
+  f32x4 acc[MT];
+#pragma unroll
+  for (int dt = 0; dt < MT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int qpos0 = p0 + tq0;
+  const int col_lim = min(p0 + col_tok, kmax - 1);  // last key the column may see
+
+  if (nkb > 0) {
+    fill_bt(0);
+    load_tile(0);
+    store_tile();
+    if (nkb > 1) load_tile(1);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; ++kb) {
+      const int k0 = kb * BN;
+      f32x4 s[4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) s[kt] = f32x4{negm, negm, negm, negm};
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          const f32x4 k4 = *(const f32x4*)&ks[(16 * kt + c) * KROW + 16 * m + 4 * g];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[kt] = mfma_f32_k4(k4[r], qreg[m][r], s[kt]);
+        }
+      // only tiles that cross the causal diagonal or the last key are masked
+      if (!(k0 + BN - 1 <= qpos0 && k0 + BN <= kmax)) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (k0 + 16 * kt + 4 * g + r > col_lim) s[kt][r] = kNegInf;
+      }
+      float mx = kNegInf;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
+      mx = wave_max_groups_swap(mx);  // relative to m; finite on the first tile (key 0 is always visible)
+      const bool first = kb == 0;
+      const bool grow = first || mx > kRescaleSlack;
+      if (__any(grow)) {
+        const float d = grow ? mx : 0.f;  // the max moves up by d
+        if (!first) {
+          const float alpha = fast_exp2(-d);
+          l *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < MT; ++dt) acc[dt] *= alpha;
+        }
+        negm -= d;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) s[kt] -= d;
+      }
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          s[kt][r] = fast_exp2(s[kt][r]);
+          l += s[kt][r];
+        }
+#pragma unroll
+      for (int dt = 0; dt < MT; ++dt)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          const f32x4 v4 = *(const f32x4*)&vt[(16 * dt + c) * VROW + 16 * kt + 4 * g];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[dt] = mfma_f32_k4(v4[r], s[kt][r], acc[dt]);
+        }
+      __syncthreads();  // every wavefront is done with tile kb
+      if (kb + 1 < nkb) {
+        store_tile();
+        if (kb + 2 < nkb) load_tile(kb + 2);
+      }
+      __syncthreads();
+    }
+  }
+  if (bad) flag_error(a.err, IR_ERR_BLOCK_RANGE);
+  const float lsum = wave_sum_groups_swap(l);
+  if (!col_ok) return;
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  float* orow = (float*)a.out + (int64_t)(q_lo + col_tok) * a.o_tok + (int64_t)col_head * a.o_head;
+#pragma unroll
+  for (int dt = 0; dt < MT; ++dt) *(f32x4*)(orow + 16 * dt + 4 * g) = acc[dt] * inv;
+}
+
+// The fp32 launch: the step's K/V write (when given) as its own launch first,
+// then one workgroup per (query block, KV head, sequence); no plan.
+template <int D>
+int launch_prefill_f32(PrefillArgs a, hipStream_t s) {
+  if (a.k_new != nullptr) {
+    const int rc = ir_kv_scatter(a.k_new, a.kn_tok, a.kn_head, a.v_new, a.vn_tok, a.vn_head, (void*)a.kc,
+                                 (void*)a.vc, a.c_slot, a.c_head, a.num_blocks * a.bs, a.write_slots, a.n_write,
+                                 a.num_kv_heads, D, IR_DTYPE_F32, a.err, (ir_stream_t)s);
+    if (rc != IR_OK) return rc;
+  }
+  const int64_t grid = (int64_t)a.n_qblocks * a.num_kv_heads * a.num_seqs;
+  if (grid <= 0) return ok();
+  if (grid > 0x7fffffff) return fail(IR_EINVAL, "ir_paged_prefill: grid of %lld workgroups too large", (long long)grid);
+  const int64_t slots = a.num_blocks * a.bs;
+  const bool fast = a.bs_shift >= 0 && slots < (1 << 23) && a.c_slot < (1 << 23) &&
+                    (slots * a.c_slot + a.c_head * a.num_kv_heads) < ((int64_t)1 << 31);
+  if (fast)
+    hipLaunchKernelGGL((paged_prefill_f32_kernel<D, true>), dim3((unsigned)grid), dim3(kF32Threads), 0, s, a);
+  else
+    hipLaunchKernelGGL((paged_prefill_f32_kernel<D, false>), dim3((unsigned)grid), dim3(kF32Threads), 0, s, a);
+  return check_launch("ir_paged_prefill");
+}
+
 // ---------------------------------------------------------------- plan
 //
 // The dispatcher hands workgroup i to the first CU with room, in index order,
@@ -1320,14 +1572,16 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
                                 int64_t n_write, int64_t src_row0, int32_t* err_flags, ir_stream_t stream) {
   IR_REQUIRE(dtype == IR_DTYPE_BF16 || dtype == IR_DTYPE_F16 || dtype == IR_DTYPE_F32,
              "ir_paged_prefill: unknown dtype %d", dtype);
-  if (dtype == IR_DTYPE_F32)
-    return fail(IR_EUNSUPPORTED, "ir_paged_prefill: fp32 is not supported (bf16, f16); use ir_paged_attention_masked");
+  const bool f32 = dtype == IR_DTYPE_F32;
+  const int eb = f32 ? 4 : 2;
   IR_REQUIRE(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && num_q_heads > 0 && num_kv_heads > 0 &&
                  block_size > 0 && max_blocks_per_seq >= 0 && num_blocks >= 0,
              "ir_paged_prefill: bad sizes");
   IR_REQUIRE(num_q_heads % num_kv_heads == 0, "ir_paged_prefill: num_q_heads %d not a multiple of num_kv_heads %d",
              num_q_heads, num_kv_heads);
   IR_REQUIRE(num_q_heads / num_kv_heads <= 256, "ir_paged_prefill: more than 256 query heads per KV head");
+  if (f32 && num_q_heads / num_kv_heads > kF32Cols)
+    return fail(IR_EUNSUPPORTED, "ir_paged_prefill: fp32 with more than %d query heads per KV head", kF32Cols);
   if (head_dim != 64 && head_dim != 128)
     return fail(IR_EUNSUPPORTED, "ir_paged_prefill: head_dim %d not supported (64, 128)", head_dim);
   IR_REQUIRE((int64_t)max_blocks_per_seq * block_size <= (int64_t)1 << 30,
@@ -1336,11 +1590,13 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
   if (num_seqs == 0 || total_q == 0 || max_q_len == 0) return ok();
   IR_REQUIRE(q && k_cache && v_cache && block_tables && cu_seqlens_q && q_start && out,
              "ir_paged_prefill: null pointer");
-  IR_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && ((uintptr_t)out & 7u) == 0,
-             "ir_paged_prefill: q and caches must be 16-byte aligned, out 8-byte aligned");
-  IR_REQUIRE((q_tok_stride * 2) % 16 == 0 && (q_head_stride * 2) % 16 == 0 && (cache_slot_stride * 2) % 16 == 0 &&
-                 (cache_head_stride * 2) % 16 == 0 && (out_tok_stride * 2) % 8 == 0 && (out_head_stride * 2) % 8 == 0,
-             "ir_paged_prefill: q/cache strides must be multiples of 16 bytes, out strides of 8 bytes");
+  // each output store is 4 elements: 8 bytes in 16-bit dtypes, 16 in fp32
+  IR_REQUIRE(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && ((uintptr_t)out % (4 * eb)) == 0,
+             "ir_paged_prefill: q and caches must be 16-byte aligned, out %d-byte aligned", 4 * eb);
+  IR_REQUIRE((q_tok_stride * eb) % 16 == 0 && (q_head_stride * eb) % 16 == 0 && (cache_slot_stride * eb) % 16 == 0 &&
+                 (cache_head_stride * eb) % 16 == 0 && (out_tok_stride * eb) % (4 * eb) == 0 &&
+                 (out_head_stride * eb) % (4 * eb) == 0,
+             "ir_paged_prefill: q/cache strides must be multiples of 16 bytes, out strides of %d bytes", 4 * eb);
   PrefillArgs a;
   memset(&a, 0, sizeof(a));
   a.q = q;
@@ -1364,12 +1620,12 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
   a.n_rep = num_q_heads / num_kv_heads;
   const PrefillGeometry geo = prefill_geometry(max_q_len, a.n_rep);
   a.nw = geo.nw;
-  a.tq = geo.tq;
-  a.n_qblocks = geo.n_qblocks;
+  a.tq = f32 ? kF32Cols / a.n_rep : geo.tq;
+  a.n_qblocks = f32 ? (max_q_len + a.tq - 1) / a.tq : geo.n_qblocks;
   const int64_t n_items = (int64_t)num_seqs * a.n_qblocks;
   IR_REQUIRE(n_items * num_kv_heads <= 0x7fffffff, "ir_paged_prefill: %lld work items x %d KV heads",
              (long long)n_items, num_kv_heads);
-  if (plan) {
+  if (plan && !f32) {  // (fp32 runs unplanned: a plan is accepted and not read)
     const PlanLayout ly = plan_layout(geo, num_seqs, num_kv_heads, head_dim);
     IR_REQUIRE(plan_bytes >= ly.total && ((uintptr_t)plan & 255u) == 0,
                "ir_paged_prefill: plan of %lld bytes (256-byte aligned) required, got %lld (build it with "
@@ -1387,9 +1643,9 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
     IR_REQUIRE(n_write >= 1 && src_row0 >= 0 && src_row0 + total_q <= n_write,
                "ir_paged_prefill: the new rows [%lld, %lld) must lie within the %lld rows written",
                (long long)src_row0, (long long)src_row0 + total_q, (long long)n_write);
-    IR_REQUIRE(aligned16(k_new) && aligned16(v_new) && (k_new_tok_stride * 2) % 16 == 0 &&
-                   (k_new_head_stride * 2) % 16 == 0 && (v_new_tok_stride * 2) % 16 == 0 &&
-                   (v_new_head_stride * 2) % 16 == 0,
+    IR_REQUIRE(aligned16(k_new) && aligned16(v_new) && (k_new_tok_stride * eb) % 16 == 0 &&
+                   (k_new_head_stride * eb) % 16 == 0 && (v_new_tok_stride * eb) % 16 == 0 &&
+                   (v_new_head_stride * eb) % 16 == 0,
                "ir_paged_prefill: k_new / v_new must be 16-byte aligned with 16-byte strides");
     a.k_new = k_new;
     a.v_new = v_new;
@@ -1409,6 +1665,7 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
   a.scale_log2 = scale * kLog2e;
   a.err = err_flags;
   hipStream_t s = (hipStream_t)stream;
+  if (f32) return head_dim == 128 ? launch_prefill_f32<128>(a, s) : launch_prefill_f32<64>(a, s);
   if (dtype == IR_DTYPE_BF16)
     return head_dim == 128 ? launch_prefill<IR_DTYPE_BF16, 128>(a, geo.sched, s)
                            : launch_prefill<IR_DTYPE_BF16, 64>(a, geo.sched, s);

@@ -141,7 +141,7 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
         and block_tables is not None
         and cu_seqlens_q is not None
         and q_start is not None
-        and q.dtype in (torch.bfloat16, torch.float16)
+        and q.dtype in (torch.bfloat16, torch.float16, torch.float32)
     ):
         split = getattr(paged, "row_split", None)
         if not fusable:
@@ -168,7 +168,8 @@ def _attend(q: torch.Tensor, paged, mask: torch.Tensor | None, layer_idx: int, s
             # tables): when it has the decode form, run the block-table kernels
             form = pool.reference_decode_form(paged.gather_slots, mask)
         vform = None
-        if (form is None and paged.use_triton and b == 1 and q.dtype in (torch.bfloat16, torch.float16)
+        if (form is None and paged.use_triton and b == 1
+                and q.dtype in (torch.bfloat16, torch.float16, torch.float32)
                 and hasattr(pool, "reference_varlen_form") and mask.dim() == 4 and mask.shape[2] == sq):
             # the reference's packed prefill / mixed-step frame: when it has
             # that form, run the chunked-prefill kernel over derived metadata
@@ -260,8 +261,8 @@ def _prefill(q, pool, layer_idx: int, block_tables, cu_seqlens_q, q_start, max_q
     h_kv = pool.k.shape[-2]
     nseq = q_start.shape[0]
     plan = getattr(holder, "prefill_plan", None)
-    if plan is None and kernels.prefill_plan_pays(nseq, max_q, hq, h_kv, q.device,
-                                                  max_keys=block_tables.shape[1] * pool.block_size):
+    if plan is None and q.dtype != torch.float32 and kernels.prefill_plan_pays(
+            nseq, max_q, hq, h_kv, q.device, max_keys=block_tables.shape[1] * pool.block_size):
         plan = kernels.prefill_plan(
             cu_seqlens_q, q_start, block_tables, b * sq, max_q, pool.block_size, hq, h_kv, d
         )

@@ -12,7 +12,7 @@ import torch
 
 from infrared_amd import kernels
 from infrared_amd._lib import ERR_BLOCK_RANGE, ERR_CONTEXT_RANGE
-from infrared_amd.workloads import PrefillConfig, make_decode_case, make_prefill_case
+from infrared_amd.workloads import PrefillConfig, make_prefill_case
 from oracle import naive as O
 
 pytestmark = pytest.mark.gpu
@@ -147,13 +147,83 @@ def test_prefill_flags_bad_block_ids_and_overlong_context():
     assert err.item() & ERR_CONTEXT_RANGE
 
 
-def test_prefill_fp32_is_refused():
-    case = make_decode_case("qwen0.5b-fp32", DEV, num_seqs=2)
-    q = case.q.reshape(-1, case.q.shape[1], case.q.shape[2])
-    cu = torch.tensor([0, 1, 2], dtype=torch.int32, device=DEV)
-    qs = torch.tensor([3, 4], dtype=torch.int32, device=DEV)
-    with pytest.raises(RuntimeError, match="fp32"):
-        kernels.paged_prefill(q, case.k_cache, case.v_cache, case.block_tables[0], cu, qs, 1, 16, 0.125)
+F32_TOL = 1e-4  # the fp32 bar, against an fp64 restatement
+
+_F32_SWEEP = [
+    # (h_q, h_kv, d, bs): the 0.5B model's shape; one query head per KV head;
+    # GQA 7 at head_dim 128 on a 12-token block (general addressing); 64 query
+    # heads per KV head (one token per workgroup)
+    (14, 2, 64, 16),
+    (8, 8, 128, 16),
+    (28, 4, 128, 12),
+    (64, 1, 64, 16),
+]
+
+
+def _check_f32(case, plan=None):
+    cfg = case.config
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[0], case.cu_seqlens_q,
+                                case.q_start, max(case.q_lens), cfg.block_size, cfg.scale, err_flags=err, plan=plan)
+    torch.cuda.synchronize()
+    assert err.item() == 0
+    ref = O.prefill_reference(case.q.cpu(), case.k_cache.cpu(), case.v_cache.cpu(), case.block_tables[0].cpu(),
+                              case.cu_seqlens_q.cpu(), case.q_start.cpu(), cfg.block_size, cfg.scale,
+                              compute_dtype=torch.float64)
+    diff = (out.double().cpu() - ref).abs().max().item()
+    assert diff <= F32_TOL, f"{cfg.name}: max-abs {diff}"
+    return out
+
+
+@pytest.mark.parametrize("h_q,h_kv,d,bs", _F32_SWEEP)
+@pytest.mark.parametrize("layout", ["head_major", "slot_major"])
+def test_prefill_fp32_matches_the_oracle(h_q, h_kv, d, bs, layout):
+    """fp32 chunks -- the reference's fp32 path -- on their own kernel: ragged
+    chunks after prefixes that end mid-block, both pool layouts, within 1e-4
+    of an fp64 restatement."""
+    cfg = PrefillConfig(f"pf32-{h_q}-{h_kv}-{d}-{bs}", 5, 0, h_q, h_kv, d, bs, torch.float32, 0, seed=h_q + d + bs)
+    case = make_prefill_case(cfg, DEV, prefixes=[0, 17, 64, 200, 95], q_lens=[33, 64, 1, 130, 47], layout=layout)
+    _check_f32(case)
+
+
+def test_prefill_fp32_reloads_block_ids_and_ignores_a_plan():
+    """fp32, block size 1 and a 2,600-token context: the staged block ids are
+    refilled mid-walk; a work plan is accepted and not read (the same output
+    bit for bit)."""
+    cfg = PrefillConfig("pf32-bs1-long", 2, 0, 8, 2, 64, 1, torch.float32, 0, seed=3)
+    case = make_prefill_case(cfg, DEV, prefixes=[2500, 1100], q_lens=[100, 40])
+    out = _check_f32(case)
+    plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.block_tables[0], case.q.shape[0], 100,
+                                cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim)
+    assert torch.equal(_check_f32(case, plan), out)
+
+
+def test_prefill_fp32_flags_bad_block_ids_and_refuses_wide_groups():
+    """fp32: a block id outside the pool is flagged and its keys read as zeros
+    (within 1e-4 of the restatement with that block zeroed); more than 64 query
+    heads per KV head are refused."""
+    cfg = PrefillConfig("pf32-bad", 3, 0, 14, 2, 64, 16, torch.float32, 0, seed=12)
+    case = make_prefill_case(cfg, DEV, prefixes=[40, 300, 0], q_lens=[20, 50, 70])
+    bt = case.block_tables[0].clone()
+    bt[1, 2] = case.pool_blocks + 9
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = kernels.paged_prefill(case.q, case.k_cache, case.v_cache, bt, case.cu_seqlens_q, case.q_start, 70,
+                                cfg.block_size, cfg.scale, err_flags=err)
+    torch.cuda.synchronize()
+    assert err.item() == ERR_BLOCK_RANGE
+    kz, vz = case.k_cache.clone().cpu(), case.v_cache.clone().cpu()
+    zero_bt = bt.cpu().clone()
+    zero_bt[1, 2] = case.pool_blocks  # an extra all-zero block appended below
+    kz = torch.cat([kz, torch.zeros(cfg.block_size, *kz.shape[1:])])
+    vz = torch.cat([vz, torch.zeros(cfg.block_size, *vz.shape[1:])])
+    ref = O.prefill_reference(case.q.cpu(), kz, vz, zero_bt, case.cu_seqlens_q.cpu(), case.q_start.cpu(),
+                              cfg.block_size, cfg.scale, compute_dtype=torch.float64)
+    assert (out.double().cpu() - ref).abs().max().item() <= F32_TOL
+    wide = PrefillConfig("pf32-wide", 1, 0, 128, 1, 64, 16, torch.float32, 0, seed=13)
+    case = make_prefill_case(wide, DEV, prefixes=[5], q_lens=[3])
+    with pytest.raises(RuntimeError, match="fp32 with more than 64"):
+        kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[0], case.cu_seqlens_q,
+                              case.q_start, 3, wide.block_size, wide.scale)
 
 
 def _host_weights(case, tq, n_qblocks):

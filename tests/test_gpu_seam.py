@@ -470,17 +470,19 @@ def _prefill_case(kind):
     return tables, num_cached, q_lens, sum(need) + 40
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("kind", ["prefix-hit", "mixed", "chunks"])
-def test_reference_prefill_metadata_runs_the_prefill_kernel(kind):
+def test_reference_prefill_metadata_runs_the_prefill_kernel(kind, dtype):
     """Unchanged reference callers pass a packed frame (batch 1) of gather_slots
     + the varlen / causal mask for prefix-hit prefills and mixed steps. Its
     form is recognised once per step (later layers reuse the derived metadata:
     cu_seqlens_q, q_start, block tables, and for a mixed step the split of its
     decode rows), and every layer equals the block-table context's output bit
-    for bit -- the same kernels on the same metadata -- and the oracle."""
+    for bit -- the same kernels on the same metadata -- and the oracle (fp32:
+    the fp32 prefill kernel, within 1e-4 of an fp64 restatement)."""
     tables, num_cached, q_lens, num_blocks = _prefill_case(kind)
     bs, h_kv, n_rep, d, layers = 16, 4, 7, 128, 3
-    pool = PagedKVPool(layers, num_blocks, bs, h_kv, d, torch.bfloat16, device=DEV)
+    pool = PagedKVPool(layers, num_blocks, bs, h_kv, d, dtype, device=DEV)
     pool.k.normal_()
     pool.v.normal_()
     ours, _ = metadata.prefill_context(pool, tables, num_cached, q_lens)
@@ -491,17 +493,19 @@ def test_reference_prefill_metadata_runs_the_prefill_kernel(kind):
     dgen = torch.Generator(device=DEV).manual_seed(2)
     forms = []
     for layer in range(layers):
-        q = torch.randn(1, total, h_kv * n_rep, d, generator=dgen, device=DEV).bfloat16()
-        k = torch.randn(1, total, h_kv, d, generator=dgen, device=DEV).bfloat16()
-        v = torch.randn(1, total, h_kv, d, generator=dgen, device=DEV).bfloat16()
-        got = paged_attention(q, k, v, ref, mask, layer, d**-0.5, n_rep)
+        q = torch.randn(1, total, h_kv * n_rep, d, generator=dgen, device=DEV).to(dtype)
+        k = torch.randn(1, total, h_kv, d, generator=dgen, device=DEV).to(dtype)
+        v = torch.randn(1, total, h_kv, d, generator=dgen, device=DEV).to(dtype)
+        got = paged_attention(q, k, v, ref, mask.to(dtype), layer, d**-0.5, n_rep)
         forms.append(pool._ref_varlen[1])
         want = paged_attention(q, k, v, ours, None, layer, d**-0.5, n_rep)
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"layer {layer}"
+        f32 = dtype == torch.float32
         expect = O.prefill_reference(q[0].cpu(), pool.k[layer].cpu(), pool.v[layer].cpu(),
-                                     ours.block_tables.cpu(), ours.cu_seqlens_q.cpu(), num_cached, bs, d**-0.5)
-        assert (got[0].float().cpu() - expect).abs().max().item() <= 2e-2
+                                     ours.block_tables.cpu(), ours.cu_seqlens_q.cpu(), num_cached, bs, d**-0.5,
+                                     compute_dtype=torch.float64 if f32 else torch.float32)
+        assert (got[0].to(expect.dtype).cpu() - expect).abs().max().item() <= (1e-4 if f32 else 2e-2)
     f = forms[0]
     assert f is not None and all(x is f for x in forms)
     assert f.max_q_len == max(q_lens)
