@@ -60,8 +60,10 @@ enum {
 
 /* flags of ir_paged_prefill_plan, ir_paged_decode_plan and ir_paged_decode_planned */
 enum {
-  IR_PLAN_SHARE_GROUPS = 1  /* prefill: keep each shared-prefix group's KV head on one XCD;
+  IR_PLAN_SHARE_GROUPS = 1, /* prefill: keep each shared-prefix group's KV head on one XCD;
                                decode: run sequence pairs that share prefix blocks as one unit */
+  IR_PLAN_F32 = 2           /* prefill: a plan for an fp32 call (the fp32 kernel's 64-column
+                               items); a 16-bit call takes only a plan built without it */
 };
 
 /* flags of ir_decode_form */
@@ -411,7 +413,8 @@ int ir_varlen_form_tables(const int64_t* gather_slots, int64_t gs_k_stride, cons
  *                 longer than it sets IR_ERR_CONTEXT_RANGE and its rows past the bound
  *                 are not written).
  *   plan:         null, or the plan ir_paged_prefill_plan wrote for this call's
- *                 cu_seqlens_q / q_start and shapes (plan_bytes as sized by
+ *                 cu_seqlens_q / q_start, shapes and dtype (IR_PLAN_F32 for fp32,
+ *                 without it for bf16 / f16; plan_bytes as sized by
  *                 ir_paged_prefill_plan_bytes): workgroups then run the heaviest work
  *                 first, and items heavier than the mean load of a workgroup slot are cut
  *                 into key-range pieces merged in the same launch. The plan also holds
@@ -423,9 +426,9 @@ int ir_varlen_form_tables(const int64_t* gather_slots, int64_t gs_k_stride, cons
  * that block's keys read as zeros. head_dim in {64, 128}; dtype bf16, f16 or fp32. fp32
  * (the reference's fp32 path: fp32 scores, softmax and PV product) runs on its own
  * kernel of 64-column workgroups: at most 64 query heads per KV head (more returns
- * IR_EUNSUPPORTED), unplanned (a plan is accepted and not read), the fused write as
- * its own launch first; its q, out, cache and new-row strides are multiples of 16 bytes
- * and out 16-byte aligned.
+ * IR_EUNSUPPORTED), planned by a plan built with IR_PLAN_F32, the fused write as its
+ * own launch first; its q, out, cache and new-row strides are multiples of 16 bytes and
+ * out 16-byte aligned.
  * Fused K/V write (the step's PagedKVPool.write folded into the call; k_new null: none):
  *   k_new, v_new: [n_write, num_kv_heads, head_dim] (strides token, head in elements;
  *                 16-byte aligned, 16-byte strides), rows written to the caches at
@@ -459,11 +462,14 @@ int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
  * layers; so is this plan: build it once per step, pass it to every layer's
  * ir_paged_prefill.
  * ir_paged_prefill_plan_bytes: bytes of plan for these shapes (0 when there is
- *   nothing to plan).
+ *   nothing to plan), enough for a plan of either kind (IR_PLAN_F32 or not).
  * ir_paged_prefill_plan: writes the plan (one workgroup: weighs every (sequence,
  *   query block) item by the key tiles it walks, cuts the heaviest, places the
  *   pieces, clears the arrival counters). Arguments as for ir_paged_prefill,
- *   plus flags. Default placement: one global heaviest-first order, a piece's
+ *   plus flags; IR_PLAN_F32 plans an fp32 call, whose items are the fp32
+ *   kernel's (64 / n_rep query tokens, at most 64 query heads per KV head), and
+ *   only an fp32 call reads such a plan. Default placement: one global
+ *   heaviest-first order, a piece's
  *   KV heads on consecutive workgroups. IR_PLAN_SHARE_GROUPS: consecutive
  *   sequences whose block tables begin with the same block id form a share
  *   group -- the prefix cache of infrared/cache/block_manager.py:209-234

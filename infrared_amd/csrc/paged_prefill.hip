@@ -64,6 +64,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include <type_traits>
 
 #include "attn_tile.hpp"
@@ -817,9 +819,11 @@ void paged_prefill_kernel(PrefillArgs a) {
 // element (row c, k-slot g) of A and (k-slot g, column c) of B and receives
 // rows 4g..4g+3 of column c. A workgroup is 4 wavefronts of one 16-column
 // tile: 64 columns, tq = 64 / n_rep tokens of one KV head's query heads, in
-// the 16-bit kernel's unplanned order (last query blocks first). Keys walk in
-// 64-key tiles through LDS -- K row-major, V transposed, so both operands are
-// 16-byte reads -- with the next tile's loads in flight in registers. The
+// the order of a plan built with IR_PLAN_F32 (heaviest first, the heaviest
+// items cut into key-range pieces merged like the 16-bit kernel's), else the
+// last query blocks first. Keys walk in 64-key tiles through LDS -- K
+// row-major, V transposed, so both operands are 16-byte reads -- with the next
+// tile's loads in flight in registers. The
 // score product's k-slot g of step (m, r) is d = 16 m + 4 g + r (a lane's K
 // read covers its four steps); the PV product's k-slot g of step (kt, r) is
 // key 16 kt + 4 g + r, the lane's own probability of that key. Same masking,
@@ -842,10 +846,26 @@ void paged_prefill_f32_kernel(PrefillArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6, g = lane >> 4, c = lane & 15;
   const int TQ = a.tq;
-  const int per_tb = a.num_kv_heads * a.num_seqs;
-  const int tb = a.n_qblocks - 1 - (int)(blockIdx.x / per_tb);
-  const int rest = (int)(blockIdx.x % per_tb);
-  const int seq = rest % a.num_seqs, kvh = rest / a.num_seqs;
+  // which (query block, KV head, sequence) and which piece of its keys: plan
+  // entry i when a plan is given, else the last query blocks first, uncut
+  int tb, seq, kvh, nparts = 1, part = 0, pbase = 0;
+  if (a.items) {
+    const int2 e = a.items[blockIdx.x];
+    const int item = e.x < 0 ? -1 : e.x / a.num_kv_heads;
+    if (item < 0 || item >= a.num_seqs * a.n_qblocks) return;
+    kvh = e.x - item * a.num_kv_heads;
+    seq = item / a.n_qblocks;
+    tb = item - seq * a.n_qblocks;
+    nparts = max(e.y & 0xff, 1);
+    part = min((e.y >> 8) & 0xff, nparts - 1);
+    pbase = (int)((uint32_t)e.y >> 16);
+  } else {
+    const int per_tb = a.num_kv_heads * a.num_seqs;
+    tb = a.n_qblocks - 1 - (int)(blockIdx.x / per_tb);
+    const int rest = (int)(blockIdx.x % per_tb);
+    seq = rest % a.num_seqs;
+    kvh = rest / a.num_seqs;
+  }
   const int q_lo = a.cu_q[seq];
   const int q_len = a.cu_q[seq + 1] - q_lo;
   if (q_lo < 0 || q_len < 0 || (int64_t)q_lo + q_len > a.total_q) {
@@ -864,6 +884,11 @@ void paged_prefill_f32_kernel(PrefillArgs a) {
   }
   const int kmax = min(cap, p0 + min(q_len, tq0 + TQ));
   const int nkb = kmax > 0 && a.num_blocks > 0 ? (kmax + BN - 1) / BN : 0;
+  // this piece walks key tiles [t_lo, t_hi); a cut item's pieces are at
+  // least four tiles (the plan cuts only items of more than eight), so a
+  // piece's first tile lies before every column's causal limit
+  const int t_lo = (int)((int64_t)part * nkb / nparts);
+  const int t_hi = (int)((int64_t)(part + 1) * nkb / nparts);
 
   // this lane's column j = 16 w + c: token tq0 + j / n_rep, query head
   // kvh * n_rep + j % n_rep
@@ -962,13 +987,13 @@ void paged_prefill_f32_kernel(PrefillArgs a) {
   const int qpos0 = p0 + tq0;
   const int col_lim = min(p0 + col_tok, kmax - 1);  // last key the column may see
 
-  if (nkb > 0) {
-    fill_bt(0);
-    load_tile(0);
+  if (t_lo < t_hi) {
+    fill_bt(FAST ? (t_lo * BN) >> a.bs_shift : (t_lo * BN) / a.bs);
+    load_tile(t_lo);
     store_tile();
-    if (nkb > 1) load_tile(1);
+    if (t_lo + 1 < t_hi) load_tile(t_lo + 1);
     __syncthreads();
-    for (int kb = 0; kb < nkb; ++kb) {
+    for (int kb = t_lo; kb < t_hi; ++kb) {
       const int k0 = kb * BN;
       f32x4 s[4];
 #pragma unroll
@@ -992,8 +1017,8 @@ void paged_prefill_f32_kernel(PrefillArgs a) {
       float mx = kNegInf;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
-      mx = wave_max_groups_swap(mx);  // relative to m; finite on the first tile (key 0 is always visible)
-      const bool first = kb == 0;
+      mx = wave_max_groups_swap(mx);  // relative to m; finite on the piece's first tile
+      const bool first = kb == t_lo;
       const bool grow = first || mx > kRescaleSlack;
       if (__any(grow)) {
         const float d = grow ? mx : 0.f;  // the max moves up by d
@@ -1023,24 +1048,84 @@ void paged_prefill_f32_kernel(PrefillArgs a) {
           for (int r = 0; r < 4; ++r) acc[dt] = mfma_f32_k4(v4[r], s[kt][r], acc[dt]);
         }
       __syncthreads();  // every wavefront is done with tile kb
-      if (kb + 1 < nkb) {
+      if (kb + 1 < t_hi) {
         store_tile();
-        if (kb + 2 < nkb) load_tile(kb + 2);
+        if (kb + 2 < t_hi) load_tile(kb + 2);
       }
       __syncthreads();
     }
   }
   if (bad) flag_error(a.err, IR_ERR_BLOCK_RANGE);
   const float lsum = wave_sum_groups_swap(l);
-  if (!col_ok) return;
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   float* orow = (float*)a.out + (int64_t)(q_lo + col_tok) * a.o_tok + (int64_t)col_head * a.o_head;
+  if (nparts == 1) {
+    if (!col_ok) return;
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
 #pragma unroll
-  for (int dt = 0; dt < MT; ++dt) *(f32x4*)(orow + 16 * dt + 4 * g) = acc[dt] * inv;
+    for (int dt = 0; dt < MT; ++dt) *(f32x4*)(orow + 16 * dt + 4 * g) = acc[dt] * inv;
+    return;
+  }
+
+  // ---- a piece of a cut item: its partial rows (device scope) and arrival;
+  // the last piece to arrive merges all of them in part order, its own from
+  // registers (the same arithmetic whichever piece arrives last)
+  const __amdgpu_buffer_rsrc_t r_o = dev_rsrc(a.ws_o), r_ml = dev_rsrc(a.ws_ml);
+  const int row_step = a.num_kv_heads * kF32Cols;               // rows between parts of one item
+  const int row_col = (pbase * a.num_kv_heads + kvh) * kF32Cols + j;  // part 0, this column
+  {
+    const int row = row_col + part * row_step;
+#pragma unroll
+    for (int dt = 0; dt < MT; ++dt) store_dev4(r_o, (row * D + 16 * dt + 4 * g) * 4, acc[dt]);
+    if (g == 0) store_dev2(r_ml, row * 8, f32x2{-negm, lsum});
+  }
+  __shared__ int s_last;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  int32_t* ctr = a.counters + pbase * a.num_kv_heads + kvh;
+  if (tid == 0) s_last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nparts - 1;
+  __syncthreads();
+  if (!s_last) return;
+  f32x4 o_run[MT];
+  float m_run = kNegInf, l_run = 0.f;
+#pragma unroll
+  for (int dt = 0; dt < MT; ++dt) o_run[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int p = 0; p < nparts; ++p) {
+    f32x4 op[MT];
+    float mp, lp;
+    if (p == part) {
+      mp = -negm;
+      lp = lsum;
+#pragma unroll
+      for (int dt = 0; dt < MT; ++dt) op[dt] = acc[dt];
+    } else {
+      const int row = row_col + p * row_step;
+      const f32x2 ml = load_dev2(r_ml, row * 8);
+      mp = ml[0];
+      lp = ml[1];
+#pragma unroll
+      for (int dt = 0; dt < MT; ++dt) op[dt] = load_dev4(r_o, (row * D + 16 * dt + 4 * g) * 4);
+    }
+    // a part without keys has max -inf: its weight is exp2(-inf) = 0, and
+    // fmaxf keeps an (-inf) - (-inf) exponent from becoming NaN
+    const float mn = fmaxf(m_run, mp);
+    const float wa = fast_exp2(fmaxf(m_run - mn, -1e30f)), wb = fast_exp2(fmaxf(mp - mn, -1e30f));
+    l_run = wa * l_run + wb * lp;
+#pragma unroll
+    for (int dt = 0; dt < MT; ++dt) o_run[dt] = wa * o_run[dt] + wb * op[dt];
+    m_run = mn;
+  }
+  if (col_ok) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < MT; ++dt) *(f32x4*)(orow + 16 * dt + 4 * g) = o_run[dt] * inv;
+  }
+  if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The fp32 launch: the step's K/V write (when given) as its own launch first,
-// then one workgroup per (query block, KV head, sequence); no plan.
+// then one workgroup per plan entry, or per (query block, KV head, sequence)
+// unplanned.
 template <int D>
 int launch_prefill_f32(PrefillArgs a, hipStream_t s) {
   if (a.k_new != nullptr) {
@@ -1049,7 +1134,7 @@ int launch_prefill_f32(PrefillArgs a, hipStream_t s) {
                                  a.num_kv_heads, D, IR_DTYPE_F32, a.err, (ir_stream_t)s);
     if (rc != IR_OK) return rc;
   }
-  const int64_t grid = (int64_t)a.n_qblocks * a.num_kv_heads * a.num_seqs;
+  const int64_t grid = a.items ? a.n_items_grid : (int64_t)a.n_qblocks * a.num_kv_heads * a.num_seqs;
   if (grid <= 0) return ok();
   if (grid > 0x7fffffff) return fail(IR_EINVAL, "ir_paged_prefill: grid of %lld workgroups too large", (long long)grid);
   const int64_t slots = a.num_blocks * a.bs;
@@ -1438,7 +1523,7 @@ int plan_xcds() {
 // wavefronts (256 columns) when a token's query heads need more than 128
 // columns or on request. `slots`: workgroups resident at once.
 struct PrefillGeometry {
-  int nw, tq, n_qblocks, sched, slots;
+  int nw, tq, n_qblocks, sched, slots, cols;  // cols: query columns (token x head) of a work item
 };
 
 PrefillGeometry prefill_geometry(int max_q_len, int n_rep) {
@@ -1453,6 +1538,20 @@ PrefillGeometry prefill_geometry(int max_q_len, int n_rep) {
   const bool ring2 = g.nw == 8 || k.ring2 != 0;
   g.sched = ring2 ? kRing2 : kLockstep;
   g.slots = ring2 && g.nw == 4 ? 2 * cus : cus;
+  g.cols = 32 * g.nw;
+  return g;
+}
+
+// The fp32 kernel's items: 64 columns, two workgroups resident per CU
+// (n_rep <= kF32Cols).
+PrefillGeometry prefill_geometry_f32(int max_q_len, int n_rep) {
+  PrefillGeometry g;
+  g.nw = 4;
+  g.tq = kF32Cols / n_rep;
+  g.n_qblocks = (max_q_len + g.tq - 1) / g.tq;
+  g.sched = kRing2;
+  g.slots = 2 * device_cus();
+  g.cols = kF32Cols;
   return g;
 }
 
@@ -1470,7 +1569,7 @@ struct PlanLayout {
 
 PlanLayout plan_layout(const PrefillGeometry& g, int num_seqs, int num_kv_heads, int head_dim) {
   PlanLayout l;
-  l.cols = 32 * g.nw;
+  l.cols = g.cols;
   l.cap_pieces = (g.slots + num_kv_heads - 1) / num_kv_heads;
   const int64_t wgs = ((int64_t)num_seqs * g.n_qblocks + l.cap_pieces) * num_kv_heads;
   const int x = plan_xcds();
@@ -1554,8 +1653,10 @@ extern "C" int64_t ir_paged_prefill_plan_bytes(int num_seqs, int max_q_len, int 
   if (num_seqs <= 0 || max_q_len <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads ||
       num_q_heads / num_kv_heads > 256 || (head_dim != 64 && head_dim != 128))
     return 0;
-  const PrefillGeometry geo = prefill_geometry(max_q_len, num_q_heads / num_kv_heads);
-  return plan_layout(geo, num_seqs, num_kv_heads, head_dim).total;
+  const int n_rep = num_q_heads / num_kv_heads;
+  const int64_t b16 = plan_layout(prefill_geometry(max_q_len, n_rep), num_seqs, num_kv_heads, head_dim).total;
+  if (n_rep > kF32Cols) return b16;
+  return std::max(b16, plan_layout(prefill_geometry_f32(max_q_len, n_rep), num_seqs, num_kv_heads, head_dim).total);
 }
 
 extern "C" int ir_paged_prefill_plan_xcds(void) { return plan_xcds(); }
@@ -1618,14 +1719,14 @@ extern "C" int ir_paged_prefill(const void* q, int64_t q_tok_stride, int64_t q_h
   a.num_seqs = num_seqs;
   a.total_q = total_q;
   a.n_rep = num_q_heads / num_kv_heads;
-  const PrefillGeometry geo = prefill_geometry(max_q_len, a.n_rep);
+  const PrefillGeometry geo = f32 ? prefill_geometry_f32(max_q_len, a.n_rep) : prefill_geometry(max_q_len, a.n_rep);
   a.nw = geo.nw;
-  a.tq = f32 ? kF32Cols / a.n_rep : geo.tq;
-  a.n_qblocks = f32 ? (max_q_len + a.tq - 1) / a.tq : geo.n_qblocks;
+  a.tq = geo.tq;
+  a.n_qblocks = geo.n_qblocks;
   const int64_t n_items = (int64_t)num_seqs * a.n_qblocks;
   IR_REQUIRE(n_items * num_kv_heads <= 0x7fffffff, "ir_paged_prefill: %lld work items x %d KV heads",
              (long long)n_items, num_kv_heads);
-  if (plan && !f32) {  // (fp32 runs unplanned: a plan is accepted and not read)
+  if (plan) {
     const PlanLayout ly = plan_layout(geo, num_seqs, num_kv_heads, head_dim);
     IR_REQUIRE(plan_bytes >= ly.total && ((uintptr_t)plan & 255u) == 0,
                "ir_paged_prefill: plan of %lld bytes (256-byte aligned) required, got %lld (build it with "
@@ -1682,7 +1783,11 @@ extern "C" int ir_paged_prefill_plan(const int32_t* cu_seqlens_q, const int32_t*
              "ir_paged_prefill_plan: bad sizes");
   IR_REQUIRE(num_q_heads % num_kv_heads == 0, "ir_paged_prefill_plan: num_q_heads %d not a multiple of num_kv_heads %d",
              num_q_heads, num_kv_heads);
-  IR_REQUIRE((flags & ~IR_PLAN_SHARE_GROUPS) == 0, "ir_paged_prefill_plan: unknown flags 0x%x", flags);
+  IR_REQUIRE((flags & ~(IR_PLAN_SHARE_GROUPS | IR_PLAN_F32)) == 0, "ir_paged_prefill_plan: unknown flags 0x%x",
+             flags);
+  const bool f32 = (flags & IR_PLAN_F32) != 0;
+  if (f32 && num_q_heads / num_kv_heads > kF32Cols)
+    return fail(IR_EUNSUPPORTED, "ir_paged_prefill_plan: fp32 with more than %d query heads per KV head", kF32Cols);
   IR_REQUIRE((int64_t)max_blocks_per_seq * block_size <= (int64_t)1 << 30,
              "ir_paged_prefill_plan: block tables of %d x %d tokens exceed 2^30 keys", max_blocks_per_seq,
              block_size);
@@ -1695,7 +1800,8 @@ extern "C" int ir_paged_prefill_plan(const int32_t* cu_seqlens_q, const int32_t*
              "ir_paged_prefill_plan: null pointer");
   IR_REQUIRE(bt_stride >= max_blocks_per_seq, "ir_paged_prefill_plan: bt_stride %lld below max_blocks_per_seq %d",
              (long long)bt_stride, max_blocks_per_seq);
-  const PrefillGeometry geo = prefill_geometry(max_q_len, num_q_heads / num_kv_heads);
+  const int n_rep = num_q_heads / num_kv_heads;
+  const PrefillGeometry geo = f32 ? prefill_geometry_f32(max_q_len, n_rep) : prefill_geometry(max_q_len, n_rep);
   const PlanLayout ly = plan_layout(geo, num_seqs, num_kv_heads, head_dim);
   IR_REQUIRE(ly.entries <= 0x7fffffff && ly.cap_pieces < 65536 &&
                  (int64_t)num_seqs * geo.n_qblocks * num_kv_heads <= 0x7fffffff &&

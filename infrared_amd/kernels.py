@@ -458,6 +458,7 @@ def rope_kv_scatter(
 
 
 PLAN_SHARE_GROUPS = 1  # IR_PLAN_SHARE_GROUPS
+PLAN_F32 = 2  # IR_PLAN_F32
 
 
 @dataclass(frozen=True)
@@ -466,7 +467,9 @@ class PrefillPlan:
     for. ``buf`` holds the heaviest-first pieces of one step's prefill metadata
     plus their arrival counters and partial rows; every layer of the step runs
     on it with :func:`paged_prefill` (stream-ordered: the runs write into it).
-    Rebuild it when ``cu_seqlens_q``/``q_start`` change."""
+    Rebuild it when ``cu_seqlens_q``/``q_start`` change. ``f32``: built for
+    fp32 calls (``IR_PLAN_F32``: the fp32 kernel's 64-column items), which
+    read only such a plan."""
 
     buf: torch.Tensor
     num_seqs: int
@@ -474,6 +477,7 @@ class PrefillPlan:
     num_q_heads: int
     num_kv_heads: int
     head_dim: int
+    f32: bool = False
 
 
 def prefill_plan_bytes(num_seqs: int, max_q_len: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
@@ -491,7 +495,8 @@ PLAN_CUT_KEYS = 1024  # a call whose longest context exceeds this many keys is p
 
 
 def prefill_plan_pays(num_seqs: int, max_q_len: int, num_q_heads: int, num_kv_heads: int,
-                      device: torch.device | str | int | None = None, max_keys: int = 0) -> bool:
+                      device: torch.device | str | int | None = None, max_keys: int = 0,
+                      dtype: torch.dtype = torch.bfloat16) -> bool:
     """Whether a plan can shorten the call: its workgroups outnumber the CUs,
     so the dispatch order -- and cutting the heaviest items -- decides which
     CU finishes last; or its longest context (``max_keys``, e.g. the block
@@ -500,18 +505,28 @@ def prefill_plan_pays(num_seqs: int, max_q_len: int, num_q_heads: int, num_kv_he
     workgroup starts at once (one 512-token chunk after 4,096 cached: 68 vs
     110 us; two 128-token chunks after 1,024: 26 vs 32 us). Otherwise every
     workgroup starts at once with nothing worth cutting. (Items are (sequence,
-    block of 128 // n_rep query tokens), 4-wavefront workgroups.)"""
+    block of 128 // n_rep query tokens), 4-wavefront workgroups; in fp32 blocks
+    of 64 // n_rep tokens, two workgroups resident per CU, so an fp32 call is
+    planned when its workgroups outnumber twice the CUs.)"""
     if num_seqs <= 0 or max_q_len <= 0 or num_kv_heads <= 0 or num_q_heads % num_kv_heads:
         return False
+    n_rep = num_q_heads // num_kv_heads
+    if dtype == torch.float32 and n_rep > 64:
+        return False  # (the fp32 kernel refuses such groups)
     if max_keys > PLAN_CUT_KEYS:
         return True
-    n_rep = num_q_heads // num_kv_heads
-    tq = (128 if n_rep <= 128 else 256) // n_rep
+    # workgroups resident at once: the 16-bit kernel's calls that fit one per
+    # CU run a shape of their own, unplanned; the fp32 kernel holds two per CU
+    per_cu = 1
+    if dtype == torch.float32:
+        tq, per_cu = 64 // n_rep, 2
+    else:
+        tq = (128 if n_rep <= 128 else 256) // n_rep
     idx = torch.device(device if device is not None else "cuda").index
     idx = torch.cuda.current_device() if idx is None else idx
     if idx not in _CU_COUNT:
         _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
-    return num_seqs * -(-max_q_len // tq) * num_kv_heads > _CU_COUNT[idx]
+    return num_seqs * -(-max_q_len // tq) * num_kv_heads > per_cu * _CU_COUNT[idx]
 
 
 def prefill_plan(
@@ -526,6 +541,7 @@ def prefill_plan(
     head_dim: int,
     buf: torch.Tensor | None = None,
     share_groups: bool = False,
+    dtype: torch.dtype = torch.bfloat16,
 ) -> PrefillPlan:
     """Work plan of a prefill call's (sequence, query block) items, built on
     the device (``ir_paged_prefill_plan``); pass it to every layer's
@@ -535,10 +551,12 @@ def prefill_plan(
     with the same block id -- so a shared prefix is fetched into one L2
     (fewer bytes from memory; slower on a prefill that has HBM to itself);
     by default one global heaviest-first order. Tables with other ids but the
-    same shape run correctly on the plan. ``buf`` (uint8, 256-byte aligned) is
-    reused when large enough."""
+    same shape run correctly on the plan. ``dtype``: the calls' dtype (fp32
+    calls take a plan of their own kernel's items). ``buf`` (uint8, 256-byte
+    aligned) is reused when large enough."""
     dev = require_device(cu_seqlens_q, q_start, block_tables)
     b = q_start.shape[0]
+    f32 = dtype == torch.float32
     for name, t, n in (("cu_seqlens_q", cu_seqlens_q, b + 1), ("q_start", q_start, b)):
         if t.dtype != torch.int32 or t.shape != (n,) or not t.is_contiguous():
             raise RuntimeError(f"prefill_plan: {name} must be contiguous int32 [{n}]")
@@ -556,10 +574,11 @@ def prefill_plan(
     rc = lib().ir_paged_prefill_plan(
         ptr(cu_seqlens_q), ptr(q_start), ptr(block_tables), max(block_tables.stride(0), max_blocks), b,
         int(total_q), int(max_q_len), int(max_blocks), int(block_size), num_q_heads, num_kv_heads, head_dim,
-        PLAN_SHARE_GROUPS if share_groups else 0, ptr(buf), buf.numel(), stream_ptr(dev),
+        (PLAN_SHARE_GROUPS if share_groups else 0) | (PLAN_F32 if f32 else 0), ptr(buf), buf.numel(),
+        stream_ptr(dev),
     )
     check(rc, "ir_paged_prefill_plan")
-    return PrefillPlan(buf, b, int(max_q_len), num_q_heads, num_kv_heads, head_dim)
+    return PrefillPlan(buf, b, int(max_q_len), num_q_heads, num_kv_heads, head_dim, f32)
 
 
 def paged_prefill(
@@ -615,6 +634,9 @@ def paged_prefill(
         if (plan.num_seqs, plan.max_q_len, plan.num_q_heads, plan.num_kv_heads, plan.head_dim) != (
                 b, int(max_q_len), hq, h_kv, d):
             raise RuntimeError("paged_prefill: the plan was built for other shapes")
+        if plan.f32 != (q.dtype == torch.float32):
+            raise RuntimeError("paged_prefill: the plan was built for "
+                               + ("fp32" if plan.f32 else "16-bit") + f" calls, q is {q.dtype}")
     if out is None:
         out = torch.empty(total_q, hq, d, dtype=q.dtype, device=dev)
     kn = vn = slots = None

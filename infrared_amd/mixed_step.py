@@ -178,7 +178,8 @@ class MixedStep:
         self.plan: kernels.DecodePlan | None = None
         npre = batch.q_start.shape[0]
         self.ordered = kernels.prefill_plan_pays(npre, batch.max_q_len, hq, pool.num_kv_heads, dev,
-                                                 max_keys=batch.pre_tables.shape[1] * pool.block_size)
+                                                 max_keys=batch.pre_tables.shape[1] * pool.block_size,
+                                                 dtype=pool.dtype)
         self.plan_pre_buf = (torch.empty(kernels.prefill_plan_bytes(npre, batch.max_q_len, hq, pool.num_kv_heads, d),
                                          dtype=torch.uint8, device=dev) if self.ordered else None)
         self.plan_pre: kernels.PrefillPlan | None = None
@@ -251,7 +252,7 @@ class MixedStep:
             self.plan_pre = kernels.prefill_plan(
                 b.cu_seqlens_q, b.q_start, b.pre_tables, self.inputs.q_pre.shape[1], b.max_q_len,
                 self.pool.block_size, self.inputs.q_pre.shape[2], self.pool.num_kv_heads,
-                self.inputs.q_pre.shape[3], buf=self.plan_pre_buf,
+                self.inputs.q_pre.shape[3], buf=self.plan_pre_buf, dtype=self.inputs.q_pre.dtype,
             )
         for layer in range(self.pool.num_layers):
             self._layer(layer)

@@ -261,10 +261,12 @@ def _prefill(q, pool, layer_idx: int, block_tables, cu_seqlens_q, q_start, max_q
     h_kv = pool.k.shape[-2]
     nseq = q_start.shape[0]
     plan = getattr(holder, "prefill_plan", None)
-    if plan is None and q.dtype != torch.float32 and kernels.prefill_plan_pays(
-            nseq, max_q, hq, h_kv, q.device, max_keys=block_tables.shape[1] * pool.block_size):
+    if plan is not None and plan.f32 != (q.dtype == torch.float32):
+        plan = None  # (a plan of the other kind: rebuilt below and kept)
+    if plan is None and kernels.prefill_plan_pays(
+            nseq, max_q, hq, h_kv, q.device, max_keys=block_tables.shape[1] * pool.block_size, dtype=q.dtype):
         plan = kernels.prefill_plan(
-            cu_seqlens_q, q_start, block_tables, b * sq, max_q, pool.block_size, hq, h_kv, d
+            cu_seqlens_q, q_start, block_tables, b * sq, max_q, pool.block_size, hq, h_kv, d, dtype=q.dtype
         )
         try:
             holder.prefill_plan = plan

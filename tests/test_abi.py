@@ -128,19 +128,20 @@ def test_decode_plan_helpers():
     assert lib.ir_paged_decode_planned_workspace_bytes(64, 28, 4, 128) >= 256 * 16 * 128 * 4
 
 
-def _plan_bytes(num_seqs, max_q, n_rep, h_kv, d, cus=256, xcds=1):
+def _plan_bytes(num_seqs, max_q, n_rep, h_kv, d, cus=256, xcds=1, cols=128):
     """The plan layout the header documents, restated: 4-wavefront workgroups of
-    128 // n_rep query tokens (two resident per CU), one entry per workgroup --
-    (items + the piece capacity, one piece per KV head of every workgroup
-    slot) x KV heads, 1.5x that rounded to the XCD count when the plan places
-    work on XCDs -- the counters, and (max, sum) + D fp32 per partial row of
-    128 columns; each region 256-byte aligned."""
+    cols // n_rep query tokens (two resident per CU; 128 columns, 64 for an
+    fp32 plan), one entry per workgroup -- (items + the piece capacity, one
+    piece per KV head of every workgroup slot) x KV heads, 1.5x that rounded
+    to the XCD count when the plan places work on XCDs -- the counters, and
+    (max, sum) + D fp32 per partial row of `cols` columns; each region
+    256-byte aligned."""
     a = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    tq = 128 // n_rep
+    tq = cols // n_rep
     nqb = -(-max_q // tq)
     slots = 2 * cus
     cap = -(-slots // h_kv)
-    rows = cap * h_kv * 128
+    rows = cap * h_kv * cols
     wgs = (num_seqs * nqb + cap) * h_kv
     entries = xcds * -(-(wgs * 3 // 2) // xcds) if xcds > 1 else wgs
     return a(entries * 8) + a(cap * h_kv * 4) + a(rows * 8) + a(rows * d * 4)
@@ -154,8 +155,13 @@ def test_prefill_plan_helpers():
     lib = _lib.lib()
     x = lib.ir_paged_prefill_plan_xcds()
     assert x >= 1
-    assert lib.ir_paged_prefill_plan_bytes(8, 512, 28, 4, 128) == _plan_bytes(8, 512, 7, 4, 128, xcds=x)
-    assert lib.ir_paged_prefill_plan_bytes(2, 512, 28, 4, 64) == _plan_bytes(2, 512, 7, 4, 64, xcds=x)
+    # enough for either kind of plan: 16-bit (128 columns) or fp32 (64)
+    for args in ((8, 512, 7, 4, 128), (2, 512, 7, 4, 64), (1, 4096, 1, 8, 128)):
+        b, q_len, n_rep, h_kv, d = args
+        want = max(_plan_bytes(*args, xcds=x), _plan_bytes(*args, xcds=x, cols=64))
+        assert lib.ir_paged_prefill_plan_bytes(b, q_len, n_rep * h_kv, h_kv, d) == want, args
+    # more than 64 query heads per KV head: no fp32 plan, the 16-bit size
+    assert lib.ir_paged_prefill_plan_bytes(1, 64, 100, 1, 64) == _plan_bytes(1, 64, 100, 1, 64, xcds=x)
     assert lib.ir_paged_prefill_plan_bytes(0, 512, 28, 4, 128) == 0
     assert lib.ir_paged_prefill_plan_bytes(8, 512, 28, 3, 128) == 0
     assert lib.ir_paged_prefill_plan_bytes(8, 512, 28, 4, 96) == 0

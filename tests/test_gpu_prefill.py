@@ -186,16 +186,44 @@ def test_prefill_fp32_matches_the_oracle(h_q, h_kv, d, bs, layout):
     _check_f32(case)
 
 
-def test_prefill_fp32_reloads_block_ids_and_ignores_a_plan():
+def _cut_entries(plan, n):
+    """nparts of the plan's first n entries (heaviest first)."""
+    items = plan.buf[: 8 * n].view(torch.int32).view(n, 2).cpu()
+    return (items[:, 1] & 0xFF).tolist()
+
+
+def test_prefill_fp32_reloads_block_ids_and_runs_its_plan():
     """fp32, block size 1 and a 2,600-token context: the staged block ids are
-    refilled mid-walk; a work plan is accepted and not read (the same output
-    bit for bit)."""
+    refilled mid-walk. A plan built for fp32 (IR_PLAN_F32) cuts the long items
+    into key-range pieces: within 1e-4 of the restatement, within fp32 merge
+    rounding of the unplanned call, and the same bit for bit on a second call
+    (its arrival counters reset); a 16-bit plan is refused."""
     cfg = PrefillConfig("pf32-bs1-long", 2, 0, 8, 2, 64, 1, torch.float32, 0, seed=3)
     case = make_prefill_case(cfg, DEV, prefixes=[2500, 1100], q_lens=[100, 40])
     out = _check_f32(case)
     plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.block_tables[0], case.q.shape[0], 100,
-                                cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim)
-    assert torch.equal(_check_f32(case, plan), out)
+                                cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, dtype=torch.float32)
+    assert plan.f32 and max(_cut_entries(plan, 8)) > 1  # the heaviest items are cut
+    planned = _check_f32(case, plan)
+    assert (planned - out).abs().max().item() <= 1e-5
+    assert torch.equal(_check_f32(case, plan), planned)
+    plan16 = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.block_tables[0], case.q.shape[0], 100,
+                                  cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim)
+    with pytest.raises(RuntimeError, match="16-bit"):
+        _check_f32(case, plan16)
+
+
+@pytest.mark.parametrize("share_groups", [False, True])
+def test_prefill_fp32_planned_long_prefixes(share_groups):
+    """fp32 chunks after long prefixes that pairs share, on a plan (global
+    order or share groups): cut items merged within 1e-4 of the restatement."""
+    cfg = PrefillConfig("pf32-plan", 4, 0, 28, 4, 128, 16, torch.float32, 0, seed=21)
+    case = make_prefill_case(cfg, DEV, prefixes=[3000, 3500, 200, 5000], q_lens=[64, 17, 96, 40])
+    plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.block_tables[0], case.q.shape[0], 96,
+                                cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim,
+                                share_groups=share_groups, dtype=torch.float32)
+    assert max(_cut_entries(plan, 8)) > 1
+    _check_f32(case, plan)
 
 
 def test_prefill_fp32_flags_bad_block_ids_and_refuses_wide_groups():

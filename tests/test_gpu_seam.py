@@ -120,6 +120,13 @@ def test_prefill_step_builds_its_work_plan_once(case):
         num_cached, q_lens = [3000], [200]
         assert not kernels.prefill_plan_pays(1, 200, h_kv * n_rep, h_kv, DEV)
         assert kernels.prefill_plan_pays(1, 200, h_kv * n_rep, h_kv, DEV, max_keys=3200)
+        # fp32 items are 9 tokens, two workgroups resident per CU: 4 x 256
+        # tokens (464 workgroups) start at once, 8 x 256 do not
+        cus = torch.cuda.get_device_properties(DEV).multi_processor_count
+        for nseq in (4, 8):
+            wgs = nseq * -(-256 // 9) * h_kv
+            assert kernels.prefill_plan_pays(nseq, 256, h_kv * n_rep, h_kv, DEV, dtype=torch.float32) == (
+                wgs > 2 * cus)
     nblk = sum(metadata.blocks_for(c + n, bs) for c, n in zip(num_cached, q_lens))
     perm = torch.randperm(nblk + 10, generator=g).tolist()
     tables, off = [], 0

@@ -160,6 +160,9 @@ def test_prefill_plan_pays_for_long_contexts_on_any_grid():
     assert kernels.prefill_plan_pays(1, 200, 28, 4, "cpu", max_keys=keys + 1)
     assert not kernels.prefill_plan_pays(0, 200, 28, 4, "cpu", max_keys=keys + 1)  # nothing to plan
     assert not kernels.prefill_plan_pays(1, 200, 28, 5, "cpu", max_keys=keys + 1)  # heads not grouped
+    assert kernels.prefill_plan_pays(1, 200, 28, 4, "cpu", max_keys=keys + 1, dtype=torch.float32)
+    # fp32 groups wider than its kernel's 64 columns are refused, not planned
+    assert not kernels.prefill_plan_pays(1, 200, 65, 1, "cpu", max_keys=keys + 1, dtype=torch.float32)
 
 
 def test_seam_folds_the_write_only_for_rows_the_prefill_kernel_can_take():
