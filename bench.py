@@ -60,6 +60,7 @@ import torch
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
+MFMA_F32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, published
 METRIC = "paged decode attn µs/call + achieved KV HBM GB/s (% of peak), Qwen2.5-7B shape"
 
 
@@ -84,6 +85,8 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--placement", choices=("global", "share-groups"), default="global",
                    help="prefill: the work plan's placement -- one global heaviest-first order, or each "
                    "(shared-prefix group, KV head) on one XCD (fewer bytes fetched)")
+    p.add_argument("--dtype", choices=("bf16", "fp32"), default="bf16",
+                   help="prefill: the chunks' dtype (fp32: the fp32 kernel, planned with IR_PLAN_F32)")
     p.add_argument("--layers", type=int, default=28,
                    help="calls per decode / prefill plan (layers of one step sharing its metadata)")
     p.add_argument("--cpu-iters", type=int, default=5, help="timed CPU-baseline iterations (0 = skip)")
@@ -344,10 +347,15 @@ def _traffic(name: str) -> tuple[int | None, str | None]:
 
 def _bench_prefill(args) -> dict:
     """8 x 512-token chunks after cached prefixes: one prefill call per step."""
-    from infrared_amd import kernels
-    from infrared_amd.workloads import make_prefill_case
+    import dataclasses
 
-    case = make_prefill_case("qwen7b-prefill", "cuda", rotations=args.rotations)
+    from infrared_amd import kernels
+    from infrared_amd.workloads import PREFILL_CONFIGS, make_prefill_case
+
+    f32 = args.dtype == "fp32"
+    base = PREFILL_CONFIGS["qwen7b-prefill"]
+    case = make_prefill_case(dataclasses.replace(base, dtype=torch.float32) if f32 else base, "cuda",
+                             rotations=args.rotations)
     cfg = case.config
     out = torch.empty_like(case.q)
     total_q = case.q.shape[0]
@@ -355,7 +363,7 @@ def _bench_prefill(args) -> dict:
     # every --layers calls as an engine step would
     planned = args.schedule == "planned" or (args.schedule == "auto" and kernels.prefill_plan_pays(
         cfg.num_seqs, cfg.chunk, cfg.num_q_heads, cfg.num_kv_heads,
-        max_keys=case.block_tables[0].shape[1] * cfg.block_size))
+        max_keys=case.block_tables[0].shape[1] * cfg.block_size, dtype=cfg.dtype))
     plan_buf = torch.empty(max(256, kernels.prefill_plan_bytes(cfg.num_seqs, cfg.chunk, cfg.num_q_heads,
                                                                cfg.num_kv_heads, cfg.head_dim)),
                            dtype=torch.uint8, device="cuda")
@@ -366,7 +374,7 @@ def _bench_prefill(args) -> dict:
             bt = case.block_tables[i % len(case.block_tables)]
             plan[0] = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, bt, total_q, cfg.chunk, cfg.block_size,
                                            cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim, buf=plan_buf,
-                                           share_groups=args.placement == "share-groups")
+                                           share_groups=args.placement == "share-groups", dtype=cfg.dtype)
         kernels.paged_prefill(case.q, case.k_cache, case.v_cache, case.block_tables[i % len(case.block_tables)],
                               case.cu_seqlens_q, case.q_start, cfg.chunk, cfg.block_size, cfg.scale, out=out,
                               plan=plan[0])
@@ -396,22 +404,25 @@ def _bench_prefill(args) -> dict:
                "min_us": round(t_lo * 1e6, 1), "max_us": round(t_hi * 1e6, 1), **_cpu_host(), "kind": "port",
                "algorithmic_flops": fl, "executed_flops": fl_exec,
                "sample": f"sequence 0 only ({n} queries after a {pre}-token prefix), naive gather+repeat_kv+masked "
-               f"softmax in bf16, median of {args.cpu_iters} after 1 warm-up, torch CPU"}
+               f"softmax in {args.dtype}, median of {args.cpu_iters} after 1 warm-up, torch CPU"}
+    peak = MFMA_F32_PEAK_TFLOPS if f32 else MFMA_BF16_PEAK_TFLOPS
+    traffic_name = ("prefill_f32_qwen7b-prefill" if f32 else "prefill_qwen7b-prefill") + (
+        "" if args.placement == "global" else "-share-groups")
     return {
-        "metric": "paged prefill TFLOP/s (unmasked pairs), 8 x 512-token chunks after cached prefixes, Qwen2.5-7B shape",
+        "metric": "paged prefill TFLOP/s (unmasked pairs), 8 x 512-token chunks after cached prefixes, Qwen2.5-7B shape"
+                  + (", fp32" if f32 else ""),
         "value": round(tflops, 2), "unit": "TFLOP/s", "us_per_call": round(ms * 1e3, 2),
         "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16", "data": "synthetic",
+        "dtype": "f32" if f32 else "bf16", "data": "synthetic",
         "config": {"workload": f"{cfg.name}: {cfg.num_seqs} chunks of {cfg.chunk} after prefixes {case.prefixes}, "
                    f"{cfg.num_q_heads}q/{cfg.num_kv_heads}kv heads, head_dim {cfg.head_dim}, block {cfg.block_size}",
                    "flops_per_call": case.flops, "kv_bytes_per_call": case.kv_bytes, "rotations": args.rotations,
                    "schedule": "work plan (heaviest first, heavy items cut)" if planned else "unplanned",
                    "placement": args.placement if planned else None,
                    "layers_per_plan": args.layers if planned else None},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "measured_peak": _measured_peak("mfma"),
-                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": _traffic("prefill_qwen7b-prefill" if args.placement == "global"
-                                                             else "prefill_qwen7b-prefill-share-groups")[0],
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
+                     "measured_peak": _measured_peak("mfma", torch.float32 if f32 else torch.bfloat16),
+                     "frac": round(tflops / peak, 4), "traffic": _traffic(traffic_name)[0],
                      "timed": f"prefill call, {args.mode} launches, events on the launch stream"},
         "cpu_baseline": cpu,
     }
@@ -1016,13 +1027,13 @@ def _bench_reference_form(args) -> dict:
     }
 
 
-def _measured_peak(bound: str) -> dict:
+def _measured_peak(bound: str, dtype: torch.dtype = torch.bfloat16) -> dict:
     """The roof the kernel is held against, measured on this device beside the
     published figure. HBM-bound kernels: a read-only stream of 4 GiB with the
     decode kernels' load form (``ir_hbm_read``: non-temporal 16-byte loads,
     ``value``) and a 1 GiB device-to-device copy (read + write bytes). MFMA-bound
-    ones: an 8192^3 bf16 matmul through torch's BLAS. Events around 10 runs
-    after 3 warm-ups; the buffers exceed the 256 MB MALL."""
+    ones: an 8192^3 matmul of the kernel's dtype through torch's BLAS. Events
+    around 10 runs after 3 warm-ups; the buffers exceed the 256 MB MALL."""
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
     def rate(run, work):
@@ -1050,9 +1061,10 @@ def _measured_peak(bound: str) -> dict:
         return {"value": read, "unit": "GB/s", "how": "4 GiB read-only stream (ir_hbm_read, non-temporal 16 B loads)",
                 "copy": copy, "copy_how": "1 GiB device copy, read + write bytes"}
     n = 8192
-    x = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
-    y = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
-    return {"value": rate(lambda: x @ y, 2 * n**3 / 1e12), "unit": "TFLOP/s", "how": "8192^3 bf16 matmul (torch BLAS)"}
+    x = torch.randn(n, n, device="cuda", dtype=dtype)
+    y = torch.randn(n, n, device="cuda", dtype=dtype)
+    name = "fp32" if dtype == torch.float32 else "bf16"
+    return {"value": rate(lambda: x @ y, 2 * n**3 / 1e12), "unit": "TFLOP/s", "how": f"8192^3 {name} matmul (torch BLAS)"}
 
 
 def _time_eager(call, args) -> float:
