@@ -16,30 +16,37 @@ DEV = "cuda"
 SMALL = MixedConfig("mixed-small", 3, 12, 1, 300, 2, 64, 40, 28, 4, 128, 16, torch.bfloat16, seed=9)
 # 72 decode rows x 4 KV heads >= one unit per CU: the decode rows take the planned schedule
 WIDE = MixedConfig("mixed-wide", 2, 72, 1, 600, 1, 64, 40, 28, 4, 128, 16, torch.bfloat16, seed=10)
+# fp32 (the reference's fp32 path): 72 decode rows on the plan, two 300-token
+# chunks after 1,100 cached tokens on the fp32 prefill kernel's own plan
+WIDE32 = MixedConfig("mixed-wide-f32", 2, 72, 1, 600, 2, 300, 1100, 28, 4, 64, 16, torch.float32, seed=11)
 
 
-def _oracle_step(cfg, pool_k, pool_v, batch, inputs):
+def _oracle_step(cfg, pool_k, pool_v, batch, inputs, compute_dtype=torch.float32):
     """Scatter then attend, layer by layer, on CPU copies of the pool."""
     outs = []
     for layer in range(cfg.num_layers):
         k, v = pool_k[layer], pool_v[layer]
         O.pool_write(k, v, inputs.k_new[layer].cpu(), inputs.v_new[layer].cpu(), batch.write_slots.cpu())
         dec = O.decode_reference(inputs.q_dec[layer].cpu(), k, v, batch.dec_tables.cpu(), batch.dec_ctx.cpu(),
-                                 cfg.block_size, cfg.scale)
+                                 cfg.block_size, cfg.scale, compute_dtype=compute_dtype)
         pre = O.prefill_reference(inputs.q_pre[layer].cpu(), k, v, batch.pre_tables.cpu(), batch.cu_seqlens_q.cpu(),
-                                  batch.q_start.cpu(), cfg.block_size, cfg.scale)
+                                  batch.q_start.cpu(), cfg.block_size, cfg.scale, compute_dtype=compute_dtype)
         outs.append((dec, pre))
     return outs
 
 
-@pytest.mark.parametrize("config,planned", [(SMALL, False), (WIDE, True)])
+@pytest.mark.parametrize("config,planned", [(SMALL, False), (WIDE, True), (WIDE32, True)])
 @pytest.mark.parametrize("mode", ["fused-write", "separate-write", "overlap"])
 def test_mixed_step_eager_matches_oracle_and_graph_replays(mode, config, planned):
     """Both decode schedules inside the step: the fixed partitions (12 rows) and
     the plan built once per step and captured with the layers (72 rows); the
     step's K/V write inside the prefill launch (the default), as its own
-    launch, and with the chunks on a second stream."""
+    launch, and with the chunks on a second stream. In fp32 (1e-4 against an
+    fp64 restatement) the prefill launch writes the rows first, then attends
+    on its own plan."""
     cfg, pool, batch, inputs = make_mixed_case(config, DEV)
+    f32 = cfg.dtype == torch.float32
+    tol = 1e-4 if f32 else 2e-2
     pk = [pool.k[i].cpu().clone() for i in range(cfg.num_layers)]
     pv = [pool.v[i].cpu().clone() for i in range(cfg.num_layers)]
     step = MixedStep(pool, batch, inputs, cfg.scale, overlap=mode == "overlap", fused=mode == "fused-write")
@@ -48,12 +55,14 @@ def test_mixed_step_eager_matches_oracle_and_graph_replays(mode, config, planned
     step.eager()
     torch.cuda.synchronize()
     assert step.err.item() == 0
-    ref = _oracle_step(cfg, pk, pv, batch, inputs)
+    if f32:
+        assert step.ordered  # the chunks' fp32 plan (1,100 cached keys)
+    ref = _oracle_step(cfg, pk, pv, batch, inputs, torch.float64 if f32 else torch.float32)
     for layer in range(cfg.num_layers):
         assert torch.equal(pool.k[layer].cpu(), pk[layer]) and torch.equal(pool.v[layer].cpu(), pv[layer])
         dec, pre = ref[layer]
-        assert (step.out_dec[layer].float().cpu() - dec).abs().max().item() <= 2e-2
-        assert (step.out_pre[layer].float().cpu() - pre).abs().max().item() <= 2e-2
+        assert (step.out_dec[layer].double().cpu() - dec).abs().max().item() <= tol
+        assert (step.out_pre[layer].double().cpu() - pre).abs().max().item() <= tol
     eager_dec, eager_pre = step.out_dec.clone(), step.out_pre.clone()
     step.capture()
     for _ in range(3):
