@@ -215,10 +215,11 @@ def test_prefill_fp32_reloads_block_ids_and_runs_its_plan():
 
 @pytest.mark.parametrize("share_groups", [False, True])
 def test_prefill_fp32_planned_long_prefixes(share_groups):
-    """fp32 chunks after long prefixes that pairs share, on a plan (global
-    order or share groups): cut items merged within 1e-4 of the restatement."""
-    cfg = PrefillConfig("pf32-plan", 4, 0, 28, 4, 128, 16, torch.float32, 0, seed=21)
-    case = make_prefill_case(cfg, DEV, prefixes=[3000, 3500, 200, 5000], q_lens=[64, 17, 96, 40])
+    """fp32 chunks after long prefixes that pairs share, and an empty chunk, on
+    a plan (global order or share groups): cut items merged within 1e-4 of the
+    restatement."""
+    cfg = PrefillConfig("pf32-plan", 5, 0, 28, 4, 128, 16, torch.float32, 0, seed=21)
+    case = make_prefill_case(cfg, DEV, prefixes=[3000, 3500, 200, 5000, 64], q_lens=[64, 17, 96, 40, 0])
     plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.block_tables[0], case.q.shape[0], 96,
                                 cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim,
                                 share_groups=share_groups, dtype=torch.float32)
