@@ -149,8 +149,9 @@ def prefill_context(
 
     ``with_mask`` also builds the reference's packed metadata -- ``gather_slots``
     ``[1, K]`` over the union of the sequences' keys and the varlen mask
-    ``[1, 1, Q, K]`` -- for the gather_slots + mask kernel (fp32, or
-    ``use_triton=False``); it is quadratic in the step size.
+    ``[1, 1, Q, K]`` -- for the gather_slots + mask kernel
+    (``use_triton=False``) or the reference-form path; it is quadratic in the
+    step size.
     """
     dev = pool.device
     bs = pool.block_size
