@@ -213,18 +213,21 @@ def test_prefill_fp32_reloads_block_ids_and_runs_its_plan():
         _check_f32(case, plan16)
 
 
-@pytest.mark.parametrize("share_groups", [False, True])
-def test_prefill_fp32_planned_long_prefixes(share_groups):
+def test_prefill_fp32_planned_long_prefixes():
     """fp32 chunks after long prefixes that pairs share, and an empty chunk, on
-    a plan (global order or share groups): cut items merged within 1e-4 of the
-    restatement."""
+    a plan: cut items merged within 1e-4 of the restatement, and a plan
+    placing share groups gives the same outputs bit for bit (the placement
+    changes the schedule only)."""
     cfg = PrefillConfig("pf32-plan", 5, 0, 28, 4, 128, 16, torch.float32, 0, seed=21)
     case = make_prefill_case(cfg, DEV, prefixes=[3000, 3500, 200, 5000, 64], q_lens=[64, 17, 96, 40, 0])
-    plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.block_tables[0], case.q.shape[0], 96,
-                                cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim,
-                                share_groups=share_groups, dtype=torch.float32)
-    assert max(_cut_entries(plan, 8)) > 1
-    _check_f32(case, plan)
+    outs = []
+    for share_groups in (False, True):
+        plan = kernels.prefill_plan(case.cu_seqlens_q, case.q_start, case.block_tables[0], case.q.shape[0], 96,
+                                    cfg.block_size, cfg.num_q_heads, cfg.num_kv_heads, cfg.head_dim,
+                                    share_groups=share_groups, dtype=torch.float32)
+        assert max(_cut_entries(plan, 8)) > 1
+        outs.append(_check_f32(case, plan))
+    assert torch.equal(outs[0], outs[1])
 
 
 def test_prefill_fp32_flags_bad_block_ids_and_refuses_wide_groups():
